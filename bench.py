@@ -1,0 +1,299 @@
+"""Benchmark: effective quantized-payload GB/s of the MatVec hot path on one MI355X.
+
+Headline workload: Ternary2 MatVec 4096x4096, block 128, batch 1 (FP32 weights ~N(0,1) from seed 1729,
+quantized by Ternary2Matrix.Quantize; x ~ U(-1, 1)). One 4096x4096 matrix is 4.72 MB, far below the
+256 MB Infinity Cache and below launch latency, so a step is one pass over G distinct resident copies
+of it (G * 4.72 MB >= 1 GiB), issued as ONE grouped launch (satori_hip_group_execute): every step streams
+>= 1 GiB of payload from HBM. GB/s = G * payload bytes / step time (the reference's method: payload
+bytes including scales and padding, activations and outputs excluded). Inputs are resident in HBM
+before the timed region; no host transfer is timed.
+
+The same line carries, labelled:
+  formats:   the same measurement for Q8_0 4096^2, Q4_0 11008x4096 and 4096x11008, Q4_K and Q6_K at the
+             Qwen-1.5B shapes (K formats on the Q8_K integer path: quantize + product per step),
+             and Ternary2 at the other block sizes;
+  single:    one launch per matrix (rotating copies), which includes launch gaps;
+  cache:     the grouped launch over G references to ONE copy (cache resident, not an HBM figure);
+  roofline:  for the headline kernel, from HIP events on the launch stream;
+  cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import satori_amd as S  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+ROTATION_BYTES = 1 << 30
+BQ = S.BlockQuantization
+METRIC = "effective quantized-payload GB/s (% of MI355X HBM peak) per format, 4096² batch 1"
+PUBLISHED_AVX2_T2_4096_B128 = 1.31  # GB/s, Ternary2 AVX2 4096^2 B128, docs/benchmarks/avx2-2026-10-12 run 1
+
+
+class HipEvents:
+    """hipEvent timing on a given stream, through the HIP runtime the library already loaded."""
+
+    def __init__(self):
+        S._ffi.lib()
+        self.rt = ctypes.CDLL("libamdhip64.so.7")
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.rt.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, event, stream):
+        assert self.rt.hipEventRecord(event, ctypes.c_void_p(stream)) == 0
+
+    def elapsed_ms(self, start, stop) -> float:
+        assert self.rt.hipEventSynchronize(stop) == 0
+        ms = ctypes.c_float()
+        assert self.rt.hipEventElapsedTime(ctypes.byref(ms), start, stop) == 0
+        return ms.value
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def make_ternary2(rows, columns, block, seed=1729):
+    g = rng(seed)
+    w = g.standard_normal((rows, columns), dtype=np.float32)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    return S.Ternary2Matrix.quantize(w, rows, columns, block).data, x
+
+
+def make_gguf(fmt, rows, columns, seed=20261014):
+    g = rng(seed + rows + columns)
+    w = (g.standard_normal((rows, columns), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = g.standard_normal(columns, dtype=np.float32)
+    return S.quantize_weights(w, rows, columns, fmt), x
+
+
+class Case:
+    """G resident copies of one matrix plus device input/outputs, and the launches to time."""
+
+    def __init__(self, ctx, name, create, payload_bytes, rows, columns, x, quantized, copies=None):
+        self.ctx, self.name, self.payload_bytes, self.rows, self.columns = ctx, name, payload_bytes, rows, columns
+        self.quantized = quantized
+        self.copies = copies or max(1, math.ceil(ROTATION_BYTES / payload_bytes))
+        first = create()
+        self.mats = [first] + [first.clone() for _ in range(self.copies - 1)]
+        self.dx = ctx.alloc(x.nbytes)
+        ctx.upload(self.dx, x)
+        self.dy = [ctx.alloc(4 * rows) for _ in range(self.copies)]
+        self.group = S.HipGroup(ctx, self.mats, [self.dx] * self.copies, self.dy, quantized)
+        self.cache_group = S.HipGroup(ctx, [first] * self.copies, [self.dx] * self.copies, self.dy, quantized)
+
+    def run_group(self):
+        self.group.execute()
+
+    def run_cache(self):
+        self.cache_group.execute()
+
+    def run_single(self):
+        for m, y in zip(self.mats, self.dy):
+            if self.quantized:
+                m.execute_batch_device(self.dx, 1, y)
+            else:
+                m.execute_device(self.dx, y)
+
+    def close(self):
+        self.group.dispose()
+        self.cache_group.dispose()
+        for m in self.mats:
+            m.dispose()
+        for y in self.dy:
+            self.ctx.free(y)
+        self.ctx.free(self.dx)
+
+
+def time_launches(ctx, events, fn, steps, warmup) -> float:
+    """Milliseconds per call of fn() over `steps` timed calls on the context stream."""
+    for _ in range(warmup):
+        fn()
+    ctx.synchronize()
+    start, stop = events.event(), events.event()
+    events.record(start, ctx.stream)
+    for _ in range(steps):
+        fn()
+    events.record(stop, ctx.stream)
+    ms = events.elapsed_ms(start, stop)
+    ctx.synchronize()
+    return ms / steps
+
+
+def progress(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
+    progress(f"{case.name}: {case.copies} copies x {case.payload_bytes} B")
+    group_ms = time_launches(ctx, events, case.run_group, steps, warmup)
+    step_bytes = case.copies * case.payload_bytes
+    out = {
+        "shape": [case.rows, case.columns],
+        "payload_bytes": case.payload_bytes,
+        "copies": case.copies,
+        "gbs": step_bytes / (group_ms * 1e-3) / 1e9,
+        "launch_us": group_ms * 1e3,
+        "rows_per_s": case.copies * case.rows / (group_ms * 1e-3),
+    }
+    out["pct_hbm"] = 100.0 * out["gbs"] / HBM_PEAK_GBS
+    cache_ms = time_launches(ctx, events, case.run_cache, max(2, steps // 2), 1)
+    out["cache_resident_gbs"] = step_bytes / (cache_ms * 1e-3) / 1e9
+    if single:
+        single_ms = time_launches(ctx, events, case.run_single, max(2, steps // 4), 1)
+        out["single_launch_us"] = single_ms * 1e3 / case.copies
+        out["single_launch_gbs"] = step_bytes / (single_ms * 1e-3) / 1e9
+    return out
+
+
+def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
+    """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample."""
+    from oracle import oracle as O
+
+    try:
+        core = sorted(os.sched_getaffinity(0))[0]
+        os.sched_setaffinity(0, {core})
+    except (AttributeError, OSError):
+        core = None
+    y = np.zeros(rows, np.float32)
+    O.t2_matvec_avx2(payload, rows, columns, block, x, y)  # warm
+    iterations, start = 0, time.perf_counter()
+    samples = []
+    while time.perf_counter() - start < seconds:
+        t0 = time.perf_counter()
+        O.t2_matvec_avx2(payload, rows, columns, block, x, y)
+        samples.append(time.perf_counter() - t0)
+        iterations += 1
+    elapsed = time.perf_counter() - start
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {
+        "value": payload.size * iterations / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"restated reference AVX2 Ternary2Avx2Kernel (oracle/satori_oracle_avx2.c, -O3 -mavx2 -mfma) "
+                   f"on the same 4096x4096 B128 payload and x, {iterations} MatVecs over {elapsed:.1f} s, "
+                   f"1 thread pinned to core {core}; min {min(samples) * 1e3:.3f} ms, "
+                   f"median {sorted(samples)[len(samples) // 2] * 1e3:.3f} ms; host: {model}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--quick", action="store_true", help="headline workload only, no other formats")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs the MatVec on a single MI355X "
+              "(multi-GPU row sharding is design-only); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    ctx = S.HipContext(0)
+    events = HipEvents()
+
+    rows = columns = 4096
+    block = 128
+    payload, x = make_ternary2(rows, columns, block)
+    head = Case(ctx, "ternary2-4096-b128", lambda: ctx.create_ternary2(rows, columns, block, payload),
+                payload.size, rows, columns, x, False)
+    headline = measure(ctx, events, head, args.steps, args.warmup)
+    # Timed region of the headline itself, for the contract fields.
+    ms_per_step = headline["launch_us"] * 1e-3
+    head.close()
+
+    formats = {"ternary2-4096-b128": headline}
+    if not args.quick:
+        for b in (64, 256):
+            p, xb = make_ternary2(rows, columns, b)
+            c = Case(ctx, f"ternary2-4096-b{b}", lambda: ctx.create_ternary2(rows, columns, b, p), p.size, rows,
+                     columns, xb, False)
+            formats[c.name] = measure(ctx, events, c, max(20, args.steps // 4), 5, single=False)
+            c.close()
+        for fmt, r, cc, quantized, label in (
+                (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
+                (BQ.Q4_0, 11008, 4096, False, "q4_0-11008x4096"),
+                (BQ.Q4_0, 4096, 11008, False, "q4_0-4096x11008"),
+                (BQ.Q4_K, 8960, 1536, True, "q4_k-8960x1536-q8k"),
+                (BQ.Q4_K, 1536, 8960, True, "q4_k-1536x8960-q8k"),
+                (BQ.Q6_K, 8960, 1536, True, "q6_k-8960x1536-q8k"),
+                (BQ.Q6_K, 1536, 8960, True, "q6_k-1536x8960-q8k")):
+            data, xf = make_gguf(fmt, r, cc)
+            shape = S.QuantizedMatrixShape(r, cc, fmt)
+            c = Case(ctx, label, lambda: ctx.create(data, shape), data.size, r, cc, xf, quantized)
+            formats[label] = measure(ctx, events, c, max(20, args.steps // 4), 5, single=False)
+            c.close()
+
+    progress("cpu baseline")
+    cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
+    value = headline["gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / PUBLISHED_AVX2_T2_4096_B128, 1),
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"Ternary2 MatVec 4096x4096 block 128, batch 1, FP32 x; one step = one grouped launch "
+                         f"over {headline['copies']} resident copies ({headline['copies'] * payload.size / 1e9:.2f} GB "
+                         f"of payload) so every step streams from HBM"),
+            "payload_bytes_per_matvec": int(payload.size),
+            "seed": 1729,
+            "pct_of_hbm_peak": round(headline["pct_hbm"], 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(value, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "gemv_float_kernel<Ternary2Chunk<128>, 64, true, true> (grouped)",
+            "launch_us": round(headline["launch_us"], 2),
+            "algorithmic_bytes_per_launch": headline["copies"] * int(payload.size),
+        },
+        "cpu_baseline": cpu,
+        "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in formats.items()},
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,194 @@
+/*
+ * satori_hip.h: C ABI of libsatori_hip.so, the MI355X (gfx950) backend for Satori's quantized
+ * MatVec hot path (Ternary2 blocks of 64/128/256, GGUF Q8_0 / Q4_0 / Q4_K / Q6_K).
+ *
+ * The library is the drop-in under the reference's C# surfaces. Each entry point below names the
+ * reference member it stands in for (paths relative to the reference repository root). Plain
+ * pointers and sizes only; no C++ or torch types cross this boundary.
+ *
+ * Conventions
+ *  - Every function returns a satori_hip_status. A non-zero status maps 1:1 to the exception the
+ *    reference throws for the same condition; satori_hip_last_error() returns the message (per
+ *    calling thread, valid until that thread's next call).
+ *  - Host-pointer MatVec calls are synchronous and commit the output only on success: on any
+ *    failure the caller's output buffer is left untouched
+ *    (src/Satori.Core/IQuantizedMatrix.cs:6).
+ *  - Weight payloads are copied (uploaded) before the create call returns; the caller may release
+ *    or unmap them immediately afterwards (docs/vulkan-backend-v1.md:21).
+ *  - A context serialises its calls with a mutex and owns one HIP stream at default priority.
+ *    Calls on different contexts may run concurrently.
+ */
+#ifndef SATORI_HIP_H
+#define SATORI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SATORI_HIP_ABI_VERSION 1
+
+typedef struct satori_hip_context satori_hip_context;
+typedef struct satori_hip_matrix satori_hip_matrix;
+typedef struct satori_hip_group satori_hip_group;
+
+typedef enum satori_hip_status {
+    SATORI_HIP_OK = 0,
+    SATORI_HIP_E_ARGUMENT = 1,                 /* System.ArgumentException */
+    SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE = 2,    /* System.ArgumentOutOfRangeException */
+    SATORI_HIP_E_INVALID_DATA = 3,             /* System.IO.InvalidDataException */
+    SATORI_HIP_E_NOT_SUPPORTED = 4,            /* System.NotSupportedException */
+    SATORI_HIP_E_OBJECT_DISPOSED = 5,          /* System.ObjectDisposedException */
+    SATORI_HIP_E_PLATFORM_NOT_SUPPORTED = 6,   /* System.PlatformNotSupportedException (no gfx950 device) */
+    SATORI_HIP_E_OUT_OF_MEMORY = 7,            /* System.OutOfMemoryException */
+    SATORI_HIP_E_DEVICE = 8,                   /* System.InvalidOperationException: HIP runtime failure */
+    SATORI_HIP_E_OVERFLOW = 9,                 /* System.OverflowException (checked arithmetic) */
+    SATORI_HIP_E_ARGUMENT_NULL = 10            /* System.ArgumentNullException */
+} satori_hip_status;
+
+/* Values of Satori.Core.BlockQuantization (src/Satori.Core/BlockQuantization.cs:3), plus Ternary2. */
+typedef enum satori_hip_format {
+    SATORI_HIP_Q8_0 = 0,
+    SATORI_HIP_Q4_0 = 1,
+    SATORI_HIP_Q4_K = 2,
+    SATORI_HIP_Q6_K = 3,
+    SATORI_HIP_TERNARY2 = 16
+} satori_hip_format;
+
+/* ---- library ---- */
+
+int satori_hip_abi_version(void);
+
+/* Message of the calling thread's last failure ("" after success). */
+const char* satori_hip_last_error(void);
+
+/* Number of gfx950 devices visible to the process. */
+int satori_hip_device_count(int* count);
+
+/* ---- context: stands in for VulkanContext.TryCreate / Dispose
+ *      (src/Satori.Backends.Vulkan/VulkanContext.cs:57), the IQuantizedMatrixFactory owner ---- */
+
+int satori_hip_context_create(int device, satori_hip_context** context);
+/* Idempotent: NULL is accepted. Matrices created on the context must be destroyed first. */
+int satori_hip_context_destroy(satori_hip_context* context);
+/* The context's HIP stream (hipStream_t), for the *_device entry points and resident pipelines. */
+int satori_hip_context_stream(satori_hip_context* context, void** stream);
+
+/* ---- matrices ---- */
+
+/* Ternary2Matrix.FromPacked (src/Satori.Core/Ternary2Matrix.cs:73-81) + ValidatePayload (:83-101),
+ * then upload. Also the upload step of MappedTernary2Matrix (src/Satori.Core/MappedTernary2Matrix.cs:9-35):
+ * pass the mapped payload window. */
+int satori_hip_ternary2_create(satori_hip_context* context, int rows, int columns, int block_size,
+                               const void* payload, size_t payload_length, satori_hip_matrix** matrix);
+
+/* IQuantizedMatrixFactory.Create (src/Satori.Core/IQuantizedMatrixFactory.cs:6) with the
+ * QuantizedMatrixShape checks (src/Satori.Core/QuantizedMatrixShape.cs:5-22) and
+ * QuantizedMatVec.ValidatePayload (src/Satori.Core/QuantizedMatVec.cs:28-42), then upload. */
+int satori_hip_quantized_create(satori_hip_context* context, int rows, int columns, int format,
+                                const void* payload, size_t payload_length, satori_hip_matrix** matrix);
+
+/* MappedTernary2Matrix(path) (src/Satori.Core/MappedTernary2Matrix.cs:9-35): opens an STQ2 file,
+ * validates header and payload, uploads; corrupt files fail with SATORI_HIP_E_INVALID_DATA. */
+int satori_hip_ternary2_open(satori_hip_context* context, const char* path, satori_hip_matrix** matrix);
+
+/* A second resident copy of already validated weights (device-to-device; no reference counterpart):
+ * distinct copies for rotating-buffer measurements or for use from several streams. */
+int satori_hip_matrix_clone(satori_hip_matrix* source, satori_hip_matrix** clone);
+
+/* IDisposable.Dispose: idempotent per handle; NULL is accepted. */
+int satori_hip_matrix_destroy(satori_hip_matrix* matrix);
+
+/* Shape query: format is a satori_hip_format; block_size is 64/128/256 for Ternary2, else the
+ * format's block elements; byte_length is the payload length. Any out pointer may be NULL. */
+int satori_hip_matrix_shape(const satori_hip_matrix* matrix, int* rows, int* columns, int* format,
+                            int* block_size, int64_t* byte_length);
+
+/* ---- MatVec, host buffers, synchronous ----
+ * Ternary2MatVec.Execute (src/Satori.Core/Ternary2MatVec.cs:9), MappedTernary2Matrix.Execute
+ * (src/Satori.Core/MappedTernary2Matrix.cs:43), QuantizedMatVec.Execute
+ * (src/Satori.Core/QuantizedMatVec.cs:12), GgufQuantizedMatrix.Execute
+ * (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:38) and IQuantizedMatrix.Execute
+ * (src/Satori.Core/IQuantizedMatrix.cs:7): FP32 activations for every format (K formats use the
+ * float decode of Q4KCodec.DotBlock / Q6KCodec.DotBlock). input_length must equal columns and
+ * output_length rows; overlapping buffers and non-finite inputs are rejected (ArgumentException,
+ * as src/Satori.Backends.Vulkan/VulkanQ8Matrix.cs:82-83). */
+int satori_hip_matvec(satori_hip_matrix* matrix, const float* input, size_t input_length, float* output,
+                      size_t output_length);
+
+/* QuantizedMatVec.ExecuteBatch (src/Satori.Core/QuantizedMatVec.cs:104-120) and
+ * GgufQuantizedMatrix.ExecuteBatch (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:43-48):
+ * input [positions][columns] -> output [positions][rows]. K formats quantize each position to
+ * Q8_K on the device and use the integer product (at most 256 positions, as
+ * src/Satori.Core/QuantizedKAvx2Kernel.cs:50-51); Q8_0 / Q4_0 use the FP32 product. Ternary2 is
+ * rejected with SATORI_HIP_E_NOT_SUPPORTED (the reference has no batched Ternary2 product). */
+int satori_hip_matvec_batch(satori_hip_matrix* matrix, const float* input, size_t input_length, int positions,
+                            float* output, size_t output_length);
+
+/* Q8KCodec.QuantizeRow (src/Satori.Core/Q8KCodec.cs:85-93) on the device: columns a positive
+ * multiple of 256, output_length = columns / 256 * 292; bytes identical to the reference. */
+int satori_hip_quantize_q8k(satori_hip_context* context, const float* input, int columns, void* output,
+                            size_t output_length);
+
+/* ---- MatVec, device buffers, asynchronous (resident pipelines and benchmarks) ----
+ * Same arithmetic as the host-buffer calls. input/output are device pointers; the work is enqueued on
+ * `stream` (NULL = the context stream) and the call returns without waiting. No input validation
+ * beyond shapes; the caller keeps the buffers alive until the stream has passed the work. */
+int satori_hip_matvec_device(satori_hip_matrix* matrix, const float* input, float* output, void* stream);
+int satori_hip_matvec_batch_device(satori_hip_matrix* matrix, const float* input, int positions, float* output,
+                                   void* stream);
+
+/* ---- device buffers for the *_device entry points (no counterpart in the reference, whose buffers
+ *      are host spans; a resident caller needs device activations) ---- */
+
+int satori_hip_device_alloc(satori_hip_context* context, size_t bytes, void** device_ptr);
+int satori_hip_device_free(satori_hip_context* context, void* device_ptr);
+/* Copies `bytes` between host and device memory in the direction `kind` (1: host to device, 2: device to
+ * host, 3: device to device), ordered on the context stream, and waits for completion. */
+int satori_hip_copy(satori_hip_context* context, void* destination, const void* source, size_t bytes, int kind);
+/* Waits for all work enqueued on the context stream. */
+int satori_hip_synchronize(satori_hip_context* context);
+
+/* ---- projection groups: one launch for several matrices of one format and width ----
+ * Members share format, block size and column count (row counts may differ); member i reads
+ * inputs[i] and writes outputs[i] (device pointers fixed at creation). quantized_activations
+ * selects the Q8_K integer product for K formats (as ExecuteBatch at one position) instead of
+ * the FP32 one. This has no counterpart in the reference: it is the launch shape the decode step
+ * of DenseForward.Step (src/Satori.Core/Model/DenseForward.cs:100-162) needs for projections that
+ * share an input (q/k/v, gate/up). */
+int satori_hip_group_create(satori_hip_context* context, satori_hip_matrix* const* matrices, int count,
+                            const float* const* inputs, float* const* outputs, int quantized_activations,
+                            satori_hip_group** group);
+int satori_hip_group_execute(satori_hip_group* group, void* stream);
+int satori_hip_group_destroy(satori_hip_group* group);
+
+/* ---- host-only entry points (CPU; no device needed, never on the MatVec path) ---- */
+
+/* Ternary2Shape.ByteLength (src/Satori.Core/Ternary2Shape.cs:5-15) when format is SATORI_HIP_TERNARY2
+ * (block_size 64/128/256), else QuantizedMatrixShape.ByteLength (src/Satori.Core/QuantizedMatrixShape.cs:5-22;
+ * block_size ignored). Invalid shapes fail as the constructors do. */
+int satori_hip_payload_length(int format, int rows, int columns, int block_size, int64_t* length);
+
+/* Ternary2Matrix.FromPacked checks (src/Satori.Core/Ternary2Matrix.cs:73-101). */
+int satori_hip_ternary2_validate(int rows, int columns, int block_size, const void* payload, size_t payload_length);
+
+/* QuantizedMatrix constructor checks (src/Satori.Core/QuantizedMatrix.cs:8-13, QuantizedMatVec.cs:28-42). */
+int satori_hip_quantized_validate(int rows, int columns, int format, const void* payload, size_t payload_length);
+
+/* Ternary2Matrix.Quantize (src/Satori.Core/Ternary2Matrix.cs:38-71): FP32 weights [rows][columns] to a
+ * Ternary2 payload (absmean FP32 block scale, FP64 threshold); non-finite weights are rejected. */
+int satori_hip_ternary2_quantize(const float* weights, int rows, int columns, int block_size, void* payload,
+                                 size_t payload_length);
+
+/* Round-to-nearest Q8_0 / Q4_0 / Q4_K / Q6_K quantizers used to build seeded synthetic matrices. No
+ * counterpart in the reference, which only decodes these formats; the packing is the exact inverse of
+ * its decoders (Q4KCodec.GetScaleMin, Q4KCodec.DecodeBlock, Q6KCodec.DecodeBlock). */
+int satori_hip_quantize_weights(int format, const float* weights, int rows, int columns, void* payload,
+                                size_t payload_length);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SATORI_HIP_H */

@@ -1,0 +1,467 @@
+"""satori_amd: MI355X (gfx950) backend for Satori's quantized MatVec hot path.
+
+Host-side mirror of the reference's surfaces over the C ABI of libsatori_hip.so (include/satori_hip.h).
+Names, argument meaning and exceptions follow the reference (src/Satori.Core, src/Satori.Formats.Gguf):
+
+  Ternary2Matrix.quantize / from_packed / dequantize   Ternary2Matrix.cs:38-120
+  Ternary2MatVec.execute                              Ternary2MatVec.cs:9 (HIP backend)
+  MappedTernary2Matrix(path).execute                  MappedTernary2Matrix.cs:9-56 (HIP backend)
+  QuantizedMatrixShape, BlockQuantization             QuantizedMatrixShape.cs:5-33, BlockQuantization.cs:3
+  QuantizedMatVec.validate_payload / execute / execute_batch   QuantizedMatVec.cs:12-120 (HIP backend)
+  HipContext.create(payload, shape)                   IQuantizedMatrixFactory.Create (IQuantizedMatrixFactory.cs:6)
+  HipQuantizedMatrix.execute                          IQuantizedMatrix.Execute (IQuantizedMatrix.cs:7)
+  Q8KCodec.quantize_row                               Q8KCodec.cs:85-93 (on the device)
+
+Every MatVec runs on the GPU through the library; there is no CPU fallback. Importing this package needs
+the built library (``python -m satori_amd.build``); creating a HipContext needs a gfx950 device.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import threading
+
+import numpy as np
+
+from . import _ffi
+
+__all__ = [
+    "SatoriError", "ArgumentException", "ArgumentOutOfRangeException", "ArgumentNullException",
+    "InvalidDataException", "NotSupportedException", "ObjectDisposedException", "PlatformNotSupportedException",
+    "OutOfMemoryException", "InvalidOperationException", "OverflowException",
+    "BlockQuantization", "QuantizedMatrixShape", "Ternary2Matrix", "Ternary2MatVec", "MappedTernary2Matrix",
+    "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "Q8KCodec", "TERNARY2",
+    "device_count", "default_context", "payload_length", "quantize_weights",
+]
+
+TERNARY2 = 16
+
+
+# ---- exceptions: one class per status code, named after the reference's .NET exception ----
+
+class SatoriError(Exception):
+    status = -1
+
+    def __init__(self, message: str = ""):
+        super().__init__(message)
+        self.message = message
+
+
+class ArgumentException(SatoriError, ValueError):
+    status = 1
+
+
+class ArgumentOutOfRangeException(ArgumentException):
+    status = 2
+
+
+class InvalidDataException(SatoriError, IOError):
+    status = 3
+
+
+class NotSupportedException(SatoriError):
+    status = 4
+
+
+class ObjectDisposedException(SatoriError):
+    status = 5
+
+
+class PlatformNotSupportedException(NotSupportedException):
+    status = 6
+
+
+class OutOfMemoryException(SatoriError, MemoryError):
+    status = 7
+
+
+class InvalidOperationException(SatoriError):
+    status = 8
+
+
+class OverflowException(SatoriError, ArithmeticError):
+    status = 9
+
+
+class ArgumentNullException(ArgumentException):
+    status = 10
+
+
+_BY_STATUS = {cls.status: cls for cls in (
+    ArgumentException, ArgumentOutOfRangeException, InvalidDataException, NotSupportedException,
+    ObjectDisposedException, PlatformNotSupportedException, OutOfMemoryException, InvalidOperationException,
+    OverflowException, ArgumentNullException)}
+
+
+def _check(status: int) -> None:
+    if status:
+        message = _ffi.lib().satori_hip_last_error().decode("utf-8", "replace")
+        raise _BY_STATUS.get(status, SatoriError)(message)
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _as_u8(data) -> np.ndarray:
+    if isinstance(data, (bytes, bytearray, memoryview)):
+        return np.frombuffer(bytes(data), dtype=np.uint8)
+    return np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+
+
+def _as_f32(a) -> np.ndarray:
+    arr = np.asarray(a)
+    if arr.dtype != np.float32 or not arr.flags.c_contiguous:
+        raise ArgumentException("Vectors must be contiguous float32 arrays.")
+    return arr
+
+
+# ---- shapes ----
+
+class BlockQuantization(enum.IntEnum):
+    """src/Satori.Core/BlockQuantization.cs:3."""
+    Q8_0 = 0
+    Q4_0 = 1
+    Q4_K = 2
+    Q6_K = 3
+
+
+_GEOMETRY = {BlockQuantization.Q8_0: (32, 34), BlockQuantization.Q4_0: (32, 18),
+             BlockQuantization.Q4_K: (256, 144), BlockQuantization.Q6_K: (256, 210)}
+
+
+def payload_length(fmt: int, rows: int, columns: int, block_size: int = 0) -> int:
+    """Ternary2Shape / QuantizedMatrixShape byte length, with the constructors' checks."""
+    out = ctypes.c_int64()
+    _check(_ffi.lib().satori_hip_payload_length(int(fmt), rows, columns, block_size, ctypes.byref(out)))
+    return out.value
+
+
+class QuantizedMatrixShape:
+    """src/Satori.Core/QuantizedMatrixShape.cs:5-33."""
+
+    def __init__(self, rows: int, columns: int, fmt: BlockQuantization):
+        self.format = BlockQuantization(fmt) if int(fmt) in _GEOMETRY else fmt
+        self.byte_length = payload_length(int(fmt), rows, columns)
+        self.rows, self.columns = rows, columns
+        self.block_elements, self.block_bytes = _GEOMETRY[self.format]
+
+    def __eq__(self, other):
+        return isinstance(other, QuantizedMatrixShape) and (self.rows, self.columns, self.format) == (
+            other.rows, other.columns, other.format)
+
+    def __repr__(self):
+        return f"QuantizedMatrixShape({self.rows}, {self.columns}, {self.format.name})"
+
+
+def quantize_weights(weights, rows: int, columns: int, fmt: BlockQuantization) -> np.ndarray:
+    """Round-to-nearest Q8_0/Q4_0/Q4_K/Q6_K payload for synthetic matrices (no reference counterpart)."""
+    w = np.ascontiguousarray(weights, dtype=np.float32).reshape(-1)
+    if w.size != rows * columns:
+        raise ArgumentException("Weights must match matrix dimensions.")
+    out = np.zeros(payload_length(int(fmt), rows, columns), dtype=np.uint8)
+    _check(_ffi.lib().satori_hip_quantize_weights(int(fmt), _ptr(w), rows, columns, _ptr(out), out.size))
+    return out
+
+
+# ---- device ----
+
+def device_count() -> int:
+    n = ctypes.c_int()
+    _check(_ffi.lib().satori_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+class HipContext:
+    """One gfx950 device, one stream: the IQuantizedMatrixFactory of this backend
+    (stands where VulkanContext does, src/Satori.Backends.Vulkan/VulkanContext.cs:11)."""
+
+    def __init__(self, device: int = 0):
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_context_create(device, ctypes.byref(handle)))
+        self._handle = handle
+        self.device = device
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._handle
+
+    @property
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_context_stream(self._handle, ctypes.byref(s)))
+        return s.value or 0
+
+    def create(self, payload, shape: QuantizedMatrixShape) -> "HipQuantizedMatrix":
+        """IQuantizedMatrixFactory.Create: validates, copies to the device, returns executable weights."""
+        data = _as_u8(payload)
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_quantized_create(self._handle, shape.rows, shape.columns, int(shape.format),
+                                                      _ptr(data), data.size, ctypes.byref(handle)))
+        return HipQuantizedMatrix(self, handle)
+
+    def create_ternary2(self, rows: int, columns: int, block_size: int, payload) -> "HipQuantizedMatrix":
+        data = _as_u8(payload)
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_ternary2_create(self._handle, rows, columns, block_size, _ptr(data), data.size,
+                                                     ctypes.byref(handle)))
+        return HipQuantizedMatrix(self, handle)
+
+    def open_ternary2(self, path: str) -> "HipQuantizedMatrix":
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_ternary2_open(self._handle, str(path).encode(), ctypes.byref(handle)))
+        return HipQuantizedMatrix(self, handle)
+
+    def quantize_q8k(self, x) -> np.ndarray:
+        """Q8KCodec.QuantizeRow on the device (src/Satori.Core/Q8KCodec.cs:85-93)."""
+        xv = _as_f32(x).reshape(-1)
+        out = np.zeros((xv.size // 256) * 292 if xv.size % 256 == 0 else 0, dtype=np.uint8)
+        _check(_ffi.lib().satori_hip_quantize_q8k(self._handle, _ptr(xv), xv.size, _ptr(out), out.size))
+        return out
+
+    # Device buffers (for the *_device entry points and groups).
+    def alloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_device_alloc(self._handle, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def free(self, device_ptr: int) -> None:
+        _check(_ffi.lib().satori_hip_device_free(self._handle, ctypes.c_void_p(device_ptr)))
+
+    def upload(self, device_ptr: int, array: np.ndarray) -> None:
+        a = np.ascontiguousarray(array)
+        _check(_ffi.lib().satori_hip_copy(self._handle, ctypes.c_void_p(device_ptr), _ptr(a), a.nbytes, 1))
+
+    def download(self, array: np.ndarray, device_ptr: int) -> np.ndarray:
+        if not array.flags.c_contiguous:
+            raise ArgumentException("Destination must be contiguous.")
+        _check(_ffi.lib().satori_hip_copy(self._handle, _ptr(array), ctypes.c_void_p(device_ptr), array.nbytes, 2))
+        return array
+
+    def copy_device(self, destination_ptr: int, source_ptr: int, nbytes: int) -> None:
+        _check(_ffi.lib().satori_hip_copy(self._handle, ctypes.c_void_p(destination_ptr), ctypes.c_void_p(source_ptr),
+                                          nbytes, 3))
+
+    def synchronize(self) -> None:
+        _check(_ffi.lib().satori_hip_synchronize(self._handle))
+
+    def dispose(self) -> None:
+        if self._handle:
+            _check(_ffi.lib().satori_hip_context_destroy(self._handle))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.dispose()
+
+
+class HipQuantizedMatrix:
+    """Resident immutable weights (IQuantizedMatrix, src/Satori.Core/IQuantizedMatrix.cs:4-8)."""
+
+    def __init__(self, context: HipContext, handle: ctypes.c_void_p):
+        self.context = context
+        self._handle = handle
+        r, c, f, b = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        n = ctypes.c_int64()
+        _check(_ffi.lib().satori_hip_matrix_shape(handle, ctypes.byref(r), ctypes.byref(c), ctypes.byref(f),
+                                                  ctypes.byref(b), ctypes.byref(n)))
+        self.rows, self.columns, self.format, self.block_size, self.byte_length = (
+            r.value, c.value, f.value, b.value, n.value)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._handle
+
+    def execute(self, input, output) -> None:
+        """Synchronous MatVec; output is written only on success."""
+        x, y = _as_f32(input), _as_f32(output)
+        _check(_ffi.lib().satori_hip_matvec(self._handle, _ptr(x), x.size, _ptr(y), y.size))
+
+    def execute_batch(self, input, positions: int, output) -> None:
+        """QuantizedMatVec.ExecuteBatch semantics: [positions][C] -> [positions][R]."""
+        x, y = _as_f32(input), _as_f32(output)
+        _check(_ffi.lib().satori_hip_matvec_batch(self._handle, _ptr(x), x.size, positions, _ptr(y), y.size))
+
+    def execute_device(self, input_ptr: int, output_ptr: int, stream: int = 0) -> None:
+        _check(_ffi.lib().satori_hip_matvec_device(self._handle, ctypes.c_void_p(input_ptr),
+                                                   ctypes.c_void_p(output_ptr), ctypes.c_void_p(stream)))
+
+    def execute_batch_device(self, input_ptr: int, positions: int, output_ptr: int, stream: int = 0) -> None:
+        _check(_ffi.lib().satori_hip_matvec_batch_device(self._handle, ctypes.c_void_p(input_ptr), positions,
+                                                         ctypes.c_void_p(output_ptr), ctypes.c_void_p(stream)))
+
+    def clone(self) -> "HipQuantizedMatrix":
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_matrix_clone(self._handle, ctypes.byref(handle)))
+        return HipQuantizedMatrix(self.context, handle)
+
+    def dispose(self) -> None:
+        _check(_ffi.lib().satori_hip_matrix_destroy(self._handle))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.dispose()
+
+
+class HipGroup:
+    """One launch over several matrices of one format and width (device input/output pointers)."""
+
+    def __init__(self, context: HipContext, matrices, inputs, outputs, quantized_activations: bool = False):
+        n = len(matrices)
+        mats = (ctypes.c_void_p * n)(*[m.handle.value for m in matrices])
+        ins = (ctypes.c_void_p * n)(*inputs)
+        outs = (ctypes.c_void_p * n)(*outputs)
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_group_create(context.handle, mats, n, ins, outs, int(quantized_activations),
+                                                  ctypes.byref(handle)))
+        self._handle = handle
+
+    def execute(self, stream: int = 0) -> None:
+        _check(_ffi.lib().satori_hip_group_execute(self._handle, ctypes.c_void_p(stream)))
+
+    def dispose(self) -> None:
+        _check(_ffi.lib().satori_hip_group_destroy(self._handle))
+
+
+_default_lock = threading.Lock()
+_default: HipContext | None = None
+
+
+def default_context() -> HipContext:
+    """Process-wide context on device 0, created on first use (the static surfaces use it)."""
+    global _default
+    with _default_lock:
+        if _default is None:
+            _default = HipContext(0)
+        return _default
+
+
+# ---- Ternary2 ----
+
+class Ternary2Matrix:
+    """Owned, validated Ternary2 weights (src/Satori.Core/Ternary2Matrix.cs:6-124). The device copy is made
+    on first execution and kept with the matrix."""
+
+    def __init__(self, rows: int, columns: int, block_size: int, data: np.ndarray):
+        self.rows, self.columns, self.block_size = rows, columns, block_size
+        self._data = data
+        self._device: HipQuantizedMatrix | None = None
+
+    @property
+    def byte_length(self) -> int:
+        return self._data.size
+
+    @property
+    def data(self) -> np.ndarray:
+        return self._data
+
+    @staticmethod
+    def quantize(weights, rows: int, columns: int, block_size: int = 64) -> "Ternary2Matrix":
+        """Ternary2Matrix.Quantize (Ternary2Matrix.cs:38-71)."""
+        length = payload_length(TERNARY2, rows, columns, block_size)
+        w = np.ascontiguousarray(weights, dtype=np.float32).reshape(-1)
+        if w.size != rows * columns:
+            raise ArgumentException("Weights must match matrix dimensions.")
+        out = np.zeros(length, dtype=np.uint8)
+        _check(_ffi.lib().satori_hip_ternary2_quantize(_ptr(w), rows, columns, block_size, _ptr(out), out.size))
+        return Ternary2Matrix(rows, columns, block_size, out)
+
+    @staticmethod
+    def from_packed(rows: int, columns: int, block_size: int, data) -> "Ternary2Matrix":
+        """Ternary2Matrix.FromPacked (Ternary2Matrix.cs:73-81): copies and validates."""
+        owned = _as_u8(data).copy()
+        _check(_ffi.lib().satori_hip_ternary2_validate(rows, columns, block_size, _ptr(owned), owned.size))
+        return Ternary2Matrix(rows, columns, block_size, owned)
+
+    def copy_data_to(self, destination: np.ndarray) -> None:
+        destination[: self._data.size] = self._data
+
+    def save(self, path: str) -> None:
+        """Ternary2Matrix.Save (Ternary2Matrix.cs:29-36): STQ2 header + payload, new file only."""
+        header = bytearray(32)
+        header[0:4] = b"STQ2"
+        header[4:6] = (1).to_bytes(2, "little")
+        header[6:8] = (32).to_bytes(2, "little")
+        header[8:12] = self.rows.to_bytes(4, "little", signed=True)
+        header[12:16] = self.columns.to_bytes(4, "little", signed=True)
+        header[16:20] = self.block_size.to_bytes(4, "little", signed=True)
+        header[24:32] = self.byte_length.to_bytes(8, "little", signed=True)
+        with open(path, "xb") as f:
+            f.write(bytes(header))
+            f.write(self._data.tobytes())
+
+    def device(self, context: HipContext | None = None) -> HipQuantizedMatrix:
+        if self._device is None:
+            ctx = context or default_context()
+            self._device = ctx.create_ternary2(self.rows, self.columns, self.block_size, self._data)
+        return self._device
+
+
+class Ternary2MatVec:
+    """src/Satori.Core/Ternary2MatVec.cs:7-77 with the HIP backend."""
+
+    @staticmethod
+    def execute(matrix: Ternary2Matrix, input, output, context: HipContext | None = None) -> None:
+        if matrix is None:
+            raise ArgumentNullException("Value cannot be null. (Parameter 'matrix')")
+        matrix.device(context).execute(input, output)
+
+
+class MappedTernary2Matrix:
+    """src/Satori.Core/MappedTernary2Matrix.cs:4-56: opens and validates an STQ2 file once, then executes
+    on its resident device copy."""
+
+    def __init__(self, path: str, context: HipContext | None = None):
+        self._matrix = (context or default_context()).open_ternary2(path)
+        self.rows, self.columns = self._matrix.rows, self._matrix.columns
+        self.block_size, self.byte_length = self._matrix.block_size, self._matrix.byte_length
+
+    def execute(self, input, output) -> None:
+        self._matrix.execute(input, output)
+
+    def dispose(self) -> None:
+        self._matrix.dispose()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.dispose()
+
+
+# ---- GGUF block formats ----
+
+class QuantizedMatVec:
+    """src/Satori.Core/QuantizedMatVec.cs:9-370 with the HIP backend. The static calls upload the payload per
+    call, as the reference reads it per call; resident use goes through HipContext.create."""
+
+    @staticmethod
+    def validate_payload(data, shape: QuantizedMatrixShape) -> None:
+        d = _as_u8(data)
+        _check(_ffi.lib().satori_hip_quantized_validate(shape.rows, shape.columns, int(shape.format), _ptr(d), d.size))
+
+    @staticmethod
+    def execute(data, shape: QuantizedMatrixShape, input, output, context: HipContext | None = None) -> None:
+        with (context or default_context()).create(data, shape) as m:
+            m.execute(input, output)
+
+    @staticmethod
+    def execute_batch(data, shape: QuantizedMatrixShape, input, positions: int, output, threads: int = 1,
+                      context: HipContext | None = None) -> None:
+        if threads <= 0:
+            raise ArgumentOutOfRangeException("threads must be positive.")
+        with (context or default_context()).create(data, shape) as m:
+            m.execute_batch(input, positions, output)
+
+
+class Q8KCodec:
+    """src/Satori.Core/Q8KCodec.cs: the activation codec, quantized on the device."""
+    ELEMENTS_PER_BLOCK = 256
+    BYTES_PER_BLOCK = 292
+
+    @staticmethod
+    def quantize_row(input, context: HipContext | None = None) -> np.ndarray:
+        return (context or default_context()).quantize_q8k(input)

@@ -1,0 +1,475 @@
+// FP32-activation MatVec over packed blocks for gfx950: Ternary2 (B = 64/128/256), Q8_0, Q4_0, Q4_K and
+// Q6_K, computed directly on the payload without materialising weights.
+//
+// Work decomposition. A row is cut into fixed "chunks" (a 16-byte code segment of a Ternary2 block, one
+// Q8_0/Q4_0 block, an eighth of a Q4_K block, a quarter of a Q6_K block). A wave64 handles 64 / L rows
+// at a time with L lanes per row; lane j of a row owns chunks j, j + L, ... Consecutive lanes read
+// consecutive chunks, so a row's payload is read by contiguous 128-bit loads. The activation vector is
+// staged once per workgroup in LDS; when every row has at most L chunks (C <= 4096 for Ternary2) each
+// lane pulls its chunk's activations into registers once and keeps them for every row it visits.
+// Row sums are reduced across the L lanes by cross-lane shuffles.
+//
+// Arithmetic per format follows the reference decoders (file:line cited on each decoder); products
+// and sums are FP32, accumulated in a different order from the scalar reference, which the tests bound
+// by the reference's own 1e-5 * sum|w*x| criterion.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace satori {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRowUnroll = 2;
+
+// ------------------------------------------------------------------------------------------------
+// Ternary2: f32 scale + 2-bit codes, 4 per byte LSB first, 01 = +1, 10 = -1
+// (docs/ternary2-v1.md; Ternary2MatVec.ExecuteScalarCore, src/Satori.Core/Ternary2MatVec.cs:52-76).
+// A chunk is 16 code bytes = 64 weights. Codes become FP8 bytes through a v_perm lookup table, then
+// v_cvt_pk_f32_fp8 yields exact +-1.0 / 0.0, so each weight costs one FMA and no per-weight compare.
+// ------------------------------------------------------------------------------------------------
+template <int B>
+struct Ternary2Chunk {
+    static constexpr int kWeights = 64;
+    static constexpr int kPadShift = 6;
+    static constexpr int kPerBlock = B / 64;
+    static constexpr int kBlockBytes = 4 + B / 4;
+    struct Regs {
+        u32x4 codes;
+        float scale;
+    };
+    struct Consts {
+        uint32_t lut;  // bytes: code 0 -> fp8(0), 1 -> fp8(+1), 2 -> fp8(-1), 3 -> fp8(0)
+    };
+    __device__ static Consts consts() {
+        // The hardware's own encoding of +1 and -1, so the table matches v_cvt_pk_f32_fp8 by construction.
+        const uint32_t e = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(1.0f, -1.0f, 0, false));
+        return Consts{((e & 0xFFu) << 8) | (((e >> 8) & 0xFFu) << 16)};
+    }
+    __device__ static int chunks(const LaunchShape& s) { return s.blocks * kPerBlock; }
+    __device__ static int padded_columns(const LaunchShape& s) { return s.blocks * B; }
+    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
+        const uint8_t* block = row + (chunk / kPerBlock) * kBlockBytes;
+        r.scale = __uint_as_float(load4_a4(block));
+        r.codes = load16_a4(block + 4 + 16 * (chunk % kPerBlock));
+    }
+    template <class XF>
+    __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
+#pragma unroll
+        for (int j = 0; j < kWeights; ++j) x[j] = xf(64 * chunk + j);
+    }
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts& k) {
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t w = r.codes[d];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t sel = (w >> (2 * q)) & 0x03030303u;  // codes 16d + q + {0, 4, 8, 12}
+                const uint32_t f8 = __builtin_amdgcn_perm(0u, k.lut, sel);
+                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(f8), false);
+                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(f8), true);
+                acc0 = __builtin_fmaf(lo[0], x[16 * d + q], acc0);
+                acc1 = __builtin_fmaf(lo[1], x[16 * d + 4 + q], acc1);
+                acc0 = __builtin_fmaf(hi[0], x[16 * d + 8 + q], acc0);
+                acc1 = __builtin_fmaf(hi[1], x[16 * d + 12 + q], acc1);
+            }
+        }
+        return (acc0 + acc1) * r.scale;
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
+// Q8_0: f16 d + 32 int8, w = d * q (docs/gguf-subset-v1.md:94; QuantizedMatVec.ExecuteScalar,
+// src/Satori.Core/QuantizedMatVec.cs:66-74). 34-byte blocks are 2-byte aligned: codes are assembled from
+// aligned dword loads with v_alignbyte; int8 -> float is one SDWA conversion per weight.
+// ------------------------------------------------------------------------------------------------
+struct Q8_0Chunk {
+    static constexpr int kWeights = 32;
+    static constexpr int kPadShift = 5;
+    struct Regs {
+        uint32_t q[8];
+        float scale;
+    };
+    struct Consts {};
+    __device__ static Consts consts() { return Consts{}; }
+    __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
+    __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
+    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
+        const uint8_t* block = row + chunk * 34;
+        uint32_t head[1];
+        load_unaligned<1>(block, head);
+        r.scale = half_bits_to_float(head[0] & 0xFFFFu);
+        load_unaligned<8>(block + 2, r.q);
+    }
+    template <class XF>
+    __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
+#pragma unroll
+        for (int j = 0; j < kWeights; ++j) x[j] = xf(32 * chunk + j);
+    }
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            acc0 = __builtin_fmaf(sbyte_to_float(r.q[d], 0), x[4 * d + 0], acc0);
+            acc1 = __builtin_fmaf(sbyte_to_float(r.q[d], 1), x[4 * d + 1], acc1);
+            acc0 = __builtin_fmaf(sbyte_to_float(r.q[d], 2), x[4 * d + 2], acc0);
+            acc1 = __builtin_fmaf(sbyte_to_float(r.q[d], 3), x[4 * d + 3], acc1);
+        }
+        return r.scale * (acc0 + acc1);
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
+// Q4_0: f16 d + 16 bytes, w[j] = d * ((b[j] & 15) - 8), w[j + 16] = d * ((b[j] >> 4) - 8)
+// (docs/gguf-subset-v1.md:93; QuantizedMatVec.cs:71-72). Each nibble is turned into the signed byte
+// 16 * (q - 8) by one XOR and one mask per four weights, so the conversion is one SDWA op per weight;
+// the factor 16 is removed exactly with the power-of-two scale 1/16.
+// ------------------------------------------------------------------------------------------------
+struct Q4_0Chunk {
+    static constexpr int kWeights = 32;
+    static constexpr int kPadShift = 5;
+    struct Regs {
+        uint32_t q[4];
+        float scale;
+    };
+    struct Consts {};
+    __device__ static Consts consts() { return Consts{}; }
+    __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
+    __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
+    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
+        const uint8_t* block = row + chunk * 18;
+        uint32_t head[1];
+        load_unaligned<1>(block, head);
+        r.scale = half_bits_to_float(head[0] & 0xFFFFu);
+        load_unaligned<4>(block + 2, r.q);
+    }
+    template <class XF>
+    __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
+#pragma unroll
+        for (int j = 0; j < kWeights; ++j) x[j] = xf(32 * chunk + j);
+    }
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t v = r.q[d] ^ 0x88888888u;        // nibble q -> q ^ 8, whose signed 4-bit value is q - 8
+            const uint32_t lo = (v << 4) & 0xF0F0F0F0u;      // bytes 16 * (q_low - 8): weights 4d + i
+            const uint32_t hi = v & 0xF0F0F0F0u;             // bytes 16 * (q_high - 8): weights 16 + 4d + i
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc0 = __builtin_fmaf(sbyte_to_float(lo, i), x[4 * d + i], acc0);
+                acc1 = __builtin_fmaf(sbyte_to_float(hi, i), x[16 + 4 * d + i], acc1);
+            }
+        }
+        return r.scale * ((acc0 + acc1) * 0.0625f);
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
+// Q4_K, FP32 activations (Q4KCodec.DotBlock, src/Satori.Core/Q4KCodec.cs:39-65): 144-byte super-block,
+// f16 d @0, f16 dmin @2, 6-bit scales/mins @4..15 (Q4KCodec.GetScaleMin, :24-36), nibbles @16.
+// Chunk k of a block (k = 0..7) is qs[16k .. 16k + 16): low nibbles are weights 64g + 16h + i of
+// sub-block 2g, high nibbles weights 64g + 32 + 16h + i of sub-block 2g + 1 (g = k / 2, h = k % 2).
+// The weight d*s*q - dmin*m is one FMA.
+// ------------------------------------------------------------------------------------------------
+// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) on the scales[12] bytes held in three dwords.
+__device__ __forceinline__ int q4k_scale_byte(const u32x4& head, int i) {
+    return static_cast<int>((head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
+}
+
+__device__ __forceinline__ void q4k_scale_min(int j, const u32x4& head, int& scale, int& min) {
+    if (j < 4) {
+        scale = q4k_scale_byte(head, j) & 63;
+        min = q4k_scale_byte(head, j + 4) & 63;
+    } else {
+        scale = (q4k_scale_byte(head, j + 4) & 0xF) | ((q4k_scale_byte(head, j - 4) >> 6) << 4);
+        min = (q4k_scale_byte(head, j + 4) >> 4) | ((q4k_scale_byte(head, j) >> 6) << 4);
+    }
+}
+
+struct Q4_KChunk {
+    static constexpr int kWeights = 32;
+    static constexpr int kPadShift = 6;
+    struct Regs {
+        u32x4 head;
+        u32x4 qs;
+        int g;
+    };
+    struct Consts {};
+    __device__ static Consts consts() { return Consts{}; }
+    __device__ static int chunks(const LaunchShape& s) { return s.blocks * 8; }
+    __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
+    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
+        const uint8_t* block = row + (chunk >> 3) * 144;
+        r.head = load16_a4(block);
+        r.qs = load16_a4(block + 16 + 16 * (chunk & 7));
+        r.g = (chunk & 7) >> 1;
+    }
+    template <class XF>
+    __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
+        const int base = (chunk >> 3) * 256 + 64 * ((chunk & 7) >> 1) + 16 * (chunk & 1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[i] = xf(base + i);
+            x[16 + i] = xf(base + 32 + i);
+        }
+    }
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+        const float d = half_bits_to_float(r.head[0] & 0xFFFFu);
+        const float dmin = half_bits_to_float(r.head[0] >> 16);
+        int s0, m0, s1, m1;
+        q4k_scale_min(2 * r.g, r.head, s0, m0);
+        q4k_scale_min(2 * r.g + 1, r.head, s1, m1);
+        const float dl = d * static_cast<float>(s0), ml = dmin * static_cast<float>(m0);
+        const float dh = d * static_cast<float>(s1), mh = dmin * static_cast<float>(m1);
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t lo = r.qs[w] & 0x0F0F0F0Fu;
+            const uint32_t hi = (r.qs[w] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc0 = __builtin_fmaf(__builtin_fmaf(dl, byte_to_float(lo, i), -ml), x[4 * w + i], acc0);
+                acc1 = __builtin_fmaf(__builtin_fmaf(dh, byte_to_float(hi, i), -mh), x[16 + 4 * w + i], acc1);
+            }
+        }
+        return acc0 + acc1;
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
+// Q6_K, FP32 activations (Q6KCodec.DotBlock, src/Satori.Core/Q6KCodec.cs:22-51): 210-byte super-block,
+// ql[128] @0, qh[64] @128, int8 scales[16] @192, f16 d @208. Chunk (h, t), h = half, t = 16-lane slice:
+// l in [16t, 16t + 16) for all four quarters k, i.e. weights 128h + 32k + l with scale 8h + 2k + t.
+// Weight d*sc*(q - 32) is fma(d*sc, q, -32*d*sc), the same single rounding of the same product as the
+// reference's (d*sc)*(q-32) since 32*d*sc is exact.
+// ------------------------------------------------------------------------------------------------
+struct Q6_KChunk {
+    static constexpr int kWeights = 64;
+    static constexpr int kPadShift = 7;
+    struct Regs {
+        uint32_t qla[4], qlb[4], qh[4];
+        uint32_t sc[4];  // bytes 192..207
+        float d;
+        int h, t;
+    };
+    struct Consts {};
+    __device__ static Consts consts() { return Consts{}; }
+    __device__ static int chunks(const LaunchShape& s) { return s.blocks * 4; }
+    __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
+    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
+        const uint8_t* block = row + (chunk >> 2) * 210;
+        r.h = (chunk & 3) >> 1;
+        r.t = chunk & 1;
+        load_unaligned<4>(block + 64 * r.h + 16 * r.t, r.qla);
+        load_unaligned<4>(block + 64 * r.h + 32 + 16 * r.t, r.qlb);
+        load_unaligned<4>(block + 128 + 32 * r.h + 16 * r.t, r.qh);
+        load_unaligned<4>(block + 192, r.sc);
+        uint32_t tail[1];
+        load_unaligned<1>(block + 208, tail);
+        r.d = half_bits_to_float(tail[0] & 0xFFFFu);
+    }
+    template <class XF>
+    __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
+        const int base = (chunk >> 2) * 256 + 128 * ((chunk & 3) >> 1) + 16 * (chunk & 1);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[16 * k + i] = xf(base + 32 * k + i);
+    }
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+        float ds[4], bias[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int index = 8 * r.h + 2 * k + r.t;
+            const int8_t s = static_cast<int8_t>(r.sc[index >> 2] >> (8 * (index & 3)));
+            ds[k] = r.d * static_cast<float>(s);
+            bias[k] = -32.0f * ds[k];
+        }
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t a = r.qla[w], b = r.qlb[w], h = r.qh[w];
+            const uint32_t q[4] = {
+                (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u),
+                (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u),
+                ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u),
+                ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u),
+            };
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float weight = __builtin_fmaf(ds[k], byte_to_float(q[k], i), bias[k]);
+                    if (i & 1)
+                        acc1 = __builtin_fmaf(weight, x[16 * k + 4 * w + i], acc1);
+                    else
+                        acc0 = __builtin_fmaf(weight, x[16 * k + 4 * w + i], acc0);
+                }
+        }
+        return acc0 + acc1;
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
+// The kernel. Grid: x = row tiles of s.rows_per_wg rows, y = group member, z = position.
+// ONE: every row has at most L chunks, so a lane's activations are loaded once per workgroup.
+// XLDS: the activations fit the LDS budget; otherwise they are read from global memory (L2).
+// ------------------------------------------------------------------------------------------------
+template <class F, int L, bool ONE, bool XLDS>
+__global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const MatDesc* __restrict__ group,
+                                                               LaunchShape s) {
+    const MatDesc m = group ? group[blockIdx.y] : one;
+    const int row_begin = blockIdx.x * s.rows_per_wg;
+    if (row_begin >= m.rows) return;  // whole workgroup leaves together
+    const int row_end = min(row_begin + s.rows_per_wg, m.rows);
+    const int position = blockIdx.z;
+    const float* __restrict__ x = m.x + static_cast<int64_t>(position) * s.columns;
+    float* __restrict__ y = m.y + static_cast<int64_t>(position) * m.rows;
+    const int columns = s.columns;
+
+    // Staged activations: element i lives at i + 4 * (i >> kPadShift), which spreads the 128-bit reads
+    // of neighbouring lanes over all 32 LDS banks.
+    extern __shared__ float xs[];
+    if constexpr (XLDS) {
+        const int padded = F::padded_columns(s);
+        for (int i = threadIdx.x; i < padded; i += kThreads)
+            xs[i + ((i >> F::kPadShift) << 2)] = i < columns ? x[i] : 0.0f;
+        __syncthreads();
+    }
+    auto xf = [&](int i) -> float {
+        if constexpr (XLDS)
+            return xs[i + ((i >> F::kPadShift) << 2)];
+        else
+            return i < columns ? x[i] : 0.0f;
+    };
+
+    constexpr int kRowsPerPass = 64 / L;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = lane / L;
+    const int lr = lane % L;
+    const int nchunks = F::chunks(s);
+    const typename F::Consts k = F::consts();
+    const int64_t row_bytes = s.row_bytes;
+
+    float xr[F::kWeights];
+    if constexpr (ONE) {
+        if (lr < nchunks) {
+            F::load_x(xf, lr, xr);
+        } else {
+#pragma unroll
+            for (int j = 0; j < F::kWeights; ++j) xr[j] = 0.0f;
+        }
+    }
+
+    constexpr int kStep = kWaves * kRowsPerPass * kRowUnroll;
+    for (int r0 = row_begin + wave * kRowsPerPass; r0 < row_end; r0 += kStep) {
+        float acc[kRowUnroll];
+        int row[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+            row[u] = r0 + u * kWaves * kRowsPerPass + sub;
+            acc[u] = 0.0f;
+        }
+        if constexpr (ONE) {
+            typename F::Regs regs[kRowUnroll];
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u)
+                if (row[u] < row_end && lr < nchunks) F::load(m.w + row[u] * row_bytes, lr, regs[u]);
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u)
+                if (row[u] < row_end && lr < nchunks) acc[u] = F::dot(regs[u], xr, k);
+        } else {
+            for (int c = lr; c < nchunks; c += L) {
+                F::load_x(xf, c, xr);
+                typename F::Regs regs[kRowUnroll];
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u)
+                    if (row[u] < row_end) F::load(m.w + row[u] * row_bytes, c, regs[u]);
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u)
+                    if (row[u] < row_end) acc[u] += F::dot(regs[u], xr, k);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+            const float total = group_sum<L>(acc[u]);
+            if (lr == 0 && row[u] < row_end) y[row[u]] = total;
+        }
+    }
+}
+
+// LDS budget for the staged activations.
+constexpr int kMaxLdsBytes = 64 * 1024;
+
+template <class F, int L, bool ONE>
+hipError_t launch_variant(const MatDesc& one, const MatDesc* group, int count, const LaunchShape& s, dim3 grid,
+                          int padded, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(padded + 4 * (padded >> F::kPadShift) + 4) * sizeof(float);
+    if (lds <= kMaxLdsBytes)
+        gemv_float_kernel<F, L, ONE, true><<<grid, kThreads, lds, stream>>>(one, group, s);
+    else
+        gemv_float_kernel<F, L, ONE, false><<<grid, kThreads, 0, stream>>>(one, group, s);
+    return hipGetLastError();
+}
+
+template <class F>
+hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, int chunks,
+                         int padded, hipStream_t stream) {
+    // Lanes per row: enough for one chunk per lane when the row is short, capped at the wave.
+    int lanes = 8;
+    while (lanes < 64 && lanes < chunks) lanes <<= 1;
+    const int rows_per_pass = 64 / lanes;
+    const int rows_per_iteration = kWaves * rows_per_pass * kRowUnroll;
+    // Rows per workgroup: at least one full iteration; grow while the grid keeps >= 2048 workgroups
+    // (8 per CU on 256 CUs), so small matrices still spread over the whole chip.
+    int64_t groups_total = static_cast<int64_t>(count) * s.positions;
+    int rows_per_wg = rows_per_iteration;
+    while (rows_per_wg < 1024 &&
+           groups_total * ((s.rows_max + 2 * rows_per_wg - 1) / (2 * rows_per_wg)) >= 2048)
+        rows_per_wg *= 2;
+    s.rows_per_wg = rows_per_wg;
+    dim3 grid((s.rows_max + rows_per_wg - 1) / rows_per_wg, count, s.positions);
+    const bool one_chunk = chunks <= lanes;
+    switch (lanes) {
+        case 8:
+            return one_chunk ? launch_variant<F, 8, true>(one, group, count, s, grid, padded, stream)
+                             : launch_variant<F, 8, false>(one, group, count, s, grid, padded, stream);
+        case 16:
+            return one_chunk ? launch_variant<F, 16, true>(one, group, count, s, grid, padded, stream)
+                             : launch_variant<F, 16, false>(one, group, count, s, grid, padded, stream);
+        case 32:
+            return one_chunk ? launch_variant<F, 32, true>(one, group, count, s, grid, padded, stream)
+                             : launch_variant<F, 32, false>(one, group, count, s, grid, padded, stream);
+        default:
+            return one_chunk ? launch_variant<F, 64, true>(one, group, count, s, grid, padded, stream)
+                             : launch_variant<F, 64, false>(one, group, count, s, grid, padded, stream);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemv_float(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
+                             hipStream_t stream) {
+    if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
+    switch (s.format) {
+        case kTernary2: {
+            const int padded = s.blocks * s.block_size;
+            switch (s.block_size) {
+                case 64: return launch_format<Ternary2Chunk<64>>(one, group, count, s, s.blocks, padded, stream);
+                case 128: return launch_format<Ternary2Chunk<128>>(one, group, count, s, s.blocks * 2, padded, stream);
+                case 256: return launch_format<Ternary2Chunk<256>>(one, group, count, s, s.blocks * 4, padded, stream);
+                default: return hipErrorInvalidValue;
+            }
+        }
+        case kQ8_0: return launch_format<Q8_0Chunk>(one, group, count, s, s.blocks, s.columns, stream);
+        case kQ4_0: return launch_format<Q4_0Chunk>(one, group, count, s, s.blocks, s.columns, stream);
+        case kQ4_K: return launch_format<Q4_KChunk>(one, group, count, s, s.blocks * 8, s.columns, stream);
+        case kQ6_K: return launch_format<Q6_KChunk>(one, group, count, s, s.blocks * 4, s.columns, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace satori

@@ -1,0 +1,271 @@
+// Q8_K activation quantizer and the integer K-format products (Q4_K x Q8_K, Q6_K x Q8_K) for gfx950.
+//
+// Both reproduce the reference bit for bit:
+//  - the quantizer is Q8KCodec.QuantizeBlock (src/Satori.Core/Q8KCodec.cs:44-76): first-largest |x| with
+//    a strict comparison, -127/max and 1/inverse as correctly rounded divisions, the product and the
+//    12582912 add rounded separately (the library is compiled with -ffp-contract=off and the operations
+//    are spelled with explicit round-to-nearest intrinsics);
+//  - the products are exact int32 sums (v_dot4_i32_i8), and the per-block FP32 expression and the
+//    block-order accumulation of each row are those of QuantizedKAvx2Kernel.ExecuteQuantizedTiled
+//    (src/Satori.Core/QuantizedKAvx2Kernel.cs:47-99), so each output equals the reference's float.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace satori {
+namespace {
+
+// ------------------------------------------------------------------------------------------------
+// Q8_K quantizer: one wave per 256-element block, four consecutive elements per lane.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restrict__ x, int columns,
+                                                          uint8_t* __restrict__ out) {
+    const int block = blockIdx.x;
+    const int position = blockIdx.y;
+    const int blocks = columns / 256;
+    const int lane = threadIdx.x;
+    const float* src = x + static_cast<int64_t>(position) * columns + block * 256;
+    uint8_t* dst = out + (static_cast<int64_t>(position) * blocks + block) * kQ8KBlockBytes;
+
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = src[4 * lane + i];
+
+    // First index of the largest magnitude; NaN never wins (its comparison is false, Q8KCodec.cs:53).
+    float best = 0.0f;
+    int index = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = __builtin_fabsf(v[i]);
+        if (a > best) {
+            best = a;
+            index = 4 * lane + i;
+        }
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        const float other = __shfl_xor(best, offset, 64);
+        const int other_index = __shfl_xor(index, offset, 64);
+        if (other > best || (other == best && other_index < index)) {
+            best = other;
+            index = other_index;
+        }
+    }
+    if (best == 0.0f) {  // magnitude 0: the block is all zero bytes (Q8KCodec.cs:59-63)
+        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+        for (int i = lane; i < kQ8KBlockBytes / 4; i += 64) d32[i] = 0u;
+        return;
+    }
+    const float max = src[index];
+    const float inverse = __fdiv_rn(-127.0f, max);
+    uint32_t packed = 0;
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float shifted = __fadd_rn(__fmul_rn(inverse, v[i]), 12582912.0f);
+        int n = static_cast<int>(__float_as_uint(shifted) & 0x007FFFFFu) - 0x00400000;  // NearestInteger, :120-125
+        n = n < 127 ? n : 127;
+        const int8_t code = static_cast<int8_t>(n);
+        sum += code;
+        packed |= (static_cast<uint32_t>(static_cast<uint8_t>(code))) << (8 * i);
+    }
+    // Group sums of 16 codes = 4 lanes, as int16 (Q8KCodec.cs:68-74).
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    reinterpret_cast<uint32_t*>(dst + 4)[lane] = packed;
+    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(dst + 260)[lane >> 2] = static_cast<int16_t>(sum);
+    if (lane == 0) reinterpret_cast<float*>(dst)[0] = __fdiv_rn(1.0f, inverse);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Integer product. A workgroup owns kTileRows rows of one member at one position. The position's Q8_K
+// row is staged in LDS as separate arrays (codes, group sums, scales) so code reads are 16-byte aligned.
+// Work items are (row, block) pairs, G lanes each (Q4_K: 8 lanes x 32 weights, Q6_K: 4 lanes x 64
+// weights); the G lanes' int32 partials are summed exactly, the pair's leader forms the block's FP32
+// term and stores it in LDS, and finally one thread per row adds its terms in block order.
+// ------------------------------------------------------------------------------------------------
+constexpr int kThreads = 256;
+constexpr int kTileRows = 32;
+
+// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) on the scales[12] bytes held in three dwords.
+__device__ __forceinline__ int q4k_scale_byte(const u32x4& head, int i) {
+    return static_cast<int>((head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
+}
+
+__device__ __forceinline__ void q4k_scale_min(int j, const u32x4& head, int& scale, int& min) {
+    if (j < 4) {
+        scale = q4k_scale_byte(head, j) & 63;
+        min = q4k_scale_byte(head, j + 4) & 63;
+    } else {
+        scale = (q4k_scale_byte(head, j + 4) & 0xF) | ((q4k_scale_byte(head, j - 4) >> 6) << 4);
+        min = (q4k_scale_byte(head, j + 4) >> 4) | ((q4k_scale_byte(head, j) >> 6) << 4);
+    }
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+struct ActTile {
+    uint32_t* codes;   // [blocks][64] dwords
+    int16_t* sums;     // [blocks][16]
+    float* scales;     // [blocks]
+};
+
+// Q4_K pair, lane c of 8: chunk qs[16c, 16c + 16) (Q4KCodec.DotProduct / MinProduct, Q4KCodec.cs:117-153).
+__device__ __forceinline__ void q4k_pair(const uint8_t* block, const ActTile& act, int b, int c, int& dot,
+                                         int& min_part, u32x4& head) {
+    head = load16_a4(block);
+    const u32x4 qs = load16_a4(block + 16 + 16 * c);
+    const int g = c >> 1, h = c & 1;
+    int s0, m0, s1, m1;
+    q4k_scale_min(2 * g, head, s0, m0);
+    q4k_scale_min(2 * g + 1, head, s1, m1);
+    const u32x4 lo_codes = *reinterpret_cast<const u32x4*>(act.codes + 64 * b + 16 * g + 4 * h);
+    const u32x4 hi_codes = *reinterpret_cast<const u32x4*>(act.codes + 64 * b + 16 * g + 8 + 4 * h);
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        lo = sdot4(qs[w] & 0x0F0F0F0Fu, lo_codes[w], lo);
+        hi = sdot4((qs[w] >> 4) & 0x0F0F0F0Fu, hi_codes[w], hi);
+    }
+    dot = s0 * lo + s1 * hi;
+    const int16_t* sums = act.sums + 16 * b;
+    min_part = h == 0 ? m0 * (sums[4 * g] + sums[4 * g + 1]) + m1 * (sums[4 * g + 2] + sums[4 * g + 3]) : 0;
+}
+
+// Q6_K pair, lane c of 4: half h = c / 2, slice t = c % 2, i.e. weights 128h + 32k + 16t + i
+// (Q6KCodec.DotProduct, Q6KCodec.cs:114-146, with the -32 centring applied through the group sums:
+// sum sc * (q - 32) * code = sum sc * q * code - 32 * sum sc * bsum, both exact).
+__device__ __forceinline__ int q6k_pair(const uint8_t* block, const ActTile& act, int b, int c, float& d) {
+    const int h = c >> 1, t = c & 1;
+    uint32_t qla[4], qlb[4], qh[4], sc[4], tail[1];
+    load_unaligned<4>(block + 64 * h + 16 * t, qla);
+    load_unaligned<4>(block + 64 * h + 32 + 16 * t, qlb);
+    load_unaligned<4>(block + 128 + 32 * h + 16 * t, qh);
+    load_unaligned<4>(block + 192, sc);
+    load_unaligned<1>(block + 208, tail);
+    d = half_bits_to_float(tail[0] & 0xFFFFu);
+    int dotk[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t a = qla[w], bq = qlb[w], hb = qh[w];
+        const uint32_t q[4] = {
+            (a & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u),
+            (bq & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u),
+            ((a >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u),
+            ((bq >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u),
+        };
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dotk[k] = sdot4(q[k], act.codes[64 * b + 32 * h + 8 * k + 4 * t + w], dotk[k]);
+    }
+    const int16_t* sums = act.sums + 16 * b;
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int index = 8 * h + 2 * k + t;
+        const int s = static_cast<int8_t>(sc[index >> 2] >> (8 * (index & 3)));
+        total += s * (dotk[k] - 32 * sums[index]);
+    }
+    return total;
+}
+
+template <int FORMAT>
+__global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const MatDesc* __restrict__ group,
+                                                              LaunchShape s) {
+    constexpr int G = FORMAT == kQ4_K ? 8 : 4;       // lanes per (row, block) pair
+    constexpr int kBlockBytes = FORMAT == kQ4_K ? 144 : 210;
+    const MatDesc m = group ? group[blockIdx.y] : one;
+    const int row_begin = blockIdx.x * kTileRows;
+    if (row_begin >= m.rows) return;
+    const int rows = min(kTileRows, m.rows - row_begin);
+    const int position = blockIdx.z;
+    const int nb = s.blocks;
+
+    extern __shared__ uint32_t smem[];
+    ActTile act;
+    act.codes = smem;                                                  // 64 * nb dwords
+    act.scales = reinterpret_cast<float*>(smem + 64 * nb);             // nb
+    act.sums = reinterpret_cast<int16_t*>(smem + 65 * nb);             // 16 * nb int16 = 8 * nb dwords
+    float* terms = reinterpret_cast<float*>(smem + 73 * nb);           // kTileRows * nb
+
+    const uint8_t* arow = m.a + static_cast<int64_t>(position) * nb * kQ8KBlockBytes;
+    for (int i = threadIdx.x; i < 73 * nb; i += kThreads) {
+        const int b = i / 73, word = i % 73;
+        const uint32_t value = reinterpret_cast<const uint32_t*>(arow + b * kQ8KBlockBytes)[word];
+        if (word == 0)
+            act.scales[b] = __uint_as_float(value);
+        else if (word <= 64)
+            act.codes[64 * b + word - 1] = value;
+        else
+            reinterpret_cast<uint32_t*>(act.sums)[8 * b + word - 65] = value;
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int c = lane % G;
+    const int pairs = rows * nb;
+    const int64_t row_bytes = s.row_bytes;
+    for (int p0 = (threadIdx.x / G); p0 < pairs + 0; p0 += kThreads / G) {
+        // All G lanes of a pair share p0, so the group reductions below stay inside the pair.
+        const int r = p0 / nb, b = p0 % nb;
+        const uint8_t* block = m.w + (row_begin + r) * row_bytes + b * kBlockBytes;
+        float term = 0.0f;
+        if constexpr (FORMAT == kQ4_K) {
+            int dot, min_part;
+            u32x4 head;
+            q4k_pair(block, act, b, c, dot, min_part, head);
+            dot = group_sum_int<G>(dot);
+            min_part = group_sum_int<G>(min_part);
+            const float a = act.scales[b];
+            if (a != 0.0f) {  // zero activation block: skipped (QuantizedKAvx2Kernel.cs:86)
+                const float dA = __fmul_rn(half_bits_to_float(head[0] & 0xFFFFu), a);
+                const float dminA = __fmul_rn(half_bits_to_float(head[0] >> 16), a);
+                term = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot)), __fmul_rn(dminA, static_cast<float>(min_part)));
+            }
+        } else {
+            float d;
+            int dot = q6k_pair(block, act, b, c, d);
+            dot = group_sum_int<G>(dot);
+            const float a = act.scales[b];
+            if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, d), static_cast<float>(dot));
+        }
+        if (c == 0) terms[r * nb + b] = term;
+    }
+    __syncthreads();
+    if (threadIdx.x < rows) {
+        // Block order from +0, as the reference accumulator (QuantizedKAvx2Kernel.cs:63, 90-94). A skipped
+        // block stored +0, and adding +0 to a sum that starts at +0 never changes it.
+        float acc = 0.0f;
+        const float* t = terms + threadIdx.x * nb;
+        for (int b = 0; b < nb; ++b) acc = __fadd_rn(acc, t[b]);
+        m.y[static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x] = acc;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8_t* out, hipStream_t stream) {
+    if (columns <= 0 || positions <= 0) return hipSuccess;
+    dim3 grid(columns / 256, positions);
+    q8k_quantize_kernel<<<grid, 64, 0, stream>>>(x, columns, out);
+    return hipGetLastError();
+}
+
+size_t kint_lds_bytes(int blocks) { return static_cast<size_t>(73 + kTileRows) * blocks * sizeof(uint32_t); }
+
+hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
+                            hipStream_t stream) {
+    if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
+    dim3 grid((s.rows_max + kTileRows - 1) / kTileRows, count, s.positions);
+    const size_t lds = kint_lds_bytes(s.blocks);
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    if (s.format == kQ4_K)
+        gemv_kint_kernel<kQ4_K><<<grid, kThreads, lds, stream>>>(one, group, s);
+    else if (s.format == kQ6_K)
+        gemv_kint_kernel<kQ6_K><<<grid, kThreads, lds, stream>>>(one, group, s);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace satori

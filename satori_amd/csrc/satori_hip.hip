@@ -1,0 +1,720 @@
+// Host runtime of libsatori_hip.so: contexts, resident matrices, launches, and the C ABI declared in
+// include/satori_hip.h. Every entry point converts internal failures into a status code plus a per-thread
+// message, and host-buffer MatVec calls copy into the caller's output only after the stream has
+// completed without error (IQuantizedMatrix contract, src/Satori.Core/IQuantizedMatrix.cs:6).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/satori_hip.h"
+#include "host_shapes.hpp"
+#include "kernels.hpp"
+
+namespace satori {
+namespace {
+
+thread_local std::string g_last_error;
+
+// Slack after every payload: the misaligned-block loaders read up to 4 bytes past a block.
+constexpr size_t kPayloadSlack = 256;
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        fail(e == hipErrorOutOfMemory ? SATORI_HIP_E_OUT_OF_MEMORY : SATORI_HIP_E_DEVICE,
+             std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Device buffer that only grows.
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    void reserve(size_t need) {
+        if (need <= bytes) return;
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+        check_hip(hipMalloc(&ptr, need), "hipMalloc");
+        bytes = need;
+    }
+    void release() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+};
+
+struct PinnedBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    void reserve(size_t need) {
+        if (need <= bytes) return;
+        if (ptr) (void)hipHostFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+        check_hip(hipHostMalloc(&ptr, need, hipHostMallocDefault), "hipHostMalloc");
+        bytes = need;
+    }
+    void release() {
+        if (ptr) (void)hipHostFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+};
+
+}  // namespace
+}  // namespace satori
+
+struct satori_hip_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex lock;
+    bool live = true;
+    int matrices = 0;
+    satori::DeviceBuffer x, y, q8k;
+    satori::PinnedBuffer host_x, host_y;
+};
+
+struct satori_hip_matrix {
+    satori_hip_context* context = nullptr;
+    satori::Shape shape;
+    uint8_t* payload = nullptr;  // device
+    bool live = true;
+};
+
+struct satori_hip_group {
+    satori_hip_context* context = nullptr;
+    satori::Shape shape;
+    int count = 0;
+    bool quantized = false;
+    int rows_max = 0;
+    satori::MatDesc* descriptors = nullptr;   // device
+    std::vector<const float*> inputs;          // distinct inputs, quantized path
+    std::vector<uint8_t*> q8k;                 // one Q8_K row per distinct input (device)
+    bool live = true;
+};
+
+namespace satori {
+namespace {
+
+int succeed() {
+    g_last_error.clear();
+    return SATORI_HIP_OK;
+}
+
+template <class F>
+int guarded(F&& body) {
+    try {
+        body();
+        return succeed();
+    } catch (const Failure& f) {
+        g_last_error = f.message;
+        return f.status;
+    } catch (const std::bad_alloc&) {
+        g_last_error = "Out of host memory.";
+        return SATORI_HIP_E_OUT_OF_MEMORY;
+    } catch (...) {
+        g_last_error = "Unexpected failure.";
+        return SATORI_HIP_E_DEVICE;
+    }
+}
+
+void require(const void* p, const char* name) {
+    if (!p) fail(SATORI_HIP_E_ARGUMENT_NULL, std::string("Value cannot be null. (Parameter '") + name + "')");
+}
+
+void require_live(const satori_hip_context* c) {
+    require(c, "context");
+    if (!c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_context'.");
+}
+
+void require_live(const satori_hip_matrix* m) {
+    require(m, "matrix");
+    if (!m->live || !m->context->live)
+        fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_matrix'.");
+}
+
+void set_device(const satori_hip_context* c) { check_hip(hipSetDevice(c->device), "hipSetDevice"); }
+
+LaunchShape launch_shape(const Shape& s, int positions, int rows_max) {
+    LaunchShape l{};
+    l.format = s.format == SATORI_HIP_TERNARY2 ? kTernary2 : s.format;
+    l.columns = s.columns;
+    l.block_size = s.block_size;
+    l.blocks = s.blocks;
+    l.row_bytes = s.row_bytes;
+    l.positions = positions;
+    l.rows_max = rows_max;
+    return l;
+}
+
+bool is_k(const Shape& s) { return s.format == SATORI_HIP_Q4_K || s.format == SATORI_HIP_Q6_K; }
+
+size_t kint_lds_limit_blocks() { return (64 * 1024) / ((73 + 32) * 4); }
+
+// Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers.
+void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
+    MatDesc d{m->payload, x, nullptr, y, m->shape.rows, 0};
+    check_hip(launch_gemv_float(d, nullptr, 1, launch_shape(m->shape, positions, m->shape.rows), stream),
+              "gemv launch");
+}
+
+// Enqueue the Q8_K integer product: quantize positions rows into `q8k`, then the product.
+void enqueue_kint(const satori_hip_matrix* m, const float* x, int positions, float* y, uint8_t* q8k,
+                  hipStream_t stream) {
+    check_hip(launch_q8k_quantize(x, m->shape.columns, positions, q8k, stream), "Q8_K launch");
+    MatDesc d{m->payload, nullptr, q8k, y, m->shape.rows, 0};
+    check_hip(launch_gemv_kint(d, nullptr, 1, launch_shape(m->shape, positions, m->shape.rows), stream),
+              "integer gemv launch");
+}
+
+void check_kint_width(const Shape& s) {
+    if (static_cast<size_t>(s.blocks) > kint_lds_limit_blocks())
+        fail(SATORI_HIP_E_NOT_SUPPORTED, "Integer K-format product supports at most " +
+                                             std::to_string(kint_lds_limit_blocks() * 256) + " columns.");
+}
+
+bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + b_bytes && b0 < a0 + a_bytes;
+}
+
+satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
+    set_device(c);
+    uint8_t* device = nullptr;
+    check_hip(hipMalloc(reinterpret_cast<void**>(&device), static_cast<size_t>(s.byte_length) + kPayloadSlack),
+              "hipMalloc");
+    hipError_t e = hipMemcpy(device, payload, static_cast<size_t>(s.byte_length), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(device + s.byte_length, 0, kPayloadSlack);
+    if (e != hipSuccess) {
+        (void)hipFree(device);
+        check_hip(e, "weight upload");
+    }
+    auto* m = new satori_hip_matrix();
+    m->context = c;
+    m->shape = s;
+    m->payload = device;
+    c->matrices++;
+    return m;
+}
+
+// Host-buffer MatVec shared by matvec and matvec_batch.
+void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, int positions, float* output,
+                 size_t output_length, bool batch) {
+    require(m, "matrix");
+    satori_hip_context* c = m->context;
+    std::lock_guard<std::mutex> guard(c->lock);
+    require_live(m);
+    require(input, "input");
+    require(output, "output");
+    const Shape& s = m->shape;
+    if (batch) {
+        if (positions <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "positions must be positive.");
+        if (s.format == SATORI_HIP_TERNARY2)
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "The batched product is defined for the GGUF block formats only.");
+        const int64_t in_need = static_cast<int64_t>(positions) * s.columns;
+        const int64_t out_need = static_cast<int64_t>(positions) * s.rows;
+        if (in_need > INT32_MAX || out_need > INT32_MAX)
+            fail(SATORI_HIP_E_OVERFLOW, "Arithmetic operation resulted in an overflow.");
+        if (static_cast<int64_t>(input_length) != in_need)
+            fail(SATORI_HIP_E_ARGUMENT, "Input must hold one vector per position.");
+        if (static_cast<int64_t>(output_length) != out_need)
+            fail(SATORI_HIP_E_ARGUMENT, "Output must hold one vector per position.");
+        if (is_k(s) && positions > 256)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "At most 256 positions per call.");
+    } else {
+        positions = 1;
+        if (input_length != static_cast<size_t>(s.columns) || output_length != static_cast<size_t>(s.rows))
+            fail(SATORI_HIP_E_ARGUMENT, "Vector lengths must match matrix dimensions.");
+    }
+    const size_t in_bytes = input_length * sizeof(float), out_bytes = output_length * sizeof(float);
+    if (overlaps(input, in_bytes, output, out_bytes))
+        fail(SATORI_HIP_E_ARGUMENT, "Output must not overlap input.");
+    for (size_t i = 0; i < input_length; ++i)
+        if (!std::isfinite(input[i])) fail(SATORI_HIP_E_ARGUMENT, "Expected finite FP32 input.");
+
+    set_device(c);
+    c->x.reserve(in_bytes);
+    c->y.reserve(out_bytes);
+    c->host_x.reserve(in_bytes);
+    c->host_y.reserve(out_bytes);
+    const bool integer = batch && is_k(s);
+    if (integer) {
+        check_kint_width(s);
+        c->q8k.reserve(static_cast<size_t>(positions) * s.blocks * kQ8KBlockBytes);
+    }
+    std::memcpy(c->host_x.ptr, input, in_bytes);
+    check_hip(hipMemcpyAsync(c->x.ptr, c->host_x.ptr, in_bytes, hipMemcpyHostToDevice, c->stream), "input copy");
+    if (integer)
+        enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr),
+                     static_cast<uint8_t*>(c->q8k.ptr), c->stream);
+    else
+        enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
+    check_hip(hipMemcpyAsync(c->host_y.ptr, c->y.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "output copy");
+    check_hip(hipStreamSynchronize(c->stream), "stream");
+    std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
+}
+
+}  // namespace
+}  // namespace satori
+
+using namespace satori;
+
+extern "C" {
+
+int satori_hip_abi_version(void) { return SATORI_HIP_ABI_VERSION; }
+
+const char* satori_hip_last_error(void) { return g_last_error.c_str(); }
+
+int satori_hip_device_count(int* count) {
+    return guarded([&] {
+        require(count, "count");
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+        int gfx950 = 0;
+        for (int i = 0; i < n; ++i) {
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, i) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+                gfx950++;
+        }
+        *count = gfx950;
+    });
+}
+
+int satori_hip_context_create(int device, satori_hip_context** context) {
+    return guarded([&] {
+        require(context, "context");
+        *context = nullptr;
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+            fail(SATORI_HIP_E_PLATFORM_NOT_SUPPORTED, "No HIP device is available.");
+        if (device < 0 || device >= n) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "device is out of range.");
+        hipDeviceProp_t prop;
+        check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            fail(SATORI_HIP_E_PLATFORM_NOT_SUPPORTED, std::string("Device is ") + prop.gcnArchName + ", not gfx950.");
+        check_hip(hipSetDevice(device), "hipSetDevice");
+        auto* c = new satori_hip_context();
+        c->device = device;
+        const hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete c;
+            check_hip(e, "hipStreamCreate");
+        }
+        *context = c;
+    });
+}
+
+int satori_hip_context_destroy(satori_hip_context* c) {
+    return guarded([&] {
+        if (!c) return;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!c->live) return;
+        if (c->matrices > 0)
+            fail(SATORI_HIP_E_ARGUMENT, "Matrices created on the context must be destroyed first.");
+        (void)hipSetDevice(c->device);
+        (void)hipStreamSynchronize(c->stream);
+        c->x.release();
+        c->y.release();
+        c->q8k.release();
+        c->host_x.release();
+        c->host_y.release();
+        (void)hipStreamDestroy(c->stream);
+        c->stream = nullptr;
+        c->live = false;  // the handle stays valid as a tombstone so a second destroy is a no-op
+    });
+}
+
+int satori_hip_context_stream(satori_hip_context* c, void** stream) {
+    return guarded([&] {
+        require_live(c);
+        require(stream, "stream");
+        *stream = c->stream;
+    });
+}
+
+int satori_hip_ternary2_create(satori_hip_context* c, int rows, int columns, int block_size, const void* payload,
+                               size_t payload_length, satori_hip_matrix** matrix) {
+    return guarded([&] {
+        require(matrix, "matrix");
+        *matrix = nullptr;
+        require_live(c);
+        const Shape s = ternary2_shape(rows, columns, block_size);
+        require(payload, "payload");
+        if (static_cast<int64_t>(payload_length) != s.byte_length)
+            fail(SATORI_HIP_E_ARGUMENT, "Payload length must match matrix dimensions.");
+        validate_ternary2(s, static_cast<const uint8_t*>(payload));
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        *matrix = upload(c, s, static_cast<const uint8_t*>(payload));
+    });
+}
+
+int satori_hip_quantized_create(satori_hip_context* c, int rows, int columns, int format, const void* payload,
+                                size_t payload_length, satori_hip_matrix** matrix) {
+    return guarded([&] {
+        require(matrix, "matrix");
+        *matrix = nullptr;
+        require_live(c);
+        const Shape s = quantized_shape(rows, columns, format);
+        require(payload, "payload");
+        if (static_cast<int64_t>(payload_length) != s.byte_length)
+            fail(SATORI_HIP_E_ARGUMENT, "Incorrect quantized payload length.");
+        validate_quantized(s, static_cast<const uint8_t*>(payload));
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        *matrix = upload(c, s, static_cast<const uint8_t*>(payload));
+    });
+}
+
+int satori_hip_ternary2_open(satori_hip_context* c, const char* path, satori_hip_matrix** matrix) {
+    return guarded([&] {
+        require(matrix, "matrix");
+        *matrix = nullptr;
+        require_live(c);
+        require(path, "path");
+        const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+        if (fd < 0) fail(SATORI_HIP_E_ARGUMENT, std::string("Cannot open ") + path + ".");
+        struct stat st;
+        if (::fstat(fd, &st) != 0) {
+            ::close(fd);
+            fail(SATORI_HIP_E_ARGUMENT, std::string("Cannot stat ") + path + ".");
+        }
+        const size_t length = static_cast<size_t>(st.st_size);
+        if (length < 32) {
+            ::close(fd);
+            fail(SATORI_HIP_E_INVALID_DATA, "Truncated Ternary2 header.");  // MappedTernary2Matrix.cs:14-15
+        }
+        void* map = ::mmap(nullptr, length, PROT_READ, MAP_PRIVATE, fd, 0);
+        ::close(fd);
+        if (map == MAP_FAILED) fail(SATORI_HIP_E_ARGUMENT, std::string("Cannot map ") + path + ".");
+        struct Unmap {
+            void* p;
+            size_t n;
+            ~Unmap() { ::munmap(p, n); }
+        } unmap{map, length};
+        const uint8_t* h = static_cast<const uint8_t*>(map);
+        // Ternary2FileFormat.ReadHeader (src/Satori.Core/Ternary2FileFormat.cs:21-35).
+        int32_t rows, columns, block, reserved;
+        int64_t declared;
+        std::memcpy(&rows, h + 8, 4);
+        std::memcpy(&columns, h + 12, 4);
+        std::memcpy(&block, h + 16, 4);
+        std::memcpy(&reserved, h + 20, 4);
+        std::memcpy(&declared, h + 24, 8);
+        if (std::memcmp(h, "STQ2", 4) != 0 || u16_at(h + 4) != 1 || u16_at(h + 6) != 32 || reserved != 0)
+            fail(SATORI_HIP_E_INVALID_DATA, "Unsupported Ternary2 header.");
+        Shape s;
+        try {
+            s = ternary2_shape(rows, columns, block);
+            if (declared != s.byte_length) fail(SATORI_HIP_E_INVALID_DATA, "Payload length disagrees with matrix shape.");
+            if (static_cast<int64_t>(length) != 32 + s.byte_length)
+                fail(SATORI_HIP_E_INVALID_DATA, "Truncated payload or trailing file data.");
+            validate_ternary2(s, h + 32);
+        } catch (const Failure& f) {
+            // MappedTernary2Matrix.cs:25-28: shape and payload failures surface as InvalidDataException.
+            if (f.status == SATORI_HIP_E_ARGUMENT || f.status == SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE ||
+                f.status == SATORI_HIP_E_OVERFLOW)
+                fail(SATORI_HIP_E_INVALID_DATA, "Invalid Ternary2 shape or payload.");
+            throw;
+        }
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        *matrix = upload(c, s, h + 32);
+    });
+}
+
+int satori_hip_matrix_clone(satori_hip_matrix* source, satori_hip_matrix** clone) {
+    return guarded([&] {
+        require(clone, "clone");
+        *clone = nullptr;
+        require(source, "source");
+        satori_hip_context* c = source->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(source);
+        set_device(c);
+        uint8_t* device = nullptr;
+        const size_t bytes = static_cast<size_t>(source->shape.byte_length) + kPayloadSlack;
+        check_hip(hipMalloc(reinterpret_cast<void**>(&device), bytes), "hipMalloc");
+        hipError_t e = hipMemcpyAsync(device, source->payload, bytes, hipMemcpyDeviceToDevice, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(device);
+            check_hip(e, "clone copy");
+        }
+        auto* m = new satori_hip_matrix();
+        m->context = c;
+        m->shape = source->shape;
+        m->payload = device;
+        c->matrices++;
+        *clone = m;
+    });
+}
+
+int satori_hip_matrix_destroy(satori_hip_matrix* m) {
+    return guarded([&] {
+        if (!m) return;
+        satori_hip_context* c = m->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!m->live) return;
+        if (c->live) {
+            (void)hipSetDevice(c->device);
+            (void)hipStreamSynchronize(c->stream);
+        }
+        (void)hipFree(m->payload);
+        m->payload = nullptr;
+        m->live = false;  // tombstone: later calls report ObjectDisposed, a second destroy is a no-op
+        c->matrices--;
+    });
+}
+
+int satori_hip_matrix_shape(const satori_hip_matrix* m, int* rows, int* columns, int* format, int* block_size,
+                            int64_t* byte_length) {
+    return guarded([&] {
+        require_live(m);
+        if (rows) *rows = m->shape.rows;
+        if (columns) *columns = m->shape.columns;
+        if (format) *format = m->shape.format;
+        if (block_size) *block_size = m->shape.block_size;
+        if (byte_length) *byte_length = m->shape.byte_length;
+    });
+}
+
+int satori_hip_matvec(satori_hip_matrix* m, const float* input, size_t input_length, float* output,
+                      size_t output_length) {
+    return guarded([&] { host_matvec(m, input, input_length, 1, output, output_length, false); });
+}
+
+int satori_hip_matvec_batch(satori_hip_matrix* m, const float* input, size_t input_length, int positions,
+                            float* output, size_t output_length) {
+    return guarded([&] { host_matvec(m, input, input_length, positions, output, output_length, true); });
+}
+
+int satori_hip_quantize_q8k(satori_hip_context* c, const float* input, int columns, void* output,
+                            size_t output_length) {
+    return guarded([&] {
+        require_live(c);
+        require(input, "input");
+        require(output, "output");
+        if (columns <= 0 || columns % 256 != 0)
+            fail(SATORI_HIP_E_ARGUMENT, "Invalid Q8_K row dimensions.");  // Q8KCodec.QuantizeRow, :88-89
+        const size_t out_bytes = static_cast<size_t>(columns / 256) * kQ8KBlockBytes;
+        if (output_length != out_bytes) fail(SATORI_HIP_E_ARGUMENT, "Invalid Q8_K row dimensions.");
+        const size_t in_bytes = static_cast<size_t>(columns) * sizeof(float);
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        set_device(c);
+        c->x.reserve(in_bytes);
+        c->q8k.reserve(out_bytes);
+        c->host_x.reserve(in_bytes);
+        c->host_y.reserve(out_bytes);
+        std::memcpy(c->host_x.ptr, input, in_bytes);
+        check_hip(hipMemcpyAsync(c->x.ptr, c->host_x.ptr, in_bytes, hipMemcpyHostToDevice, c->stream), "input copy");
+        check_hip(launch_q8k_quantize(static_cast<const float*>(c->x.ptr), columns, 1,
+                                      static_cast<uint8_t*>(c->q8k.ptr), c->stream),
+                  "Q8_K launch");
+        check_hip(hipMemcpyAsync(c->host_y.ptr, c->q8k.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream),
+                  "output copy");
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+        std::memcpy(output, c->host_y.ptr, out_bytes);
+    });
+}
+
+int satori_hip_matvec_device(satori_hip_matrix* m, const float* input, float* output, void* stream) {
+    return guarded([&] {
+        require(m, "matrix");
+        std::lock_guard<std::mutex> guard(m->context->lock);
+        require_live(m);
+        require(input, "input");
+        require(output, "output");
+        set_device(m->context);
+        enqueue_float(m, input, 1, output, stream ? static_cast<hipStream_t>(stream) : m->context->stream);
+    });
+}
+
+int satori_hip_matvec_batch_device(satori_hip_matrix* m, const float* input, int positions, float* output,
+                                   void* stream) {
+    return guarded([&] {
+        require(m, "matrix");
+        satori_hip_context* c = m->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(m);
+        require(input, "input");
+        require(output, "output");
+        if (positions <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "positions must be positive.");
+        if (m->shape.format == SATORI_HIP_TERNARY2)
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "The batched product is defined for the GGUF block formats only.");
+        set_device(c);
+        hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        if (is_k(m->shape)) {
+            if (positions > 256) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "At most 256 positions per call.");
+            check_kint_width(m->shape);
+            // The workspace is shared by the context's calls; a caller's stream other than the context
+            // stream must be ordered with the context stream before the workspace is reused.
+            c->q8k.reserve(static_cast<size_t>(positions) * m->shape.blocks * kQ8KBlockBytes);
+            enqueue_kint(m, input, positions, output, static_cast<uint8_t*>(c->q8k.ptr), st);
+        } else {
+            enqueue_float(m, input, positions, output, st);
+        }
+    });
+}
+
+int satori_hip_device_alloc(satori_hip_context* c, size_t bytes, void** device_ptr) {
+    return guarded([&] {
+        require(device_ptr, "device_ptr");
+        *device_ptr = nullptr;
+        require_live(c);
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (bytes == 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "bytes must be positive.");
+        set_device(c);
+        check_hip(hipMalloc(device_ptr, bytes), "hipMalloc");
+    });
+}
+
+int satori_hip_device_free(satori_hip_context* c, void* device_ptr) {
+    return guarded([&] {
+        require_live(c);
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!device_ptr) return;
+        set_device(c);
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+        check_hip(hipFree(device_ptr), "hipFree");
+    });
+}
+
+int satori_hip_copy(satori_hip_context* c, void* destination, const void* source, size_t bytes, int kind) {
+    return guarded([&] {
+        require_live(c);
+        require(destination, "destination");
+        require(source, "source");
+        hipMemcpyKind k;
+        switch (kind) {
+            case 1: k = hipMemcpyHostToDevice; break;
+            case 2: k = hipMemcpyDeviceToHost; break;
+            case 3: k = hipMemcpyDeviceToDevice; break;
+            default: fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "kind must be 1, 2 or 3.");
+        }
+        std::lock_guard<std::mutex> guard(c->lock);
+        set_device(c);
+        check_hip(hipMemcpyAsync(destination, source, bytes, k, c->stream), "hipMemcpyAsync");
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+    });
+}
+
+int satori_hip_synchronize(satori_hip_context* c) {
+    return guarded([&] {
+        require_live(c);
+        std::lock_guard<std::mutex> guard(c->lock);
+        set_device(c);
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+    });
+}
+
+int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* matrices, int count,
+                            const float* const* inputs, float* const* outputs, int quantized_activations,
+                            satori_hip_group** group) {
+    return guarded([&] {
+        require(group, "group");
+        *group = nullptr;
+        require_live(c);
+        require(matrices, "matrices");
+        require(inputs, "inputs");
+        require(outputs, "outputs");
+        if (count <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "count must be positive.");
+        std::lock_guard<std::mutex> guard(c->lock);
+        const Shape& first = matrices[0] ? matrices[0]->shape : Shape{};
+        std::vector<MatDesc> host(count);
+        auto* g = new satori_hip_group();
+        g->context = c;
+        g->count = count;
+        try {
+            for (int i = 0; i < count; ++i) {
+                require_live(matrices[i]);
+                if (matrices[i]->context != c) fail(SATORI_HIP_E_ARGUMENT, "Every member must belong to the context.");
+                const Shape& s = matrices[i]->shape;
+                if (s.format != first.format || s.columns != first.columns || s.block_size != first.block_size)
+                    fail(SATORI_HIP_E_ARGUMENT, "Group members must share format, block size and column count.");
+                require(inputs[i], "inputs[i]");
+                require(outputs[i], "outputs[i]");
+                host[i] = MatDesc{matrices[i]->payload, inputs[i], nullptr, outputs[i], s.rows, 0};
+                g->rows_max = std::max(g->rows_max, s.rows);
+            }
+            g->shape = first;
+            g->quantized = quantized_activations != 0 && is_k(first);
+            if (g->quantized) {
+                check_kint_width(first);
+                set_device(c);
+                for (int i = 0; i < count; ++i) {
+                    size_t k = 0;
+                    while (k < g->inputs.size() && g->inputs[k] != inputs[i]) ++k;
+                    if (k == g->inputs.size()) {
+                        g->inputs.push_back(inputs[i]);
+                        uint8_t* buffer = nullptr;
+                        check_hip(hipMalloc(reinterpret_cast<void**>(&buffer),
+                                            static_cast<size_t>(first.blocks) * kQ8KBlockBytes),
+                                  "hipMalloc");
+                        g->q8k.push_back(buffer);
+                    }
+                    host[i].a = g->q8k[k];
+                }
+            }
+            set_device(c);
+            check_hip(hipMalloc(reinterpret_cast<void**>(&g->descriptors), sizeof(MatDesc) * count), "hipMalloc");
+            check_hip(hipMemcpy(g->descriptors, host.data(), sizeof(MatDesc) * count, hipMemcpyHostToDevice),
+                      "descriptor upload");
+        } catch (...) {
+            for (uint8_t* b : g->q8k) (void)hipFree(b);
+            if (g->descriptors) (void)hipFree(g->descriptors);
+            delete g;
+            throw;
+        }
+        *group = g;
+    });
+}
+
+int satori_hip_group_execute(satori_hip_group* g, void* stream) {
+    return guarded([&] {
+        require(g, "group");
+        satori_hip_context* c = g->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!g->live || !c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
+        set_device(c);
+        hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
+        const MatDesc none{};
+        if (g->quantized) {
+            for (size_t k = 0; k < g->inputs.size(); ++k)
+                check_hip(launch_q8k_quantize(g->inputs[k], g->shape.columns, 1, g->q8k[k], st), "Q8_K launch");
+            check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
+        } else {
+            check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
+        }
+    });
+}
+
+int satori_hip_group_destroy(satori_hip_group* g) {
+    return guarded([&] {
+        if (!g) return;
+        satori_hip_context* c = g->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!g->live) return;
+        if (c->live) {
+            (void)hipSetDevice(c->device);
+            (void)hipStreamSynchronize(c->stream);
+        }
+        for (uint8_t* b : g->q8k) (void)hipFree(b);
+        g->q8k.clear();
+        (void)hipFree(g->descriptors);
+        g->descriptors = nullptr;
+        g->live = false;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,514 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI (satori_amd -> libsatori_hip.so).
+
+Bars (the tolerance is written in each test):
+  * FP32-activation products (Ternary2, Q8_0, Q4_0, Q4_K, Q6_K): |y_gpu - y_ref| <= 1e-5 * sum_i |w_i x_i|
+    per row (+ the reference's subnormal floor), against the FP64 product on the decoded weights and the
+    oracle's scalar restatement; plus the reference's own gamma bounds where its tests use them.
+  * Q8_K activation bytes: identical.
+  * Integer K products (ExecuteBatch): identical FP32 outputs to the oracle's ExecuteQuantizedTiled
+    composition.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import satori_amd as S
+from helpers import (fp64_matvec, gguf_tensor, hexbytes, load_json, relative_bound, rng, ternary2_bound)
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TINY = float(np.finfo(np.float32).smallest_subnormal)
+BQ = S.BlockQuantization
+
+
+def assert_within(actual, expected, bound, what=""):
+    actual = np.asarray(actual, dtype=np.float64)
+    err = np.abs(actual - np.asarray(expected, dtype=np.float64))
+    assert np.all(np.isfinite(actual)), f"{what}: non-finite output"
+    bad = np.nonzero(err > bound)[0]
+    assert bad.size == 0, f"{what}: rows {bad[:8]} err {err[bad[:8]]} bound {np.asarray(bound)[bad[:8]]}"
+
+
+def run(matrix: S.HipQuantizedMatrix, x: np.ndarray) -> np.ndarray:
+    y = np.zeros(matrix.rows, dtype=np.float32)
+    matrix.execute(x.astype(np.float32), y)
+    return y
+
+
+# ---------------------------------------------------------------------------------------------
+# Ternary2
+# ---------------------------------------------------------------------------------------------
+
+def test_ternary2_demo_matches_reference_output(context):
+    # src/Satori.Console/Program.cs:169-175 and README.md:27: [4, -2.6666667], 40 bytes.
+    m = S.Ternary2Matrix.quantize(np.array([2, -2, 0, 0, 1, -1], np.float32), 2, 3)
+    assert m.byte_length == 40
+    y = np.zeros(2, np.float32)
+    S.Ternary2MatVec.execute(m, np.array([2, -1, 3], np.float32), y, context)
+    assert y.tolist() == O.t2_matvec_scalar(m.data, 2, 3, 64, [2, -1, 3]).tolist() == [4.0, np.float32(-8 / 3)]
+
+
+def _critical_cases(block: int):
+    """NumericalCorpus.CriticalCases (validation/Satori.Validation/NumericalCorpus.cs:18-38)."""
+    def pattern(name, rows, columns, weight, activation):
+        w = np.array([weight(i) for i in range(rows * columns)], dtype=np.float32).reshape(rows, columns)
+        x = np.array([activation(i) for i in range(columns)], dtype=np.float32)
+        return name, w, x
+
+    fmax = np.finfo(np.float32).max
+    w, x = O.corpus_random_matrix(7, block * 2 + 3)
+    yield "random", w, x
+    yield pattern("zeros", 3, block + 1, lambda i: 0, lambda i: 1)
+    yield pattern("alternating", 5, block * 2 + 1, lambda i: 1 if i % 2 == 0 else -1, lambda i: 1)
+    yield pattern("sparse", 3, block - 1, lambda i: 4 if i % 17 == 0 else 0, lambda i: i % 3 - 1)
+    yield pattern("small-scale", 3, block + 3, lambda i: 1e-30 if i % 2 == 0 else -1e-30, lambda i: 1)
+    yield pattern("large-scale", 3, block + 3, lambda i: 1e30 if i % 2 == 0 else -1e30, lambda i: 1e-10)
+    yield pattern("subnormal", 2, block + 1, lambda i: TINY if i % 2 == 0 else -TINY, lambda i: 1)
+    yield pattern("max-scale", 2, block + 1, lambda i: fmax if i % 2 == 0 else -fmax, lambda i: 1e-38)
+    yield pattern("single-weight", 1, 1, lambda i: -2, lambda i: 3)
+
+
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_critical_corpus_within_reference_bound(context, block):
+    # Ternary2Avx2Tests.cs:115-125 / NumericalCorpusTests.cs:149-158: error/bound <= 1 for every row.
+    for name, w, x in _critical_cases(block):
+        rows, columns = w.shape
+        payload = O.t2_quantize(w, rows, columns, block)
+        m = context.create_ternary2(rows, columns, block, payload)
+        y = run(m, x)
+        wq = O.t2_dequantize(payload, rows, columns, block)
+        expected = fp64_matvec(wq, x)
+        assert_within(y, expected, ternary2_bound(wq, x, block), f"{name} B{block}")
+        scalar = O.t2_matvec_scalar(payload, rows, columns, block, x)
+        assert_within(y, scalar, relative_bound(wq, x) + (columns + 8) * TINY, f"{name} B{block} vs scalar")
+        m.dispose()
+
+
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_column_tails(context, block):
+    # Ternary2Avx2Tests.cs:120-124: columns 1..17, 63..65, 127..129, 255..257, corpus rows.
+    for columns in list(range(1, 18)) + [63, 64, 65, 127, 128, 129, 255, 256, 257, 4099]:
+        w, x = O.corpus_random_matrix(3, columns)
+        payload = O.t2_quantize(w, 3, columns, block)
+        m = context.create_ternary2(3, columns, block, payload)
+        y = run(m, x)
+        wq = O.t2_dequantize(payload, 3, columns, block)
+        assert_within(y, fp64_matvec(wq, x), ternary2_bound(wq, x, block), f"C={columns} B{block}")
+        m.dispose()
+
+
+@pytest.mark.parametrize("size", [1024, 2048, 4096])
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_benchmark_shapes_match_scalar_reference(context, size, block):
+    # The benchmark matrices: N(0,1) weights quantized by Ternary2Matrix.Quantize, x ~ U(-1, 1).
+    g = rng(1729 + size + block)
+    w = g.standard_normal((size, size), dtype=np.float32)
+    x = g.uniform(-1, 1, size).astype(np.float32)
+    payload = S.Ternary2Matrix.quantize(w, size, size, block).data
+    assert np.array_equal(payload, O.t2_quantize(w, size, size, block)), "quantizer bytes differ from oracle"
+    m = context.create_ternary2(size, size, block, payload)
+    y = run(m, x)
+    wq = O.t2_dequantize(payload, size, size, block)
+    bound = relative_bound(wq, x)
+    assert_within(y, O.t2_matvec_scalar(payload, size, size, block, x), bound, "vs scalar reference")
+    assert_within(y, fp64_matvec(wq, x), bound, "vs FP64")
+    m.dispose()
+
+
+def test_ternary2_zero_rows_are_exactly_zero(context):
+    # Ternary2Tests.cs:57-58: an all-zero row next to non-zero rows.
+    w, x = O.corpus_random_matrix(7, 2 * 128 + 3)
+    w[1] = 0
+    payload = O.t2_quantize(w, 7, w.shape[1], 128)
+    m = context.create_ternary2(7, w.shape[1], 128, payload)
+    y = run(m, x)
+    assert y[1] == 0.0 and not np.signbit(y[1])
+    m.dispose()
+
+
+def test_mapped_ternary2_equals_owned(context, tmp_path):
+    # MappedTernary2Tests.cs:9-30: mapped == owned bitwise.
+    g = rng(7)
+    w = g.standard_normal((33, 300), dtype=np.float32)
+    x = g.uniform(-1, 1, 300).astype(np.float32)
+    matrix = S.Ternary2Matrix.quantize(w, 33, 300, 64)
+    path = tmp_path / "m.stq2"
+    matrix.save(str(path))
+    owned = context.create_ternary2(33, 300, 64, matrix.data)
+    with S.MappedTernary2Matrix(str(path), context) as mapped:
+        y1 = np.zeros(33, np.float32)
+        mapped.execute(x, y1)
+    assert np.array_equal(y1, run(owned, x))
+    owned.dispose()
+
+
+def test_mapped_ternary2_rejects_corrupt_files(context, tmp_path):
+    # MappedTernary2Tests.cs:47-68: corrupt headers and payloads are InvalidDataException.
+    matrix = S.Ternary2Matrix.quantize(np.ones((2, 64), np.float32), 2, 64, 64)
+    good = O.stq2_header(2, 64, 64) + matrix.data.tobytes()
+    corruptions = {
+        "magic": lambda b: b"XTQ2" + b[4:],
+        "version": lambda b: b[:4] + b"\x02\x00" + b[6:],
+        "header": lambda b: b[:6] + b"\x20\x01" + b[8:],
+        "reserved": lambda b: b[:20] + b"\x01" + b[21:],
+        "length": lambda b: b[:24] + b"\x00\x00\x00\x00\x00\x00\x00\x00" + b[32:],
+        "truncated": lambda b: b[:-1],
+        "trailing": lambda b: b + b"\x00",
+        "block": lambda b: b[:16] + (100).to_bytes(4, "little") + b[20:],
+        "rows": lambda b: b[:8] + (0).to_bytes(4, "little") + b[12:],
+        "code3": lambda b: b[:36] + b"\x03" + b[37:],
+        "negative-scale": lambda b: b[:32] + np.float32(-1).tobytes() + b[36:],
+        "short": lambda b: b[:20],
+    }
+    for name, corrupt in corruptions.items():
+        path = tmp_path / f"{name}.stq2"
+        path.write_bytes(corrupt(good))
+        with pytest.raises(S.InvalidDataException):
+            S.MappedTernary2Matrix(str(path), context)
+
+
+# ---------------------------------------------------------------------------------------------
+# Q8_0 / Q4_0
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name,fmt", [("q8_0.gguf", BQ.Q8_0), ("q4_0.gguf", BQ.Q4_0)])
+def test_golden_gguf_ones_dot(context, name, fmt):
+    # QuantizedTests.cs:168-184: the golden tensors dot a ones vector to exactly -8.
+    payload, entry = gguf_tensor(name)
+    shape = S.QuantizedMatrixShape(entry["dimensions"][1], entry["dimensions"][0], fmt)
+    m = context.create(payload, shape)
+    assert run(m, np.ones(32, np.float32)).tolist() == [-8.0]
+    m.dispose()
+
+
+def _special_scale_payload(fmt, rows, columns, scales):
+    # QuantizedTests.cs:186-214 (Q8_0) and Q4Tests.cs:239-268 (Q4_0): signed, zero, -0, subnormal, 65504.
+    e, nb = O.GEOMETRY[int(fmt)]
+    blocks = columns // 32
+    data = np.zeros(rows * blocks * nb, np.uint8)
+    for row in range(rows):
+        for b in range(blocks):
+            off = (row * blocks + b) * nb
+            data[off:off + 2] = np.frombuffer(np.float16(scales[row % len(scales)]).tobytes(), np.uint8)
+            if fmt == BQ.Q8_0:
+                for j in range(32):
+                    data[off + 2 + j] = ((row * 32 + b * 17 + j * 7) % 256 - 128) & 0xFF
+            else:
+                for j in range(16):
+                    lo, hi = (j + b) % 16, (15 - j + b) % 16
+                    data[off + 2 + j] = lo | (hi << 4)
+    return data
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+def test_legacy_special_scales_match_fp64(context, fmt):
+    scales = [0.5, -2.0, 0.0, -0.0, float(np.float16(2 ** -24)), 65504.0, 1.0]
+    rows, columns = 7, 96
+    data = _special_scale_payload(fmt, rows, columns, scales)
+    x = np.array([(i % 13 - 6) / 16 for i in range(columns)], np.float32)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = run(m, x)
+    wq = O.decode_matrix(data, rows, columns, int(fmt))
+    expected = fp64_matvec(wq, x)
+    assert_within(y, expected, np.full(rows, 0.001), "reference tolerance 0.001")
+    assert_within(y, expected, relative_bound(wq, x) + 64 * TINY, "1e-5 gate")
+    m.dispose()
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+def test_legacy_critical_cases_within_gamma_bound(context, fmt):
+    # Q8Validation.CriticalCases / Compare (validation/Satori.Validation/Q8Validation.cs:9-53) and
+    # QuantizedAvx2Tests.cs:280-321: gamma(C + C/32 + 2) * sum|product| + n * float.Epsilon.
+    scales = [0.5, -2.0, 0.0, -0.0, float(np.float16(2 ** -24)), 65504.0, 1.0]
+    for rows in (1, 7, 63, 64, 65, 129):
+        for columns in (32, 64, 96, 288, 768):
+            data = _special_scale_payload(fmt, rows, columns, scales)
+            x = np.array([(i * 17 % 31 - 15) / 16 for i in range(columns)], np.float32)
+            m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+            y = run(m, x)
+            wq = O.decode_matrix(data, rows, columns, int(fmt))
+            n = columns + columns / 32 + 2
+            u = 2.0 ** -24
+            g = n * u / (1 - n * u)
+            bound = g * (np.abs(wq.astype(np.float64)) @ np.abs(x.astype(np.float64))) + n * TINY
+            assert_within(y, fp64_matvec(wq, x), bound, f"{fmt.name} {rows}x{columns}")
+            m.dispose()
+
+
+@pytest.mark.parametrize("fmt,rows,columns", [(BQ.Q8_0, 4096, 4096), (BQ.Q4_0, 11008, 4096),
+                                              (BQ.Q4_0, 4096, 11008), (BQ.Q8_0, 65, 96)])
+def test_legacy_benchmark_shapes_match_scalar_reference(context, fmt, rows, columns):
+    g = rng(20261014 + rows + columns)
+    w = (g.standard_normal((rows, columns), dtype=np.float32) * 0.02).astype(np.float32)
+    x = g.standard_normal(columns, dtype=np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    O.q_validate(data, rows, columns, int(fmt))
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = run(m, x)
+    scalar = O.q_matvec_scalar(data, rows, columns, int(fmt), x)
+    wq = O.decode_matrix(data, rows, columns, int(fmt)) if rows * columns <= 1 << 20 else None
+    if wq is not None:
+        bound = relative_bound(wq, x)
+        assert_within(y, fp64_matvec(wq, x), bound, "vs FP64")
+    else:
+        # Sum |w x| via the oracle on |payload|-decoded weights is costly at this size; bound by the
+        # scalar kernel's own magnitudes: |w_i x_i| summed with the absolute input against |w|.
+        absolute = np.zeros(rows, np.float64)
+        e = 32
+        blocks = columns // e
+        nb = O.GEOMETRY[int(fmt)][1]
+        d = data.reshape(rows, blocks, nb)
+        scales = np.abs(d[:, :, :2].copy().view(np.float16).astype(np.float64)[:, :, 0])
+        if fmt == BQ.Q8_0:
+            q = np.abs(d[:, :, 2:].view(np.int8).astype(np.float64))
+        else:
+            lo = (d[:, :, 2:] & 15).astype(np.float64) - 8
+            hi = (d[:, :, 2:] >> 4).astype(np.float64) - 8
+            q = np.abs(np.concatenate([lo, hi], axis=2))
+        absolute = np.einsum("rb,rbj,bj->r", scales, q, np.abs(x.astype(np.float64)).reshape(blocks, e))
+        bound = 1e-5 * absolute
+    assert_within(y, scalar, bound, f"{fmt.name} {rows}x{columns} vs scalar reference")
+    m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# K formats, FP32 activations (Execute)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fixture,fmt", [("q4k-v1.json", BQ.Q4_K), ("q6k-v1.json", BQ.Q6_K)])
+def test_k_fixture_blocks_dot(context, fixture, fmt):
+    # Q4KCodecTests.cs:413-429 / Q6KCodecTests.cs: one-block matrices against the FP64 fixture dot.
+    for case in load_json(fixture)["cases"]:
+        block = hexbytes(case["block_hex"])
+        x = np.array(case["input"], np.float32)
+        m = context.create(block, S.QuantizedMatrixShape(1, 256, fmt))
+        y = run(m, x)
+        ref = case["dot"]
+        assert abs(y[0] - ref) <= 1e-2 + 1e-4 * abs(ref), (case["name"], y[0], ref)
+        wq = O.decode_block(block, int(fmt)).reshape(1, 256)
+        assert_within(y, O.q_matvec_scalar(block, 1, 256, int(fmt), x), relative_bound(wq, x) + 8 * TINY,
+                      case["name"])
+        m.dispose()
+
+
+def test_k_real_tensor_blocks(context):
+    # KParityTests.cs:177-212: real Q4_K / Q6_K bytes against the fixture's FP64 dots.
+    for case in load_json("k-real-v1.json")["cases"]:
+        fmt = BQ.Q4_K if case["name"].startswith("q4k:") else BQ.Q6_K
+        raw = hexbytes(case["block_hex"])
+        x = np.array(case["input"], np.float32)
+        nb = O.GEOMETRY[int(fmt)][1]
+        for b in range(case["blocks"]):
+            block = raw[b * nb:(b + 1) * nb]
+            m = context.create(block, S.QuantizedMatrixShape(1, 256, fmt))
+            y = run(m, x)
+            ref = case["dots"][b]
+            assert abs(y[0] - ref) <= 1e-2 + 1e-4 * abs(ref), (case["name"], b, y[0], ref)
+            m.dispose()
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("rows,columns", [(8960, 1536), (1536, 8960), (1536, 1536), (256, 1536), (17, 512)])
+def test_k_float_path_matches_scalar_reference(context, fmt, rows, columns):
+    g = rng(20261014 + rows * 7 + columns)
+    w = (g.standard_normal((rows, columns), dtype=np.float32) * 0.02).astype(np.float32)
+    x = g.standard_normal(columns, dtype=np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = run(m, x)
+    wq = O.decode_matrix(data, rows, columns, int(fmt)) if rows * columns <= 1 << 21 else None
+    scalar = O.q_matvec_scalar(data, rows, columns, int(fmt), x)
+    if wq is None:
+        sub = slice(0, rows, 37)  # the row bound needs the decoded rows; check a deterministic subset
+        wq_rows = np.stack([O.decode_matrix(data.reshape(rows, -1)[r], 1, columns, int(fmt))[0]
+                            for r in range(rows)[sub]])
+        assert_within(y[sub], scalar[sub], relative_bound(wq_rows, x), "vs scalar (row subset)")
+        # every row: a looser size-independent check against the scalar path
+        assert np.allclose(y, scalar, rtol=1e-4, atol=1e-4)
+    else:
+        assert_within(y, scalar, relative_bound(wq, x), "vs scalar")
+        assert_within(y, fp64_matvec(wq, x), relative_bound(wq, x), "vs FP64")
+    m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# Q8_K and the integer K products (ExecuteBatch): bit-exact
+# ---------------------------------------------------------------------------------------------
+
+def test_q8k_quantizer_matches_fixture_bytes(context):
+    # Q8KCodecTests.cs:22-35: block bytes identical to the reference quantizer.
+    for case in load_json("q8k-v1.json")["cases"]:
+        x = np.array(case["input"], np.float32)
+        assert np.array_equal(context.quantize_q8k(x), hexbytes(case["block_hex"])), case["name"]
+    for case in load_json("q6k-q8k-v1.json")["cases"]:
+        x = np.array(case["input"], np.float32)
+        assert np.array_equal(context.quantize_q8k(x), hexbytes(case["activation_hex"])), case["name"]
+
+
+def test_q8k_quantizer_matches_oracle_on_edge_cases(context):
+    g = rng(99)
+    tiny = TINY
+    cases = {
+        "normal": g.standard_normal(8960).astype(np.float32),
+        "uniform": g.uniform(-1, 1, 1536).astype(np.float32),
+        "zeros": np.zeros(512, np.float32),
+        "one-zero-block": np.concatenate([np.zeros(256), g.standard_normal(256)]).astype(np.float32),
+        "ties": np.tile(np.array([1, -1, 0.5, -0.5], np.float32), 64 * 3),
+        "negative-max-first": np.concatenate([[-3.0], g.uniform(-3, 3, 255)]).astype(np.float32),
+        "subnormal": np.full(256, tiny, np.float32) * np.sign(g.standard_normal(256)).astype(np.float32),
+        "half-steps": (np.arange(256, dtype=np.float32) - 127.5) / 127.0,
+        "large": (g.standard_normal(768) * 1e30).astype(np.float32),
+        "sin": np.sin(np.arange(768) * 0.01).astype(np.float32),
+    }
+    for name, x in cases.items():
+        assert np.array_equal(context.quantize_q8k(x), O.q8k_quantize_row(x)), name
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("rows,columns", [(8960, 1536), (1536, 8960), (1536, 1536), (256, 1536), (17, 3584)])
+def test_k_integer_batch_is_bit_exact(context, fmt, rows, columns):
+    # Q6KQuantizedProductTests.cs:284-308 and KParityTests.cs:214-244: the projection equals the
+    # composition of the public codecs, summed block by block; here the oracle's restatement of
+    # ExecuteQuantizedTiled, compared bit for bit.
+    g = rng(20261014 + rows + 3 * columns)
+    w = (g.standard_normal((rows, columns), dtype=np.float32) * 0.02).astype(np.float32)
+    x = g.standard_normal(columns, dtype=np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.zeros(rows, np.float32)
+    m.execute_batch(x, 1, y)
+    expected = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x))
+    assert np.array_equal(y.view(np.uint32), expected.view(np.uint32))
+    if rows <= 2048 and columns <= 2048:
+        assert np.array_equal(y.view(np.uint32), O.q_matvec_batch(data, rows, columns, int(fmt), x, 1).view(np.uint32))
+    m.dispose()
+
+
+@pytest.mark.parametrize("fmt,fixture", [(BQ.Q4_K, "q4k-v1.json"), (BQ.Q6_K, "q6k-v1.json")])
+def test_k_integer_batch_multi_position_on_fixture_blocks(context, fmt, fixture):
+    # BatchedMatVecTests.cs:45-113: payloads tiled from the fixture blocks, several positions.
+    blocks = [hexbytes(c["block_hex"]) for c in load_json(fixture)["cases"]]
+    for rows, columns, positions in ((2, 512, 4), (3, 512, 1), (2, 256, 8), (7, 512, 5), (40, 1024, 3)):
+        nbr = columns // 256
+        data = np.concatenate([blocks[i % len(blocks)] for i in range(rows * nbr)])
+        x = np.array([[np.sin(p * 0.37 + c * 0.011) * 1.5 for c in range(columns)] for p in range(positions)],
+                     np.float32)
+        m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+        y = np.zeros(positions * rows, np.float32)
+        m.execute_batch(x.reshape(-1), positions, y)
+        expected = O.q_matvec_batch(data, rows, columns, int(fmt), x.reshape(-1), positions)
+        assert np.array_equal(y.view(np.uint32), expected.view(np.uint32)), (rows, columns, positions)
+        m.dispose()
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+def test_legacy_batch_matches_per_position(context, fmt):
+    # BatchedMatVecTests.cs:61-88 (float path): each position within 1e-5 * sum|w x| of the scalar product.
+    g = rng(5)
+    rows, columns, positions = 37, 288, 6
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.zeros(positions * rows, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    wq = O.decode_matrix(data, rows, columns, int(fmt))
+    batch_ref = O.q_matvec_batch(data, rows, columns, int(fmt), x.reshape(-1), positions)
+    for p in range(positions):
+        bound = relative_bound(wq, x[p])
+        assert_within(y[p * rows:(p + 1) * rows], fp64_matvec(wq, x[p]), bound, f"position {p}")
+        assert_within(y[p * rows:(p + 1) * rows], batch_ref[p * rows:(p + 1) * rows], bound, f"position {p} batch")
+    m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# Contract: errors, output commit, disposal, device and group entry points
+# ---------------------------------------------------------------------------------------------
+
+def test_failed_execution_leaves_output_unchanged(context):
+    # IQuantizedMatrix.cs:6 and VulkanQ8Tests.cs:73-97 (sentinel output).
+    payload, entry = gguf_tensor("q8_0.gguf")
+    m = context.create(payload, S.QuantizedMatrixShape(1, 32, BQ.Q8_0))
+    sentinel = np.full(1, 123.5, np.float32)
+    with pytest.raises(S.ArgumentException):
+        m.execute(np.ones(31, np.float32), sentinel)
+    bad = np.ones(32, np.float32)
+    bad[3] = np.inf
+    with pytest.raises(S.ArgumentException):
+        m.execute(bad, sentinel)
+    assert sentinel[0] == 123.5
+    with pytest.raises(S.ArgumentException):
+        m.execute(np.ones(32, np.float32), np.zeros(2, np.float32))
+    buf = np.ones(64, np.float32)
+    with pytest.raises(S.ArgumentException):  # overlapping input and output
+        m.execute(buf[:32], buf[31:32])
+    m.dispose()
+    m.dispose()  # idempotent
+    with pytest.raises(S.ObjectDisposedException):
+        m.execute(np.ones(32, np.float32), sentinel)
+
+
+def test_create_rejects_invalid_payloads(context):
+    with pytest.raises(S.InvalidDataException):
+        context.create(np.frombuffer(b"\x00\x7c" + bytes(32), np.uint8), S.QuantizedMatrixShape(1, 32, BQ.Q8_0))
+    with pytest.raises(S.ArgumentException):
+        context.create(np.zeros(33, np.uint8), S.QuantizedMatrixShape(1, 32, BQ.Q8_0))
+    payload = np.zeros(20, np.uint8)
+    payload[:4] = np.frombuffer(np.float32(1).tobytes(), np.uint8)
+    payload[4] = 3
+    with pytest.raises(S.ArgumentException):
+        context.create_ternary2(1, 1, 64, payload)
+
+
+def test_k_batch_rejects_too_many_positions(context):
+    data = S.quantize_weights(np.zeros((2, 256), np.float32), 2, 256, BQ.Q4_K)
+    m = context.create(data, S.QuantizedMatrixShape(2, 256, BQ.Q4_K))
+    with pytest.raises(S.ArgumentOutOfRangeException):
+        m.execute_batch(np.zeros(257 * 256, np.float32), 257, np.zeros(257 * 2, np.float32))
+    with pytest.raises(S.ArgumentOutOfRangeException):
+        m.execute_batch(np.zeros(256, np.float32), 0, np.zeros(2, np.float32))
+    m.dispose()
+
+
+def test_device_and_group_entry_points_match_host_calls(context):
+    # One launch over several matrices sharing an input (the q/k/v shape of the decode step) must equal
+    # the per-matrix host calls bit for bit, for the FP32 and the Q8_K integer products.
+    g = rng(11)
+    columns = 1536
+    mats = []
+    for i in range(3):
+        rows = 300 + 64 * i
+        w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+        data = S.quantize_weights(w, rows, columns, BQ.Q4_K)
+        mats.append(context.create(data, S.QuantizedMatrixShape(rows, columns, BQ.Q4_K)))
+    x = g.standard_normal(columns).astype(np.float32)
+    dx = context.alloc(x.nbytes)
+    context.upload(dx, x)
+    for quantized in (False, True):
+        ys = [context.alloc(4 * m.rows) for m in mats]
+        group = S.HipGroup(context, mats, [dx] * 3, ys, quantized)
+        group.execute()
+        context.synchronize()
+        for m, dy in zip(mats, ys):
+            ref = np.zeros(m.rows, np.float32)
+            if quantized:
+                m.execute_batch(x, 1, ref)
+            else:
+                m.execute(x, ref)
+            got = context.download(np.zeros(m.rows, np.float32), dy)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+            if quantized:
+                m.execute_batch_device(dx, 1, dy)
+            else:
+                m.execute_device(dx, dy)
+            context.synchronize()
+            got = context.download(np.zeros(m.rows, np.float32), dy)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        group.dispose()
+        for dy in ys:
+            context.free(dy)
+    context.free(dx)
+    for m in mats:
+        m.dispose()
