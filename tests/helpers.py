@@ -58,3 +58,47 @@ def relative_bound(weights: np.ndarray, x: np.ndarray, tolerance: float = 1e-5) 
 
 def fp64_matvec(weights: np.ndarray, x: np.ndarray) -> np.ndarray:
     return weights.astype(np.float64) @ x.astype(np.float64)
+
+
+def critical_cases(block: int):
+    """NumericalCorpus.CriticalCases (validation/Satori.Validation/NumericalCorpus.cs:18-38)."""
+    def pattern(name, rows, columns, weight, activation):
+        w = np.array([weight(i) for i in range(rows * columns)], dtype=np.float32).reshape(rows, columns)
+        x = np.array([activation(i) for i in range(columns)], dtype=np.float32)
+        return name, w, x
+
+    from oracle import oracle as O
+
+    TINY = float(np.finfo(np.float32).smallest_subnormal)
+    fmax = np.finfo(np.float32).max
+    w, x = O.corpus_random_matrix(7, block * 2 + 3)
+    yield "random", w, x
+    yield pattern("zeros", 3, block + 1, lambda i: 0, lambda i: 1)
+    yield pattern("alternating", 5, block * 2 + 1, lambda i: 1 if i % 2 == 0 else -1, lambda i: 1)
+    yield pattern("sparse", 3, block - 1, lambda i: 4 if i % 17 == 0 else 0, lambda i: i % 3 - 1)
+    yield pattern("small-scale", 3, block + 3, lambda i: 1e-30 if i % 2 == 0 else -1e-30, lambda i: 1)
+    yield pattern("large-scale", 3, block + 3, lambda i: 1e30 if i % 2 == 0 else -1e30, lambda i: 1e-10)
+    yield pattern("subnormal", 2, block + 1, lambda i: TINY if i % 2 == 0 else -TINY, lambda i: 1)
+    yield pattern("max-scale", 2, block + 1, lambda i: fmax if i % 2 == 0 else -fmax, lambda i: 1e-38)
+    yield pattern("single-weight", 1, 1, lambda i: -2, lambda i: 3)
+
+
+def special_scale_payload(fmt, rows, columns, scales):
+    # QuantizedTests.cs:186-214 (Q8_0) and Q4Tests.cs:239-268 (Q4_0): signed, zero, -0, subnormal, 65504.
+    from oracle import oracle as O
+
+    e, nb = O.GEOMETRY[int(fmt)]
+    blocks = columns // 32
+    data = np.zeros(rows * blocks * nb, np.uint8)
+    for row in range(rows):
+        for b in range(blocks):
+            off = (row * blocks + b) * nb
+            data[off:off + 2] = np.frombuffer(np.float16(scales[row % len(scales)]).tobytes(), np.uint8)
+            if int(fmt) == 0:
+                for j in range(32):
+                    data[off + 2 + j] = ((row * 32 + b * 17 + j * 7) % 256 - 128) & 0xFF
+            else:
+                for j in range(16):
+                    lo, hi = (j + b) % 16, (15 - j + b) % 16
+                    data[off + 2 + j] = lo | (hi << 4)
+    return data

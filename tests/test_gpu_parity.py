@@ -14,7 +14,8 @@ import numpy as np
 import pytest
 
 import satori_amd as S
-from helpers import (fp64_matvec, gguf_tensor, hexbytes, load_json, relative_bound, rng, ternary2_bound)
+from helpers import (critical_cases as _critical_cases, fp64_matvec, gguf_tensor, hexbytes, load_json,
+                     relative_bound, rng, special_scale_payload as _special_scale_payload, ternary2_bound)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -48,26 +49,6 @@ def test_ternary2_demo_matches_reference_output(context):
     y = np.zeros(2, np.float32)
     S.Ternary2MatVec.execute(m, np.array([2, -1, 3], np.float32), y, context)
     assert y.tolist() == O.t2_matvec_scalar(m.data, 2, 3, 64, [2, -1, 3]).tolist() == [4.0, np.float32(-8 / 3)]
-
-
-def _critical_cases(block: int):
-    """NumericalCorpus.CriticalCases (validation/Satori.Validation/NumericalCorpus.cs:18-38)."""
-    def pattern(name, rows, columns, weight, activation):
-        w = np.array([weight(i) for i in range(rows * columns)], dtype=np.float32).reshape(rows, columns)
-        x = np.array([activation(i) for i in range(columns)], dtype=np.float32)
-        return name, w, x
-
-    fmax = np.finfo(np.float32).max
-    w, x = O.corpus_random_matrix(7, block * 2 + 3)
-    yield "random", w, x
-    yield pattern("zeros", 3, block + 1, lambda i: 0, lambda i: 1)
-    yield pattern("alternating", 5, block * 2 + 1, lambda i: 1 if i % 2 == 0 else -1, lambda i: 1)
-    yield pattern("sparse", 3, block - 1, lambda i: 4 if i % 17 == 0 else 0, lambda i: i % 3 - 1)
-    yield pattern("small-scale", 3, block + 3, lambda i: 1e-30 if i % 2 == 0 else -1e-30, lambda i: 1)
-    yield pattern("large-scale", 3, block + 3, lambda i: 1e30 if i % 2 == 0 else -1e30, lambda i: 1e-10)
-    yield pattern("subnormal", 2, block + 1, lambda i: TINY if i % 2 == 0 else -TINY, lambda i: 1)
-    yield pattern("max-scale", 2, block + 1, lambda i: fmax if i % 2 == 0 else -fmax, lambda i: 1e-38)
-    yield pattern("single-weight", 1, 1, lambda i: -2, lambda i: 3)
 
 
 @pytest.mark.parametrize("block", [64, 128, 256])
@@ -181,25 +162,6 @@ def test_golden_gguf_ones_dot(context, name, fmt):
     m = context.create(payload, shape)
     assert run(m, np.ones(32, np.float32)).tolist() == [-8.0]
     m.dispose()
-
-
-def _special_scale_payload(fmt, rows, columns, scales):
-    # QuantizedTests.cs:186-214 (Q8_0) and Q4Tests.cs:239-268 (Q4_0): signed, zero, -0, subnormal, 65504.
-    e, nb = O.GEOMETRY[int(fmt)]
-    blocks = columns // 32
-    data = np.zeros(rows * blocks * nb, np.uint8)
-    for row in range(rows):
-        for b in range(blocks):
-            off = (row * blocks + b) * nb
-            data[off:off + 2] = np.frombuffer(np.float16(scales[row % len(scales)]).tobytes(), np.uint8)
-            if fmt == BQ.Q8_0:
-                for j in range(32):
-                    data[off + 2 + j] = ((row * 32 + b * 17 + j * 7) % 256 - 128) & 0xFF
-            else:
-                for j in range(16):
-                    lo, hi = (j + b) % 16, (15 - j + b) % 16
-                    data[off + 2 + j] = lo | (hi << 4)
-    return data
 
 
 @pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
