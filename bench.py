@@ -38,6 +38,7 @@ import satori_amd as S  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 ROTATION_BYTES = 1 << 30
+CALIBRATION_BYTES = 1 << 30
 BQ = S.BlockQuantization
 METRIC = "effective quantized-payload GB/s (% of MI355X HBM peak) per format, 4096² batch 1"
 PUBLISHED_AVX2_T2_4096_B128 = 1.31  # GB/s, Ternary2 AVX2 4096^2 B128, docs/benchmarks/avx2-2026-10-12 run 1
@@ -167,6 +168,20 @@ def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     return out
 
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch of the headline kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (calibrated against a copy of known size); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1]), "profiles/" + name
+    except OSError:
+        pass
+    return None, None
+
+
 def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
     """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample."""
     from oracle import oracle as O
@@ -211,6 +226,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline workload only, no other formats")
+    ap.add_argument("--profile", action="store_true",
+                    help="only the headline grouped launches (for rocprofv3 kernel statistics), no other timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the MatVec on a single MI355X "
@@ -225,6 +242,21 @@ def main() -> int:
     payload, x = make_ternary2(rows, columns, block)
     head = Case(ctx, "ternary2-4096-b128", lambda: ctx.create_ternary2(rows, columns, block, payload),
                 payload.size, rows, columns, x, False)
+    if args.profile:
+        ms = time_launches(ctx, events, head.run_group, args.steps, args.warmup)
+        gbs = head.copies * payload.size / (ms * 1e-3) / 1e9
+        # Calibration for the HBM byte counters: one device-to-device copy of a known size (the runtime's
+        # copy kernel reads and writes CALIBRATION_BYTES each).
+        src, dst = ctx.alloc(CALIBRATION_BYTES), ctx.alloc(CALIBRATION_BYTES)
+        ctx.copy_device(dst, src, CALIBRATION_BYTES)
+        ctx.free(src)
+        ctx.free(dst)
+        print(json.dumps({"profile": "ternary2-4096-b128 grouped", "launches": args.steps + args.warmup,
+                          "launch_us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "copies": head.copies,
+                          "algorithmic_bytes_per_launch": head.copies * int(payload.size),
+                          "calibration_copy_bytes": CALIBRATION_BYTES}))
+        head.close()
+        return 0
     headline = measure(ctx, events, head, args.steps, args.warmup)
     # Timed region of the headline itself, for the contract fields.
     ms_per_step = headline["launch_us"] * 1e-3
@@ -255,6 +287,7 @@ def main() -> int:
     progress("cpu baseline")
     cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
     value = headline["gbs"]
+    traffic, traffic_source = profiled_traffic("ternary2_4096_b128_grouped.md")
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -282,7 +315,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": "gemv_float_kernel<Ternary2Chunk<128>, 64, true, true> (grouped)",
             "launch_us": round(headline["launch_us"], 2),
             "algorithmic_bytes_per_launch": headline["copies"] * int(payload.size),

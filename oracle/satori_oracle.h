@@ -11,7 +11,8 @@
  * with -ffp-contract=off so no multiply-add is fused that the C# JIT would not fuse (RyuJIT
  * fuses only explicit Fma.MultiplyAdd calls).
  *
- * Parity pinning of every function is listed in oracle/README.md; none is "parity unpinned".
+ * Every function is pinned by tests/test_oracle.py against the reference's golden fixtures, its tests'
+ * known answers, FP64 brute force or an exact integer identity; none is "parity unpinned".
  */
 #ifndef SATORI_ORACLE_H
 #define SATORI_ORACLE_H

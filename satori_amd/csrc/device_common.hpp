@@ -5,27 +5,34 @@
 
 #include <cstdint>
 
+#define SATORI_GLOBAL __attribute__((address_space(1)))
+
 namespace satori {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// 16-byte load from a 4-byte aligned global address (one global_load_dwordx4).
+// Loads through the global address space (global_load_* rather than flat_*): every pointer the kernels
+// dereference with these helpers is device memory returned by hipMalloc.
 __device__ __forceinline__ u32x4 load16_a4(const uint8_t* p) {
-    return *reinterpret_cast<const u32x4_a4*>(p);
+    return *(const SATORI_GLOBAL u32x4_a4*)(p);
 }
 
 __device__ __forceinline__ uint32_t load4_a4(const uint8_t* p) {
-    return *reinterpret_cast<const uint32_t*>(p);
+    return *(const SATORI_GLOBAL uint32_t*)(p);
 }
+
+__device__ __forceinline__ float load_f32(const float* p) { return *(const SATORI_GLOBAL float*)(p); }
+
+__device__ __forceinline__ void store_f32(float* p, float v) { *(SATORI_GLOBAL float*)(p) = v; }
 
 // N little-endian dwords starting at a 2-byte aligned address, assembled from N + 1 aligned dword loads
 // and v_alignbyte. Reads up to 4 bytes past p + 4N; every payload allocation carries slack for that.
 template <int N>
 __device__ __forceinline__ void load_unaligned(const uint8_t* p, uint32_t (&out)[N]) {
     const uintptr_t address = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(address & ~uintptr_t(3));
+    const SATORI_GLOBAL uint32_t* base = (const SATORI_GLOBAL uint32_t*)(address & ~uintptr_t(3));
     const uint32_t shift = static_cast<uint32_t>(address & 3);
     uint32_t d[N + 1];
 #pragma unroll
@@ -50,18 +57,33 @@ __device__ __forceinline__ float sbyte_to_float(uint32_t word, int index) {
     return static_cast<float>(static_cast<int8_t>(word >> (8 * index)));
 }
 
-// Sum over aligned groups of L lanes (L a power of two <= 64); every lane of a group gets the sum.
+// DPP lane moves within 16-lane rows (row_shr:n) and across rows (row_bcast:15 / row_bcast:31).
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, BOUND_ZERO);
+}
+
+// Sum over aligned groups of L lanes (L a power of two, 2..64) with DPP adds: the total of each group is
+// valid in the group's LAST lane (lane % L == L - 1); other lanes hold partial sums.
 template <int L>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int offset = L / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+__device__ __forceinline__ float group_sum_last(float v) {
+    if constexpr (L >= 2) v += __int_as_float(dpp<0x111, 0xF, true>(__float_as_int(v)));
+    if constexpr (L >= 4) v += __int_as_float(dpp<0x112, 0xF, true>(__float_as_int(v)));
+    if constexpr (L >= 8) v += __int_as_float(dpp<0x114, 0xF, true>(__float_as_int(v)));
+    if constexpr (L >= 16) v += __int_as_float(dpp<0x118, 0xF, true>(__float_as_int(v)));
+    if constexpr (L >= 32) v += __int_as_float(dpp<0x142, 0xA, false>(__float_as_int(v)));
+    if constexpr (L >= 64) v += __int_as_float(dpp<0x143, 0xC, false>(__float_as_int(v)));
     return v;
 }
 
 template <int L>
-__device__ __forceinline__ int group_sum_int(int v) {
-#pragma unroll
-    for (int offset = L / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+__device__ __forceinline__ int group_sum_last_int(int v) {
+    if constexpr (L >= 2) v += dpp<0x111, 0xF, true>(v);
+    if constexpr (L >= 4) v += dpp<0x112, 0xF, true>(v);
+    if constexpr (L >= 8) v += dpp<0x114, 0xF, true>(v);
+    if constexpr (L >= 16) v += dpp<0x118, 0xF, true>(v);
+    if constexpr (L >= 32) v += dpp<0x142, 0xA, false>(v);
+    if constexpr (L >= 64) v += dpp<0x143, 0xC, false>(v);
     return v;
 }
 

@@ -20,7 +20,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRowUnroll = 2;
 
 // ------------------------------------------------------------------------------------------------
 // Ternary2: f32 scale + 2-bit codes, 4 per byte LSB first, 01 = +1, 10 = -1
@@ -30,6 +29,7 @@ constexpr int kRowUnroll = 2;
 // ------------------------------------------------------------------------------------------------
 template <int B>
 struct Ternary2Chunk {
+    static constexpr int kRowUnroll = 2;
     static constexpr int kWeights = 64;
     static constexpr int kPadShift = 6;
     static constexpr int kPerBlock = B / 64;
@@ -85,6 +85,7 @@ struct Ternary2Chunk {
 // aligned dword loads with v_alignbyte; int8 -> float is one SDWA conversion per weight.
 // ------------------------------------------------------------------------------------------------
 struct Q8_0Chunk {
+    static constexpr int kRowUnroll = 2;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 5;
     struct Regs {
@@ -127,6 +128,7 @@ struct Q8_0Chunk {
 // the factor 16 is removed exactly with the power-of-two scale 1/16.
 // ------------------------------------------------------------------------------------------------
 struct Q4_0Chunk {
+    static constexpr int kRowUnroll = 2;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 5;
     struct Regs {
@@ -189,6 +191,7 @@ __device__ __forceinline__ void q4k_scale_min(int j, const u32x4& head, int& sca
 }
 
 struct Q4_KChunk {
+    static constexpr int kRowUnroll = 2;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 6;
     struct Regs {
@@ -246,6 +249,7 @@ struct Q4_KChunk {
 // reference's (d*sc)*(q-32) since 32*d*sc is exact.
 // ------------------------------------------------------------------------------------------------
 struct Q6_KChunk {
+    static constexpr int kRowUnroll = 1;
     static constexpr int kWeights = 64;
     static constexpr int kPadShift = 7;
     struct Regs {
@@ -335,17 +339,20 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
     if constexpr (XLDS) {
         const int padded = F::padded_columns(s);
         for (int i = threadIdx.x; i < padded; i += kThreads)
-            xs[i + ((i >> F::kPadShift) << 2)] = i < columns ? x[i] : 0.0f;
+            xs[i + ((i >> F::kPadShift) << 2)] = i < columns ? load_f32(x + i) : 0.0f;
         __syncthreads();
     }
     auto xf = [&](int i) -> float {
         if constexpr (XLDS)
             return xs[i + ((i >> F::kPadShift) << 2)];
         else
-            return i < columns ? x[i] : 0.0f;
+            return i < columns ? load_f32(x + i) : 0.0f;
     };
 
     constexpr int kRowsPerPass = 64 / L;
+    constexpr int kStride = kWaves * kRowsPerPass;  // rows between a lane's consecutive rows
+    constexpr int kRowUnroll = F::kRowUnroll;
+    constexpr int kStep = kStride * kRowUnroll;      // rows per iteration of the whole workgroup
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane / L;
@@ -353,50 +360,66 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
     const int nchunks = F::chunks(s);
     const typename F::Consts k = F::consts();
     const int64_t row_bytes = s.row_bytes;
+    const int first = row_begin + wave * kRowsPerPass;  // wave-uniform
 
     float xr[F::kWeights];
     if constexpr (ONE) {
-        if (lr < nchunks) {
+        // Each lane owns one chunk of every row: its activations stay in registers, and the next
+        // iteration's rows are loaded while the current ones are computed.
+        const bool active = lr < nchunks;
+        if (active) {
             F::load_x(xf, lr, xr);
         } else {
 #pragma unroll
             for (int j = 0; j < F::kWeights; ++j) xr[j] = 0.0f;
         }
-    }
-
-    constexpr int kStep = kWaves * kRowsPerPass * kRowUnroll;
-    for (int r0 = row_begin + wave * kRowsPerPass; r0 < row_end; r0 += kStep) {
-        float acc[kRowUnroll];
-        int row[kRowUnroll];
+        typename F::Regs cur[kRowUnroll], nxt[kRowUnroll];
 #pragma unroll
         for (int u = 0; u < kRowUnroll; ++u) {
-            row[u] = r0 + u * kWaves * kRowsPerPass + sub;
-            acc[u] = 0.0f;
+            const int row = first + u * kStride + sub;
+            if (active && row < row_end) F::load(m.w + row * row_bytes, lr, cur[u]);
         }
-        if constexpr (ONE) {
-            typename F::Regs regs[kRowUnroll];
+        for (int base = first; base < row_end; base += kStep) {
 #pragma unroll
-            for (int u = 0; u < kRowUnroll; ++u)
-                if (row[u] < row_end && lr < nchunks) F::load(m.w + row[u] * row_bytes, lr, regs[u]);
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int row = base + kStep + u * kStride + sub;
+                if (active && row < row_end) F::load(m.w + row * row_bytes, lr, nxt[u]);
+            }
 #pragma unroll
-            for (int u = 0; u < kRowUnroll; ++u)
-                if (row[u] < row_end && lr < nchunks) acc[u] = F::dot(regs[u], xr, k);
-        } else {
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int row = base + u * kStride + sub;
+                const float partial = (active && row < row_end) ? F::dot(cur[u], xr, k) : 0.0f;
+                const float total = group_sum_last<L>(partial);
+                if (lr == L - 1 && row < row_end) store_f32(y + row, total);
+            }
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) cur[u] = nxt[u];
+        }
+    } else {
+        for (int base = first; base < row_end; base += kStep) {
+            float acc[kRowUnroll];
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) acc[u] = 0.0f;
             for (int c = lr; c < nchunks; c += L) {
                 F::load_x(xf, c, xr);
                 typename F::Regs regs[kRowUnroll];
 #pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u)
-                    if (row[u] < row_end) F::load(m.w + row[u] * row_bytes, c, regs[u]);
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int row = base + u * kStride + sub;
+                    if (row < row_end) F::load(m.w + row * row_bytes, c, regs[u]);
+                }
 #pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u)
-                    if (row[u] < row_end) acc[u] += F::dot(regs[u], xr, k);
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int row = base + u * kStride + sub;
+                    if (row < row_end) acc[u] += F::dot(regs[u], xr, k);
+                }
             }
-        }
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-            const float total = group_sum<L>(acc[u]);
-            if (lr == 0 && row[u] < row_end) y[row[u]] = total;
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int row = base + u * kStride + sub;
+                const float total = group_sum_last<L>(acc[u]);
+                if (lr == L - 1 && row < row_end) store_f32(y + row, total);
+            }
         }
     }
 }
@@ -422,7 +445,7 @@ hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, La
     int lanes = 8;
     while (lanes < 64 && lanes < chunks) lanes <<= 1;
     const int rows_per_pass = 64 / lanes;
-    const int rows_per_iteration = kWaves * rows_per_pass * kRowUnroll;
+    const int rows_per_iteration = kWaves * rows_per_pass * F::kRowUnroll;
     // Rows per workgroup: at least one full iteration; grow while the grid keeps >= 2048 workgroups
     // (8 per CU on 256 CUs), so small matrices still spread over the whole chip.
     int64_t groups_total = static_cast<int64_t>(count) * s.positions;

@@ -8,6 +8,8 @@
 //  - the products are exact int32 sums (v_dot4_i32_i8), and the per-block FP32 expression and the
 //    block-order accumulation of each row are those of QuantizedKAvx2Kernel.ExecuteQuantizedTiled
 //    (src/Satori.Core/QuantizedKAvx2Kernel.cs:47-99), so each output equals the reference's float.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -79,12 +81,11 @@ __global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restric
 // ------------------------------------------------------------------------------------------------
 // Integer product. A workgroup owns kTileRows rows of one member at one position. The position's Q8_K
 // row is staged in LDS as separate arrays (codes, group sums, scales) so code reads are 16-byte aligned.
-// Work items are (row, block) pairs, G lanes each (Q4_K: 8 lanes x 32 weights, Q6_K: 4 lanes x 64
-// weights); the G lanes' int32 partials are summed exactly, the pair's leader forms the block's FP32
+// Work items are (row, block) pairs, 4 lanes of 64 weights each; the G lanes' int32 partials are summed exactly, the pair's leader forms the block's FP32
 // term and stores it in LDS, and finally one thread per row adds its terms in block order.
 // ------------------------------------------------------------------------------------------------
 constexpr int kThreads = 256;
-constexpr int kTileRows = 32;
+constexpr int kTileRows = 64;
 
 // Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) on the scales[12] bytes held in three dwords.
 __device__ __forceinline__ int q4k_scale_byte(const u32x4& head, int i) {
@@ -111,44 +112,61 @@ struct ActTile {
     float* scales;     // [blocks]
 };
 
-// Q4_K pair, lane c of 8: chunk qs[16c, 16c + 16) (Q4KCodec.DotProduct / MinProduct, Q4KCodec.cs:117-153).
-__device__ __forceinline__ void q4k_pair(const uint8_t* block, const ActTile& act, int b, int c, int& dot,
-                                         int& min_part, u32x4& head) {
-    head = load16_a4(block);
-    const u32x4 qs = load16_a4(block + 16 + 16 * c);
-    const int g = c >> 1, h = c & 1;
+// Q4_K pair, lane c of 4 = group g: qs[32g, 32g + 32), low nibbles are weights 64g + i of sub-block 2g,
+// high nibbles weights 64g + 32 + i of sub-block 2g + 1 (Q4KCodec.DotProduct / MinProduct, Q4KCodec.cs:117-153).
+struct Q4KRaw {
+    u32x4 head;  // d, dmin, scales[12]
+    u32x4 qs0, qs1;
+};
+
+__device__ __forceinline__ void q4k_load(const uint8_t* block, int c, Q4KRaw& r) {
+    r.head = load16_a4(block);
+    r.qs0 = load16_a4(block + 16 + 32 * c);
+    r.qs1 = load16_a4(block + 32 + 32 * c);
+}
+
+__device__ __forceinline__ void q4k_dot(const Q4KRaw& r, const ActTile& act, int b, int g, int& dot, int& min_part) {
     int s0, m0, s1, m1;
-    q4k_scale_min(2 * g, head, s0, m0);
-    q4k_scale_min(2 * g + 1, head, s1, m1);
-    const u32x4 lo_codes = *reinterpret_cast<const u32x4*>(act.codes + 64 * b + 16 * g + 4 * h);
-    const u32x4 hi_codes = *reinterpret_cast<const u32x4*>(act.codes + 64 * b + 16 * g + 8 + 4 * h);
+    q4k_scale_min(2 * g, r.head, s0, m0);
+    q4k_scale_min(2 * g + 1, r.head, s1, m1);
+    const uint32_t* codes = act.codes + 64 * b + 16 * g;
+    const u32x4 lo0 = *reinterpret_cast<const u32x4*>(codes), lo1 = *reinterpret_cast<const u32x4*>(codes + 4);
+    const u32x4 hi0 = *reinterpret_cast<const u32x4*>(codes + 8), hi1 = *reinterpret_cast<const u32x4*>(codes + 12);
     int lo = 0, hi = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        lo = sdot4(qs[w] & 0x0F0F0F0Fu, lo_codes[w], lo);
-        hi = sdot4((qs[w] >> 4) & 0x0F0F0F0Fu, hi_codes[w], hi);
+        lo = sdot4(r.qs0[w] & 0x0F0F0F0Fu, lo0[w], lo);
+        lo = sdot4(r.qs1[w] & 0x0F0F0F0Fu, lo1[w], lo);
+        hi = sdot4((r.qs0[w] >> 4) & 0x0F0F0F0Fu, hi0[w], hi);
+        hi = sdot4((r.qs1[w] >> 4) & 0x0F0F0F0Fu, hi1[w], hi);
     }
     dot = s0 * lo + s1 * hi;
     const int16_t* sums = act.sums + 16 * b;
-    min_part = h == 0 ? m0 * (sums[4 * g] + sums[4 * g + 1]) + m1 * (sums[4 * g + 2] + sums[4 * g + 3]) : 0;
+    min_part = m0 * (sums[4 * g] + sums[4 * g + 1]) + m1 * (sums[4 * g + 2] + sums[4 * g + 3]);
 }
 
 // Q6_K pair, lane c of 4: half h = c / 2, slice t = c % 2, i.e. weights 128h + 32k + 16t + i
 // (Q6KCodec.DotProduct, Q6KCodec.cs:114-146, with the -32 centring applied through the group sums:
 // sum sc * (q - 32) * code = sum sc * q * code - 32 * sum sc * bsum, both exact).
-__device__ __forceinline__ int q6k_pair(const uint8_t* block, const ActTile& act, int b, int c, float& d) {
-    const int h = c >> 1, t = c & 1;
+struct Q6KRaw {
     uint32_t qla[4], qlb[4], qh[4], sc[4], tail[1];
-    load_unaligned<4>(block + 64 * h + 16 * t, qla);
-    load_unaligned<4>(block + 64 * h + 32 + 16 * t, qlb);
-    load_unaligned<4>(block + 128 + 32 * h + 16 * t, qh);
-    load_unaligned<4>(block + 192, sc);
-    load_unaligned<1>(block + 208, tail);
-    d = half_bits_to_float(tail[0] & 0xFFFFu);
+};
+
+__device__ __forceinline__ void q6k_load(const uint8_t* block, int c, Q6KRaw& r) {
+    const int h = c >> 1, t = c & 1;
+    load_unaligned<4>(block + 64 * h + 16 * t, r.qla);
+    load_unaligned<4>(block + 64 * h + 32 + 16 * t, r.qlb);
+    load_unaligned<4>(block + 128 + 32 * h + 16 * t, r.qh);
+    load_unaligned<4>(block + 192, r.sc);
+    load_unaligned<1>(block + 208, r.tail);
+}
+
+__device__ __forceinline__ int q6k_dot(const Q6KRaw& r, const ActTile& act, int b, int c) {
+    const int h = c >> 1, t = c & 1;
     int dotk[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        const uint32_t a = qla[w], bq = qlb[w], hb = qh[w];
+        const uint32_t a = r.qla[w], bq = r.qlb[w], hb = r.qh[w];
         const uint32_t q[4] = {
             (a & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u),
             (bq & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u),
@@ -163,8 +181,8 @@ __device__ __forceinline__ int q6k_pair(const uint8_t* block, const ActTile& act
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int index = 8 * h + 2 * k + t;
-        const int s = static_cast<int8_t>(sc[index >> 2] >> (8 * (index & 3)));
-        total += s * (dotk[k] - 32 * sums[index]);
+        const int sc = static_cast<int8_t>(r.sc[index >> 2] >> (8 * (index & 3)));
+        total += sc * (dotk[k] - 32 * sums[index]);
     }
     return total;
 }
@@ -172,8 +190,10 @@ __device__ __forceinline__ int q6k_pair(const uint8_t* block, const ActTile& act
 template <int FORMAT>
 __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const MatDesc* __restrict__ group,
                                                               LaunchShape s) {
-    constexpr int G = FORMAT == kQ4_K ? 8 : 4;       // lanes per (row, block) pair
+    constexpr int G = 4;  // lanes per (row, block) pair
     constexpr int kBlockBytes = FORMAT == kQ4_K ? 144 : 210;
+    constexpr int kPairsPerStep = kThreads / G;
+    using Raw = typename std::conditional<FORMAT == kQ4_K, Q4KRaw, Q6KRaw>::type;
     const MatDesc m = group ? group[blockIdx.y] : one;
     const int row_begin = blockIdx.x * kTileRows;
     if (row_begin >= m.rows) return;
@@ -191,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     const uint8_t* arow = m.a + static_cast<int64_t>(position) * nb * kQ8KBlockBytes;
     for (int i = threadIdx.x; i < 73 * nb; i += kThreads) {
         const int b = i / 73, word = i % 73;
-        const uint32_t value = reinterpret_cast<const uint32_t*>(arow + b * kQ8KBlockBytes)[word];
+        const uint32_t value = load4_a4(arow + b * kQ8KBlockBytes + 4 * word);
         if (word == 0)
             act.scales[b] = __uint_as_float(value);
         else if (word <= 64)
@@ -199,37 +219,54 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
         else
             reinterpret_cast<uint32_t*>(act.sums)[8 * b + word - 65] = value;
     }
-    __syncthreads();
 
+    // Work items are (row, block) pairs in row-major order; the G lanes of a pair share its index, so the
+    // DPP group sums stay inside the pair. The next pair's payload is loaded before the current one is
+    // reduced.
     const int lane = threadIdx.x & 63;
     const int c = lane % G;
     const int pairs = rows * nb;
-    const int64_t row_bytes = s.row_bytes;
-    for (int p0 = (threadIdx.x / G); p0 < pairs + 0; p0 += kThreads / G) {
-        // All G lanes of a pair share p0, so the group reductions below stay inside the pair.
-        const int r = p0 / nb, b = p0 % nb;
-        const uint8_t* block = m.w + (row_begin + r) * row_bytes + b * kBlockBytes;
+    const uint8_t* tile = m.w + static_cast<int64_t>(row_begin) * s.row_bytes;
+    auto block_of = [&](int p) { return tile + (p / nb) * s.row_bytes + (p % nb) * kBlockBytes; };
+    int p0 = threadIdx.x / G;
+    Raw cur, nxt;
+    if (p0 < pairs) {
+        if constexpr (FORMAT == kQ4_K)
+            q4k_load(block_of(p0), c, cur);
+        else
+            q6k_load(block_of(p0), c, cur);
+    }
+    __syncthreads();  // activations staged
+    for (; p0 < pairs; p0 += kPairsPerStep) {
+        const int pn = p0 + kPairsPerStep;
+        if (pn < pairs) {
+            if constexpr (FORMAT == kQ4_K)
+                q4k_load(block_of(pn), c, nxt);
+            else
+                q6k_load(block_of(pn), c, nxt);
+        }
+        const int b = p0 % nb;
         float term = 0.0f;
         if constexpr (FORMAT == kQ4_K) {
             int dot, min_part;
-            u32x4 head;
-            q4k_pair(block, act, b, c, dot, min_part, head);
-            dot = group_sum_int<G>(dot);
-            min_part = group_sum_int<G>(min_part);
+            q4k_dot(cur, act, b, c, dot, min_part);
+            dot = group_sum_last_int<G>(dot);
+            min_part = group_sum_last_int<G>(min_part);
             const float a = act.scales[b];
             if (a != 0.0f) {  // zero activation block: skipped (QuantizedKAvx2Kernel.cs:86)
-                const float dA = __fmul_rn(half_bits_to_float(head[0] & 0xFFFFu), a);
-                const float dminA = __fmul_rn(half_bits_to_float(head[0] >> 16), a);
+                const float dA = __fmul_rn(half_bits_to_float(cur.head[0] & 0xFFFFu), a);
+                const float dminA = __fmul_rn(half_bits_to_float(cur.head[0] >> 16), a);
                 term = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot)), __fmul_rn(dminA, static_cast<float>(min_part)));
             }
         } else {
-            float d;
-            int dot = q6k_pair(block, act, b, c, d);
-            dot = group_sum_int<G>(dot);
+            int dot = q6k_dot(cur, act, b, c);
+            dot = group_sum_last_int<G>(dot);
             const float a = act.scales[b];
+            const float d = half_bits_to_float(cur.tail[0] & 0xFFFFu);
             if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, d), static_cast<float>(dot));
         }
-        if (c == 0) terms[r * nb + b] = term;
+        if (c == G - 1) terms[p0] = term;  // p0 = r * nb + b
+        cur = nxt;
     }
     __syncthreads();
     if (threadIdx.x < rows) {
@@ -238,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
         float acc = 0.0f;
         const float* t = terms + threadIdx.x * nb;
         for (int b = 0; b < nb; ++b) acc = __fadd_rn(acc, t[b]);
-        m.y[static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x] = acc;
+        store_f32(m.y + static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x, acc);
     }
 }
 
@@ -252,6 +289,8 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
 }
 
 size_t kint_lds_bytes(int blocks) { return static_cast<size_t>(73 + kTileRows) * blocks * sizeof(uint32_t); }
+
+int kint_tile_rows() { return kTileRows; }
 
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
                             hipStream_t stream) {
