@@ -317,7 +317,7 @@ def main() -> int:
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
-            "kernel": "gemv_float_kernel<Ternary2Chunk<128>, 64, true, true> (grouped)",
+            "kernel": "t2_kernel<128, 2> (grouped)",
             "launch_us": round(headline["launch_us"], 2),
             "algorithmic_bytes_per_launch": headline["copies"] * int(payload.size),
         },

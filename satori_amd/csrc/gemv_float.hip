@@ -1,12 +1,12 @@
-// FP32-activation MatVec over packed blocks for gfx950: Ternary2 (B = 64/128/256), Q8_0, Q4_0, Q4_K and
-// Q6_K, computed directly on the payload without materialising weights.
+// FP32-activation MatVec over packed GGUF blocks for gfx950: Q8_0, Q4_0, Q4_K and Q6_K, computed directly
+// on the payload without materialising weights (Ternary2 has its own kernel on a panel layout).
 //
-// Work decomposition. A row is cut into fixed "chunks" (a 16-byte code segment of a Ternary2 block, one
-// Q8_0/Q4_0 block, an eighth of a Q4_K block, a quarter of a Q6_K block). A wave64 handles 64 / L rows
-// at a time with L lanes per row; lane j of a row owns chunks j, j + L, ... Consecutive lanes read
-// consecutive chunks, so a row's payload is read by contiguous 128-bit loads. The activation vector is
-// staged once per workgroup in LDS; when every row has at most L chunks (C <= 4096 for Ternary2) each
-// lane pulls its chunk's activations into registers once and keeps them for every row it visits.
+// Work decomposition. A row is cut into fixed "chunks" (one Q8_0/Q4_0 block, an eighth of a Q4_K block, a
+// quarter of a Q6_K block). A wave64 handles 64 / L rows at a time with L lanes per row; lane j of a row
+// owns chunks j, j + L, ... Consecutive lanes read consecutive chunks, so a row's payload is read by
+// contiguous loads. The activation vector is staged once per workgroup in LDS; when every row has at most
+// L chunks each lane pulls its chunk's activations into registers once and keeps them for every row it
+// visits.
 // Row sums are reduced across the L lanes by cross-lane shuffles.
 //
 // Arithmetic per format follows the reference decoders (file:line cited on each decoder); products
@@ -20,64 +20,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-
-// ------------------------------------------------------------------------------------------------
-// Ternary2: f32 scale + 2-bit codes, 4 per byte LSB first, 01 = +1, 10 = -1
-// (docs/ternary2-v1.md; Ternary2MatVec.ExecuteScalarCore, src/Satori.Core/Ternary2MatVec.cs:52-76).
-// A chunk is 16 code bytes = 64 weights. Codes become FP8 bytes through a v_perm lookup table, then
-// v_cvt_pk_f32_fp8 yields exact +-1.0 / 0.0, so each weight costs one FMA and no per-weight compare.
-// ------------------------------------------------------------------------------------------------
-template <int B>
-struct Ternary2Chunk {
-    static constexpr int kRowUnroll = 2;
-    static constexpr int kWeights = 64;
-    static constexpr int kPadShift = 6;
-    static constexpr int kPerBlock = B / 64;
-    static constexpr int kBlockBytes = 4 + B / 4;
-    struct Regs {
-        u32x4 codes;
-        float scale;
-    };
-    struct Consts {
-        uint32_t lut;  // bytes: code 0 -> fp8(0), 1 -> fp8(+1), 2 -> fp8(-1), 3 -> fp8(0)
-    };
-    __device__ static Consts consts() {
-        // The hardware's own encoding of +1 and -1, so the table matches v_cvt_pk_f32_fp8 by construction.
-        const uint32_t e = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(1.0f, -1.0f, 0, false));
-        return Consts{((e & 0xFFu) << 8) | (((e >> 8) & 0xFFu) << 16)};
-    }
-    __device__ static int chunks(const LaunchShape& s) { return s.blocks * kPerBlock; }
-    __device__ static int padded_columns(const LaunchShape& s) { return s.blocks * B; }
-    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
-        const uint8_t* block = row + (chunk / kPerBlock) * kBlockBytes;
-        r.scale = __uint_as_float(load4_a4(block));
-        r.codes = load16_a4(block + 4 + 16 * (chunk % kPerBlock));
-    }
-    template <class XF>
-    __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
-#pragma unroll
-        for (int j = 0; j < kWeights; ++j) x[j] = xf(64 * chunk + j);
-    }
-    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts& k) {
-        float acc0 = 0.0f, acc1 = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t w = r.codes[d];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t sel = (w >> (2 * q)) & 0x03030303u;  // codes 16d + q + {0, 4, 8, 12}
-                const uint32_t f8 = __builtin_amdgcn_perm(0u, k.lut, sel);
-                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(f8), false);
-                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(f8), true);
-                acc0 = __builtin_fmaf(lo[0], x[16 * d + q], acc0);
-                acc1 = __builtin_fmaf(lo[1], x[16 * d + 4 + q], acc1);
-                acc0 = __builtin_fmaf(hi[0], x[16 * d + 8 + q], acc0);
-                acc1 = __builtin_fmaf(hi[1], x[16 * d + 12 + q], acc1);
-            }
-        }
-        return (acc0 + acc1) * r.scale;
-    }
-};
 
 // ------------------------------------------------------------------------------------------------
 // Q8_0: f16 d + 32 int8, w = d * q (docs/gguf-subset-v1.md:94; QuantizedMatVec.ExecuteScalar,
@@ -478,15 +420,6 @@ hipError_t launch_gemv_float(const MatDesc& one, const MatDesc* group, int count
                              hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
     switch (s.format) {
-        case kTernary2: {
-            const int padded = s.blocks * s.block_size;
-            switch (s.block_size) {
-                case 64: return launch_format<Ternary2Chunk<64>>(one, group, count, s, s.blocks, padded, stream);
-                case 128: return launch_format<Ternary2Chunk<128>>(one, group, count, s, s.blocks * 2, padded, stream);
-                case 256: return launch_format<Ternary2Chunk<256>>(one, group, count, s, s.blocks * 4, padded, stream);
-                default: return hipErrorInvalidValue;
-            }
-        }
         case kQ8_0: return launch_format<Q8_0Chunk>(one, group, count, s, s.blocks, s.columns, stream);
         case kQ4_0: return launch_format<Q4_0Chunk>(one, group, count, s, s.blocks, s.columns, stream);
         case kQ4_K: return launch_format<Q4_KChunk>(one, group, count, s, s.blocks * 8, s.columns, stream);

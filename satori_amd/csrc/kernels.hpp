@@ -35,10 +35,58 @@ struct LaunchShape {
     int rows_per_wg;    // rows one workgroup owns (launcher-chosen)
 };
 
-// FP32-activation MatVec for every format (Ternary2, Q8_0, Q4_0, Q4_K, Q6_K). `group` is a device array
-// of `count` descriptors or nullptr, in which case `one` is used and count must be 1.
+// FP32-activation MatVec for the GGUF formats (Q8_0, Q4_0, Q4_K, Q6_K) on the packed row-major payload.
+// `group` is a device array of `count` descriptors or nullptr, in which case `one` is used and count must be 1.
 hipError_t launch_gemv_float(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape,
                              hipStream_t stream);
+
+// ---- Ternary2 device layout ("panels") ----
+// The device copy of a Ternary2 matrix is regrouped so that one wave (64 lanes, one row each) reads whole
+// cache lines: rows form panels of 64; a row's code stream (2 bits per column, LSB first, padded to whole
+// blocks) is cut into 64-column chunks of 16 bytes; chunk k of the 64 rows of panel p is stored as 64
+// consecutive 16-byte records. Block scales follow all codes, 64 consecutive floats per (panel, block slot).
+// Chunks per row are rounded up to an even number (one 128-column tile = two chunks); padding rows, chunks
+// and slots are zero. The total equals the packed payload up to that padding.
+constexpr int kT2PanelRows = 64;
+constexpr int kT2TileColumns = 128;
+
+struct T2Layout {
+    int panels;           // ceil(rows / 64)
+    int tiles;            // 128-column tiles per row
+    int chunks;           // 2 * tiles
+    int slots;            // scale slots per panel row: chunks * 64 / B
+    int64_t codes_bytes;  // panels * chunks * 1024
+    int64_t bytes;        // codes_bytes + panels * slots * 256
+};
+
+inline T2Layout t2_layout(int rows, int columns, int block_size) {
+    T2Layout l{};
+    const int blocks = (columns + block_size - 1) / block_size;
+    l.panels = (rows + kT2PanelRows - 1) / kT2PanelRows;
+    l.tiles = (blocks * block_size + kT2TileColumns - 1) / kT2TileColumns;
+    l.chunks = 2 * l.tiles;
+    l.slots = l.chunks * 64 / block_size;
+    l.codes_bytes = static_cast<int64_t>(l.panels) * l.chunks * 1024;
+    l.bytes = l.codes_bytes + static_cast<int64_t>(l.panels) * l.slots * 256;
+    return l;
+}
+
+// How a Ternary2 launch is cut: each workgroup owns 4 * panels_per_wave panels and a range of
+// tiles_per_split tiles; with splits > 1 the per-split row sums go to a partial buffer of
+// t2_partial_floats() floats and a second kernel adds them in split order.
+struct T2Plan {
+    int panels_per_wave;  // 1 or 2
+    int splits;
+    int tiles_per_split;
+};
+
+T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positions);
+size_t t2_partial_floats(const T2Plan& plan, int rows_max, int count, int positions);
+
+// Ternary2 MatVec on the panel layout (MatDesc::w points at it). `partials` must hold
+// t2_partial_floats(plan, ...) floats when plan.splits > 1 and may be null otherwise.
+hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape, const T2Plan& plan,
+                     float* partials, hipStream_t stream);
 
 // Q8_K quantization of `positions` rows of `columns` floats (columns a multiple of 256), bit-exact with
 // Q8KCodec.QuantizeRow. Output [positions][columns / 256 * 292].

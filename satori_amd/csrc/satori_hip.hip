@@ -85,7 +85,10 @@ struct satori_hip_context {
 struct satori_hip_matrix {
     satori_hip_context* context = nullptr;
     satori::Shape shape;
-    uint8_t* payload = nullptr;  // device
+    uint8_t* payload = nullptr;  // device: the packed payload, or the panel layout for Ternary2
+    int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
+    satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
+    float* partials = nullptr;   // Ternary2 split row sums (device), when plan.splits > 1
     bool live = true;
 };
 
@@ -96,6 +99,8 @@ struct satori_hip_group {
     bool quantized = false;
     int rows_max = 0;
     satori::MatDesc* descriptors = nullptr;   // device
+    satori::T2Plan plan{};                     // Ternary2 groups
+    float* partials = nullptr;                 // Ternary2 split row sums (device)
     std::vector<const float*> inputs;          // distinct inputs, quantized path
     std::vector<uint8_t*> q8k;                 // one Q8_K row per distinct input (device)
     bool live = true;
@@ -162,8 +167,11 @@ size_t kint_lds_limit_blocks() { return (64 * 1024) / ((73 + static_cast<size_t>
 // Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers.
 void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
     MatDesc d{m->payload, x, nullptr, y, m->shape.rows, 0};
-    check_hip(launch_gemv_float(d, nullptr, 1, launch_shape(m->shape, positions, m->shape.rows), stream),
-              "gemv launch");
+    const LaunchShape l = launch_shape(m->shape, positions, m->shape.rows);
+    if (m->shape.format == SATORI_HIP_TERNARY2)
+        check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->partials, stream), "Ternary2 launch");
+    else
+        check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");
 }
 
 // Enqueue the Q8_K integer product: quantize positions rows into `q8k`, then the product.
@@ -186,21 +194,69 @@ bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
     return a0 < b0 + b_bytes && b0 < a0 + a_bytes;
 }
 
+// Regroups a validated packed Ternary2 payload (rows of [f32 scale][B / 4 code bytes] blocks) into the
+// panel layout: row r is lane r % 64 of panel r / 64; its 16-byte code chunks and block scales land at the
+// T2Layout positions; padding stays zero.
+std::vector<uint8_t> ternary2_panels(const Shape& s, const uint8_t* packed) {
+    const T2Layout l = t2_layout(s.rows, s.columns, s.block_size);
+    std::vector<uint8_t> out(static_cast<size_t>(l.bytes), 0);
+    const int chunks_per_block = s.block_size / 64;
+    for (int r = 0; r < s.rows; ++r) {
+        const int64_t panel = r / kT2PanelRows, lane = r % kT2PanelRows;
+        const uint8_t* row = packed + static_cast<int64_t>(r) * s.row_bytes;
+        for (int b = 0; b < s.blocks; ++b) {
+            const uint8_t* block = row + static_cast<int64_t>(b) * s.block_bytes;
+            std::memcpy(&out[l.codes_bytes + ((panel * l.slots + b) * 64 + lane) * 4], block, 4);
+            for (int i = 0; i < chunks_per_block; ++i) {
+                const int64_t chunk = static_cast<int64_t>(b) * chunks_per_block + i;
+                std::memcpy(&out[((panel * l.chunks + chunk) * 64 + lane) * 16], block + 4 + 16 * i, 16);
+            }
+        }
+    }
+    return out;
+}
+
+// Device allocations of one matrix: the weights (+ slack) and, for a split Ternary2 plan, its partials.
+void allocate_matrix(satori_hip_matrix* m, int64_t device_bytes) {
+    check_hip(hipMalloc(reinterpret_cast<void**>(&m->payload), static_cast<size_t>(device_bytes) + kPayloadSlack),
+              "hipMalloc");
+    m->device_bytes = device_bytes;
+    if (m->shape.format == SATORI_HIP_TERNARY2) {
+        m->plan = t2_plan(m->shape.rows, m->shape.columns, m->shape.block_size, 1, 1);
+        const size_t floats = t2_partial_floats(m->plan, m->shape.rows, 1, 1);
+        if (floats) check_hip(hipMalloc(reinterpret_cast<void**>(&m->partials), floats * sizeof(float)), "hipMalloc");
+    }
+}
+
+void free_matrix(satori_hip_matrix* m) {
+    if (m->payload) (void)hipFree(m->payload);
+    if (m->partials) (void)hipFree(m->partials);
+    m->payload = nullptr;
+    m->partials = nullptr;
+}
+
 satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
     set_device(c);
-    uint8_t* device = nullptr;
-    check_hip(hipMalloc(reinterpret_cast<void**>(&device), static_cast<size_t>(s.byte_length) + kPayloadSlack),
-              "hipMalloc");
-    hipError_t e = hipMemcpy(device, payload, static_cast<size_t>(s.byte_length), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(device + s.byte_length, 0, kPayloadSlack);
-    if (e != hipSuccess) {
-        (void)hipFree(device);
-        check_hip(e, "weight upload");
+    std::vector<uint8_t> panels;
+    const uint8_t* source = payload;
+    int64_t bytes = s.byte_length;
+    if (s.format == SATORI_HIP_TERNARY2) {
+        panels = ternary2_panels(s, payload);
+        source = panels.data();
+        bytes = static_cast<int64_t>(panels.size());
     }
     auto* m = new satori_hip_matrix();
     m->context = c;
     m->shape = s;
-    m->payload = device;
+    try {
+        allocate_matrix(m, bytes);
+        check_hip(hipMemcpy(m->payload, source, static_cast<size_t>(bytes), hipMemcpyHostToDevice), "weight upload");
+        check_hip(hipMemset(m->payload + bytes, 0, kPayloadSlack), "weight upload");
+    } catch (...) {
+        free_matrix(m);
+        delete m;
+        throw;
+    }
     c->matrices++;
     return m;
 }
@@ -440,19 +496,20 @@ int satori_hip_matrix_clone(satori_hip_matrix* source, satori_hip_matrix** clone
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(source);
         set_device(c);
-        uint8_t* device = nullptr;
-        const size_t bytes = static_cast<size_t>(source->shape.byte_length) + kPayloadSlack;
-        check_hip(hipMalloc(reinterpret_cast<void**>(&device), bytes), "hipMalloc");
-        hipError_t e = hipMemcpyAsync(device, source->payload, bytes, hipMemcpyDeviceToDevice, c->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-        if (e != hipSuccess) {
-            (void)hipFree(device);
-            check_hip(e, "clone copy");
-        }
         auto* m = new satori_hip_matrix();
         m->context = c;
         m->shape = source->shape;
-        m->payload = device;
+        try {
+            allocate_matrix(m, source->device_bytes);
+            const size_t bytes = static_cast<size_t>(source->device_bytes) + kPayloadSlack;
+            check_hip(hipMemcpyAsync(m->payload, source->payload, bytes, hipMemcpyDeviceToDevice, c->stream),
+                      "clone copy");
+            check_hip(hipStreamSynchronize(c->stream), "clone copy");
+        } catch (...) {
+            free_matrix(m);
+            delete m;
+            throw;
+        }
         c->matrices++;
         *clone = m;
     });
@@ -468,8 +525,7 @@ int satori_hip_matrix_destroy(satori_hip_matrix* m) {
             (void)hipSetDevice(c->device);
             (void)hipStreamSynchronize(c->stream);
         }
-        (void)hipFree(m->payload);
-        m->payload = nullptr;
+        free_matrix(m);
         m->live = false;  // tombstone: later calls report ObjectDisposed, a second destroy is a no-op
         c->matrices--;
     });
@@ -648,6 +704,13 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
             }
             g->shape = first;
             g->quantized = quantized_activations != 0 && is_k(first);
+            if (first.format == SATORI_HIP_TERNARY2) {
+                g->plan = t2_plan(g->rows_max, first.columns, first.block_size, count, 1);
+                const size_t floats = t2_partial_floats(g->plan, g->rows_max, count, 1);
+                set_device(c);
+                if (floats)
+                    check_hip(hipMalloc(reinterpret_cast<void**>(&g->partials), floats * sizeof(float)), "hipMalloc");
+            }
             if (g->quantized) {
                 check_kint_width(first);
                 set_device(c);
@@ -672,6 +735,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
         } catch (...) {
             for (uint8_t* b : g->q8k) (void)hipFree(b);
             if (g->descriptors) (void)hipFree(g->descriptors);
+            if (g->partials) (void)hipFree(g->partials);
             delete g;
             throw;
         }
@@ -693,6 +757,8 @@ int satori_hip_group_execute(satori_hip_group* g, void* stream) {
             for (size_t k = 0; k < g->inputs.size(); ++k)
                 check_hip(launch_q8k_quantize(g->inputs[k], g->shape.columns, 1, g->q8k[k], st), "Q8_K launch");
             check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
+        } else if (g->shape.format == SATORI_HIP_TERNARY2) {
+            check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->partials, st), "Ternary2 launch");
         } else {
             check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
         }
@@ -713,6 +779,8 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         g->q8k.clear();
         (void)hipFree(g->descriptors);
         g->descriptors = nullptr;
+        if (g->partials) (void)hipFree(g->partials);
+        g->partials = nullptr;
         g->live = false;
     });
 }

@@ -98,6 +98,77 @@ def test_ternary2_benchmark_shapes_match_scalar_reference(context, size, block):
     m.dispose()
 
 
+def _t2_random_payload(g, rows: int, columns: int, block: int) -> np.ndarray:
+    """Valid Ternary2 payload with uniform codes in {0, +1, -1} and positive scales; padding codes zero."""
+    blocks = -(-columns // block)
+    codes = g.integers(0, 3, size=(rows, blocks * block), dtype=np.uint8)
+    codes[:, columns:] = 0
+    packed = codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6)
+    scales = g.uniform(0.01, 2.0, size=(rows, blocks)).astype(np.float32)
+    out = np.concatenate([scales.view(np.uint8).reshape(rows, blocks, 4),
+                          packed.reshape(rows, blocks, block // 4)], axis=2)
+    return np.ascontiguousarray(out.reshape(-1))
+
+
+# Ternary2 launches split the columns over workgroups (with a second, reducing kernel) unless the rows
+# alone give about 1024 workgroups of 4 or 8 panels of 64 rows. Small shapes above cover the split plans;
+# the tests below cover the unsplit ones (one and two panels per wave) through very tall matrices and
+# grouped launches, with ragged columns, an odd block count for B = 64, members whose rows end inside a
+# panel, and the widest slice one workgroup stages (14,336 columns).
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_tall_matrix_pair_tables(context, block):
+    g = rng(4242 + block)
+    base_rows, columns = 1031, 1050
+    base = _t2_random_payload(g, base_rows, columns, block)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    rows = 1024 * 256 + 77
+    row_bytes = base.size // base_rows
+    payload = np.tile(base.reshape(base_rows, row_bytes), (-(-rows // base_rows), 1))[:rows].reshape(-1)
+    m = context.create_ternary2(rows, columns, block, payload)
+    y = run(m, x)
+    m.dispose()
+    wq = O.t2_dequantize(base, base_rows, columns, block)
+    scalar = O.t2_matvec_scalar(base, base_rows, columns, block, x)
+    index = np.arange(rows) % base_rows
+    assert_within(y, scalar[index], relative_bound(wq, x)[index], f"tall B{block} vs scalar")
+    assert_within(y, fp64_matvec(wq, x)[index], relative_bound(wq, x)[index], f"tall B{block} vs FP64")
+
+
+@pytest.mark.parametrize("columns,members", [(4099, 128), (14336, 64)])
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_grouped_pair_tables(context, block, columns, members):
+    g = rng(777 + block + columns)
+    shapes = [4096, 4001]
+    payloads = [_t2_random_payload(g, r, columns, block) for r in shapes]
+    mats = [context.create_ternary2(r, columns, block, p) for r, p in zip(shapes, payloads)]
+    xs = [g.uniform(-1, 1, columns).astype(np.float32) for _ in range(3)]
+    dxs = []
+    for x in xs:
+        dxs.append(context.alloc(x.nbytes))
+        context.upload(dxs[-1], x)
+    order = [(i % 2, i % 3) for i in range(members)]
+    ys = [context.alloc(4 * shapes[k]) for k, _ in order]
+    group = S.HipGroup(context, [mats[k] for k, _ in order], [dxs[j] for _, j in order], ys)
+    group.execute()
+    context.synchronize()
+    expected = {}
+    for k in range(2):
+        wq = O.t2_dequantize(payloads[k], shapes[k], columns, block)
+        for j in range(3):
+            expected[k, j] = (O.t2_matvec_scalar(payloads[k], shapes[k], columns, block, xs[j]),
+                              fp64_matvec(wq, xs[j]), relative_bound(wq, xs[j]))
+    for i, (k, j) in enumerate(order):
+        got = context.download(np.zeros(shapes[k], np.float32), ys[i])
+        scalar, exact, bound = expected[k, j]
+        assert_within(got, scalar, bound, f"member {i} B{block} C={columns} vs scalar")
+        assert_within(got, exact, bound, f"member {i} B{block} C={columns} vs FP64")
+    group.dispose()
+    for p in ys + dxs:
+        context.free(p)
+    for m in mats:
+        m.dispose()
+
+
 def test_ternary2_zero_rows_are_exactly_zero(context):
     # Ternary2Tests.cs:57-58: an all-zero row next to non-zero rows.
     w, x = O.corpus_random_matrix(7, 2 * 128 + 3)
