@@ -25,10 +25,23 @@ __device__ __forceinline__ uint32_t load4_a4(const uint8_t* p) {
 
 __device__ __forceinline__ float load_f32(const float* p) { return *(const SATORI_GLOBAL float*)(p); }
 
+// Non-temporal loads for data that one instruction reads exactly once per launch (the Ternary2 panel
+// layout): streamed past the caches instead of evicting the activations and partial sums that are reused.
+// Layouts whose lines are touched again by later instructions (block headers shared by several chunks,
+// misaligned blocks) must use the plain loads above.
+__device__ __forceinline__ u32x4 stream16(const uint8_t* p) {  // 16-byte aligned
+    return __builtin_nontemporal_load((const SATORI_GLOBAL u32x4*)(p));
+}
+
+__device__ __forceinline__ uint32_t stream4(const uint8_t* p) {
+    return __builtin_nontemporal_load((const SATORI_GLOBAL uint32_t*)(p));
+}
+
 __device__ __forceinline__ void store_f32(float* p, float v) { *(SATORI_GLOBAL float*)(p) = v; }
 
 // N little-endian dwords starting at a 2-byte aligned address, assembled from N + 1 aligned dword loads
 // and v_alignbyte. Reads up to 4 bytes past p + 4N; every payload allocation carries slack for that.
+// (Plain loads: neighbouring lanes and the next instruction read the same lines again.)
 template <int N>
 __device__ __forceinline__ void load_unaligned(const uint8_t* p, uint32_t (&out)[N]) {
     const uintptr_t address = reinterpret_cast<uintptr_t>(p);

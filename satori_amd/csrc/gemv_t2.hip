@@ -13,8 +13,10 @@
 //
 // Block sums are multiplied by the block scale and added to the row sum in block order, as the reference
 // does; only the order of the FP32 additions inside a block differs (pair sums first). When rows alone
-// cannot fill the chip the columns are split over workgroups; each split's row sums go to a partial buffer
-// and a second kernel adds the splits in order, so results do not depend on scheduling.
+// cannot fill the chip the columns are split over workgroups: each split stores its row sums in a scratch
+// buffer and a second kernel adds them in split order, so results do not depend on scheduling. (Letting
+// the last-arriving workgroup add them needs device-scope release/acquire fences per workgroup, which on
+// gfx950 write back and invalidate the L2 and cost more than the second launch.)
 #include <algorithm>
 #include <type_traits>
 
@@ -30,7 +32,9 @@ constexpr int kTile = kT2TileColumns;
 constexpr int kPairs = kTile / 2;        // pair tables per tile
 constexpr int kTableFloats = kPairs * 16;
 constexpr int kLdsLimit = 64 * 1024;
-constexpr int kMaxTilesPerSplit = (kLdsLimit - 2 * kTableFloats * 4) / (kTile * 4);  // 112 tiles = 14,336 columns
+// Tiles one workgroup stages: 64 KB less the tables, rounded down to an even count (B = 256 splits hold
+// whole blocks): 112 tiles = 14,336 columns.
+constexpr int kMaxTilesPerSplit = ((kLdsLimit - 2 * kTableFloats * 4) / (kTile * 4)) & ~1;
 constexpr int kTargetWorkgroups = 1024;  // four per CU
 
 struct T2Args {
@@ -41,7 +45,7 @@ struct T2Args {
     int splits;
     int tiles_per_split;
     int count;
-    int rows_pad;     // partial-buffer stride: panels of the tallest member * 64
+    int rows_pad;     // partial stride: panels of the tallest member * 64
     float* partials;  // [positions][count][splits][rows_pad] when splits > 1
 };
 
@@ -94,16 +98,16 @@ struct TileData {
 
 template <int B>
 __device__ __forceinline__ void load_tile(const uint8_t* codes, const uint8_t* scales, int u, int t, TileData& d) {
-    d.c0 = *(const SATORI_GLOBAL u32x4*)(codes + (2 * u) * 1024);
-    d.c1 = *(const SATORI_GLOBAL u32x4*)(codes + (2 * u + 1) * 1024);
+    d.c0 = stream16(codes + (2 * u) * 1024);
+    d.c1 = stream16(codes + (2 * u + 1) * 1024);
     if constexpr (B == 64) {
-        d.s0 = __uint_as_float(load4_a4(scales + (2 * t) * 256));
-        d.s1 = __uint_as_float(load4_a4(scales + (2 * t + 1) * 256));
+        d.s0 = __uint_as_float(stream4(scales + (2 * t) * 256));
+        d.s1 = __uint_as_float(stream4(scales + (2 * t + 1) * 256));
     } else if constexpr (B == 128) {
-        d.s0 = __uint_as_float(load4_a4(scales + t * 256));
+        d.s0 = __uint_as_float(stream4(scales + t * 256));
         d.s1 = 0.0f;
     } else {
-        d.s0 = __uint_as_float(load4_a4(scales + (t >> 1) * 256));
+        d.s0 = __uint_as_float(stream4(scales + (t >> 1) * 256));
         d.s1 = 0.0f;
     }
 }
@@ -120,12 +124,6 @@ __global__ __launch_bounds__(kThreads) void t2_kernel(MatDesc one, const MatDesc
     const int position = blockIdx.z;
     const float* x = m.x + static_cast<int64_t>(position) * a.columns + t0 * kTile;
     const int available = a.columns - t0 * kTile;
-
-    __shared__ float tables[2][kTableFloats];  // static, so every table read has a constant base
-    extern __shared__ float xs[];              // nt * 128 activations of this split, zero past the last column
-    for (int i = threadIdx.x; i < nt * kTile; i += kThreads) xs[i] = i < available ? load_f32(x + i) : 0.0f;
-    __syncthreads();
-    build_tables<0>(tables, xs, 0);
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t codes_bytes = static_cast<int64_t>(panels) * a.chunks * 1024;
@@ -144,7 +142,13 @@ __global__ __launch_bounds__(kThreads) void t2_kernel(MatDesc one, const MatDesc
     }
     TileData cur[R], nxt[R];
 #pragma unroll
-    for (int j = 0; j < R; ++j) load_tile<B>(codes[j], scales[j], 0, t0, cur[j]);
+    for (int j = 0; j < R; ++j) load_tile<B>(codes[j], scales[j], 0, t0, cur[j]);  // in flight while x is staged
+
+    __shared__ float tables[2][kTableFloats];  // static, so every table read has a constant base
+    extern __shared__ float xs[];              // nt * 128 activations of this split, zero past the last column
+    for (int i = threadIdx.x; i < nt * kTile; i += kThreads) xs[i] = i < available ? load_f32(x + i) : 0.0f;
+    __syncthreads();
+    build_tables<0>(tables, xs, 0);
     float acc[R], part[R];
 #pragma unroll
     for (int j = 0; j < R; ++j) acc[j] = part[j] = 0.0f;
@@ -184,19 +188,21 @@ __global__ __launch_bounds__(kThreads) void t2_kernel(MatDesc one, const MatDesc
         if (u + 1 < nt) tile(std::integral_constant<int, 1>{}, u + 1);
     }
 
+    float* y = m.y + static_cast<int64_t>(position) * m.rows;
+    if (a.splits == 1) {
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-        if (!live[j] || row[j] >= m.rows) continue;
-        if (a.splits == 1) {
-            store_f32(m.y + static_cast<int64_t>(position) * m.rows + row[j], acc[j]);
-        } else {
-            const int64_t slab = (static_cast<int64_t>(position) * a.count + blockIdx.y) * a.splits + split;
-            store_f32(a.partials + slab * a.rows_pad + row[j], acc[j]);
-        }
+        for (int j = 0; j < R; ++j)
+            if (live[j] && row[j] < m.rows) store_f32(y + row[j], acc[j]);
+        return;
     }
+
+    const int64_t slab = (static_cast<int64_t>(position) * a.count + blockIdx.y) * a.splits + split;
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+        if (live[j] && row[j] < m.rows) store_f32(a.partials + slab * a.rows_pad + row[j], acc[j]);
 }
 
-// y[row] = sum of the splits' row sums, in split order from +0.
+// y[row] = sum of the splits' row sums in split order from +0; loads are issued eight at a time.
 __global__ __launch_bounds__(kThreads) void t2_reduce_kernel(MatDesc one, const MatDesc* __restrict__ group,
                                                               T2Args a) {
     const MatDesc m = group ? group[blockIdx.y] : one;
@@ -204,9 +210,17 @@ __global__ __launch_bounds__(kThreads) void t2_reduce_kernel(MatDesc one, const 
     if (row >= m.rows) return;
     const float* p =
         a.partials + (static_cast<int64_t>(blockIdx.z) * a.count + blockIdx.y) * a.splits * a.rows_pad + row;
-    float acc = 0.0f;
-    for (int s = 0; s < a.splits; ++s) acc += load_f32(p + static_cast<int64_t>(s) * a.rows_pad);
-    store_f32(m.y + static_cast<int64_t>(blockIdx.z) * m.rows + row, acc);
+    float sum = 0.0f;
+    int s = 0;
+    for (; s + 8 <= a.splits; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = load_f32(p + static_cast<int64_t>(s + k) * a.rows_pad);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sum += v[k];
+    }
+    for (; s < a.splits; ++s) sum += load_f32(p + static_cast<int64_t>(s) * a.rows_pad);
+    store_f32(m.y + static_cast<int64_t>(blockIdx.z) * m.rows + row, sum);
 }
 
 template <int B, int R>
@@ -233,25 +247,25 @@ T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positio
     return p;
 }
 
-size_t t2_partial_floats(const T2Plan& plan, int rows_max, int count, int positions) {
+size_t t2_scratch_bytes(const T2Plan& plan, int rows_max, int count, int positions) {
     if (plan.splits <= 1) return 0;
     const size_t rows_pad = static_cast<size_t>((rows_max + kT2PanelRows - 1) / kT2PanelRows) * kT2PanelRows;
-    return static_cast<size_t>(positions) * count * plan.splits * rows_pad;
+    return static_cast<size_t>(positions) * count * plan.splits * rows_pad * sizeof(float);
 }
 
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, const T2Plan& plan,
-                     float* partials, hipStream_t stream) {
+                     void* scratch, hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
     const T2Layout l = t2_layout(s.rows_max, s.columns, s.block_size);
     const int R = plan.panels_per_wave;
     if ((R != 1 && R != 2) || plan.splits < 1 || plan.tiles_per_split < 1 ||
         plan.tiles_per_split > kMaxTilesPerSplit || static_cast<int64_t>(plan.splits) * plan.tiles_per_split < l.tiles ||
         (plan.splits - 1) * plan.tiles_per_split >= l.tiles || (s.block_size == 256 && (plan.tiles_per_split & 1)) ||
-        (plan.splits > 1 && partials == nullptr))
+        (plan.splits > 1 && scratch == nullptr))
         return hipErrorInvalidValue;
-    const T2Args a{s.columns, l.tiles, l.chunks, l.slots, plan.splits, plan.tiles_per_split, count,
-                   l.panels * kT2PanelRows, partials};
     const int groups = (l.panels + kWaves * R - 1) / (kWaves * R);
+    const T2Args a{s.columns, l.tiles, l.chunks, l.slots, plan.splits, plan.tiles_per_split, count,
+                   l.panels * kT2PanelRows, static_cast<float*>(scratch)};
     const dim3 grid(static_cast<unsigned>(groups * plan.splits), static_cast<unsigned>(count),
                     static_cast<unsigned>(s.positions));
     const size_t lds = static_cast<size_t>(plan.tiles_per_split) * kTile * sizeof(float);

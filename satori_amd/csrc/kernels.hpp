@@ -72,8 +72,9 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
 }
 
 // How a Ternary2 launch is cut: each workgroup owns 4 * panels_per_wave panels and a range of
-// tiles_per_split tiles; with splits > 1 the per-split row sums go to a partial buffer of
-// t2_partial_floats() floats and a second kernel adds them in split order.
+// tiles_per_split tiles. With splits > 1 the launch needs a device scratch buffer of t2_scratch_bytes()
+// bytes for the per-split row sums, which a second kernel adds in split order. Launches that share a
+// scratch buffer must not overlap in time.
 struct T2Plan {
     int panels_per_wave;  // 1 or 2
     int splits;
@@ -81,12 +82,12 @@ struct T2Plan {
 };
 
 T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positions);
-size_t t2_partial_floats(const T2Plan& plan, int rows_max, int count, int positions);
+size_t t2_scratch_bytes(const T2Plan& plan, int rows_max, int count, int positions);
 
-// Ternary2 MatVec on the panel layout (MatDesc::w points at it). `partials` must hold
-// t2_partial_floats(plan, ...) floats when plan.splits > 1 and may be null otherwise.
+// Ternary2 MatVec on the panel layout (MatDesc::w points at it); `scratch` may be null when
+// plan.splits == 1.
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape, const T2Plan& plan,
-                     float* partials, hipStream_t stream);
+                     void* scratch, hipStream_t stream);
 
 // Q8_K quantization of `positions` rows of `columns` floats (columns a multiple of 256), bit-exact with
 // Q8KCodec.QuantizeRow. Output [positions][columns / 256 * 292].

@@ -88,7 +88,7 @@ struct satori_hip_matrix {
     uint8_t* payload = nullptr;  // device: the packed payload, or the panel layout for Ternary2
     int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
-    float* partials = nullptr;   // Ternary2 split row sums (device), when plan.splits > 1
+    void* scratch = nullptr;     // Ternary2 split scratch (device), when plan.splits > 1
     bool live = true;
 };
 
@@ -100,7 +100,7 @@ struct satori_hip_group {
     int rows_max = 0;
     satori::MatDesc* descriptors = nullptr;   // device
     satori::T2Plan plan{};                     // Ternary2 groups
-    float* partials = nullptr;                 // Ternary2 split row sums (device)
+    void* scratch = nullptr;                   // Ternary2 split scratch (device)
     std::vector<const float*> inputs;          // distinct inputs, quantized path
     std::vector<uint8_t*> q8k;                 // one Q8_K row per distinct input (device)
     bool live = true;
@@ -169,7 +169,7 @@ void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, fl
     MatDesc d{m->payload, x, nullptr, y, m->shape.rows, 0};
     const LaunchShape l = launch_shape(m->shape, positions, m->shape.rows);
     if (m->shape.format == SATORI_HIP_TERNARY2)
-        check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->partials, stream), "Ternary2 launch");
+        check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->scratch, stream), "Ternary2 launch");
     else
         check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");
 }
@@ -216,23 +216,33 @@ std::vector<uint8_t> ternary2_panels(const Shape& s, const uint8_t* packed) {
     return out;
 }
 
-// Device allocations of one matrix: the weights (+ slack) and, for a split Ternary2 plan, its partials.
+// Scratch for a split Ternary2 plan (null when the plan has one split).
+void* allocate_t2_scratch(const T2Plan& plan, int rows_max, int count) {
+    const size_t bytes = t2_scratch_bytes(plan, rows_max, count, 1);
+    if (!bytes) return nullptr;
+    void* p = nullptr;
+    check_hip(hipMalloc(&p, bytes), "hipMalloc");
+    return p;
+}
+
+// Device allocations of one matrix: the weights (+ slack) and, for a split Ternary2 plan, its scratch.
+// Executions of one matrix that overlap in time (device entry points on different streams) share that
+// scratch and must be serialised by the caller.
 void allocate_matrix(satori_hip_matrix* m, int64_t device_bytes) {
     check_hip(hipMalloc(reinterpret_cast<void**>(&m->payload), static_cast<size_t>(device_bytes) + kPayloadSlack),
               "hipMalloc");
     m->device_bytes = device_bytes;
     if (m->shape.format == SATORI_HIP_TERNARY2) {
         m->plan = t2_plan(m->shape.rows, m->shape.columns, m->shape.block_size, 1, 1);
-        const size_t floats = t2_partial_floats(m->plan, m->shape.rows, 1, 1);
-        if (floats) check_hip(hipMalloc(reinterpret_cast<void**>(&m->partials), floats * sizeof(float)), "hipMalloc");
+        m->scratch = allocate_t2_scratch(m->plan, m->shape.rows, 1);
     }
 }
 
 void free_matrix(satori_hip_matrix* m) {
     if (m->payload) (void)hipFree(m->payload);
-    if (m->partials) (void)hipFree(m->partials);
+    if (m->scratch) (void)hipFree(m->scratch);
     m->payload = nullptr;
-    m->partials = nullptr;
+    m->scratch = nullptr;
 }
 
 satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
@@ -706,10 +716,8 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
             g->quantized = quantized_activations != 0 && is_k(first);
             if (first.format == SATORI_HIP_TERNARY2) {
                 g->plan = t2_plan(g->rows_max, first.columns, first.block_size, count, 1);
-                const size_t floats = t2_partial_floats(g->plan, g->rows_max, count, 1);
                 set_device(c);
-                if (floats)
-                    check_hip(hipMalloc(reinterpret_cast<void**>(&g->partials), floats * sizeof(float)), "hipMalloc");
+                g->scratch = allocate_t2_scratch(g->plan, g->rows_max, count);
             }
             if (g->quantized) {
                 check_kint_width(first);
@@ -735,7 +743,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
         } catch (...) {
             for (uint8_t* b : g->q8k) (void)hipFree(b);
             if (g->descriptors) (void)hipFree(g->descriptors);
-            if (g->partials) (void)hipFree(g->partials);
+            if (g->scratch) (void)hipFree(g->scratch);
             delete g;
             throw;
         }
@@ -758,7 +766,7 @@ int satori_hip_group_execute(satori_hip_group* g, void* stream) {
                 check_hip(launch_q8k_quantize(g->inputs[k], g->shape.columns, 1, g->q8k[k], st), "Q8_K launch");
             check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
         } else if (g->shape.format == SATORI_HIP_TERNARY2) {
-            check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->partials, st), "Ternary2 launch");
+            check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
         } else {
             check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
         }
@@ -779,8 +787,8 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         g->q8k.clear();
         (void)hipFree(g->descriptors);
         g->descriptors = nullptr;
-        if (g->partials) (void)hipFree(g->partials);
-        g->partials = nullptr;
+        if (g->scratch) (void)hipFree(g->scratch);
+        g->scratch = nullptr;
         g->live = false;
     });
 }

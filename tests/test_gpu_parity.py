@@ -91,6 +91,8 @@ def test_ternary2_benchmark_shapes_match_scalar_reference(context, size, block):
     assert np.array_equal(payload, O.t2_quantize(w, size, size, block)), "quantizer bytes differ from oracle"
     m = context.create_ternary2(size, size, block, payload)
     y = run(m, x)
+    again = run(m, x)  # repeated calls agree bitwise
+    assert np.array_equal(y.view(np.uint32), again.view(np.uint32))
     wq = O.t2_dequantize(payload, size, size, block)
     bound = relative_bound(wq, x)
     assert_within(y, O.t2_matvec_scalar(payload, size, size, block, x), bound, "vs scalar reference")
@@ -110,11 +112,11 @@ def _t2_random_payload(g, rows: int, columns: int, block: int) -> np.ndarray:
     return np.ascontiguousarray(out.reshape(-1))
 
 
-# Ternary2 launches split the columns over workgroups (with a second, reducing kernel) unless the rows
+# Ternary2 launches split the columns over workgroups (a second kernel adds the splits) unless the rows
 # alone give about 1024 workgroups of 4 or 8 panels of 64 rows. Small shapes above cover the split plans;
 # the tests below cover the unsplit ones (one and two panels per wave) through very tall matrices and
 # grouped launches, with ragged columns, an odd block count for B = 64, members whose rows end inside a
-# panel, and the widest slice one workgroup stages (14,336 columns).
+# panel, the widest slice one workgroup stages (14,336 columns) and a grouped launch split for width.
 @pytest.mark.parametrize("block", [64, 128, 256])
 def test_ternary2_tall_matrix_pair_tables(context, block):
     g = rng(4242 + block)
@@ -134,7 +136,7 @@ def test_ternary2_tall_matrix_pair_tables(context, block):
     assert_within(y, fp64_matvec(wq, x)[index], relative_bound(wq, x)[index], f"tall B{block} vs FP64")
 
 
-@pytest.mark.parametrize("columns,members", [(4099, 128), (14336, 64)])
+@pytest.mark.parametrize("columns,members", [(4099, 128), (14336, 64), (14337, 64)])
 @pytest.mark.parametrize("block", [64, 128, 256])
 def test_ternary2_grouped_pair_tables(context, block, columns, members):
     g = rng(777 + block + columns)
@@ -151,6 +153,9 @@ def test_ternary2_grouped_pair_tables(context, block, columns, members):
     group = S.HipGroup(context, [mats[k] for k, _ in order], [dxs[j] for _, j in order], ys)
     group.execute()
     context.synchronize()
+    first = [context.download(np.zeros(shapes[k], np.float32), ys[i]) for i, (k, _) in enumerate(order)]
+    group.execute()  # a second launch must give the same bits
+    context.synchronize()
     expected = {}
     for k in range(2):
         wq = O.t2_dequantize(payloads[k], shapes[k], columns, block)
@@ -159,6 +164,7 @@ def test_ternary2_grouped_pair_tables(context, block, columns, members):
                               fp64_matvec(wq, xs[j]), relative_bound(wq, xs[j]))
     for i, (k, j) in enumerate(order):
         got = context.download(np.zeros(shapes[k], np.float32), ys[i])
+        assert np.array_equal(got.view(np.uint32), first[i].view(np.uint32)), f"member {i}: launches differ"
         scalar, exact, bound = expected[k, j]
         assert_within(got, scalar, bound, f"member {i} B{block} C={columns} vs scalar")
         assert_within(got, exact, bound, f"member {i} B{block} C={columns} vs FP64")
