@@ -12,11 +12,15 @@
 // double-buffered: the tables of tile t + 1 are built while tile t is consumed, one barrier per tile.
 //
 // Block sums are multiplied by the block scale and added to the row sum in block order, as the reference
-// does; only the order of the FP32 additions inside a block differs (pair sums first). When rows alone
-// cannot fill the chip the columns are split over workgroups: each split stores its row sums in a scratch
-// buffer and a second kernel adds them in split order, so results do not depend on scheduling. (Letting
-// the last-arriving workgroup add them needs device-scope release/acquire fences per workgroup, which on
-// gfx950 write back and invalidate the L2 and cost more than the second launch.)
+// does; only the order of the FP32 additions inside a block differs (pair sums first).
+//
+// Work is balanced stream-K style: an item is the `W` panels of one member that one workgroup covers, a
+// launch is items x tiles units of work, and a fixed number of workgroups (what the CUs hold at once) each
+// take an equal contiguous range of units. A range covers whole items, written straight to y, plus at
+// most a partial item at each end, whose row sums go to a per-workgroup scratch slot; a second, small
+// kernel adds the pieces of every split item in range order, so results do not depend on scheduling.
+// (Letting the last workgroup of an item add them itself needs device-scope release/acquire fences per
+// workgroup, which on gfx950 write back and invalidate the L2 and cost more than the second launch.)
 #include <algorithm>
 #include <type_traits>
 
@@ -26,65 +30,84 @@
 namespace satori {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
 constexpr int kTile = kT2TileColumns;
 constexpr int kPairs = kTile / 2;        // pair tables per tile
 constexpr int kTableFloats = kPairs * 16;
 constexpr int kLdsLimit = 64 * 1024;
-// Tiles one workgroup stages: 64 KB less the tables, rounded down to an even count (B = 256 splits hold
-// whole blocks): 112 tiles = 14,336 columns.
-constexpr int kMaxTilesPerSplit = ((kLdsLimit - 2 * kTableFloats * 4) / (kTile * 4)) & ~1;
-constexpr int kTargetWorkgroups = 1024;  // four per CU
+// Tiles of activations one workgroup stages at a time: 64 KB less the tables, rounded down to an even
+// count (B = 256 ranges hold whole blocks): 112 tiles = 14,336 columns.
+constexpr int kMaxStagedTiles = ((kLdsLimit - 2 * kTableFloats * 4) / (kTile * 4)) & ~1;
 
 struct T2Args {
     int columns;
     int tiles;
     int chunks;
     int slots;
-    int splits;
-    int tiles_per_split;
-    int count;
-    int rows_pad;     // partial stride: panels of the tallest member * 64
-    float* partials;  // [positions][count][splits][rows_pad] when splits > 1
+    int count;          // members per position
+    int groups;         // items per member: panel groups of the tallest member
+    int step;           // tiles per unit of the range split: 1, or 2 for B = 256 (whole blocks)
+    int workgroups;     // P
+    int64_t steps;      // items * tiles / step
+    float* partials;    // [P][2][64 * W]: a workgroup's first and last piece of a split item
 };
+
+// First tile (in the launch's item-major tile order) of workgroup g's range; g = P gives the end.
+__device__ __forceinline__ int64_t range_begin(int64_t g, const T2Args& a) {
+    return (g * a.steps / a.workgroups) * a.step;
+}
+
+// The workgroup whose range holds tile u.
+__device__ __forceinline__ int range_owner(int64_t u, const T2Args& a) {
+    return static_cast<int>(((u / a.step + 1) * a.workgroups - 1) / a.steps);
+}
 
 // Builds the 64 pair tables of local tile u into buffer BUF: thread k writes entry k & 15 of pairs
 // k / 16 + 16 i. v(c0) x0 + v(c1) x1 is formed as fma(v1, x1, v0 * x0): both products are exact, so the
 // entry is the correctly rounded pair sum (a zero entry may be -0, which adds like +0 to sums that start
 // at +0).
-template <int BUF>
+template <int BUF, int THREADS>
 __device__ __forceinline__ void build_tables(float (*tables)[kTableFloats], const float* xs, int u) {
     const int e = threadIdx.x & 15;
     const int c0 = e & 3, c1 = e >> 2;
     const float v0 = c0 == 1 ? 1.0f : (c0 == 2 ? -1.0f : 0.0f);
     const float v1 = c1 == 1 ? 1.0f : (c1 == 2 ? -1.0f : 0.0f);
 #pragma unroll
-    for (int k = 0; k < kTableFloats / kThreads; ++k) {
-        const int pair = (threadIdx.x >> 4) + k * (kThreads / 16);
+    for (int k = 0; k < kTableFloats / THREADS; ++k) {
+        const int pair = (threadIdx.x >> 4) + k * (THREADS / 16);
         const float2 xp = *reinterpret_cast<const float2*>(xs + kTile * u + 2 * pair);
         tables[BUF][pair * 16 + e] = __builtin_fmaf(v1, xp.y, v0 * xp.x);
     }
 }
 
-// Sum over the 32 pairs of one 16-byte code chunk (pairs [P0, P0 + 32) of the tile) with buffer BUF's
-// tables. Byte k of `lo` is 4 * (low nibble of code byte k) and of `hi` 4 * (high nibble): the byte
-// address inside the pair's table; the table's own position is an immediate offset of the LDS read.
+// Sum over the 32 pairs of one 16-byte code record (pairs [P0, P0 + 32) of the tile) with buffer BUF's
+// tables. The record is stored rotated left by 2 bits (T2Layout), so bits 2-5 of every byte hold the low
+// nibble of the original byte: `lo` = record & 0x3C3C3C3C gives 4 * (low nibble) per byte, and shifting
+// the record right by 4 bits (dword pairs joined by v_alignbit, the last with the first) brings the high
+// nibble to the same place. Each byte is then the byte address inside its pair's table; the table's own
+// position is an immediate offset of the LDS read. The sums start from the first lookup (no add to +0:
+// an entry of -0 then starts a sum at -0, which the +0-started row sum absorbs).
 template <int BUF, int P0>
-__device__ __forceinline__ float chunk_sum(const u32x4& codes, const float (*tables)[kTableFloats]) {
+__device__ __forceinline__ float chunk_sum(const u32x4& record, const float (*tables)[kTableFloats]) {
     float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-        const uint32_t lo = (codes[d] << 2) & 0x3C3C3C3Cu;
-        const uint32_t hi = (codes[d] >> 2) & 0x3C3C3C3Cu;
+        const uint32_t lo = record[d] & 0x3C3C3C3Cu;
+        const uint32_t hi = __builtin_amdgcn_alignbit(record[(d + 1) & 3], record[d], 4) & 0x3C3C3C3Cu;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int pair = P0 + 8 * d + 2 * k;
             const uint32_t a = __builtin_amdgcn_perm(0u, lo, 0x0C0C0C00u | k);
             const uint32_t b = __builtin_amdgcn_perm(0u, hi, 0x0C0C0C00u | k);
             const char* table = reinterpret_cast<const char*>(&tables[BUF][pair * 16]);
-            s0 += *reinterpret_cast<const float*>(table + a);
-            s1 += *reinterpret_cast<const float*>(table + 64 + b);
+            const float ta = *reinterpret_cast<const float*>(table + a);
+            const float tb = *reinterpret_cast<const float*>(table + 64 + b);
+            if (d == 0 && k == 0) {
+                s0 = ta;
+                s1 = tb;
+            } else {
+                s0 += ta;
+                s1 += tb;
+            }
         }
     }
     return s0 + s1;
@@ -96,7 +119,8 @@ struct TileData {
     float s0, s1;  // block scale(s): B = 64 uses both, B = 128 and 256 only s0
 };
 
-template <int B>
+// B = 256 blocks span two tiles; their scale is loaded with the second (odd) tile only, where it is used.
+template <int B, bool ODD>
 __device__ __forceinline__ void load_tile(const uint8_t* codes, const uint8_t* scales, int u, int t, TileData& d) {
     d.c0 = stream16(codes + (2 * u) * 1024);
     d.c1 = stream16(codes + (2 * u + 1) * 1024);
@@ -107,183 +131,232 @@ __device__ __forceinline__ void load_tile(const uint8_t* codes, const uint8_t* s
         d.s0 = __uint_as_float(stream4(scales + t * 256));
         d.s1 = 0.0f;
     } else {
-        d.s0 = __uint_as_float(stream4(scales + (t >> 1) * 256));
+        d.s0 = ODD ? __uint_as_float(stream4(scales + (t >> 1) * 256)) : 0.0f;
         d.s1 = 0.0f;
     }
 }
 
-template <int B, int R>
-__global__ __launch_bounds__(kThreads) void t2_kernel(MatDesc one, const MatDesc* __restrict__ group, T2Args a) {
-    const MatDesc m = group ? group[blockIdx.y] : one;
-    const int split = blockIdx.x % a.splits;
-    const int panel0 = (blockIdx.x / a.splits) * (kWaves * R);
-    const int panels = (m.rows + kT2PanelRows - 1) / kT2PanelRows;
-    if (panel0 >= panels) return;  // the whole workgroup leaves together
-    const int t0 = split * a.tiles_per_split;
-    const int nt = min(a.tiles_per_split, a.tiles - t0);
-    const int position = blockIdx.z;
-    const float* x = m.x + static_cast<int64_t>(position) * a.columns + t0 * kTile;
-    const int available = a.columns - t0 * kTile;
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t codes_bytes = static_cast<int64_t>(panels) * a.chunks * 1024;
-    const uint8_t* codes[R];
-    const uint8_t* scales[R];
-    int row[R];
-    bool live[R];
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-        const int p = panel0 + wave * R + j;
-        live[j] = p < panels;
-        const int64_t q = live[j] ? p : panel0;  // dead panels read a live one and store nothing
-        row[j] = p * kT2PanelRows + lane;
-        codes[j] = m.w + (q * a.chunks + 2 * t0) * 1024 + lane * 16;
-        scales[j] = m.w + codes_bytes + q * a.slots * 256 + lane * 4;
-    }
-    TileData cur[R], nxt[R];
-#pragma unroll
-    for (int j = 0; j < R; ++j) load_tile<B>(codes[j], scales[j], 0, t0, cur[j]);  // in flight while x is staged
-
+template <int B, int W>
+__global__ __launch_bounds__(64 * W) void t2_kernel(MatDesc one, const MatDesc* __restrict__ group, T2Args a) {
+    constexpr int kThreadsW = 64 * W;
     __shared__ float tables[2][kTableFloats];  // static, so every table read has a constant base
-    extern __shared__ float xs[];              // nt * 128 activations of this split, zero past the last column
-    for (int i = threadIdx.x; i < nt * kTile; i += kThreads) xs[i] = i < available ? load_f32(x + i) : 0.0f;
-    __syncthreads();
-    build_tables<0>(tables, xs, 0);
-    float acc[R], part[R];
-#pragma unroll
-    for (int j = 0; j < R; ++j) acc[j] = part[j] = 0.0f;
-    __syncthreads();  // tables of the first tile complete
+    extern __shared__ float xs[];              // activations of the current segment, zero past the last column
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t begin = range_begin(blockIdx.x, a), end = range_begin(blockIdx.x + 1, a);
 
-    // Local tile u uses buffer u & 1; the loop body handles an even and an odd tile so that both buffers'
-    // positions are compile-time constants.
-    auto tile = [&](auto buffer_tag, int u) {
-        constexpr int BUF = decltype(buffer_tag)::value;
-        if (u + 1 < nt) {
-            build_tables<1 - BUF>(tables, xs, u + 1);
-#pragma unroll
-            for (int j = 0; j < R; ++j) load_tile<B>(codes[j], scales[j], u + 1, t0 + u + 1, nxt[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            const float lo = chunk_sum<BUF, 0>(cur[j].c0, tables);
-            const float hi = chunk_sum<BUF, 32>(cur[j].c1, tables);
+    for (int64_t u = begin; u < end;) {
+        // Segment: tiles [t0, t0 + nt) of one item. Every decision below is uniform over the workgroup.
+        const int64_t item = u / a.tiles;
+        const int t0 = static_cast<int>(u - item * a.tiles);
+        const int nt = static_cast<int>(min(static_cast<int64_t>(a.tiles - t0), end - u));
+        const int slot = u == begin ? 0 : 1;
+        u += nt;
+        const int64_t member_position = item / a.groups;
+        const int member = static_cast<int>(member_position % a.count);
+        const int position = static_cast<int>(member_position / a.count);
+        const MatDesc m = group ? group[member] : one;
+        const int panels = (m.rows + kT2PanelRows - 1) / kT2PanelRows;
+        const int panel0 = static_cast<int>(item % a.groups) * W;
+        if (panel0 >= panels) continue;  // a shorter member of the group
+
+        // Wave w owns panel panel0 + w, one row per lane; a wave past the last panel reads panel0 and
+        // stores nothing.
+        const int panel = panel0 + wave;
+        const bool live = panel < panels;
+        const int row = panel * kT2PanelRows + lane;
+        const int64_t q = live ? panel : panel0;
+        const uint8_t* codes = m.w + (q * a.chunks + 2 * t0) * 1024 + lane * 16;
+        const uint8_t* scales =
+            m.w + static_cast<int64_t>(panels) * a.chunks * 1024 + q * a.slots * 256 + lane * 4;
+
+        // Two register sets alternate: the loads of tile v + 1 are issued while tile v is summed.
+        TileData even, odd;
+        load_tile<B, false>(codes, scales, 0, t0, even);  // in flight while x is staged
+
+        const float* x = m.x + static_cast<int64_t>(position) * a.columns + t0 * kTile;
+        const int available = a.columns - t0 * kTile;
+        for (int i = threadIdx.x; i < nt * kTile; i += kThreadsW) xs[i] = i < available ? load_f32(x + i) : 0.0f;
+        __syncthreads();
+        build_tables<0, kThreadsW>(tables, xs, 0);
+        float acc = 0.0f, part = 0.0f;
+        __syncthreads();  // tables of the first tile complete
+
+        // Local tile v uses table buffer v & 1 and register set v & 1; the loop body covers an even and an
+        // odd tile so that both are fixed at compile time (constant table offsets, no register copies).
+        auto tile = [&](auto buffer_tag, int v, const TileData& cur, TileData& next) {
+            constexpr int BUF = decltype(buffer_tag)::value;
+            if (v + 1 < nt) {
+                load_tile<B, BUF == 0>(codes, scales, v + 1, t0 + v + 1, next);  // tile v + 1 is odd if v is even
+                build_tables<1 - BUF, kThreadsW>(tables, xs, v + 1);
+            }
+            const float lo = chunk_sum<BUF, 0>(cur.c0, tables);
+            const float hi = chunk_sum<BUF, 32>(cur.c1, tables);
             if constexpr (B == 64) {
-                acc[j] += lo * cur[j].s0;  // block 2t
-                acc[j] += hi * cur[j].s1;  // block 2t + 1 (zero codes and scale in the padding slot)
+                acc += lo * cur.s0;  // block 2t
+                acc += hi * cur.s1;  // block 2t + 1 (zero codes and scale in the padding slot)
             } else if constexpr (B == 128) {
-                acc[j] += (lo + hi) * cur[j].s0;
+                acc += (lo + hi) * cur.s0;
             } else {
-                part[j] += lo + hi;
-                if (u & 1) {  // second half of the block (splits start on even tiles)
-                    acc[j] += part[j] * cur[j].s0;
-                    part[j] = 0.0f;
+                part += lo + hi;
+                if constexpr (BUF == 1) {  // second half of the block: segments start on even tiles
+                    acc += part * cur.s0;
+                    part = 0.0f;
                 }
             }
-            cur[j] = nxt[j];
+            __syncthreads();  // next tables built; this tile's tables and (last tile) the activations read
+        };
+        for (int v = 0; v < nt; v += 2) {
+            tile(std::integral_constant<int, 0>{}, v, even, odd);
+            if (v + 1 < nt) tile(std::integral_constant<int, 1>{}, v + 1, odd, even);
         }
-        __syncthreads();  // next tables built; this tile's tables no longer read
-    };
-    for (int u = 0; u < nt; u += 2) {
-        tile(std::integral_constant<int, 0>{}, u);
-        if (u + 1 < nt) tile(std::integral_constant<int, 1>{}, u + 1);
-    }
 
-    float* y = m.y + static_cast<int64_t>(position) * m.rows;
-    if (a.splits == 1) {
-#pragma unroll
-        for (int j = 0; j < R; ++j)
-            if (live[j] && row[j] < m.rows) store_f32(y + row[j], acc[j]);
-        return;
+        if (live && row < m.rows) {
+            if (t0 == 0 && nt == a.tiles)
+                store_f32(m.y + static_cast<int64_t>(position) * m.rows + row, acc);
+            else
+                store_f32(a.partials + (static_cast<int64_t>(blockIdx.x) * 2 + slot) * kThreadsW + threadIdx.x, acc);
+        }
     }
-
-    const int64_t slab = (static_cast<int64_t>(position) * a.count + blockIdx.y) * a.splits + split;
-#pragma unroll
-    for (int j = 0; j < R; ++j)
-        if (live[j] && row[j] < m.rows) store_f32(a.partials + slab * a.rows_pad + row[j], acc[j]);
 }
 
-// y[row] = sum of the splits' row sums in split order from +0; loads are issued eight at a time.
-__global__ __launch_bounds__(kThreads) void t2_reduce_kernel(MatDesc one, const MatDesc* __restrict__ group,
-                                                              T2Args a) {
-    const MatDesc m = group ? group[blockIdx.y] : one;
-    const int row = blockIdx.x * kThreads + threadIdx.x;
+// Adds the pieces of every item split between workgroups. Block g - 1 looks at the boundary between
+// ranges g - 1 and g; an item is handled at its first inner boundary, its pieces summed in range order
+// from +0 (eight loads in flight at a time).
+template <int W>
+__global__ __launch_bounds__(64 * W) void t2_fixup_kernel(MatDesc one, const MatDesc* __restrict__ group,
+                                                          T2Args a) {
+    constexpr int kThreadsW = 64 * W;
+    const int g = blockIdx.x + 1;
+    const int64_t boundary = range_begin(g, a);
+    const int64_t item = boundary / a.tiles;
+    const int64_t start = item * a.tiles;
+    if (boundary == start) return;  // no item is cut here
+    const int first = range_owner(start, a);
+    if (first + 1 != g) return;  // an earlier boundary inside the same item handles it
+    const int last = range_owner(start + a.tiles - 1, a);
+    const int64_t member_position = item / a.groups;
+    const int member = static_cast<int>(member_position % a.count);
+    const int position = static_cast<int>(member_position / a.count);
+    const MatDesc m = group ? group[member] : one;
+    const int row = static_cast<int>(item % a.groups) * W * kT2PanelRows + threadIdx.x;
     if (row >= m.rows) return;
-    const float* p =
-        a.partials + (static_cast<int64_t>(blockIdx.z) * a.count + blockIdx.y) * a.splits * a.rows_pad + row;
-    float sum = 0.0f;
-    int s = 0;
-    for (; s + 8 <= a.splits; s += 8) {
+    const float* p = a.partials + threadIdx.x;
+    const int first_slot = range_begin(first, a) == start ? 0 : 1;  // else it is `first`'s last piece
+    float sum = 0.0f + load_f32(p + (static_cast<int64_t>(first) * 2 + first_slot) * kThreadsW);
+    int h = first + 1;
+    for (; h + 8 <= last + 1; h += 8) {
         float v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = load_f32(p + static_cast<int64_t>(s + k) * a.rows_pad);
+        for (int k = 0; k < 8; ++k) v[k] = load_f32(p + static_cast<int64_t>(h + k) * 2 * kThreadsW);
 #pragma unroll
         for (int k = 0; k < 8; ++k) sum += v[k];
     }
-    for (; s < a.splits; ++s) sum += load_f32(p + static_cast<int64_t>(s) * a.rows_pad);
-    store_f32(m.y + static_cast<int64_t>(blockIdx.z) * m.rows + row, sum);
+    for (; h <= last; ++h) sum += load_f32(p + static_cast<int64_t>(h) * 2 * kThreadsW);
+    store_f32(m.y + static_cast<int64_t>(position) * m.rows + row, sum);
 }
 
-template <int B, int R>
-hipError_t launch(const MatDesc& one, const MatDesc* group, dim3 grid, size_t lds, const T2Args& a,
-                  hipStream_t stream) {
-    t2_kernel<B, R><<<grid, kThreads, lds, stream>>>(one, group, a);
-    return hipGetLastError();
+template <int B, int W>
+hipError_t launch(const MatDesc& one, const MatDesc* group, size_t lds, const T2Args& a, hipStream_t stream) {
+    t2_kernel<B, W><<<a.workgroups, 64 * W, lds, stream>>>(one, group, a);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && a.workgroups > 1) {
+        t2_fixup_kernel<W><<<a.workgroups - 1, 64 * W, 0, stream>>>(one, group, a);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+template <int B, int W>
+const void* kernel_address() {
+    return reinterpret_cast<const void*>(&t2_kernel<B, W>);
+}
+
+}  // namespace
+
+int t2_resident_workgroups(int block_size, int waves, int staged_tiles) {
+    const void* f = nullptr;
+    switch (block_size * 10 + waves) {
+        case 644: f = kernel_address<64, 4>(); break;
+        case 648: f = kernel_address<64, 8>(); break;
+        case 1284: f = kernel_address<128, 4>(); break;
+        case 1288: f = kernel_address<128, 8>(); break;
+        case 2564: f = kernel_address<256, 4>(); break;
+        case 2568: f = kernel_address<256, 8>(); break;
+        default: return 0;
+    }
+    int n = 0;
+    const size_t lds = static_cast<size_t>(staged_tiles) * kTile * sizeof(float);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 64 * waves, lds) != hipSuccess) return 0;
+    return n;
+}
+
+namespace {
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Tiles in the longest segment of a plan (what one workgroup stages at once).
+int staged_tiles(int tiles, int step, int64_t steps, int workgroups) {
+    return static_cast<int>(std::min<int64_t>(tiles, ceil_div(steps, workgroups) * step));
 }
 
 }  // namespace
 
 T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positions) {
     const T2Layout l = t2_layout(rows_max, columns, block_size);
+    const int step = block_size == 256 ? 2 : 1;
+    int cus = 0, device = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+        cus = 256;
+    // Eight waves (eight panels) per workgroup share each tile's tables when that still leaves at least
+    // eight tiles per workgroup on a full chip; otherwise four.
     const int64_t members = static_cast<int64_t>(count) * positions;
-    T2Plan p{1, 1, l.tiles};
-    if (members * ((l.panels + 2 * kWaves - 1) / (2 * kWaves)) >= kTargetWorkgroups) p.panels_per_wave = 2;
-    const int64_t groups = members * ((l.panels + kWaves * p.panels_per_wave - 1) / (kWaves * p.panels_per_wave));
-    int tps = std::min(l.tiles, kMaxTilesPerSplit);
-    // Split the columns while the grid is small, keeping at least two tiles per split.
-    while (groups * ((l.tiles + tps - 1) / tps) < kTargetWorkgroups && tps >= 4) tps = (tps + 1) / 2;
-    if (block_size == 256) tps += tps & 1;  // B = 256 blocks span two tiles: splits end on block boundaries
-    p.tiles_per_split = tps;
-    p.splits = (l.tiles + tps - 1) / tps;
+    T2Plan p{8, 1, 1};
+    const auto units = [&](int w) { return members * ceil_div(l.panels, w) * l.tiles; };
+    const auto resident = [&](int w, int staged) {
+        const int n = t2_resident_workgroups(block_size, w, staged);
+        return static_cast<int64_t>(std::max(n, 1)) * cus;
+    };
+    if (units(8) < 8 * resident(8, std::min(l.tiles, kMaxStagedTiles))) p.waves = 4;
+    const int64_t steps = units(p.waves) / step;
+    // As many workgroups as the CUs hold at once, each with at least two tiles and at most what it stages.
+    int64_t wgs = std::min(resident(p.waves, std::min(l.tiles, kMaxStagedTiles)), ceil_div(steps * step, 2));
+    wgs = std::max(wgs, ceil_div(steps * step, kMaxStagedTiles));
+    wgs = std::max<int64_t>(1, std::min(wgs, steps));
+    p.workgroups = static_cast<int>(std::min<int64_t>(wgs, INT32_MAX));
+    p.staged_tiles = staged_tiles(l.tiles, step, steps, p.workgroups);
     return p;
 }
 
-size_t t2_scratch_bytes(const T2Plan& plan, int rows_max, int count, int positions) {
-    if (plan.splits <= 1) return 0;
-    const size_t rows_pad = static_cast<size_t>((rows_max + kT2PanelRows - 1) / kT2PanelRows) * kT2PanelRows;
-    return static_cast<size_t>(positions) * count * plan.splits * rows_pad * sizeof(float);
+size_t t2_scratch_bytes(const T2Plan& plan) {
+    return plan.workgroups > 1 ? static_cast<size_t>(plan.workgroups) * 2 * 64 * plan.waves * sizeof(float) : 0;
 }
 
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, const T2Plan& plan,
                      void* scratch, hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
     const T2Layout l = t2_layout(s.rows_max, s.columns, s.block_size);
-    const int R = plan.panels_per_wave;
-    if ((R != 1 && R != 2) || plan.splits < 1 || plan.tiles_per_split < 1 ||
-        plan.tiles_per_split > kMaxTilesPerSplit || static_cast<int64_t>(plan.splits) * plan.tiles_per_split < l.tiles ||
-        (plan.splits - 1) * plan.tiles_per_split >= l.tiles || (s.block_size == 256 && (plan.tiles_per_split & 1)) ||
-        (plan.splits > 1 && scratch == nullptr))
+    const int W = plan.waves;
+    const int step = s.block_size == 256 ? 2 : 1;
+    const int groups = (l.panels + W - 1) / W;
+    const int64_t steps = static_cast<int64_t>(s.positions) * count * groups * l.tiles / step;
+    if ((W != 4 && W != 8) || plan.workgroups < 1 || plan.workgroups > steps ||
+        plan.staged_tiles > kMaxStagedTiles ||
+        staged_tiles(l.tiles, step, steps, plan.workgroups) > plan.staged_tiles ||
+        (plan.workgroups > 1 && scratch == nullptr))
         return hipErrorInvalidValue;
-    const int groups = (l.panels + kWaves * R - 1) / (kWaves * R);
-    const T2Args a{s.columns, l.tiles, l.chunks, l.slots, plan.splits, plan.tiles_per_split, count,
-                   l.panels * kT2PanelRows, static_cast<float*>(scratch)};
-    const dim3 grid(static_cast<unsigned>(groups * plan.splits), static_cast<unsigned>(count),
-                    static_cast<unsigned>(s.positions));
-    const size_t lds = static_cast<size_t>(plan.tiles_per_split) * kTile * sizeof(float);
-    hipError_t e;
-    switch (s.block_size * 4 + R) {
-        case 64 * 4 + 1: e = launch<64, 1>(one, group, grid, lds, a, stream); break;
-        case 64 * 4 + 2: e = launch<64, 2>(one, group, grid, lds, a, stream); break;
-        case 128 * 4 + 1: e = launch<128, 1>(one, group, grid, lds, a, stream); break;
-        case 128 * 4 + 2: e = launch<128, 2>(one, group, grid, lds, a, stream); break;
-        case 256 * 4 + 1: e = launch<256, 1>(one, group, grid, lds, a, stream); break;
-        case 256 * 4 + 2: e = launch<256, 2>(one, group, grid, lds, a, stream); break;
+    const T2Args a{s.columns, l.tiles, l.chunks, l.slots, count, groups, step, plan.workgroups, steps,
+                   static_cast<float*>(scratch)};
+    const size_t lds = static_cast<size_t>(plan.staged_tiles) * kTile * sizeof(float);
+    switch (s.block_size * 10 + W) {
+        case 644: return launch<64, 4>(one, group, lds, a, stream);
+        case 648: return launch<64, 8>(one, group, lds, a, stream);
+        case 1284: return launch<128, 4>(one, group, lds, a, stream);
+        case 1288: return launch<128, 8>(one, group, lds, a, stream);
+        case 2564: return launch<256, 4>(one, group, lds, a, stream);
+        case 2568: return launch<256, 8>(one, group, lds, a, stream);
         default: return hipErrorInvalidValue;
     }
-    if (e != hipSuccess || plan.splits == 1) return e;
-    const dim3 reduce_grid(static_cast<unsigned>((s.rows_max + kThreads - 1) / kThreads),
-                           static_cast<unsigned>(count), static_cast<unsigned>(s.positions));
-    t2_reduce_kernel<<<reduce_grid, kThreads, 0, stream>>>(one, group, a);
-    return hipGetLastError();
 }
 
 }  // namespace satori

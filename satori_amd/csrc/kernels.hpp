@@ -44,7 +44,9 @@ hipError_t launch_gemv_float(const MatDesc& one, const MatDesc* group, int count
 // The device copy of a Ternary2 matrix is regrouped so that one wave (64 lanes, one row each) reads whole
 // cache lines: rows form panels of 64; a row's code stream (2 bits per column, LSB first, padded to whole
 // blocks) is cut into 64-column chunks of 16 bytes; chunk k of the 64 rows of panel p is stored as 64
-// consecutive 16-byte records. Block scales follow all codes, 64 consecutive floats per (panel, block slot).
+// consecutive 16-byte records, each record rotated left by 2 bits as one 128-bit little-endian integer (so
+// a single mask exposes a nibble per byte). Block scales follow all codes, 64 consecutive floats per
+// (panel, block slot).
 // Chunks per row are rounded up to an even number (one 128-column tile = two chunks); padding rows, chunks
 // and slots are zero. The total equals the packed payload up to that padding.
 constexpr int kT2PanelRows = 64;
@@ -71,21 +73,24 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
     return l;
 }
 
-// How a Ternary2 launch is cut: each workgroup owns 4 * panels_per_wave panels and a range of
-// tiles_per_split tiles. With splits > 1 the launch needs a device scratch buffer of t2_scratch_bytes()
-// bytes for the per-split row sums, which a second kernel adds in split order. Launches that share a
-// scratch buffer must not overlap in time.
+// How a Ternary2 launch is cut: workgroups of `waves` waves (one 64-row panel each) take equal ranges of
+// the launch's (panel group, tile) units; items cut between two ranges are finished by a second kernel
+// from per-workgroup scratch of t2_scratch_bytes() bytes. Launches that share a scratch buffer must not
+// overlap in time. The plan depends on the launch's shape and member count and on the current device.
 struct T2Plan {
-    int panels_per_wave;  // 1 or 2
-    int splits;
-    int tiles_per_split;
+    int waves;         // waves per workgroup: 4 or 8
+    int workgroups;    // ranges (one workgroup each)
+    int staged_tiles;  // longest segment: activation tiles staged in LDS at once
 };
 
 T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positions);
-size_t t2_scratch_bytes(const T2Plan& plan, int rows_max, int count, int positions);
+size_t t2_scratch_bytes(const T2Plan& plan);
+
+// Workgroups of one Ternary2 kernel variant that fit on a CU at once (0 if unknown).
+int t2_resident_workgroups(int block_size, int waves, int staged_tiles);
 
 // Ternary2 MatVec on the panel layout (MatDesc::w points at it); `scratch` may be null when
-// plan.splits == 1.
+// plan.workgroups == 1.
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape, const T2Plan& plan,
                      void* scratch, hipStream_t stream);
 

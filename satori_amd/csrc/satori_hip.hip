@@ -88,7 +88,7 @@ struct satori_hip_matrix {
     uint8_t* payload = nullptr;  // device: the packed payload, or the panel layout for Ternary2
     int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
-    void* scratch = nullptr;     // Ternary2 split scratch (device), when plan.splits > 1
+    void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
     bool live = true;
 };
 
@@ -100,7 +100,7 @@ struct satori_hip_group {
     int rows_max = 0;
     satori::MatDesc* descriptors = nullptr;   // device
     satori::T2Plan plan{};                     // Ternary2 groups
-    void* scratch = nullptr;                   // Ternary2 split scratch (device)
+    void* scratch = nullptr;                   // Ternary2 range scratch (device)
     std::vector<const float*> inputs;          // distinct inputs, quantized path
     std::vector<uint8_t*> q8k;                 // one Q8_K row per distinct input (device)
     bool live = true;
@@ -194,9 +194,17 @@ bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
     return a0 < b0 + b_bytes && b0 < a0 + a_bytes;
 }
 
+// One 16-byte code record rotated left by 2 bits as a 128-bit little-endian integer.
+void rotate_record(uint8_t* out, const uint8_t* in) {
+    uint32_t w[4], r[4];
+    std::memcpy(w, in, 16);
+    for (int d = 0; d < 4; ++d) r[d] = (w[d] << 2) | (w[(d + 3) & 3] >> 30);
+    std::memcpy(out, r, 16);
+}
+
 // Regroups a validated packed Ternary2 payload (rows of [f32 scale][B / 4 code bytes] blocks) into the
-// panel layout: row r is lane r % 64 of panel r / 64; its 16-byte code chunks and block scales land at the
-// T2Layout positions; padding stays zero.
+// panel layout: row r is lane r % 64 of panel r / 64; its 16-byte code chunks (rotated) and block scales
+// land at the T2Layout positions; padding stays zero.
 std::vector<uint8_t> ternary2_panels(const Shape& s, const uint8_t* packed) {
     const T2Layout l = t2_layout(s.rows, s.columns, s.block_size);
     std::vector<uint8_t> out(static_cast<size_t>(l.bytes), 0);
@@ -209,16 +217,16 @@ std::vector<uint8_t> ternary2_panels(const Shape& s, const uint8_t* packed) {
             std::memcpy(&out[l.codes_bytes + ((panel * l.slots + b) * 64 + lane) * 4], block, 4);
             for (int i = 0; i < chunks_per_block; ++i) {
                 const int64_t chunk = static_cast<int64_t>(b) * chunks_per_block + i;
-                std::memcpy(&out[((panel * l.chunks + chunk) * 64 + lane) * 16], block + 4 + 16 * i, 16);
+                rotate_record(&out[((panel * l.chunks + chunk) * 64 + lane) * 16], block + 4 + 16 * i);
             }
         }
     }
     return out;
 }
 
-// Scratch for a split Ternary2 plan (null when the plan has one split).
-void* allocate_t2_scratch(const T2Plan& plan, int rows_max, int count) {
-    const size_t bytes = t2_scratch_bytes(plan, rows_max, count, 1);
+// Scratch for a Ternary2 plan (null when it has a single range).
+void* allocate_t2_scratch(const T2Plan& plan) {
+    const size_t bytes = t2_scratch_bytes(plan);
     if (!bytes) return nullptr;
     void* p = nullptr;
     check_hip(hipMalloc(&p, bytes), "hipMalloc");
@@ -234,7 +242,7 @@ void allocate_matrix(satori_hip_matrix* m, int64_t device_bytes) {
     m->device_bytes = device_bytes;
     if (m->shape.format == SATORI_HIP_TERNARY2) {
         m->plan = t2_plan(m->shape.rows, m->shape.columns, m->shape.block_size, 1, 1);
-        m->scratch = allocate_t2_scratch(m->plan, m->shape.rows, 1);
+        m->scratch = allocate_t2_scratch(m->plan);
     }
 }
 
@@ -717,7 +725,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
             if (first.format == SATORI_HIP_TERNARY2) {
                 g->plan = t2_plan(g->rows_max, first.columns, first.block_size, count, 1);
                 set_device(c);
-                g->scratch = allocate_t2_scratch(g->plan, g->rows_max, count);
+                g->scratch = allocate_t2_scratch(g->plan);
             }
             if (g->quantized) {
                 check_kint_width(first);
