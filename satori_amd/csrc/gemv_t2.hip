@@ -19,10 +19,14 @@
 // take an equal contiguous range of units. A range covers whole items, written straight to y, plus at
 // most a partial item at each end, whose row sums go to a per-workgroup scratch slot; a second, small
 // kernel adds the pieces of every split item in range order, so results do not depend on scheduling.
+// The range starts and the list of split items depend only on the plan: the host computes them once and
+// they sit at the start of the plan's scratch buffer.
 // (Letting the last workgroup of an item add them itself needs device-scope release/acquire fences per
 // workgroup, which on gfx950 write back and invalidate the L2 and cost more than the second launch.)
 #include <algorithm>
+#include <cstring>
 #include <type_traits>
+#include <vector>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -43,23 +47,12 @@ struct T2Args {
     int tiles;
     int chunks;
     int slots;
-    int count;          // members per position
-    int groups;         // items per member: panel groups of the tallest member
-    int step;           // tiles per unit of the range split: 1, or 2 for B = 256 (whole blocks)
-    int workgroups;     // P
-    int64_t steps;      // items * tiles / step
-    float* partials;    // [P][2][64 * W]: a workgroup's first and last piece of a split item
+    int count;                 // members per position
+    int groups;                // items per member: panel groups of the tallest member
+    const int* starts;         // [P + 1] first tile of each range (item-major tile order)
+    const T2Fixup* fixups;     // items cut between ranges
+    float* partials;           // [P][2][64 * W]: a workgroup's first and last piece of a cut item
 };
-
-// First tile (in the launch's item-major tile order) of workgroup g's range; g = P gives the end.
-__device__ __forceinline__ int64_t range_begin(int64_t g, const T2Args& a) {
-    return (g * a.steps / a.workgroups) * a.step;
-}
-
-// The workgroup whose range holds tile u.
-__device__ __forceinline__ int range_owner(int64_t u, const T2Args& a) {
-    return static_cast<int>(((u / a.step + 1) * a.workgroups - 1) / a.steps);
-}
 
 // Builds the 64 pair tables of local tile u into buffer BUF: thread k writes entry k & 15 of pairs
 // k / 16 + 16 i. v(c0) x0 + v(c1) x1 is formed as fma(v1, x1, v0 * x0): both products are exact, so the
@@ -142,125 +135,125 @@ __global__ __launch_bounds__(64 * W) void t2_kernel(MatDesc one, const MatDesc* 
     __shared__ float tables[2][kTableFloats];  // static, so every table read has a constant base
     extern __shared__ float xs[];              // activations of the current segment, zero past the last column
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t begin = range_begin(blockIdx.x, a), end = range_begin(blockIdx.x + 1, a);
+    const int begin = a.starts[blockIdx.x], end = a.starts[blockIdx.x + 1];
+    // Item of the first tile, as (panel group, member, position); later segments step through items.
+    const int first_item = begin / a.tiles;
+    int t0 = begin - first_item * a.tiles;
+    int item_group = first_item % a.groups;
+    int member = (first_item / a.groups) % a.count;
+    int position = first_item / a.groups / a.count;
 
-    for (int64_t u = begin; u < end;) {
+    for (int u = begin; u < end;) {
         // Segment: tiles [t0, t0 + nt) of one item. Every decision below is uniform over the workgroup.
-        const int64_t item = u / a.tiles;
-        const int t0 = static_cast<int>(u - item * a.tiles);
-        const int nt = static_cast<int>(min(static_cast<int64_t>(a.tiles - t0), end - u));
+        const int nt = min(a.tiles - t0, end - u);
         const int slot = u == begin ? 0 : 1;
-        u += nt;
-        const int64_t member_position = item / a.groups;
-        const int member = static_cast<int>(member_position % a.count);
-        const int position = static_cast<int>(member_position / a.count);
         const MatDesc m = group ? group[member] : one;
         const int panels = (m.rows + kT2PanelRows - 1) / kT2PanelRows;
-        const int panel0 = static_cast<int>(item % a.groups) * W;
-        if (panel0 >= panels) continue;  // a shorter member of the group
+        const int panel0 = item_group * W;
+        if (panel0 < panels) {  // else a shorter member of the group: nothing to do
+            // Wave w owns panel panel0 + w, one row per lane; a wave past the last panel reads panel0 and
+            // stores nothing.
+            const int panel = panel0 + wave;
+            const bool live = panel < panels;
+            const int row = panel * kT2PanelRows + lane;
+            const int64_t q = live ? panel : panel0;
+            const uint8_t* codes = m.w + (q * a.chunks + 2 * t0) * 1024 + lane * 16;
+            const uint8_t* scales =
+                m.w + static_cast<int64_t>(panels) * a.chunks * 1024 + q * a.slots * 256 + lane * 4;
 
-        // Wave w owns panel panel0 + w, one row per lane; a wave past the last panel reads panel0 and
-        // stores nothing.
-        const int panel = panel0 + wave;
-        const bool live = panel < panels;
-        const int row = panel * kT2PanelRows + lane;
-        const int64_t q = live ? panel : panel0;
-        const uint8_t* codes = m.w + (q * a.chunks + 2 * t0) * 1024 + lane * 16;
-        const uint8_t* scales =
-            m.w + static_cast<int64_t>(panels) * a.chunks * 1024 + q * a.slots * 256 + lane * 4;
+            // Two register sets alternate: the loads of tile v + 1 are issued while tile v is summed.
+            TileData even, odd;
+            load_tile<B, false>(codes, scales, 0, t0, even);  // in flight while x is staged
 
-        // Two register sets alternate: the loads of tile v + 1 are issued while tile v is summed.
-        TileData even, odd;
-        load_tile<B, false>(codes, scales, 0, t0, even);  // in flight while x is staged
+            const float* x = m.x + static_cast<int64_t>(position) * a.columns + t0 * kTile;
+            const int available = a.columns - t0 * kTile;
+            for (int i = threadIdx.x; i < nt * kTile; i += kThreadsW) xs[i] = i < available ? load_f32(x + i) : 0.0f;
+            __syncthreads();
+            build_tables<0, kThreadsW>(tables, xs, 0);
+            float acc = 0.0f, part = 0.0f;
+            __syncthreads();  // tables of the first tile complete
 
-        const float* x = m.x + static_cast<int64_t>(position) * a.columns + t0 * kTile;
-        const int available = a.columns - t0 * kTile;
-        for (int i = threadIdx.x; i < nt * kTile; i += kThreadsW) xs[i] = i < available ? load_f32(x + i) : 0.0f;
-        __syncthreads();
-        build_tables<0, kThreadsW>(tables, xs, 0);
-        float acc = 0.0f, part = 0.0f;
-        __syncthreads();  // tables of the first tile complete
-
-        // Local tile v uses table buffer v & 1 and register set v & 1; the loop body covers an even and an
-        // odd tile so that both are fixed at compile time (constant table offsets, no register copies).
-        auto tile = [&](auto buffer_tag, int v, const TileData& cur, TileData& next) {
-            constexpr int BUF = decltype(buffer_tag)::value;
-            if (v + 1 < nt) {
-                load_tile<B, BUF == 0>(codes, scales, v + 1, t0 + v + 1, next);  // tile v + 1 is odd if v is even
-                build_tables<1 - BUF, kThreadsW>(tables, xs, v + 1);
-            }
-            const float lo = chunk_sum<BUF, 0>(cur.c0, tables);
-            const float hi = chunk_sum<BUF, 32>(cur.c1, tables);
-            if constexpr (B == 64) {
-                acc += lo * cur.s0;  // block 2t
-                acc += hi * cur.s1;  // block 2t + 1 (zero codes and scale in the padding slot)
-            } else if constexpr (B == 128) {
-                acc += (lo + hi) * cur.s0;
-            } else {
-                part += lo + hi;
-                if constexpr (BUF == 1) {  // second half of the block: segments start on even tiles
-                    acc += part * cur.s0;
-                    part = 0.0f;
+            // Local tile v uses table buffer v & 1 and register set v & 1; the loop body covers an even and an
+            // odd tile so that both are fixed at compile time (constant table offsets, no register copies).
+            auto tile = [&](auto buffer_tag, int v, const TileData& cur, TileData& next) {
+                constexpr int BUF = decltype(buffer_tag)::value;
+                if (v + 1 < nt) {
+                    load_tile<B, BUF == 0>(codes, scales, v + 1, t0 + v + 1, next);  // tile v + 1 is odd if v is even
+                    build_tables<1 - BUF, kThreadsW>(tables, xs, v + 1);
                 }
+                const float lo = chunk_sum<BUF, 0>(cur.c0, tables);
+                const float hi = chunk_sum<BUF, 32>(cur.c1, tables);
+                if constexpr (B == 64) {
+                    acc += lo * cur.s0;  // block 2t
+                    acc += hi * cur.s1;  // block 2t + 1 (zero codes and scale in the padding slot)
+                } else if constexpr (B == 128) {
+                    acc += (lo + hi) * cur.s0;
+                } else {
+                    part += lo + hi;
+                    if constexpr (BUF == 1) {  // second half of the block: segments start on even tiles
+                        acc += part * cur.s0;
+                        part = 0.0f;
+                    }
+                }
+                __syncthreads();  // next tables built; this tile's tables and (last tile) the activations read
+            };
+            for (int v = 0; v < nt; v += 2) {
+                tile(std::integral_constant<int, 0>{}, v, even, odd);
+                if (v + 1 < nt) tile(std::integral_constant<int, 1>{}, v + 1, odd, even);
             }
-            __syncthreads();  // next tables built; this tile's tables and (last tile) the activations read
-        };
-        for (int v = 0; v < nt; v += 2) {
-            tile(std::integral_constant<int, 0>{}, v, even, odd);
-            if (v + 1 < nt) tile(std::integral_constant<int, 1>{}, v + 1, odd, even);
-        }
 
-        if (live && row < m.rows) {
-            if (t0 == 0 && nt == a.tiles)
-                store_f32(m.y + static_cast<int64_t>(position) * m.rows + row, acc);
-            else
-                store_f32(a.partials + (static_cast<int64_t>(blockIdx.x) * 2 + slot) * kThreadsW + threadIdx.x, acc);
+            if (live && row < m.rows) {
+                if (t0 == 0 && nt == a.tiles)
+                    store_f32(m.y + static_cast<int64_t>(position) * m.rows + row, acc);
+                else
+                    store_f32(a.partials + (static_cast<int64_t>(blockIdx.x) * 2 + slot) * kThreadsW + threadIdx.x,
+                              acc);
+            }
+        }
+        u += nt;
+        t0 = 0;
+        if (++item_group == a.groups) {
+            item_group = 0;
+            if (++member == a.count) {
+                member = 0;
+                ++position;
+            }
         }
     }
 }
 
-// Adds the pieces of every item split between workgroups. Block g - 1 looks at the boundary between
-// ranges g - 1 and g; an item is handled at its first inner boundary, its pieces summed in range order
-// from +0 (eight loads in flight at a time).
+// Adds the pieces of one item cut between workgroups (one workgroup per cut item), in range order from +0
+// with eight loads in flight at a time.
 template <int W>
 __global__ __launch_bounds__(64 * W) void t2_fixup_kernel(MatDesc one, const MatDesc* __restrict__ group,
                                                           T2Args a) {
     constexpr int kThreadsW = 64 * W;
-    const int g = blockIdx.x + 1;
-    const int64_t boundary = range_begin(g, a);
-    const int64_t item = boundary / a.tiles;
-    const int64_t start = item * a.tiles;
-    if (boundary == start) return;  // no item is cut here
-    const int first = range_owner(start, a);
-    if (first + 1 != g) return;  // an earlier boundary inside the same item handles it
-    const int last = range_owner(start + a.tiles - 1, a);
-    const int64_t member_position = item / a.groups;
-    const int member = static_cast<int>(member_position % a.count);
-    const int position = static_cast<int>(member_position / a.count);
-    const MatDesc m = group ? group[member] : one;
-    const int row = static_cast<int>(item % a.groups) * W * kT2PanelRows + threadIdx.x;
+    const T2Fixup f = a.fixups[blockIdx.x];
+    const MatDesc m = group ? group[f.member] : one;
+    const int row = f.panel0 * kT2PanelRows + threadIdx.x;
     if (row >= m.rows) return;
     const float* p = a.partials + threadIdx.x;
-    const int first_slot = range_begin(first, a) == start ? 0 : 1;  // else it is `first`'s last piece
-    float sum = 0.0f + load_f32(p + (static_cast<int64_t>(first) * 2 + first_slot) * kThreadsW);
-    int h = first + 1;
-    for (; h + 8 <= last + 1; h += 8) {
+    float sum = 0.0f + load_f32(p + (static_cast<int64_t>(f.first) * 2 + f.first_slot) * kThreadsW);
+    int h = f.first + 1;
+    for (; h + 8 <= f.last + 1; h += 8) {
         float v[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[k] = load_f32(p + static_cast<int64_t>(h + k) * 2 * kThreadsW);
 #pragma unroll
         for (int k = 0; k < 8; ++k) sum += v[k];
     }
-    for (; h <= last; ++h) sum += load_f32(p + static_cast<int64_t>(h) * 2 * kThreadsW);
-    store_f32(m.y + static_cast<int64_t>(position) * m.rows + row, sum);
+    for (; h <= f.last; ++h) sum += load_f32(p + static_cast<int64_t>(h) * 2 * kThreadsW);
+    store_f32(m.y + static_cast<int64_t>(f.position) * m.rows + row, sum);
 }
 
 template <int B, int W>
-hipError_t launch(const MatDesc& one, const MatDesc* group, size_t lds, const T2Args& a, hipStream_t stream) {
-    t2_kernel<B, W><<<a.workgroups, 64 * W, lds, stream>>>(one, group, a);
+hipError_t launch(const MatDesc& one, const MatDesc* group, const T2Plan& plan, const T2Args& a,
+                  hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(plan.staged_tiles) * kTile * sizeof(float);
+    t2_kernel<B, W><<<plan.workgroups, 64 * W, lds, stream>>>(one, group, a);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && a.workgroups > 1) {
-        t2_fixup_kernel<W><<<a.workgroups - 1, 64 * W, 0, stream>>>(one, group, a);
+    if (e == hipSuccess && plan.fixups > 0) {
+        t2_fixup_kernel<W><<<plan.fixups, 64 * W, 0, stream>>>(one, group, a);
         e = hipGetLastError();
     }
     return e;
@@ -294,16 +287,19 @@ namespace {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Tiles in the longest segment of a plan (what one workgroup stages at once).
-int staged_tiles(int tiles, int step, int64_t steps, int workgroups) {
-    return static_cast<int>(std::min<int64_t>(tiles, ceil_div(steps, workgroups) * step));
-}
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 }  // namespace
 
 T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positions) {
+    T2Plan p{};
+    p.rows_max = rows_max;
+    p.columns = columns;
+    p.block_size = block_size;
+    p.count = count;
+    p.positions = positions;
     const T2Layout l = t2_layout(rows_max, columns, block_size);
-    const int step = block_size == 256 ? 2 : 1;
+    const int step = block_size == 256 ? 2 : 1;  // B = 256 ranges hold whole blocks (tile pairs)
     int cus = 0, device = 0;
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
@@ -311,50 +307,83 @@ T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positio
     // Eight waves (eight panels) per workgroup share each tile's tables when that still leaves at least
     // eight tiles per workgroup on a full chip; otherwise four.
     const int64_t members = static_cast<int64_t>(count) * positions;
-    T2Plan p{8, 1, 1};
     const auto units = [&](int w) { return members * ceil_div(l.panels, w) * l.tiles; };
     const auto resident = [&](int w, int staged) {
         const int n = t2_resident_workgroups(block_size, w, staged);
         return static_cast<int64_t>(std::max(n, 1)) * cus;
     };
-    if (units(8) < 8 * resident(8, std::min(l.tiles, kMaxStagedTiles))) p.waves = 4;
-    const int64_t steps = units(p.waves) / step;
+    p.waves = units(8) < 8 * resident(8, std::min(l.tiles, kMaxStagedTiles)) ? 4 : 8;
+    const int W = p.waves;
+    const int groups = static_cast<int>(ceil_div(l.panels, W));
+    const int64_t total = units(W);
+    if (total > INT32_MAX) return p;  // workgroups == 0: not plannable
+    const int64_t steps = total / step;
     // As many workgroups as the CUs hold at once, each with at least two tiles and at most what it stages.
-    int64_t wgs = std::min(resident(p.waves, std::min(l.tiles, kMaxStagedTiles)), ceil_div(steps * step, 2));
-    wgs = std::max(wgs, ceil_div(steps * step, kMaxStagedTiles));
+    int64_t wgs = std::min(resident(W, std::min(l.tiles, kMaxStagedTiles)), ceil_div(total, 2));
+    wgs = std::max(wgs, ceil_div(total, kMaxStagedTiles));
     wgs = std::max<int64_t>(1, std::min(wgs, steps));
-    p.workgroups = static_cast<int>(std::min<int64_t>(wgs, INT32_MAX));
-    p.staged_tiles = staged_tiles(l.tiles, step, steps, p.workgroups);
-    return p;
-}
+    const int P = static_cast<int>(wgs);
+    p.workgroups = P;
 
-size_t t2_scratch_bytes(const T2Plan& plan) {
-    return plan.workgroups > 1 ? static_cast<size_t>(plan.workgroups) * 2 * 64 * plan.waves * sizeof(float) : 0;
+    std::vector<int> starts(P + 1);
+    for (int g = 0; g <= P; ++g) starts[g] = static_cast<int>((static_cast<int64_t>(g) * steps / P) * step);
+    int longest = 0;
+    for (int g = 0; g < P; ++g) longest = std::max(longest, starts[g + 1] - starts[g]);
+    p.staged_tiles = std::min(l.tiles, longest);
+    // The range holding tile u.
+    const auto owner = [&](int u) {
+        return static_cast<int>(std::upper_bound(starts.begin(), starts.end(), u) - starts.begin()) - 1;
+    };
+    std::vector<T2Fixup> fixups;
+    for (int g = 1; g < P; ++g) {
+        const int item = starts[g] / l.tiles;
+        const int start = item * l.tiles;
+        if (starts[g] == start || owner(start) + 1 != g) continue;  // no cut here, or handled at an earlier cut
+        T2Fixup f{};
+        f.member = (item / groups) % count;
+        f.position = item / groups / count;
+        f.panel0 = (item % groups) * W;
+        f.first = g - 1;
+        f.last = owner(start + l.tiles - 1);
+        f.first_slot = starts[g - 1] == start ? 0 : 1;
+        fixups.push_back(f);
+    }
+    p.fixups = static_cast<int>(fixups.size());
+    p.fixup_offset = align256(sizeof(int) * starts.size());
+    p.partial_offset = align256(p.fixup_offset + sizeof(T2Fixup) * fixups.size());
+    p.scratch_bytes = p.partial_offset + static_cast<size_t>(P) * 2 * 64 * W * sizeof(float);
+    p.tables.assign(p.partial_offset, 0);
+    std::memcpy(p.tables.data(), starts.data(), sizeof(int) * starts.size());
+    if (!fixups.empty()) std::memcpy(p.tables.data() + p.fixup_offset, fixups.data(), sizeof(T2Fixup) * fixups.size());
+    return p;
 }
 
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, const T2Plan& plan,
                      void* scratch, hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
+    if (plan.workgroups < 1 || scratch == nullptr || plan.rows_max != s.rows_max || plan.columns != s.columns ||
+        plan.block_size != s.block_size || plan.count != count || plan.positions != s.positions ||
+        plan.staged_tiles > kMaxStagedTiles)
+        return hipErrorInvalidValue;
     const T2Layout l = t2_layout(s.rows_max, s.columns, s.block_size);
     const int W = plan.waves;
-    const int step = s.block_size == 256 ? 2 : 1;
-    const int groups = (l.panels + W - 1) / W;
-    const int64_t steps = static_cast<int64_t>(s.positions) * count * groups * l.tiles / step;
-    if ((W != 4 && W != 8) || plan.workgroups < 1 || plan.workgroups > steps ||
-        plan.staged_tiles > kMaxStagedTiles ||
-        staged_tiles(l.tiles, step, steps, plan.workgroups) > plan.staged_tiles ||
-        (plan.workgroups > 1 && scratch == nullptr))
-        return hipErrorInvalidValue;
-    const T2Args a{s.columns, l.tiles, l.chunks, l.slots, count, groups, step, plan.workgroups, steps,
-                   static_cast<float*>(scratch)};
-    const size_t lds = static_cast<size_t>(plan.staged_tiles) * kTile * sizeof(float);
+    char* base = static_cast<char*>(scratch);
+    const T2Args a{s.columns,
+                   l.tiles,
+                   l.chunks,
+                   l.slots,
+                   count,
+                   static_cast<int>(ceil_div(l.panels, W)),
+                   reinterpret_cast<const int*>(base),
+                   reinterpret_cast<const T2Fixup*>(base + plan.fixup_offset),
+                   reinterpret_cast<float*>(base + plan.partial_offset)};
     switch (s.block_size * 10 + W) {
-        case 644: return launch<64, 4>(one, group, lds, a, stream);
-        case 648: return launch<64, 8>(one, group, lds, a, stream);
-        case 1284: return launch<128, 4>(one, group, lds, a, stream);
-        case 1288: return launch<128, 8>(one, group, lds, a, stream);
-        case 2564: return launch<256, 4>(one, group, lds, a, stream);
-        case 2568: return launch<256, 8>(one, group, lds, a, stream);
+        case 644: return launch<64, 4>(one, group, plan, a, stream);
+        case 648: return launch<64, 8>(one, group, plan, a, stream);
+        case 1284: return launch<128, 4>(one, group, plan, a, stream);
+        case 1288: return launch<128, 8>(one, group, plan, a, stream);
+        case 2564: return launch<256, 4>(one, group, plan, a, stream);
+        case 2568: return launch<256, 8>(one, group, plan, a, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <vector>
 
 namespace satori {
 
@@ -74,23 +75,37 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
 }
 
 // How a Ternary2 launch is cut: workgroups of `waves` waves (one 64-row panel each) take equal ranges of
-// the launch's (panel group, tile) units; items cut between two ranges are finished by a second kernel
-// from per-workgroup scratch of t2_scratch_bytes() bytes. Launches that share a scratch buffer must not
-// overlap in time. The plan depends on the launch's shape and member count and on the current device.
-struct T2Plan {
-    int waves;         // waves per workgroup: 4 or 8
-    int workgroups;    // ranges (one workgroup each)
-    int staged_tiles;  // longest segment: activation tiles staged in LDS at once
+// the launch's (panel group, tile) units; items cut between two ranges are finished by a second kernel.
+// The launch needs a device scratch buffer of `scratch_bytes` whose start holds the plan's tables (range
+// starts, cut items): copy `tables` there once before the first launch; the rest holds per-workgroup
+// partial sums. Launches that share a scratch buffer must not overlap in time. A plan is valid for the
+// launch shape, member count and positions it was made for, on the device that was current.
+struct T2Fixup {
+    int member, position, panel0;  // the cut item
+    int first, last;               // ranges holding its pieces
+    int first_slot;                // slot of the piece in range `first` (0: its first segment, 1: its last)
+    int pad_[2];
 };
 
+struct T2Plan {
+    int rows_max, columns, block_size, count, positions;  // what the plan was made for
+    int waves;                                            // waves per workgroup: 4 or 8
+    int workgroups;                                       // ranges (one workgroup each)
+    int staged_tiles;                                     // longest segment: activation tiles staged in LDS
+    int fixups;                                           // items cut between ranges
+    size_t fixup_offset, partial_offset, scratch_bytes;  // scratch layout
+    std::vector<uint8_t> tables;                         // host image of [starts][fixups]
+};
+
+// Throws nothing; returns a plan with workgroups == 0 when the launch is too large to plan (more than
+// 2^31 - 1 tiles of work).
 T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positions);
-size_t t2_scratch_bytes(const T2Plan& plan);
 
 // Workgroups of one Ternary2 kernel variant that fit on a CU at once (0 if unknown).
 int t2_resident_workgroups(int block_size, int waves, int staged_tiles);
 
-// Ternary2 MatVec on the panel layout (MatDesc::w points at it); `scratch` may be null when
-// plan.workgroups == 1.
+// Ternary2 MatVec on the panel layout (MatDesc::w points at it), with the plan made for this launch and
+// its scratch buffer (tables already copied).
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape, const T2Plan& plan,
                      void* scratch, hipStream_t stream);
 

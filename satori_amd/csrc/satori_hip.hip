@@ -224,12 +224,17 @@ std::vector<uint8_t> ternary2_panels(const Shape& s, const uint8_t* packed) {
     return out;
 }
 
-// Scratch for a Ternary2 plan (null when it has a single range).
+// Scratch of a Ternary2 plan, with the plan's tables copied to its start.
 void* allocate_t2_scratch(const T2Plan& plan) {
-    const size_t bytes = t2_scratch_bytes(plan);
-    if (!bytes) return nullptr;
+    if (plan.workgroups < 1)
+        fail(SATORI_HIP_E_NOT_SUPPORTED, "Ternary2 launch too large: more than 2^31 - 1 tiles of work.");
     void* p = nullptr;
-    check_hip(hipMalloc(&p, bytes), "hipMalloc");
+    check_hip(hipMalloc(&p, plan.scratch_bytes), "hipMalloc");
+    const hipError_t e = hipMemcpy(p, plan.tables.data(), plan.tables.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        check_hip(e, "launch table upload");
+    }
     return p;
 }
 
