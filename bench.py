@@ -330,7 +330,7 @@ def main() -> int:
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
-            "kernel": "t2_kernel<128, 2> (grouped)",
+            "kernel": "t2_kernel<128, 8> + t2_fixup_kernel<8> (one grouped launch)",
             "launch_us": round(headline["launch_us"], 2),
             "algorithmic_bytes_per_launch": headline["copies"] * int(payload.size),
         },
