@@ -54,6 +54,29 @@ __device__ __forceinline__ void load_unaligned(const uint8_t* p, uint32_t (&out)
     for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], shift);
 }
 
+// One quarter (c = 2h + t) of Q6_K block `index` from the regrouped device layout of a matrix of `blocks`
+// blocks (Q6KLayout): 48 code bytes (ql[64h + 16t, +16), ql[64h + 32 + 16t, +16), qh[32h + 16t, +16)), the
+// quarter's four scales sc[8h + 2k + t] (byte k), and d.
+struct Q6KQuarter {
+    u32x4 qla, qlb, qh;
+    uint32_t sc;
+    float d;
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16);
+
+__device__ __forceinline__ void q6k_load_quarter(const uint8_t* w, int64_t blocks, int64_t index, int c,
+                                                 Q6KQuarter& r) {
+    const uint8_t* record = w + index * 192 + 48 * c;
+    r.qla = *(const SATORI_GLOBAL u32x4*)(record);
+    r.qlb = *(const SATORI_GLOBAL u32x4*)(record + 16);
+    r.qh = *(const SATORI_GLOBAL u32x4*)(record + 32);
+    r.sc = load4_a4(w + blocks * 192 + index * 16 + 4 * c);
+    // d array: 2 bytes per block from offset blocks * 208 (a multiple of 16); read the aligned dword.
+    const uint32_t pair = load4_a4(w + blocks * 208 + (index & ~int64_t(1)) * 2);
+    r.d = half_bits_to_float(pair >> (16 * static_cast<int>(index & 1)));
+}
+
 // binary16 -> binary32, exact (v_cvt_f32_f16; FP16 denormals are kept by the kernel float mode).
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
     _Float16 h;

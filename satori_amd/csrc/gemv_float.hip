@@ -38,8 +38,8 @@ struct Q8_0Chunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
-        const uint8_t* block = row + chunk * 34;
+    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
+        const uint8_t* block = m.w + row * s.row_bytes + chunk * 34;
         uint32_t head[1];
         load_unaligned<1>(block, head);
         r.scale = half_bits_to_float(head[0] & 0xFFFFu);
@@ -81,8 +81,8 @@ struct Q4_0Chunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
-        const uint8_t* block = row + chunk * 18;
+    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
+        const uint8_t* block = m.w + row * s.row_bytes + chunk * 18;
         uint32_t head[1];
         load_unaligned<1>(block, head);
         r.scale = half_bits_to_float(head[0] & 0xFFFFu);
@@ -117,19 +117,17 @@ struct Q4_0Chunk {
 // sub-block 2g, high nibbles weights 64g + 32 + 16h + i of sub-block 2g + 1 (g = k / 2, h = k % 2).
 // The weight d*s*q - dmin*m is one FMA.
 // ------------------------------------------------------------------------------------------------
-// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) on the scales[12] bytes held in three dwords.
-__device__ __forceinline__ int q4k_scale_byte(const u32x4& head, int i) {
-    return static_cast<int>((head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
-}
-
+// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) for sub-block j (0..7), from the dwords holding
+// scales[12] (head[1..3]). Both forms are computed from fixed dwords with a per-lane shift and one is
+// selected, so no register vector is indexed by a per-lane value.
 __device__ __forceinline__ void q4k_scale_min(int j, const u32x4& head, int& scale, int& min) {
-    if (j < 4) {
-        scale = q4k_scale_byte(head, j) & 63;
-        min = q4k_scale_byte(head, j + 4) & 63;
-    } else {
-        scale = (q4k_scale_byte(head, j + 4) & 0xF) | ((q4k_scale_byte(head, j - 4) >> 6) << 4);
-        min = (q4k_scale_byte(head, j + 4) >> 4) | ((q4k_scale_byte(head, j) >> 6) << 4);
-    }
+    const int shift = 8 * (j & 3);
+    const uint32_t a = head[1] >> shift, b = head[2] >> shift, c = head[3] >> shift;  // bytes j&3, 4+(j&3), 8+(j&3)
+    const int low_scale = static_cast<int>(a & 63), low_min = static_cast<int>(b & 63);
+    const int high_scale = static_cast<int>((c & 0xFu) | (((a >> 6) & 3u) << 4));
+    const int high_min = static_cast<int>(((c >> 4) & 0xFu) | (((b >> 6) & 3u) << 4));
+    scale = j < 4 ? low_scale : high_scale;
+    min = j < 4 ? low_min : high_min;
 }
 
 struct Q4_KChunk {
@@ -145,8 +143,8 @@ struct Q4_KChunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks * 8; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
-        const uint8_t* block = row + (chunk >> 3) * 144;
+    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
+        const uint8_t* block = m.w + row * s.row_bytes + (chunk >> 3) * 144;
         r.head = load16_a4(block);
         r.qs = load16_a4(block + 16 + 16 * (chunk & 7));
         r.g = (chunk & 7) >> 1;
@@ -185,36 +183,23 @@ struct Q4_KChunk {
 
 // ------------------------------------------------------------------------------------------------
 // Q6_K, FP32 activations (Q6KCodec.DotBlock, src/Satori.Core/Q6KCodec.cs:22-51): 210-byte super-block,
-// ql[128] @0, qh[64] @128, int8 scales[16] @192, f16 d @208. Chunk (h, t), h = half, t = 16-lane slice:
-// l in [16t, 16t + 16) for all four quarters k, i.e. weights 128h + 32k + l with scale 8h + 2k + t.
-// Weight d*sc*(q - 32) is fma(d*sc, q, -32*d*sc), the same single rounding of the same product as the
-// reference's (d*sc)*(q-32) since 32*d*sc is exact.
+// ql[128] @0, qh[64] @128, int8 scales[16] @192, f16 d @208, read from the regrouped device layout
+// (Q6KLayout). Chunk = quarter c = 2h + t of a block: l in [16t, 16t + 16) for all four k, i.e. weights
+// 128h + 32k + l with scale 8h + 2k + t. Weight d*sc*(q - 32) is fma(d*sc, q, -32*d*sc), the same single
+// rounding of the same product as the reference's (d*sc)*(q-32) since 32*d*sc is exact.
 // ------------------------------------------------------------------------------------------------
 struct Q6_KChunk {
     static constexpr int kRowUnroll = 1;
     static constexpr int kWeights = 64;
     static constexpr int kPadShift = 7;
-    struct Regs {
-        uint32_t qla[4], qlb[4], qh[4];
-        uint32_t sc[4];  // bytes 192..207
-        float d;
-        int h, t;
-    };
+    using Regs = Q6KQuarter;
     struct Consts {};
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks * 4; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    __device__ static void load(const uint8_t* row, int chunk, Regs& r) {
-        const uint8_t* block = row + (chunk >> 2) * 210;
-        r.h = (chunk & 3) >> 1;
-        r.t = chunk & 1;
-        load_unaligned<4>(block + 64 * r.h + 16 * r.t, r.qla);
-        load_unaligned<4>(block + 64 * r.h + 32 + 16 * r.t, r.qlb);
-        load_unaligned<4>(block + 128 + 32 * r.h + 16 * r.t, r.qh);
-        load_unaligned<4>(block + 192, r.sc);
-        uint32_t tail[1];
-        load_unaligned<1>(block + 208, tail);
-        r.d = half_bits_to_float(tail[0] & 0xFFFFu);
+    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
+        q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * s.blocks,
+                         static_cast<int64_t>(row) * s.blocks + (chunk >> 2), chunk & 3, r);
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -228,8 +213,7 @@ struct Q6_KChunk {
         float ds[4], bias[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int index = 8 * r.h + 2 * k + r.t;
-            const int8_t s = static_cast<int8_t>(r.sc[index >> 2] >> (8 * (index & 3)));
+            const int8_t s = static_cast<int8_t>(r.sc >> (8 * k));  // scale 8h + 2k + t
             ds[k] = r.d * static_cast<float>(s);
             bias[k] = -32.0f * ds[k];
         }
@@ -301,7 +285,6 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
     const int lr = lane % L;
     const int nchunks = F::chunks(s);
     const typename F::Consts k = F::consts();
-    const int64_t row_bytes = s.row_bytes;
     const int first = row_begin + wave * kRowsPerPass;  // wave-uniform
 
     float xr[F::kWeights];
@@ -319,13 +302,13 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
 #pragma unroll
         for (int u = 0; u < kRowUnroll; ++u) {
             const int row = first + u * kStride + sub;
-            if (active && row < row_end) F::load(m.w + row * row_bytes, lr, cur[u]);
+            if (active && row < row_end) F::load(m, s, row, lr, cur[u]);
         }
         for (int base = first; base < row_end; base += kStep) {
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) {
                 const int row = base + kStep + u * kStride + sub;
-                if (active && row < row_end) F::load(m.w + row * row_bytes, lr, nxt[u]);
+                if (active && row < row_end) F::load(m, s, row, lr, nxt[u]);
             }
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) {
@@ -348,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
 #pragma unroll
                 for (int u = 0; u < kRowUnroll; ++u) {
                     const int row = base + u * kStride + sub;
-                    if (row < row_end) F::load(m.w + row * row_bytes, c, regs[u]);
+                    if (row < row_end) F::load(m, s, row, c, regs[u]);
                 }
 #pragma unroll
                 for (int u = 0; u < kRowUnroll; ++u) {

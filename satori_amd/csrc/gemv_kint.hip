@@ -87,19 +87,17 @@ __global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restric
 constexpr int kThreads = 256;
 constexpr int kTileRows = 64;
 
-// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) on the scales[12] bytes held in three dwords.
-__device__ __forceinline__ int q4k_scale_byte(const u32x4& head, int i) {
-    return static_cast<int>((head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
-}
-
+// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) for sub-block j (0..7), from the dwords holding
+// scales[12] (head[1..3]). Both forms are computed from fixed dwords with a per-lane shift and one is
+// selected, so no register vector is indexed by a per-lane value.
 __device__ __forceinline__ void q4k_scale_min(int j, const u32x4& head, int& scale, int& min) {
-    if (j < 4) {
-        scale = q4k_scale_byte(head, j) & 63;
-        min = q4k_scale_byte(head, j + 4) & 63;
-    } else {
-        scale = (q4k_scale_byte(head, j + 4) & 0xF) | ((q4k_scale_byte(head, j - 4) >> 6) << 4);
-        min = (q4k_scale_byte(head, j + 4) >> 4) | ((q4k_scale_byte(head, j) >> 6) << 4);
-    }
+    const int shift = 8 * (j & 3);
+    const uint32_t a = head[1] >> shift, b = head[2] >> shift, c = head[3] >> shift;  // bytes j&3, 4+(j&3), 8+(j&3)
+    const int low_scale = static_cast<int>(a & 63), low_min = static_cast<int>(b & 63);
+    const int high_scale = static_cast<int>((c & 0xFu) | (((a >> 6) & 3u) << 4));
+    const int high_min = static_cast<int>(((c >> 4) & 0xFu) | (((b >> 6) & 3u) << 4));
+    scale = j < 4 ? low_scale : high_scale;
+    min = j < 4 ? low_min : high_min;
 }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
@@ -147,19 +145,9 @@ __device__ __forceinline__ void q4k_dot(const Q4KRaw& r, const ActTile& act, int
 
 // Q6_K pair, lane c of 4: half h = c / 2, slice t = c % 2, i.e. weights 128h + 32k + 16t + i
 // (Q6KCodec.DotProduct, Q6KCodec.cs:114-146, with the -32 centring applied through the group sums:
-// sum sc * (q - 32) * code = sum sc * q * code - 32 * sum sc * bsum, both exact).
-struct Q6KRaw {
-    uint32_t qla[4], qlb[4], qh[4], sc[4], tail[1];
-};
-
-__device__ __forceinline__ void q6k_load(const uint8_t* block, int c, Q6KRaw& r) {
-    const int h = c >> 1, t = c & 1;
-    load_unaligned<4>(block + 64 * h + 16 * t, r.qla);
-    load_unaligned<4>(block + 64 * h + 32 + 16 * t, r.qlb);
-    load_unaligned<4>(block + 128 + 32 * h + 16 * t, r.qh);
-    load_unaligned<4>(block + 192, r.sc);
-    load_unaligned<1>(block + 208, r.tail);
-}
+// sum sc * (q - 32) * code = sum sc * q * code - 32 * sum sc * bsum, both exact), read from the regrouped
+// device layout (Q6KLayout).
+using Q6KRaw = Q6KQuarter;
 
 __device__ __forceinline__ int q6k_dot(const Q6KRaw& r, const ActTile& act, int b, int c) {
     const int h = c >> 1, t = c & 1;
@@ -180,9 +168,8 @@ __device__ __forceinline__ int q6k_dot(const Q6KRaw& r, const ActTile& act, int 
     int total = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int index = 8 * h + 2 * k + t;
-        const int sc = static_cast<int8_t>(r.sc[index >> 2] >> (8 * (index & 3)));
-        total += sc * (dotk[k] - 32 * sums[index]);
+        const int sc = static_cast<int8_t>(r.sc >> (8 * k));  // scale 8h + 2k + t
+        total += sc * (dotk[k] - 32 * sums[8 * h + 2 * k + t]);
     }
     return total;
 }
@@ -227,24 +214,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     const int c = lane % G;
     const int pairs = rows * nb;
     const uint8_t* tile = m.w + static_cast<int64_t>(row_begin) * s.row_bytes;
-    auto block_of = [&](int p) { return tile + (p / nb) * s.row_bytes + (p % nb) * kBlockBytes; };
+    auto load_pair = [&](int p, Raw& r) {
+        if constexpr (FORMAT == kQ4_K) {
+            q4k_load(tile + (p / nb) * s.row_bytes + (p % nb) * kBlockBytes, c, r);
+        } else {
+            // Q6_K: block p of the tile is block row_begin * nb + p of the matrix.
+            q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * nb, static_cast<int64_t>(row_begin) * nb + p, c, r);
+        }
+    };
     int p0 = threadIdx.x / G;
     Raw cur, nxt;
-    if (p0 < pairs) {
-        if constexpr (FORMAT == kQ4_K)
-            q4k_load(block_of(p0), c, cur);
-        else
-            q6k_load(block_of(p0), c, cur);
-    }
+    if (p0 < pairs) load_pair(p0, cur);
     __syncthreads();  // activations staged
     for (; p0 < pairs; p0 += kPairsPerStep) {
         const int pn = p0 + kPairsPerStep;
-        if (pn < pairs) {
-            if constexpr (FORMAT == kQ4_K)
-                q4k_load(block_of(pn), c, nxt);
-            else
-                q6k_load(block_of(pn), c, nxt);
-        }
+        if (pn < pairs) load_pair(pn, nxt);
         const int b = p0 % nb;
         float term = 0.0f;
         if constexpr (FORMAT == kQ4_K) {
@@ -262,8 +246,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
             int dot = q6k_dot(cur, act, b, c);
             dot = group_sum_last_int<G>(dot);
             const float a = act.scales[b];
-            const float d = half_bits_to_float(cur.tail[0] & 0xFFFFu);
-            if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, d), static_cast<float>(dot));
+            if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, cur.d), static_cast<float>(dot));
         }
         if (c == G - 1) terms[p0] = term;  // p0 = r * nb + b
         cur = nxt;

@@ -74,6 +74,12 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
     return l;
 }
 
+// ---- Q6_K device layout ----
+// The device copy of a Q6_K matrix holds the same bytes regrouped so that every load is aligned: for its
+// n = rows * blocks blocks in row-major order, n records of 192 code bytes (block quarter c = 2h + t at
+// 48c: ql[64h + 16t, +16), ql[64h + 32 + 16t, +16), qh[32h + 16t, +16)), then n records of 16 scale bytes
+// (quarter c's sc[8h + 2k + t] at 4c + k), then n FP16 d values.
+
 // How a Ternary2 launch is cut: workgroups of `waves` waves (one 64-row panel each) take equal ranges of
 // the launch's (panel group, tile) units; items cut between two ranges are finished by a second kernel.
 // The launch needs a device scratch buffer of `scratch_bytes` whose start holds the plan's tables (range

@@ -238,6 +238,29 @@ void* allocate_t2_scratch(const T2Plan& plan) {
     return p;
 }
 
+// Regroups a validated Q6_K payload into the device layout described with kernels.hpp's Q6_K layout:
+// aligned 48-byte quarter records, then each quarter's four scales, then the FP16 d values.
+std::vector<uint8_t> q6k_regroup(const Shape& s, const uint8_t* packed) {
+    const int64_t n = static_cast<int64_t>(s.rows) * s.blocks;  // blocks are contiguous row after row
+    std::vector<uint8_t> out(static_cast<size_t>(n) * 210);
+    uint8_t* codes = out.data();
+    uint8_t* scales = codes + n * 192;
+    uint8_t* ds = codes + n * 208;
+    for (int64_t i = 0; i < n; ++i) {
+        const uint8_t* block = packed + i * 210;
+        for (int c = 0; c < 4; ++c) {
+            const int h = c >> 1, t = c & 1;
+            uint8_t* record = codes + i * 192 + 48 * c;
+            std::memcpy(record, block + 64 * h + 16 * t, 16);
+            std::memcpy(record + 16, block + 64 * h + 32 + 16 * t, 16);
+            std::memcpy(record + 32, block + 128 + 32 * h + 16 * t, 16);
+            for (int k = 0; k < 4; ++k) scales[i * 16 + 4 * c + k] = block[192 + 8 * h + 2 * k + t];
+        }
+        std::memcpy(ds + i * 2, block + 208, 2);
+    }
+    return out;
+}
+
 // Device allocations of one matrix: the weights (+ slack) and, for a split Ternary2 plan, its scratch.
 // Executions of one matrix that overlap in time (device entry points on different streams) share that
 // scratch and must be serialised by the caller.
@@ -260,13 +283,16 @@ void free_matrix(satori_hip_matrix* m) {
 
 satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
     set_device(c);
-    std::vector<uint8_t> panels;
+    std::vector<uint8_t> regrouped;
     const uint8_t* source = payload;
     int64_t bytes = s.byte_length;
-    if (s.format == SATORI_HIP_TERNARY2) {
-        panels = ternary2_panels(s, payload);
-        source = panels.data();
-        bytes = static_cast<int64_t>(panels.size());
+    if (s.format == SATORI_HIP_TERNARY2)
+        regrouped = ternary2_panels(s, payload);
+    else if (s.format == SATORI_HIP_Q6_K)
+        regrouped = q6k_regroup(s, payload);
+    if (!regrouped.empty()) {
+        source = regrouped.data();
+        bytes = static_cast<int64_t>(regrouped.size());
     }
     auto* m = new satori_hip_matrix();
     m->context = c;
