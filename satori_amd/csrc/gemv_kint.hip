@@ -86,6 +86,11 @@ __global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restric
 // ------------------------------------------------------------------------------------------------
 constexpr int kThreads = 256;
 constexpr int kTileRows = 64;
+// The staged Q8_K codes of block b start at dword kCodeStride * b: 64 code dwords plus 4 of padding, so the
+// 16 (row, block) pairs of a wave, which read 16 consecutive blocks at the same offset, hit 16 different
+// groups of LDS banks instead of the same four.
+constexpr int kCodeStride = 68;
+constexpr int kActDwords = kCodeStride + 1 + 8;  // codes, scale, group sums per block
 
 // Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) for sub-block j (0..7), from the dwords holding
 // scales[12] (head[1..3]). Both forms are computed from fixed dwords with a per-lane shift and one is
@@ -127,7 +132,7 @@ __device__ __forceinline__ void q4k_dot(const Q4KRaw& r, const ActTile& act, int
     int s0, m0, s1, m1;
     q4k_scale_min(2 * g, r.head, s0, m0);
     q4k_scale_min(2 * g + 1, r.head, s1, m1);
-    const uint32_t* codes = act.codes + 64 * b + 16 * g;
+    const uint32_t* codes = act.codes + kCodeStride * b + 16 * g;
     const u32x4 lo0 = *reinterpret_cast<const u32x4*>(codes), lo1 = *reinterpret_cast<const u32x4*>(codes + 4);
     const u32x4 hi0 = *reinterpret_cast<const u32x4*>(codes + 8), hi1 = *reinterpret_cast<const u32x4*>(codes + 12);
     int lo = 0, hi = 0;
@@ -162,7 +167,8 @@ __device__ __forceinline__ int q6k_dot(const Q6KRaw& r, const ActTile& act, int 
             ((bq >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u),
         };
 #pragma unroll
-        for (int k = 0; k < 4; ++k) dotk[k] = sdot4(q[k], act.codes[64 * b + 32 * h + 8 * k + 4 * t + w], dotk[k]);
+        for (int k = 0; k < 4; ++k)
+            dotk[k] = sdot4(q[k], act.codes[kCodeStride * b + 32 * h + 8 * k + 4 * t + w], dotk[k]);
     }
     const int16_t* sums = act.sums + 16 * b;
     int total = 0;
@@ -190,10 +196,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
 
     extern __shared__ uint32_t smem[];
     ActTile act;
-    act.codes = smem;                                                  // 64 * nb dwords
-    act.scales = reinterpret_cast<float*>(smem + 64 * nb);             // nb
-    act.sums = reinterpret_cast<int16_t*>(smem + 65 * nb);             // 16 * nb int16 = 8 * nb dwords
-    float* terms = reinterpret_cast<float*>(smem + 73 * nb);           // kTileRows * nb
+    act.codes = smem;                                                          // kCodeStride * nb dwords
+    act.scales = reinterpret_cast<float*>(smem + kCodeStride * nb);            // nb
+    act.sums = reinterpret_cast<int16_t*>(smem + (kCodeStride + 1) * nb);      // 16 * nb int16 = 8 * nb dwords
+    float* terms = reinterpret_cast<float*>(smem + kActDwords * nb);           // kTileRows * nb
 
     const uint8_t* arow = m.a + static_cast<int64_t>(position) * nb * kQ8KBlockBytes;
     for (int i = threadIdx.x; i < 73 * nb; i += kThreads) {
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
         if (word == 0)
             act.scales[b] = __uint_as_float(value);
         else if (word <= 64)
-            act.codes[64 * b + word - 1] = value;
+            act.codes[kCodeStride * b + word - 1] = value;
         else
             reinterpret_cast<uint32_t*>(act.sums)[8 * b + word - 65] = value;
     }
@@ -271,9 +277,11 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
     return hipGetLastError();
 }
 
-size_t kint_lds_bytes(int blocks) { return static_cast<size_t>(73 + kTileRows) * blocks * sizeof(uint32_t); }
+size_t kint_lds_bytes(int blocks) {
+    return static_cast<size_t>(kActDwords + kTileRows) * blocks * sizeof(uint32_t);
+}
 
-int kint_tile_rows() { return kTileRows; }
+int kint_max_blocks() { return static_cast<int>((64 * 1024) / ((kActDwords + kTileRows) * sizeof(uint32_t))); }
 
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
                             hipStream_t stream) {

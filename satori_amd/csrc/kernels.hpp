@@ -124,7 +124,8 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape,
                             hipStream_t stream);
 
-// Rows one workgroup of the integer product owns (its LDS holds that many rows of block terms).
-int kint_tile_rows();
+// Widest row, in Q8_K blocks, the integer product accepts (its LDS holds the staged activation row and the
+// block terms of the workgroup's rows).
+int kint_max_blocks();
 
 }  // namespace satori

@@ -162,7 +162,7 @@ LaunchShape launch_shape(const Shape& s, int positions, int rows_max) {
 
 bool is_k(const Shape& s) { return s.format == SATORI_HIP_Q4_K || s.format == SATORI_HIP_Q6_K; }
 
-size_t kint_lds_limit_blocks() { return (64 * 1024) / ((73 + static_cast<size_t>(kint_tile_rows())) * 4); }
+size_t kint_lds_limit_blocks() { return static_cast<size_t>(kint_max_blocks()); }
 
 // Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers.
 void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
