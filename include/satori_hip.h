@@ -28,11 +28,12 @@
 extern "C" {
 #endif
 
-#define SATORI_HIP_ABI_VERSION 1
+#define SATORI_HIP_ABI_VERSION 2
 
 typedef struct satori_hip_context satori_hip_context;
 typedef struct satori_hip_matrix satori_hip_matrix;
 typedef struct satori_hip_group satori_hip_group;
+typedef struct satori_hip_step satori_hip_step;
 
 typedef enum satori_hip_status {
     SATORI_HIP_OK = 0,
@@ -162,7 +163,22 @@ int satori_hip_group_create(satori_hip_context* context, satori_hip_matrix* cons
                             const float* const* inputs, float* const* outputs, int quantized_activations,
                             satori_hip_group** group);
 int satori_hip_group_execute(satori_hip_group* group, void* stream);
+/* Fails with SATORI_HIP_E_ARGUMENT while a step replays the group. A matrix cannot be destroyed while a
+ * group launches it (same status). */
 int satori_hip_group_destroy(satori_hip_group* group);
+
+/* ---- steps: an ordered list of groups replayed as one HIP graph ----
+ * satori_hip_step_create waits for the context stream, then captures the launches of `count` groups, in
+ * order, into one graph; satori_hip_step_execute replays it on `stream` (null: the context stream), in
+ * the order the groups' launches would run eagerly, reading and writing the groups' device buffers. No
+ * counterpart in the reference: it is the resident form of the projection sequence of DenseForward.Step
+ * (src/Satori.Core/Model/DenseForward.cs:100-162), whose cost per token the reference attributes to
+ * per-call overheads; one replay replaces a launch per projection. Replays that overlap in time share
+ * the groups' scratch buffers and must be serialised by the caller. */
+int satori_hip_step_create(satori_hip_context* context, satori_hip_group* const* groups, int count,
+                           satori_hip_step** step);
+int satori_hip_step_execute(satori_hip_step* step, void* stream);
+int satori_hip_step_destroy(satori_hip_step* step);
 
 /* ---- host-only entry points (CPU; no device needed, never on the MatVec path) ---- */
 

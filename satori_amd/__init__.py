@@ -30,7 +30,7 @@ __all__ = [
     "InvalidDataException", "NotSupportedException", "ObjectDisposedException", "PlatformNotSupportedException",
     "OutOfMemoryException", "InvalidOperationException", "OverflowException",
     "BlockQuantization", "QuantizedMatrixShape", "Ternary2Matrix", "Ternary2MatVec", "MappedTernary2Matrix",
-    "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "Q8KCodec", "TERNARY2",
+    "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "HipStep", "Q8KCodec", "TERNARY2",
     "device_count", "default_context", "payload_length", "quantize_weights",
 ]
 
@@ -324,6 +324,24 @@ class HipGroup:
 
     def dispose(self) -> None:
         _check(_ffi.lib().satori_hip_group_destroy(self._handle))
+
+
+class HipStep:
+    """An ordered list of groups captured once and replayed as one HIP graph (the projection sequence of a
+    decode step). The groups must stay alive while the step exists."""
+
+    def __init__(self, context: HipContext, groups):
+        n = len(groups)
+        handles = (ctypes.c_void_p * n)(*[g._handle.value for g in groups])
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_step_create(context.handle, handles, n, ctypes.byref(handle)))
+        self._handle = handle
+
+    def execute(self, stream: int = 0) -> None:
+        _check(_ffi.lib().satori_hip_step_execute(self._handle, ctypes.c_void_p(stream)))
+
+    def dispose(self) -> None:
+        _check(_ffi.lib().satori_hip_step_destroy(self._handle))
 
 
 _default_lock = threading.Lock()

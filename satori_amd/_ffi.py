@@ -39,6 +39,9 @@ SIGNATURES = {
     "satori_hip_group_create": (I, [P, P, I, P, P, I, PP]),
     "satori_hip_group_execute": (I, [P, P]),
     "satori_hip_group_destroy": (I, [P]),
+    "satori_hip_step_create": (I, [P, P, I, PP]),
+    "satori_hip_step_execute": (I, [P, P]),
+    "satori_hip_step_destroy": (I, [P]),
     "satori_hip_device_alloc": (I, [P, SZ, PP]),
     "satori_hip_device_free": (I, [P, P]),
     "satori_hip_copy": (I, [P, P, P, SZ, I]),

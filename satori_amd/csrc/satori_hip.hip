@@ -89,6 +89,7 @@ struct satori_hip_matrix {
     int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
+    int groups = 0;              // live groups that launch this matrix
     bool live = true;
 };
 
@@ -103,6 +104,16 @@ struct satori_hip_group {
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
     std::vector<const float*> inputs;          // distinct inputs, quantized path
     std::vector<uint8_t*> q8k;                 // one Q8_K row per distinct input (device)
+    std::vector<satori_hip_matrix*> members;   // distinct member matrices (each counts this group)
+    int steps = 0;                             // live steps that replay this group
+    bool live = true;
+};
+
+struct satori_hip_step {
+    satori_hip_context* context = nullptr;
+    std::vector<satori_hip_group*> groups;  // in launch order (each counts this step)
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
     bool live = true;
 };
 
@@ -367,6 +378,27 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
 }
 
+// Enqueues one group's launches (Q8_K quantization of each distinct input, then the product) on `st`.
+void enqueue_group(satori_hip_group* g, hipStream_t st) {
+    const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
+    const MatDesc none{};
+    if (g->quantized) {
+        for (size_t k = 0; k < g->inputs.size(); ++k)
+            check_hip(launch_q8k_quantize(g->inputs[k], g->shape.columns, 1, g->q8k[k], st), "Q8_K launch");
+        check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
+    } else if (g->shape.format == SATORI_HIP_TERNARY2) {
+        check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
+    } else {
+        check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
+    }
+}
+
+void require_live(const satori_hip_group* g) {
+    require(g, "group");
+    if (!g->live || !g->context->live)
+        fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
+}
+
 }  // namespace
 }  // namespace satori
 
@@ -570,6 +602,7 @@ int satori_hip_matrix_destroy(satori_hip_matrix* m) {
         satori_hip_context* c = m->context;
         std::lock_guard<std::mutex> guard(c->lock);
         if (!m->live) return;
+        if (m->groups > 0) fail(SATORI_HIP_E_ARGUMENT, "Groups that launch the matrix must be destroyed first.");
         if (c->live) {
             (void)hipSetDevice(c->device);
             (void)hipStreamSynchronize(c->stream);
@@ -786,6 +819,11 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
             delete g;
             throw;
         }
+        for (int i = 0; i < count; ++i)
+            if (std::find(g->members.begin(), g->members.end(), matrices[i]) == g->members.end()) {
+                g->members.push_back(matrices[i]);
+                matrices[i]->groups++;
+            }
         *group = g;
     });
 }
@@ -797,18 +835,7 @@ int satori_hip_group_execute(satori_hip_group* g, void* stream) {
         std::lock_guard<std::mutex> guard(c->lock);
         if (!g->live || !c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
         set_device(c);
-        hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
-        const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
-        const MatDesc none{};
-        if (g->quantized) {
-            for (size_t k = 0; k < g->inputs.size(); ++k)
-                check_hip(launch_q8k_quantize(g->inputs[k], g->shape.columns, 1, g->q8k[k], st), "Q8_K launch");
-            check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
-        } else if (g->shape.format == SATORI_HIP_TERNARY2) {
-            check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
-        } else {
-            check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
-        }
+        enqueue_group(g, stream ? static_cast<hipStream_t>(stream) : c->stream);
     });
 }
 
@@ -818,10 +845,13 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         satori_hip_context* c = g->context;
         std::lock_guard<std::mutex> guard(c->lock);
         if (!g->live) return;
+        if (g->steps > 0) fail(SATORI_HIP_E_ARGUMENT, "Steps that replay the group must be destroyed first.");
         if (c->live) {
             (void)hipSetDevice(c->device);
             (void)hipStreamSynchronize(c->stream);
         }
+        for (satori_hip_matrix* m : g->members) m->groups--;
+        g->members.clear();
         for (uint8_t* b : g->q8k) (void)hipFree(b);
         g->q8k.clear();
         (void)hipFree(g->descriptors);
@@ -829,6 +859,80 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         if (g->scratch) (void)hipFree(g->scratch);
         g->scratch = nullptr;
         g->live = false;
+    });
+}
+
+int satori_hip_step_create(satori_hip_context* c, satori_hip_group* const* groups, int count,
+                           satori_hip_step** step) {
+    return guarded([&] {
+        require(step, "step");
+        *step = nullptr;
+        require_live(c);
+        require(groups, "groups");
+        if (count <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "count must be positive.");
+        std::lock_guard<std::mutex> guard(c->lock);
+        for (int i = 0; i < count; ++i) {
+            require_live(groups[i]);
+            if (groups[i]->context != c) fail(SATORI_HIP_E_ARGUMENT, "Every group must belong to the context.");
+        }
+        set_device(c);
+        // Everything enqueued on the context stream before the capture must not be part of the graph.
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+        check_hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph capture");
+        hipGraph_t graph = nullptr;
+        try {
+            for (int i = 0; i < count; ++i) enqueue_group(groups[i], c->stream);
+        } catch (...) {
+            (void)hipStreamEndCapture(c->stream, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        check_hip(hipStreamEndCapture(c->stream, &graph), "graph capture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            check_hip(e, "graph instantiation");
+        }
+        auto* s = new satori_hip_step();
+        s->context = c;
+        s->graph = graph;
+        s->exec = exec;
+        s->groups.assign(groups, groups + count);
+        for (satori_hip_group* g : s->groups) g->steps++;
+        *step = s;
+    });
+}
+
+int satori_hip_step_execute(satori_hip_step* s, void* stream) {
+    return guarded([&] {
+        require(s, "step");
+        satori_hip_context* c = s->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!s->live || !c->live)
+            fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_step'.");
+        set_device(c);
+        check_hip(hipGraphLaunch(s->exec, stream ? static_cast<hipStream_t>(stream) : c->stream), "graph launch");
+    });
+}
+
+int satori_hip_step_destroy(satori_hip_step* s) {
+    return guarded([&] {
+        if (!s) return;
+        satori_hip_context* c = s->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!s->live) return;
+        if (c->live) {
+            (void)hipSetDevice(c->device);
+            (void)hipStreamSynchronize(c->stream);
+        }
+        (void)hipGraphExecDestroy(s->exec);
+        (void)hipGraphDestroy(s->graph);
+        s->exec = nullptr;
+        s->graph = nullptr;
+        for (satori_hip_group* g : s->groups) g->steps--;
+        s->groups.clear();
+        s->live = false;
     });
 }
 

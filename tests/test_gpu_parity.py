@@ -551,3 +551,83 @@ def test_device_and_group_entry_points_match_host_calls(context):
     context.free(dx)
     for m in mats:
         m.dispose()
+
+
+def test_step_graph_replays_match_eager_groups(context):
+    # A two-layer projection skeleton of a decode step (q/k/v sharing one Q8_K input, o, gate/up sharing
+    # one input, down in Q6_K), plus a Q8_0 float group and a Ternary2 group (main and fix-up kernels),
+    # captured once as a graph. Every replay, with eager launches and synchronisations between replays,
+    # must write exactly the bits of the eager launches.
+    g = rng(31)
+    d, ffn = 512, 1024
+
+    def gguf(rows, columns, fmt):
+        w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+        return context.create(S.quantize_weights(w, rows, columns, fmt), S.QuantizedMatrixShape(rows, columns, fmt))
+
+    allocs = []
+
+    def buffer(values):
+        p = context.alloc(values.nbytes)
+        context.upload(p, values)
+        allocs.append(p)
+        return p
+
+    mats, groups, outs = [], [], []
+
+    def group(members, inputs, quantized):
+        ys = [context.alloc(4 * m.rows) for m in members]
+        outs.extend(zip(members, ys))
+        groups.append(S.HipGroup(context, members, inputs, ys, quantized))
+
+    for _ in range(2):
+        q, k, v, o = gguf(d, d, BQ.Q4_K), gguf(128, d, BQ.Q4_K), gguf(128, d, BQ.Q4_K), gguf(d, d, BQ.Q4_K)
+        gate, up, down = gguf(ffn, d, BQ.Q4_K), gguf(ffn, d, BQ.Q4_K), gguf(d, ffn, BQ.Q6_K)
+        mats += [q, k, v, o, gate, up, down]
+        h, attn, h2 = (buffer(g.standard_normal(d).astype(np.float32)) for _ in range(3))
+        act = buffer(g.standard_normal(ffn).astype(np.float32))
+        group([q, k, v], [h] * 3, True)
+        group([o], [attn], True)
+        group([gate, up], [h2] * 2, True)
+        group([down], [act], True)
+    q8 = [gguf(300, d, BQ.Q8_0), gguf(200, d, BQ.Q8_0)]
+    t2 = [context.create_ternary2(4096, 1024, 128, _t2_random_payload(g, 4096, 1024, 128)) for _ in range(2)]
+    mats += q8 + t2
+    xf = buffer(g.standard_normal(d).astype(np.float32))
+    xt = buffer(g.uniform(-1, 1, 1024).astype(np.float32))
+    group(q8, [xf, xf], False)
+    group(t2, [xt, xt], False)
+
+    def read_all():
+        context.synchronize()
+        return [context.download(np.zeros(m.rows, np.float32), y).view(np.uint32) for m, y in outs]
+
+    def clear_all():
+        for m, y in outs:
+            context.upload(y, np.full(m.rows, np.nan, np.float32))
+
+    for grp in groups:
+        grp.execute()
+    eager = read_all()
+    step = S.HipStep(context, groups)
+    for replay in range(3):
+        clear_all()
+        step.execute()
+        got = read_all()
+        for i, (a, b) in enumerate(zip(got, eager)):
+            assert np.array_equal(a, b), f"replay {replay}: output {i} differs from the eager launch"
+        groups[replay].execute()  # eager work between replays
+        context.synchronize()
+    with pytest.raises(S.ArgumentException):
+        groups[0].dispose()  # replayed by the step
+    with pytest.raises(S.ArgumentException):
+        mats[0].dispose()  # launched by a group
+    step.dispose()
+    for grp in groups:
+        grp.dispose()
+    for m, y in outs:
+        context.free(y)
+    for p in allocs:
+        context.free(p)
+    for m in mats:
+        m.dispose()

@@ -28,11 +28,11 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_entry_point():
     lib = ctypes.CDLL(S._ffi.LIB_PATH)
     names = declared_functions()
-    assert len(names) >= 29
+    assert len(names) >= 32
     for name in names:
         assert hasattr(lib, name), f"{name} declared in include/satori_hip.h but not exported"
     assert set(names) == set(S._ffi.SIGNATURES), "ctypes binding and header disagree"
-    assert S._ffi.lib().satori_hip_abi_version() == 1
+    assert S._ffi.lib().satori_hip_abi_version() == 2
 
 
 def test_context_without_gfx950_device_is_platform_not_supported():
