@@ -14,6 +14,8 @@ The same line carries, labelled:
              and Ternary2 at the other block sizes;
   single:    one launch per matrix (rotating copies), which includes launch gaps;
   cache:     the grouped launch over G references to ONE copy (cache resident, not an HBM figure);
+  decode_step: the 197 projections of one decode token of a Qwen-1.5B-shaped model (Q4_K/Q6_K on the Q8_K
+             integer path, 1.03 GB per token), replayed as one graph; tokens/s and GB/s;
   roofline:  for the headline kernel, from HIP events on the launch stream;
   cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core.
 
@@ -178,6 +180,81 @@ def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     return out
 
 
+def decode_step(ctx, events, steps: int, warmup: int) -> dict:
+    """The projection sequence of one decode token of a Qwen-1.5B-shaped model (28 layers of q 1536x1536,
+    k and v 256x1536, o 1536x1536, gate and up 8960x1536 in Q4_K, down 1536x8960 in Q6_K, then the output
+    projection 151936x1536 in Q6_K: 197 projections, 1,027,772,928 payload bytes per token), every matrix a
+    distinct resident copy, on the Q8_K integer path at one position. Projections that share an input form
+    one group (q/k/v, gate/up); the 113 groups of a token are captured once as a graph (satori_hip_step) and
+    replayed. Attention, norms and SwiGLU are not part of the path: their outputs are fixed random vectors.
+    Also timed: the same groups launched eagerly, one call each."""
+    d, kv, ffn, vocab = 1536, 256, 8960, 151936
+    roles = {"q": (d, d, BQ.Q4_K), "k": (kv, d, BQ.Q4_K), "v": (kv, d, BQ.Q4_K), "o": (d, d, BQ.Q4_K),
+             "gate": (ffn, d, BQ.Q4_K), "up": (ffn, d, BQ.Q4_K), "down": (d, ffn, BQ.Q6_K)}
+    first = {}
+    for name, (r, c, fmt) in roles.items():
+        data, _ = make_gguf(fmt, r, c)
+        first[name] = ctx.create(data, S.QuantizedMatrixShape(r, c, fmt))
+    # Output projection: rows of a 4096-row random Q6_K matrix repeated to 151,936 rows (rows are
+    # independent byte ranges, so the payload is a valid matrix of that shape).
+    base, _ = make_gguf(BQ.Q6_K, 4096, d)
+    row_bytes = base.size // 4096
+    tiled = np.tile(base.reshape(4096, row_bytes), (-(-vocab // 4096), 1))[:vocab].reshape(-1)
+    output = ctx.create(tiled, S.QuantizedMatrixShape(vocab, d, BQ.Q6_K))
+    g = rng(2026)
+    buffers = []
+
+    def device(values):
+        p = ctx.alloc(values.nbytes)
+        ctx.upload(p, values)
+        buffers.append(p)
+        return p
+
+    h, attn, h2 = (device(g.standard_normal(d).astype(np.float32)) for _ in range(3))
+    act = device(g.standard_normal(ffn).astype(np.float32))
+    out = {name: device(np.zeros(r, np.float32)) for name, (r, _, _) in roles.items()}
+    logits = device(np.zeros(vocab, np.float32))
+    mats, groups = [], []
+    for layer in range(28):
+        m = {name: (first[name] if layer == 0 else first[name].clone()) for name in roles}
+        mats += list(m.values())
+        groups.append(S.HipGroup(ctx, [m["q"], m["k"], m["v"]], [h] * 3, [out["q"], out["k"], out["v"]], True))
+        groups.append(S.HipGroup(ctx, [m["o"]], [attn], [out["o"]], True))
+        groups.append(S.HipGroup(ctx, [m["gate"], m["up"]], [h2] * 2, [out["gate"], out["up"]], True))
+        groups.append(S.HipGroup(ctx, [m["down"]], [act], [out["down"]], True))
+    groups.append(S.HipGroup(ctx, [output], [h], [logits], True))
+    mats.append(output)
+    payload = sum(r * (c // 256) * (144 if fmt == BQ.Q4_K else 210) for r, c, fmt in roles.values())
+    token_bytes = 28 * payload + vocab * (d // 256) * 210
+    step = S.HipStep(ctx, groups)
+    warm_up(ctx, step.execute, 0.5)
+    graph_ms = time_launches(ctx, events, step.execute, steps, warmup)
+
+    def eager():
+        for grp in groups:
+            grp.execute()
+
+    eager_ms = time_launches(ctx, events, eager, max(5, steps // 4), 2)
+    step.dispose()
+    for grp in groups:
+        grp.dispose()
+    for mat in mats:
+        mat.dispose()
+    for p in buffers:
+        ctx.free(p)
+    return {
+        "model": "Qwen-1.5B-shaped decode step, random-init Q4_K/Q6_K weights, batch 1",
+        "projections_per_token": 28 * 7 + 1,
+        "kernel_launches_per_token": len(groups),
+        "bytes_per_token": token_bytes,
+        "us_per_token": graph_ms * 1e3,
+        "tokens_per_s": 1e3 / graph_ms,
+        "gbs": token_bytes / (graph_ms * 1e-3) / 1e9,
+        "pct_hbm": 100.0 * token_bytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "eager_us_per_token": eager_ms * 1e3,
+    }
+
+
 def profiled_traffic(name: str):
     """HBM bytes per launch of the headline kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary (calibrated against a copy of known size); None when the summary is absent."""
@@ -297,6 +374,11 @@ def main() -> int:
             formats[label] = measure(ctx, events, c, max(20, args.steps // 4), 5, single=False)
             c.close()
 
+    decode = None
+    if not args.quick:
+        progress("decode step (197 projections per token)")
+        decode = decode_step(ctx, events, 50, 5)
+
     progress("cpu baseline")
     cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
     value = headline["gbs"]
@@ -335,6 +417,8 @@ def main() -> int:
             "algorithmic_bytes_per_launch": headline["copies"] * int(payload.size),
         },
         "cpu_baseline": cpu,
+        "decode_step": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode.items()}
+                        if decode else None),
         "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in formats.items()},
     }

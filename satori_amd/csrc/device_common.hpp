@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #define SATORI_GLOBAL __attribute__((address_space(1)))
 
@@ -109,6 +110,35 @@ __device__ __forceinline__ float group_sum_last(float v) {
     if constexpr (L >= 16) v += __int_as_float(dpp<0x118, 0xF, true>(__float_as_int(v)));
     if constexpr (L >= 32) v += __int_as_float(dpp<0x142, 0xA, false>(__float_as_int(v)));
     if constexpr (L >= 64) v += __int_as_float(dpp<0x143, 0xC, false>(__float_as_int(v)));
+    return v;
+}
+
+// Maximum (MAX) or minimum of an unsigned value over the whole wave, returned to every lane: DPP steps
+// within rows and across rows, then a read of lane 63. Lanes outside a step's source range contribute the
+// identity.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_extreme_u32(uint32_t v) {
+    constexpr uint32_t kIdentity = MAX ? 0u : 0xFFFFFFFFu;
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    auto step = [&](auto ctrl, auto row_mask) {
+        const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            static_cast<int>(kIdentity), static_cast<int>(v), decltype(ctrl)::value, decltype(row_mask)::value,
+            0xF, false));
+        v = op(v, other);
+    };
+    step(std::integral_constant<int, 0x111>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xF>{});
+    step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{});
+    step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{});
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// Sum over each aligned group of 4 lanes, in every lane of the group (DPP quad permutes).
+__device__ __forceinline__ int quad_sum_int(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
     return v;
 }
 

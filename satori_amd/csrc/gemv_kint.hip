@@ -19,47 +19,36 @@ namespace {
 // ------------------------------------------------------------------------------------------------
 // Q8_K quantizer: one wave per 256-element block, four consecutive elements per lane.
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restrict__ x, int columns,
-                                                          uint8_t* __restrict__ out) {
-    const int block = blockIdx.x;
-    const int position = blockIdx.y;
-    const int blocks = columns / 256;
-    const int lane = threadIdx.x;
-    const float* src = x + static_cast<int64_t>(position) * columns + block * 256;
-    uint8_t* dst = out + (static_cast<int64_t>(position) * blocks + block) * kQ8KBlockBytes;
+struct Q8KLane {
+    uint32_t packed;  // this lane's four codes (elements 4 * lane .. 4 * lane + 3)
+    int group_sum;    // sum of the 16 codes of group lane / 4 (every lane of the group holds it)
+    float scale;      // 1 / inverse (the block's float scale)
+    bool zero;        // the block is all zero: every byte of it is zero
+};
 
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = src[4 * lane + i];
-
-    // First index of the largest magnitude; NaN never wins (its comparison is false, Q8KCodec.cs:53).
-    float best = 0.0f;
+// One block from this lane's four values v = src[4 * lane .. 4 * lane + 3]. The first-largest magnitude
+// (Q8KCodec.cs:50-56: strict comparison, so the lowest index wins ties and NaN never wins) is found as the
+// wave maximum of the magnitudes' bit patterns (NaN mapped to 0; non-negative floats order like their
+// bits), then the wave minimum of the indices holding it; the signed value is read from its lane.
+__device__ __forceinline__ Q8KLane q8k_quantize_values(const float (&v)[4], int lane) {
+    uint32_t key = 0;
     int index = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float a = __builtin_fabsf(v[i]);
-        if (a > best) {
-            best = a;
+        const uint32_t k = a == a ? __float_as_uint(a) : 0u;  // NaN never wins
+        if (k > key) {
+            key = k;
             index = 4 * lane + i;
         }
     }
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        const float other = __shfl_xor(best, offset, 64);
-        const int other_index = __shfl_xor(index, offset, 64);
-        if (other > best || (other == best && other_index < index)) {
-            best = other;
-            index = other_index;
-        }
-    }
-    if (best == 0.0f) {  // magnitude 0: the block is all zero bytes (Q8KCodec.cs:59-63)
-        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-        for (int i = lane; i < kQ8KBlockBytes / 4; i += 64) d32[i] = 0u;
-        return;
-    }
-    const float max = src[index];
+    const uint32_t best = wave_extreme_u32<true>(key);
+    Q8KLane r{0u, 0, 0.0f, best == 0u};  // magnitude 0: the block is all zero bytes (Q8KCodec.cs:59-63)
+    if (r.zero) return r;
+    const int first = static_cast<int>(wave_extreme_u32<false>(key == best ? static_cast<uint32_t>(index) : 0xFFFFFFFFu));
+    const float candidate = (first & 3) == 0 ? v[0] : (first & 3) == 1 ? v[1] : (first & 3) == 2 ? v[2] : v[3];
+    const float max = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(candidate), first >> 2));
     const float inverse = __fdiv_rn(-127.0f, max);
-    uint32_t packed = 0;
     int sum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -68,19 +57,44 @@ __global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restric
         n = n < 127 ? n : 127;
         const int8_t code = static_cast<int8_t>(n);
         sum += code;
-        packed |= (static_cast<uint32_t>(static_cast<uint8_t>(code))) << (8 * i);
+        r.packed |= (static_cast<uint32_t>(static_cast<uint8_t>(code))) << (8 * i);
     }
-    // Group sums of 16 codes = 4 lanes, as int16 (Q8KCodec.cs:68-74).
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    reinterpret_cast<uint32_t*>(dst + 4)[lane] = packed;
-    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(dst + 260)[lane >> 2] = static_cast<int16_t>(sum);
-    if (lane == 0) reinterpret_cast<float*>(dst)[0] = __fdiv_rn(1.0f, inverse);
+    r.group_sum = quad_sum_int(sum);  // group sums of 16 codes = 4 lanes (Q8KCodec.cs:68-74)
+    r.scale = __fdiv_rn(1.0f, inverse);
+    return r;
+}
+
+__device__ __forceinline__ void q8k_load_values(const float* __restrict__ src, int lane, float (&v)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = load_f32(src + 4 * lane + i);
+}
+
+__global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restrict__ x, int columns,
+                                                          uint8_t* __restrict__ out) {
+    const int block = blockIdx.x;
+    const int position = blockIdx.y;
+    const int blocks = columns / 256;
+    const int lane = threadIdx.x;
+    const float* src = x + static_cast<int64_t>(position) * columns + block * 256;
+    uint8_t* dst = out + (static_cast<int64_t>(position) * blocks + block) * kQ8KBlockBytes;
+    float v[4];
+    q8k_load_values(src, lane, v);
+    const Q8KLane q = q8k_quantize_values(v, lane);
+    if (q.zero) {
+        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+        for (int i = lane; i < kQ8KBlockBytes / 4; i += 64) d32[i] = 0u;
+        return;
+    }
+    reinterpret_cast<uint32_t*>(dst + 4)[lane] = q.packed;
+    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(dst + 260)[lane >> 2] = static_cast<int16_t>(q.group_sum);
+    if (lane == 0) reinterpret_cast<float*>(dst)[0] = q.scale;
 }
 
 // ------------------------------------------------------------------------------------------------
-// Integer product. A workgroup owns kTileRows rows of one member at one position. The position's Q8_K
-// row is staged in LDS as separate arrays (codes, group sums, scales) so code reads are 16-byte aligned.
+// Integer product. A workgroup owns s.rows_per_wg rows (16, 32 or 64) of one member at one position. It quantizes the
+// position's FP32 activation row to Q8_K itself (one wave per block, bit-exact as above; every workgroup
+// computes the same bytes) straight into LDS as separate arrays (codes, group sums, scales), so no separate
+// quantization launch precedes the product and code reads are 16-byte aligned.
 // Work items are (row, block) pairs, 4 lanes of 64 weights each; the G lanes' int32 partials are summed exactly, the pair's leader forms the block's FP32
 // term and stores it in LDS, and finally one thread per row adds its terms in block order.
 // ------------------------------------------------------------------------------------------------
@@ -188,9 +202,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     constexpr int kPairsPerStep = kThreads / G;
     using Raw = typename std::conditional<FORMAT == kQ4_K, Q4KRaw, Q6KRaw>::type;
     const MatDesc m = group ? group[blockIdx.y] : one;
-    const int row_begin = blockIdx.x * kTileRows;
+    const int tile_rows = s.rows_per_wg;
+    const int row_begin = blockIdx.x * tile_rows;
     if (row_begin >= m.rows) return;
-    const int rows = min(kTileRows, m.rows - row_begin);
+    const int rows = min(tile_rows, m.rows - row_begin);
     const int position = blockIdx.z;
     const int nb = s.blocks;
 
@@ -199,19 +214,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     act.codes = smem;                                                          // kCodeStride * nb dwords
     act.scales = reinterpret_cast<float*>(smem + kCodeStride * nb);            // nb
     act.sums = reinterpret_cast<int16_t*>(smem + (kCodeStride + 1) * nb);      // 16 * nb int16 = 8 * nb dwords
-    float* terms = reinterpret_cast<float*>(smem + kActDwords * nb);           // kTileRows * nb
-
-    const uint8_t* arow = m.a + static_cast<int64_t>(position) * nb * kQ8KBlockBytes;
-    for (int i = threadIdx.x; i < 73 * nb; i += kThreads) {
-        const int b = i / 73, word = i % 73;
-        const uint32_t value = load4_a4(arow + b * kQ8KBlockBytes + 4 * word);
-        if (word == 0)
-            act.scales[b] = __uint_as_float(value);
-        else if (word <= 64)
-            act.codes[kCodeStride * b + word - 1] = value;
-        else
-            reinterpret_cast<uint32_t*>(act.sums)[8 * b + word - 65] = value;
-    }
+    float* terms = reinterpret_cast<float*>(smem + kActDwords * nb);           // tile_rows * nb
 
     // Work items are (row, block) pairs in row-major order; the G lanes of a pair share its index, so the
     // DPP group sums stay inside the pair. The next pair's payload is loaded before the current one is
@@ -230,7 +233,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     };
     int p0 = threadIdx.x / G;
     Raw cur, nxt;
-    if (p0 < pairs) load_pair(p0, cur);
+    if (p0 < pairs) load_pair(p0, cur);  // in flight while the activations are quantized
+
+    // Q8_K of the position's activations: each wave quantizes four blocks per pass, their loads in flight
+    // together.
+    const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
+    {
+        constexpr int kBatch = 4;
+        const int wave = threadIdx.x >> 6;
+        for (int b0 = kBatch * wave; b0 < nb; b0 += kBatch * (kThreads / 64)) {
+            float v[kBatch][4];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j)
+                if (b0 + j < nb) q8k_load_values(xrow + 256 * (b0 + j), lane, v[j]);
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int b = b0 + j;
+                if (b >= nb) break;
+                const Q8KLane q = q8k_quantize_values(v[j], lane);
+                act.codes[kCodeStride * b + lane] = q.packed;  // zero block: all codes, sums and the scale are 0
+                if ((lane & 3) == 0) act.sums[16 * b + (lane >> 2)] = static_cast<int16_t>(q.group_sum);
+                if (lane == 0) act.scales[b] = q.scale;
+            }
+        }
+    }
     __syncthreads();  // activations staged
     for (; p0 < pairs; p0 += kPairsPerStep) {
         const int pn = p0 + kPairsPerStep;
@@ -286,7 +312,13 @@ int kint_max_blocks() { return static_cast<int>((64 * 1024) / ((kActDwords + kTi
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
                             hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
-    dim3 grid((s.rows_max + kTileRows - 1) / kTileRows, count, s.positions);
+    // Rows per workgroup: 64, halved (down to 16) while the grid has fewer than 512 workgroups, so the
+    // small projections of a decode step still spread over the chip.
+    const int64_t members = static_cast<int64_t>(count) * s.positions;
+    int tile = kTileRows;
+    while (tile > 16 && members * ((s.rows_max + tile - 1) / tile) < 512) tile /= 2;
+    s.rows_per_wg = tile;
+    dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
     const size_t lds = kint_lds_bytes(s.blocks);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     if (s.format == kQ4_K)

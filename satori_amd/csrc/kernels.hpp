@@ -16,9 +16,8 @@ constexpr int kQ8KBlockBytes = 292;
 
 // One matrix of a launch. Row-major payload: row r starts at w + r * row_bytes.
 struct MatDesc {
-    const uint8_t* w;   // packed payload (device)
-    const float* x;     // FP32 activations [positions][columns] (float products)
-    const uint8_t* a;   // Q8_K activations [positions][blocks * 292] (integer products)
+    const uint8_t* w;   // weights (device; the payload, or its regrouped device layout)
+    const float* x;     // FP32 activations [positions][columns]
     float* y;           // output [positions][rows]
     int rows;
     int pad_;
@@ -119,7 +118,8 @@ hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, Launch
 // Q8KCodec.QuantizeRow. Output [positions][columns / 256 * 292].
 hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8_t* out, hipStream_t stream);
 
-// Integer K-format product against Q8_K activations (Q4_K or Q6_K), bit-exact with the reference's
+// Integer K-format product (Q4_K or Q6_K) against the Q8_K quantization of the FP32 activations, which each
+// workgroup computes itself (bit-exact with Q8KCodec.QuantizeRow); outputs bit-exact with the reference's
 // ExecuteQuantizedTiled composition.
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape,
                             hipStream_t stream);

@@ -102,8 +102,6 @@ struct satori_hip_group {
     satori::MatDesc* descriptors = nullptr;   // device
     satori::T2Plan plan{};                     // Ternary2 groups
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
-    std::vector<const float*> inputs;          // distinct inputs, quantized path
-    std::vector<uint8_t*> q8k;                 // one Q8_K row per distinct input (device)
     std::vector<satori_hip_matrix*> members;   // distinct member matrices (each counts this group)
     int steps = 0;                             // live steps that replay this group
     bool live = true;
@@ -177,7 +175,7 @@ size_t kint_lds_limit_blocks() { return static_cast<size_t>(kint_max_blocks()); 
 
 // Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers.
 void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
-    MatDesc d{m->payload, x, nullptr, y, m->shape.rows, 0};
+    MatDesc d{m->payload, x, y, m->shape.rows, 0};
     const LaunchShape l = launch_shape(m->shape, positions, m->shape.rows);
     if (m->shape.format == SATORI_HIP_TERNARY2)
         check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->scratch, stream), "Ternary2 launch");
@@ -185,11 +183,9 @@ void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, fl
         check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");
 }
 
-// Enqueue the Q8_K integer product: quantize positions rows into `q8k`, then the product.
-void enqueue_kint(const satori_hip_matrix* m, const float* x, int positions, float* y, uint8_t* q8k,
-                  hipStream_t stream) {
-    check_hip(launch_q8k_quantize(x, m->shape.columns, positions, q8k, stream), "Q8_K launch");
-    MatDesc d{m->payload, nullptr, q8k, y, m->shape.rows, 0};
+// Enqueue the Q8_K integer product (the kernel quantizes the activations itself).
+void enqueue_kint(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
+    MatDesc d{m->payload, x, y, m->shape.rows, 0};
     check_hip(launch_gemv_kint(d, nullptr, 1, launch_shape(m->shape, positions, m->shape.rows), stream),
               "integer gemv launch");
 }
@@ -362,15 +358,11 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     c->host_x.reserve(in_bytes);
     c->host_y.reserve(out_bytes);
     const bool integer = batch && is_k(s);
-    if (integer) {
-        check_kint_width(s);
-        c->q8k.reserve(static_cast<size_t>(positions) * s.blocks * kQ8KBlockBytes);
-    }
+    if (integer) check_kint_width(s);
     std::memcpy(c->host_x.ptr, input, in_bytes);
     check_hip(hipMemcpyAsync(c->x.ptr, c->host_x.ptr, in_bytes, hipMemcpyHostToDevice, c->stream), "input copy");
     if (integer)
-        enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr),
-                     static_cast<uint8_t*>(c->q8k.ptr), c->stream);
+        enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
     else
         enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
     check_hip(hipMemcpyAsync(c->host_y.ptr, c->y.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "output copy");
@@ -378,13 +370,11 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
 }
 
-// Enqueues one group's launches (Q8_K quantization of each distinct input, then the product) on `st`.
+// Enqueues one group's launch on `st`.
 void enqueue_group(satori_hip_group* g, hipStream_t st) {
     const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
     const MatDesc none{};
     if (g->quantized) {
-        for (size_t k = 0; k < g->inputs.size(); ++k)
-            check_hip(launch_q8k_quantize(g->inputs[k], g->shape.columns, 1, g->q8k[k], st), "Q8_K launch");
         check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
     } else if (g->shape.format == SATORI_HIP_TERNARY2) {
         check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
@@ -694,10 +684,7 @@ int satori_hip_matvec_batch_device(satori_hip_matrix* m, const float* input, int
         if (is_k(m->shape)) {
             if (positions > 256) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "At most 256 positions per call.");
             check_kint_width(m->shape);
-            // The workspace is shared by the context's calls; a caller's stream other than the context
-            // stream must be ordered with the context stream before the workspace is reused.
-            c->q8k.reserve(static_cast<size_t>(positions) * m->shape.blocks * kQ8KBlockBytes);
-            enqueue_kint(m, input, positions, output, static_cast<uint8_t*>(c->q8k.ptr), st);
+            enqueue_kint(m, input, positions, output, st);
         } else {
             enqueue_float(m, input, positions, output, st);
         }
@@ -781,7 +768,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
                     fail(SATORI_HIP_E_ARGUMENT, "Group members must share format, block size and column count.");
                 require(inputs[i], "inputs[i]");
                 require(outputs[i], "outputs[i]");
-                host[i] = MatDesc{matrices[i]->payload, inputs[i], nullptr, outputs[i], s.rows, 0};
+                host[i] = MatDesc{matrices[i]->payload, inputs[i], outputs[i], s.rows, 0};
                 g->rows_max = std::max(g->rows_max, s.rows);
             }
             g->shape = first;
@@ -791,29 +778,12 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
                 set_device(c);
                 g->scratch = allocate_t2_scratch(g->plan);
             }
-            if (g->quantized) {
-                check_kint_width(first);
-                set_device(c);
-                for (int i = 0; i < count; ++i) {
-                    size_t k = 0;
-                    while (k < g->inputs.size() && g->inputs[k] != inputs[i]) ++k;
-                    if (k == g->inputs.size()) {
-                        g->inputs.push_back(inputs[i]);
-                        uint8_t* buffer = nullptr;
-                        check_hip(hipMalloc(reinterpret_cast<void**>(&buffer),
-                                            static_cast<size_t>(first.blocks) * kQ8KBlockBytes),
-                                  "hipMalloc");
-                        g->q8k.push_back(buffer);
-                    }
-                    host[i].a = g->q8k[k];
-                }
-            }
+            if (g->quantized) check_kint_width(first);
             set_device(c);
             check_hip(hipMalloc(reinterpret_cast<void**>(&g->descriptors), sizeof(MatDesc) * count), "hipMalloc");
             check_hip(hipMemcpy(g->descriptors, host.data(), sizeof(MatDesc) * count, hipMemcpyHostToDevice),
                       "descriptor upload");
         } catch (...) {
-            for (uint8_t* b : g->q8k) (void)hipFree(b);
             if (g->descriptors) (void)hipFree(g->descriptors);
             if (g->scratch) (void)hipFree(g->scratch);
             delete g;
@@ -852,8 +822,6 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         }
         for (satori_hip_matrix* m : g->members) m->groups--;
         g->members.clear();
-        for (uint8_t* b : g->q8k) (void)hipFree(b);
-        g->q8k.clear();
         (void)hipFree(g->descriptors);
         g->descriptors = nullptr;
         if (g->scratch) (void)hipFree(g->scratch);
