@@ -160,6 +160,7 @@ def progress(message: str) -> None:
 
 def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     progress(f"{case.name}: {case.copies} copies x {case.payload_bytes} B")
+    warm_up(ctx, case.run_group, 0.25)
     group_ms = time_launches(ctx, events, case.run_group, steps, warmup)
     step_bytes = case.copies * case.payload_bytes
     out = {
@@ -358,7 +359,7 @@ def main() -> int:
             p, xb = make_ternary2(rows, columns, b)
             c = Case(ctx, f"ternary2-4096-b{b}", lambda: ctx.create_ternary2(rows, columns, b, p), p.size, rows,
                      columns, xb, False)
-            formats[c.name] = measure(ctx, events, c, max(20, args.steps // 4), 5, single=False)
+            formats[c.name] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
             c.close()
         for fmt, r, cc, quantized, label in (
                 (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
@@ -371,7 +372,7 @@ def main() -> int:
             data, xf = make_gguf(fmt, r, cc)
             shape = S.QuantizedMatrixShape(r, cc, fmt)
             c = Case(ctx, label, lambda: ctx.create(data, shape), data.size, r, cc, xf, quantized)
-            formats[label] = measure(ctx, events, c, max(20, args.steps // 4), 5, single=False)
+            formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
             c.close()
 
     decode = None

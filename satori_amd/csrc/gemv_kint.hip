@@ -312,11 +312,12 @@ int kint_max_blocks() { return static_cast<int>((64 * 1024) / ((kActDwords + kTi
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
                             hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
-    // Rows per workgroup: 64, halved (down to 16) while the grid has fewer than 512 workgroups, so the
-    // small projections of a decode step still spread over the chip.
+    // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and a
+    // workgroup keeps more than 128 (row, block) pairs, so the small projections of a decode step spread
+    // over the chip without each workgroup's activation quantization outweighing its share of the product.
     const int64_t members = static_cast<int64_t>(count) * s.positions;
     int tile = kTileRows;
-    while (tile > 16 && members * ((s.rows_max + tile - 1) / tile) < 512) tile /= 2;
+    while (tile > 4 && tile * s.blocks > 128 && members * ((s.rows_max + tile - 1) / tile) < 1024) tile /= 2;
     s.rows_per_wg = tile;
     dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
     const size_t lds = kint_lds_bytes(s.blocks);
