@@ -16,6 +16,8 @@ The same line carries, labelled:
   cache:     the grouped launch over G references to ONE copy (cache resident, not an HBM figure);
   decode_step: the 197 projections of one decode token of a Qwen-1.5B-shaped model (Q4_K/Q6_K on the Q8_K
              integer path, 1.03 GB per token), replayed as one graph; tokens/s and GB/s;
+  prefill:   the same model's projections over 512 positions (ExecuteBatch in 256-position chunks);
+             tokens/s and int8 TOP/s;
   roofline:  for the headline kernel, from HIP events on the launch stream;
   cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core.
 
@@ -181,52 +183,67 @@ def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     return out
 
 
-def decode_step(ctx, events, steps: int, warmup: int) -> dict:
-    """The projection sequence of one decode token of a Qwen-1.5B-shaped model (28 layers of q 1536x1536,
-    k and v 256x1536, o 1536x1536, gate and up 8960x1536 in Q4_K, down 1536x8960 in Q6_K, then the output
-    projection 151936x1536 in Q6_K: 197 projections, 1,027,772,928 payload bytes per token), every matrix a
-    distinct resident copy, on the Q8_K integer path at one position. Projections that share an input form
-    one group (q/k/v, gate/up); the 113 groups of a token are captured once as a graph (satori_hip_step) and
-    replayed. Attention, norms and SwiGLU are not part of the path: their outputs are fixed random vectors.
-    Also timed: the same groups launched eagerly, one call each."""
-    d, kv, ffn, vocab = 1536, 256, 8960, 151936
-    roles = {"q": (d, d, BQ.Q4_K), "k": (kv, d, BQ.Q4_K), "v": (kv, d, BQ.Q4_K), "o": (d, d, BQ.Q4_K),
-             "gate": (ffn, d, BQ.Q4_K), "up": (ffn, d, BQ.Q4_K), "down": (d, ffn, BQ.Q6_K)}
-    first = {}
-    for name, (r, c, fmt) in roles.items():
-        data, _ = make_gguf(fmt, r, c)
-        first[name] = ctx.create(data, S.QuantizedMatrixShape(r, c, fmt))
-    # Output projection: rows of a 4096-row random Q6_K matrix repeated to 151,936 rows (rows are
-    # independent byte ranges, so the payload is a valid matrix of that shape).
-    base, _ = make_gguf(BQ.Q6_K, 4096, d)
-    row_bytes = base.size // 4096
-    tiled = np.tile(base.reshape(4096, row_bytes), (-(-vocab // 4096), 1))[:vocab].reshape(-1)
-    output = ctx.create(tiled, S.QuantizedMatrixShape(vocab, d, BQ.Q6_K))
-    g = rng(2026)
-    buffers = []
+class DecodeModel:
+    """A Qwen-1.5B-shaped model's projections: 28 layers of q 1536x1536, k and v 256x1536, o 1536x1536, gate and
+    up 8960x1536 in Q4_K, down 1536x8960 in Q6_K, then the output projection 151936x1536 in Q6_K (197
+    projections, 1,027,772,928 payload bytes). Random-init weights, every matrix a distinct resident copy."""
 
-    def device(values):
-        p = ctx.alloc(values.nbytes)
-        ctx.upload(p, values)
-        buffers.append(p)
+    D, KV, FFN, VOCAB, LAYERS = 1536, 256, 8960, 151936, 28
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        d, kv, ffn, vocab = self.D, self.KV, self.FFN, self.VOCAB
+        self.roles = {"q": (d, d, BQ.Q4_K), "k": (kv, d, BQ.Q4_K), "v": (kv, d, BQ.Q4_K), "o": (d, d, BQ.Q4_K),
+                      "gate": (ffn, d, BQ.Q4_K), "up": (ffn, d, BQ.Q4_K), "down": (d, ffn, BQ.Q6_K)}
+        first = {}
+        for name, (r, c, fmt) in self.roles.items():
+            data, _ = make_gguf(fmt, r, c)
+            first[name] = ctx.create(data, S.QuantizedMatrixShape(r, c, fmt))
+        # Output projection: rows of a 4096-row random Q6_K matrix repeated to 151,936 rows (rows are
+        # independent byte ranges, so the payload is a valid matrix of that shape).
+        base, _ = make_gguf(BQ.Q6_K, 4096, d)
+        row_bytes = base.size // 4096
+        tiled = np.tile(base.reshape(4096, row_bytes), (-(-vocab // 4096), 1))[:vocab].reshape(-1)
+        self.output = ctx.create(tiled, S.QuantizedMatrixShape(vocab, d, BQ.Q6_K))
+        self.layers = [{name: (first[name] if layer == 0 else first[name].clone()) for name in self.roles}
+                       for layer in range(self.LAYERS)]
+        payload = sum(r * (c // 256) * (144 if fmt == BQ.Q4_K else 210) for r, c, fmt in self.roles.values())
+        self.token_bytes = self.LAYERS * payload + vocab * (d // 256) * 210
+        self.buffers = []
+
+    def device(self, values):
+        p = self.ctx.alloc(values.nbytes)
+        self.ctx.upload(p, values)
+        self.buffers.append(p)
         return p
 
-    h, attn, h2 = (device(g.standard_normal(d).astype(np.float32)) for _ in range(3))
-    act = device(g.standard_normal(ffn).astype(np.float32))
-    out = {name: device(np.zeros(r, np.float32)) for name, (r, _, _) in roles.items()}
-    logits = device(np.zeros(vocab, np.float32))
-    mats, groups = [], []
-    for layer in range(28):
-        m = {name: (first[name] if layer == 0 else first[name].clone()) for name in roles}
-        mats += list(m.values())
+    def close(self):
+        for layer in self.layers:
+            for m in layer.values():
+                m.dispose()
+        self.output.dispose()
+        for p in self.buffers:
+            self.ctx.free(p)
+
+
+def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int) -> dict:
+    """The projection sequence of one decode token (197 projections, batch 1) on the Q8_K integer path.
+    Projections that share an input form one group (q/k/v, gate/up); the 113 groups of a token are
+    captured once as a graph (satori_hip_step) and replayed. Attention, norms and SwiGLU are not part of
+    the path: their outputs are fixed random vectors. Also timed: the same groups launched eagerly."""
+    d, ffn, vocab = model.D, model.FFN, model.VOCAB
+    g = rng(2026)
+    h, attn, h2 = (model.device(g.standard_normal(d).astype(np.float32)) for _ in range(3))
+    act = model.device(g.standard_normal(ffn).astype(np.float32))
+    out = {name: model.device(np.zeros(r, np.float32)) for name, (r, _, _) in model.roles.items()}
+    logits = model.device(np.zeros(vocab, np.float32))
+    groups = []
+    for m in model.layers:
         groups.append(S.HipGroup(ctx, [m["q"], m["k"], m["v"]], [h] * 3, [out["q"], out["k"], out["v"]], True))
         groups.append(S.HipGroup(ctx, [m["o"]], [attn], [out["o"]], True))
         groups.append(S.HipGroup(ctx, [m["gate"], m["up"]], [h2] * 2, [out["gate"], out["up"]], True))
         groups.append(S.HipGroup(ctx, [m["down"]], [act], [out["down"]], True))
-    groups.append(S.HipGroup(ctx, [output], [h], [logits], True))
-    mats.append(output)
-    payload = sum(r * (c // 256) * (144 if fmt == BQ.Q4_K else 210) for r, c, fmt in roles.values())
-    token_bytes = 28 * payload + vocab * (d // 256) * 210
+    groups.append(S.HipGroup(ctx, [model.output], [h], [logits], True))
     step = S.HipStep(ctx, groups)
     warm_up(ctx, step.execute, 0.5)
     graph_ms = time_launches(ctx, events, step.execute, steps, warmup)
@@ -239,20 +256,52 @@ def decode_step(ctx, events, steps: int, warmup: int) -> dict:
     step.dispose()
     for grp in groups:
         grp.dispose()
-    for mat in mats:
-        mat.dispose()
-    for p in buffers:
-        ctx.free(p)
     return {
         "model": "Qwen-1.5B-shaped decode step, random-init Q4_K/Q6_K weights, batch 1",
         "projections_per_token": 28 * 7 + 1,
         "kernel_launches_per_token": len(groups),
-        "bytes_per_token": token_bytes,
+        "bytes_per_token": model.token_bytes,
         "us_per_token": graph_ms * 1e3,
         "tokens_per_s": 1e3 / graph_ms,
-        "gbs": token_bytes / (graph_ms * 1e-3) / 1e9,
-        "pct_hbm": 100.0 * token_bytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "gbs": model.token_bytes / (graph_ms * 1e-3) / 1e9,
+        "pct_hbm": 100.0 * model.token_bytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "eager_us_per_token": eager_ms * 1e3,
+    }
+
+
+def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions: int = 512) -> dict:
+    """The projections of a 512-token prefill: every layer projection over all positions through
+    ExecuteBatch in chunks of 256 positions (the reference's chunk, and the ABI's limit for K formats),
+    and the output projection for the last position only (DenseSession.cs:156-159). The FLOP-based rate
+    counts 2 int8 operations per weight per position."""
+    d, ffn = model.D, model.FFN
+    g = rng(2027)
+    h, attn, h2 = (model.device(g.standard_normal(positions * d).astype(np.float32)) for _ in range(3))
+    act = model.device(g.standard_normal(positions * ffn).astype(np.float32))
+    out = {name: model.device(np.zeros(positions * r, np.float32)) for name, (r, _, _) in model.roles.items()}
+    logits = model.device(np.zeros(model.VOCAB, np.float32))
+    inputs = {"q": h, "k": h, "v": h, "o": attn, "gate": h2, "up": h2, "down": act}
+    chunk = 256
+
+    def run():
+        for m in model.layers:
+            for name, mat in m.items():
+                r, c, _ = model.roles[name]
+                for p0 in range(0, positions, chunk):
+                    n = min(chunk, positions - p0)
+                    mat.execute_batch_device(inputs[name] + 4 * p0 * c, n, out[name] + 4 * p0 * r)
+        model.output.execute_batch_device(h + 4 * (positions - 1) * d, 1, logits)
+
+    run()
+    ms = time_launches(ctx, events, run, steps, warmup)
+    weights = sum(r * c for r, c, _ in model.roles.values()) * model.LAYERS
+    ops = 2.0 * weights * positions + 2.0 * model.VOCAB * d
+    return {
+        "positions": positions,
+        "ms": ms,
+        "tokens_per_s": positions / (ms * 1e-3),
+        "int8_tops": ops / (ms * 1e-3) / 1e12,
+        "pct_int8_peak": 100.0 * ops / (ms * 1e-3) / 5.0e15,
     }
 
 
@@ -375,10 +424,14 @@ def main() -> int:
             formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
             c.close()
 
-    decode = None
+    decode = pre = None
     if not args.quick:
         progress("decode step (197 projections per token)")
-        decode = decode_step(ctx, events, 50, 5)
+        model = DecodeModel(ctx)
+        decode = decode_step(ctx, events, model, 50, 5)
+        progress("prefill (512 positions)")
+        pre = prefill(ctx, events, model, 3, 1)
+        model.close()
 
     progress("cpu baseline")
     cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
@@ -420,6 +473,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_step": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode.items()}
                         if decode else None),
+        "prefill": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in pre.items()} if pre else None),
         "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in formats.items()},
     }
