@@ -106,18 +106,6 @@ constexpr int kTileRows = 64;
 constexpr int kCodeStride = 68;
 constexpr int kActDwords = kCodeStride + 1 + 8;  // codes, scale, group sums per block
 
-// Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) for sub-block j (0..7), from the dwords holding
-// scales[12] (head[1..3]). Both forms are computed from fixed dwords with a per-lane shift and one is
-// selected, so no register vector is indexed by a per-lane value.
-__device__ __forceinline__ void q4k_scale_min(int j, const u32x4& head, int& scale, int& min) {
-    const int shift = 8 * (j & 3);
-    const uint32_t a = head[1] >> shift, b = head[2] >> shift, c = head[3] >> shift;  // bytes j&3, 4+(j&3), 8+(j&3)
-    const int low_scale = static_cast<int>(a & 63), low_min = static_cast<int>(b & 63);
-    const int high_scale = static_cast<int>((c & 0xFu) | (((a >> 6) & 3u) << 4));
-    const int high_min = static_cast<int>(((c >> 4) & 0xFu) | (((b >> 6) & 3u) << 4));
-    scale = j < 4 ? low_scale : high_scale;
-    min = j < 4 ? low_min : high_min;
-}
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);

@@ -89,6 +89,7 @@ struct satori_hip_matrix {
     int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
+    satori::DeviceBuffer q8k;    // K formats: Q8_K activations of the last many-position product
     int groups = 0;              // live groups that launch this matrix
     bool live = true;
 };
@@ -183,11 +184,21 @@ void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, fl
         check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");
 }
 
-// Enqueue the Q8_K integer product (the kernel quantizes the activations itself).
-void enqueue_kint(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
-    MatDesc d{m->payload, x, y, m->shape.rows, 0};
-    check_hip(launch_gemv_kint(d, nullptr, 1, launch_shape(m->shape, positions, m->shape.rows), stream),
-              "integer gemv launch");
+// Enqueue the Q8_K integer product. Few positions: one kernel that quantizes the activations itself; many:
+// quantize all positions into the matrix's Q8_K buffer, then the matrix-core product (same outputs). The
+// buffer belongs to the matrix, so many-position executions of one matrix that overlap in time race.
+void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
+    const Shape& s = m->shape;
+    if (positions >= kmfma_min_positions()) {
+        m->q8k.reserve(static_cast<size_t>(positions) * s.blocks * kQ8KBlockBytes);
+        uint8_t* act = static_cast<uint8_t*>(m->q8k.ptr);
+        check_hip(launch_q8k_quantize(x, s.columns, positions, act, stream), "Q8_K launch");
+        check_hip(launch_gemv_kmfma(m->payload, s.format, act, y, s.rows, s.blocks, s.row_bytes, positions, stream),
+                  "matrix-core gemv launch");
+        return;
+    }
+    MatDesc d{m->payload, x, y, s.rows, 0};
+    check_hip(launch_gemv_kint(d, nullptr, 1, launch_shape(s, positions, s.rows), stream), "integer gemv launch");
 }
 
 void check_kint_width(const Shape& s) {
@@ -282,6 +293,7 @@ void allocate_matrix(satori_hip_matrix* m, int64_t device_bytes) {
 }
 
 void free_matrix(satori_hip_matrix* m) {
+    m->q8k.release();
     if (m->payload) (void)hipFree(m->payload);
     if (m->scratch) (void)hipFree(m->scratch);
     m->payload = nullptr;

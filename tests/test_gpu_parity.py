@@ -442,6 +442,34 @@ def test_k_integer_batch_multi_position_on_fixture_blocks(context, fmt, fixture)
         m.dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("rows,columns,positions", [(17, 512, 16), (129, 768, 37), (300, 1536, 64),
+                                                    (1536, 1536, 100), (8960, 1536, 256), (256, 8960, 65)])
+def test_k_matrix_core_batch_equals_per_position(context, fmt, rows, columns, positions):
+    # BatchedMatVecTests.cs:45-113: a batch equals its positions run one at a time. Sixteen positions and
+    # more take the matrix-core kernel, one position the single-position integer kernel (bit-exact against
+    # the oracle above), so the two must agree bit for bit. Ragged row and position counts, a zero
+    # position, a zero block inside a position and a position of large magnitude are included.
+    g = rng(7 + rows + columns + positions)
+    w = (g.standard_normal((rows, columns), dtype=np.float32) * 0.02).astype(np.float32)
+    x = g.standard_normal((positions, columns), dtype=np.float32)
+    x[1] = 0.0
+    x[2, 256:512] = 0.0
+    x[3] *= 1e20
+    data = S.quantize_weights(w, rows, columns, fmt)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.full(positions * rows, np.nan, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    single = np.zeros(rows, np.float32)
+    for p in range(positions):
+        m.execute_batch(x[p], 1, single)
+        assert np.array_equal(y[p * rows:(p + 1) * rows].view(np.uint32), single.view(np.uint32)), p
+    if rows * columns * positions <= 1536 * 1536 * 100:
+        expected = O.q_matvec_batch(data, rows, columns, int(fmt), x.reshape(-1), positions)
+        assert np.array_equal(y.view(np.uint32), expected.view(np.uint32))
+    m.dispose()
+
+
 @pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
 def test_legacy_batch_matches_per_position(context, fmt):
     # BatchedMatVecTests.cs:61-88 (float path): each position within 1e-5 * sum|w x| of the scalar product.
