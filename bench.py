@@ -367,6 +367,10 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline workload only, no other formats")
     ap.add_argument("--profile", action="store_true",
                     help="only the headline grouped launches (for rocprofv3 kernel statistics), no other timing")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="only the 512-position prefill (steps and warmup as given), for rocprofv3")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="only the decode step (steps and warmup as given), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the MatVec on a single MI355X "
@@ -375,6 +379,16 @@ def main() -> int:
 
     ctx = S.HipContext(0)
     events = HipEvents()
+
+    if args.profile_prefill or args.profile_decode:
+        model = DecodeModel(ctx)
+        if args.profile_prefill:
+            result = {"profile": "prefill", **prefill(ctx, events, model, args.steps, args.warmup)}
+        else:
+            result = {"profile": "decode step", **decode_step(ctx, events, model, args.steps, args.warmup)}
+        model.close()
+        print(json.dumps(result))
+        return 0
 
     rows = columns = 4096
     block = 128

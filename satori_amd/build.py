@@ -26,6 +26,9 @@ SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]
 HIP_ONLY = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             "-fno-gpu-rdc"]
+# Per-file additions. The matrix-core product consumes its MFMA results on the VALU: the VGPR form of the
+# MFMA instructions writes them where the VALU reads them (no accumulator-register copies).
+EXTRA = {"gemv_kmfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -39,7 +42,7 @@ def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
     path = os.path.join(CSRC, src)
     if src.endswith(".hip"):
-        cmd = [hipcc(), *HIP_ONLY, *COMMON, "-c", path, "-o", obj]
+        cmd = [hipcc(), *HIP_ONLY, *COMMON, *EXTRA.get(src, []), "-c", path, "-o", obj]
     else:
         cmd = [hipcc(), *COMMON, "-c", path, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -24,6 +24,8 @@ __device__ __forceinline__ uint32_t load4_a4(const uint8_t* p) {
     return *(const SATORI_GLOBAL uint32_t*)(p);
 }
 
+__device__ __forceinline__ uint64_t load8_a8(const uint8_t* p) { return *(const SATORI_GLOBAL uint64_t*)(p); }
+
 __device__ __forceinline__ float load_f32(const float* p) { return *(const SATORI_GLOBAL float*)(p); }
 
 // Non-temporal loads for data that one instruction reads exactly once per launch (the Ternary2 panel
@@ -39,6 +41,7 @@ __device__ __forceinline__ uint32_t stream4(const uint8_t* p) {
 }
 
 __device__ __forceinline__ void store_f32(float* p, float v) { *(SATORI_GLOBAL float*)(p) = v; }
+__device__ __forceinline__ void store_u32(uint32_t* p, uint32_t v) { *(SATORI_GLOBAL uint32_t*)(p) = v; }
 
 // N little-endian dwords starting at a 2-byte aligned address, assembled from N + 1 aligned dword loads
 // and v_alignbyte. Reads up to 4 bytes past p + 4N; every payload allocation carries slack for that.

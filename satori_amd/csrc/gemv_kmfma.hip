@@ -7,19 +7,24 @@
 // expression, added to the (row, position) sum in block order from +0, so the outputs equal the
 // single-position integer kernel's bit for bit.
 //
-// Orientation: the MFMA computes D = C x W^T with the positions' Q8_K codes as the first operand (M =
-// positions) and the weights' codes as the second (N = rows). Every output a lane holds then belongs to
-// the lane's own weight row, so the per-row block scales are lane-local. A workgroup (4 waves) owns 128
-// rows (32 per wave) and 64 positions (two 32-position MFMA tiles); blocks are walked in order with the
-// positions' codes for the current block staged in LDS.
+// Two launches. The pack kernel quantizes every (position, block) to Q8_K (the same bytes as the reference
+// quantizer) and stores the codes in the order the MFMA operands are read, with the block scales in a
+// separate array; the product kernel then needs no LDS and no barriers.
+//
+// Product orientation: D = C x W^T with the positions' codes as the first operand (M = 32 positions) and the
+// weights as the second (N = 32 rows). Lane l = 32h + r then holds the 16 outputs of row r at positions
+// 8(i/4) + 4h + i%4 (i = 0..15), so the per-row block scales are lane-local. One wave owns one 32-row x
+// 32-position tile and walks its blocks in order, loading block b+1 while it computes block b.
 //
 // Q4_K: Dot = sum_j s_j * D_j with D_j = sum over sub-block j (32 weights) of q * c: one 32x32x32 MFMA per
-// sub-block and an int32 multiply-add by s_j; Min = sum_j m_j * sum_j c is one more MFMA chain whose weight
+// sub-block and an int24 multiply-add by s_j; Min = sum_j m_j * sum_j c is an MFMA chain whose weight
 // operand is m_j repeated over the sub-block. Q6_K: Dot = sum_k sc_k * (D_k - 32 * sum_k c) over the 16
-// groups of 16 weights: one 32x32x16 MFMA per group and a multiply-add by sc_k; the centring term is an
-// MFMA chain whose weight operand is sc_k repeated over the group.
+// groups of 16 weights: one 32x32x16 MFMA per group and a multiply-add by sc_k; the centring sum is an
+// MFMA chain whose weight operand is sc_k repeated over the group. All magnitudes stay below 2^23 before
+// the int24 multiply (|D_j| <= 32 * 15 * 127, |D_k| <= 16 * 63 * 127) and below 2^31 after.
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "q8k_device.hpp"
 
 namespace satori {
 namespace {
@@ -27,11 +32,7 @@ namespace {
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
-constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerGroup = 4 * kRowsPerWave;  // rows per workgroup
-constexpr int kPositions = 64;                   // positions per workgroup (two MFMA tiles)
-constexpr int kCodeStride = 272;                 // bytes per staged position: 256 codes + 16 of padding
+constexpr int kTile = 32;      // rows and positions per wave tile
 
 __device__ __forceinline__ i32x16 mfma32(const i32x4& c, const i32x4& w, const i32x16& acc) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(c, w, acc, 0, 0, 0);
@@ -41,28 +42,89 @@ __device__ __forceinline__ i32x16 mfma16(long c, long w, const i32x16& acc) {
     return __builtin_amdgcn_mfma_i32_32x32x16_i8(c, w, acc, 0, 0, 0);
 }
 
-// The (row, block) data one lane needs: Q4_K head (d, dmin, scales) and its half of every 32-byte group of
-// nibbles.
-struct Q4KLane {
-    u32x4 head;
-    u32x4 qs[4];  // qs[32g + 16h, +16) for g = 0..3, h = the lane's half
+// Signed 24-bit multiply-add (v_mad_i32_i24): both factors must fit in 24 bits. The empty asm makes the
+// result opaque to the optimizer, so each dot sum stays a sequential chain (the compiler would otherwise
+// reassociate it into a tree of products that holds every MFMA result of the block in registers at once).
+// It emits no instruction: the multiply-add itself is compiled code, so the compiler inserts the wait
+// states a VALU read of an MFMA result needs.
+__device__ __forceinline__ int mad24(int a, int b, int c) {
+    int d = __mul24(a, b) + c;
+    asm volatile("" : "+v"(d));
+    return d;
+}
+
+// Packed activations. For block b and position tile t the 256 codes of the tile's 32 positions fill 8 KB
+// at (b * tiles + t) * 8192, split into `chunks` chunks of 256 / chunks codes (8 for Q4_K: the 32x32x32
+// operand, 16 for Q6_K: the 32x32x16 operand); chunk j's lane l = 32h + r holds the codes
+// j * (256 / chunks) + h * (128 / chunks) .. + 128 / chunks of position 32t + r, at byte l * (128 / chunks).
+// Scales: float at (b * tiles + t) * 32 + r. Positions past the last are zero codes and scale 0.
+__device__ __forceinline__ int64_t pack_code_offset(int b, int t, int tiles, int chunks, int k, int r) {
+    const int per = 256 / chunks, half = per / 2;
+    const int j = k / per, h = (k % per) / half;
+    return (static_cast<int64_t>(b) * tiles + t) * 8192 + j * (8192 / chunks) + (32 * h + r) * half + k % half;
+}
+
+// One wave per (position, block): four blocks of one position per workgroup.
+__global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict__ x, int columns, int positions,
+                                                         int tiles, int chunks, uint8_t* __restrict__ codes,
+                                                         float* __restrict__ scales) {
+    const int blocks = columns / 256;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= blocks) return;
+    const int lane = threadIdx.x & 63;
+    const int p = blockIdx.y;
+    const int t = p >> 5, r = p & 31;
+    Q8KLane q{0u, 0, 0.0f, true};
+    if (p < positions) {
+        float v[4];
+        q8k_load_values(x + static_cast<int64_t>(p) * columns + 256 * b, lane, v);
+        q = q8k_quantize_values(v, lane);
+    }
+    store_u32(reinterpret_cast<uint32_t*>(codes + pack_code_offset(b, t, tiles, chunks, 4 * lane, r)), q.packed);
+    if (lane == 0) store_f32(scales + (static_cast<int64_t>(b) * tiles + t) * 32 + r, q.scale);
+}
+
+// The data one lane needs for one block: the weights of its row (its k half of every chunk) and the codes
+// and scales of the tile's positions.
+struct Q4KRegs {
+    u32x4 head;   // d, dmin, packed 6-bit scales and mins
+    u32x4 qs[4];  // qs[32g + 16h, +16) for g = 0..3
+    i32x4 c[8];   // codes of sub-block j, this lane's half
+    f32x4 a[4];   // scales of positions 8q + 4h .. + 3
 };
 
-__device__ __forceinline__ void q4k_lane_load(const uint8_t* block, int h, Q4KLane& r) {
+struct Q6KRegs {
+    uint32_t qla[4][2], qlb[4][2], qh[4][2];  // this lane's 8 bytes of each quarter's arrays
+    u32x4 sc;                                 // quarter c's scale of form kk at byte 4c + kk
+    uint32_t dpair;                           // the FP16 d of this block (and its neighbour)
+    long c[16];                               // codes of group k, this lane's half
+    f32x4 a[4];
+};
+
+__device__ __forceinline__ void load_codes_scales(const uint8_t* ct, const float* st, i32x4 (&c)[8], f32x4 (&a)[4]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const u32x4 v = load16_a4(ct + 1024 * j);
+        c[j] = i32x4{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]), static_cast<int>(v[3])};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(st + 8 * q));
+        a[q] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+    }
+}
+
+__device__ __forceinline__ void load_block(const uint8_t* wrow, int b, int h, const uint8_t* ct, const float* st,
+                                           Q4KRegs& r) {
+    const uint8_t* block = wrow + static_cast<int64_t>(b) * 144;
     r.head = load16_a4(block);
 #pragma unroll
     for (int g = 0; g < 4; ++g) r.qs[g] = load16_a4(block + 16 + 32 * g + 16 * h);
+    load_codes_scales(ct, st, r.c, r.a);
 }
 
-// Q6_K from the regrouped device layout: the lane's half (8 bytes) of each quarter's ql / ql / qh arrays,
-// the quarter scales and d.
-struct Q6KLane {
-    uint32_t qla[4][2], qlb[4][2], qh[4][2];
-    u32x4 sc;  // quarter c's scale for form kk at byte 4c + kk
-    float d;
-};
-
-__device__ __forceinline__ void q6k_lane_load(const uint8_t* w, int64_t blocks, int64_t index, int h, Q6KLane& r) {
+__device__ __forceinline__ void load_block(const uint8_t* w, int64_t count, int64_t index, int h, const uint8_t* ct,
+                                           const float* st, Q6KRegs& r) {
     const uint8_t* record = w + index * 192;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -74,9 +136,17 @@ __device__ __forceinline__ void q6k_lane_load(const uint8_t* w, int64_t blocks, 
         r.qh[c][0] = load4_a4(q + 32);
         r.qh[c][1] = load4_a4(q + 36);
     }
-    r.sc = load16_a4(w + blocks * 192 + index * 16);
-    const uint32_t pair = load4_a4(w + blocks * 208 + (index & ~int64_t(1)) * 2);
-    r.d = half_bits_to_float(pair >> (16 * static_cast<int>(index & 1)));
+    r.sc = load16_a4(w + count * 192 + index * 16);
+    r.dpair = load4_a4(w + count * 208 + (index & ~int64_t(1)) * 2);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        r.c[k] = static_cast<long>(load8_a8(ct + 512 * k));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(st + 8 * q));
+        r.a[q] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+    }
 }
 
 __device__ __forceinline__ uint32_t q6k_form(uint32_t a, uint32_t b, uint32_t hb, int kk) {
@@ -88,153 +158,300 @@ __device__ __forceinline__ uint32_t q6k_form(uint32_t a, uint32_t b, uint32_t hb
     }
 }
 
-template <int FORMAT>
-__global__ __launch_bounds__(kThreads) void gemv_kmfma_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act,
-                                                             float* __restrict__ y, int rows, int blocks,
-                                                             int64_t row_bytes, int positions) {
-    __shared__ __attribute__((aligned(16))) uint8_t codes[kPositions * kCodeStride];
-    __shared__ float pscale[kPositions];
+// The block's FP32 terms of the lane's 16 (row, position) outputs. A zero activation block contributes +0
+// (the reference skips it, QuantizedKAvx2Kernel.cs:86; adding +0 is the same, since a sum that starts at +0
+// is never -0). The sub-block (group) products are software-pipelined: the MFMA of sub-block j + 1 is issued
+// before the results of j are scaled, and a scheduling barrier per step keeps the compiler from hoisting
+// every MFMA of the block (which would hold all their result tiles in registers at once).
+__device__ __forceinline__ i32x4 q4k_weights(const Q4KRegs& r, int j) {
+    const u32x4 raw = r.qs[j >> 1];
+    const int shift = 4 * (j & 1);
+    return i32x4{static_cast<int>((raw[0] >> shift) & 0x0F0F0F0Fu), static_cast<int>((raw[1] >> shift) & 0x0F0F0F0Fu),
+                 static_cast<int>((raw[2] >> shift) & 0x0F0F0F0Fu), static_cast<int>((raw[3] >> shift) & 0x0F0F0F0Fu)};
+}
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int h = lane >> 5;                                            // k half of the lane
-    const int row = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave + (lane & 31);
-    const bool row_live = row < rows;
-    const int row_c = row_live ? row : rows - 1;                        // dead rows read a live one
-    const int p0 = blockIdx.y * kPositions;
-
-    float acc[2][16];
+__device__ __forceinline__ void block_terms(const Q4KRegs& r, float (&term)[16]) {
+    const float d = half_bits_to_float(r.head[0] & 0xFFFFu), dmin = half_bits_to_float(r.head[0] >> 16);
+    int dot[16];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int i = 0; i < 16; ++i) dot[i] = 0;
+    i32x16 mins = {};
+    int sj, mj;
+    q4k_scale_min(0, r.head, sj, mj);
+    i32x16 cur = mfma32(r.c[0], q4k_weights(r, 0), i32x16{});
+    mins = mfma32(r.c[0], i32x4{mj * 0x01010101, mj * 0x01010101, mj * 0x01010101, mj * 0x01010101}, mins);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
-
-    for (int b = 0; b < blocks; ++b) {
-        // Stage the 64 positions' codes and scales of block b (zero past the last position).
-        __syncthreads();  // the previous block's codes are no longer read
-        for (int i = threadIdx.x; i < kPositions * 16; i += kThreads) {
-            const int p = i >> 4, part = i & 15;
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (p0 + p < positions)
-                v = load16_a4(act + (static_cast<int64_t>(p0 + p) * blocks + b) * kQ8KBlockBytes + 4 + 16 * part);
-            *reinterpret_cast<u32x4*>(codes + p * kCodeStride + 16 * part) = v;
+    for (int j = 0; j < 8; ++j) {
+        i32x16 next;
+        int sn = 0, mn = 0;
+        if (j + 1 < 8) {
+            q4k_scale_min(j + 1, r.head, sn, mn);
+            next = mfma32(r.c[j + 1], q4k_weights(r, j + 1), i32x16{});
+            mins = mfma32(r.c[j + 1], i32x4{mn * 0x01010101, mn * 0x01010101, mn * 0x01010101, mn * 0x01010101}, mins);
         }
-        if (threadIdx.x < kPositions) {
-            const int p = threadIdx.x;
-            pscale[p] = p0 + p < positions
-                            ? load_f32(reinterpret_cast<const float*>(act + (static_cast<int64_t>(p0 + p) * blocks + b) *
-                                                                                kQ8KBlockBytes))
-                            : 0.0f;
-        }
-        // This lane's weights for block b, then each 32-position tile in turn: integer dot and min (Q4_K) or
-        // centring (Q6_K) sums for the block, and the block's FP32 term added in block order.
-        if constexpr (FORMAT == kQ4_K) {
-            Q4KLane r;
-            q4k_lane_load(w + row_c * row_bytes + static_cast<int64_t>(b) * 144, h, r);
-            const float d = half_bits_to_float(r.head[0] & 0xFFFFu), dmin = half_bits_to_float(r.head[0] >> 16);
-            __syncthreads();  // codes staged
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                int dot[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) dot[i] = 0;
-                i32x16 mins = {};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    int sj, mj;
-                    q4k_scale_min(j, r.head, sj, mj);
-                    const u32x4 raw = r.qs[j >> 1];
-                    const i32x4 wq = {static_cast<int>((raw[0] >> (4 * (j & 1))) & 0x0F0F0F0Fu),
-                                      static_cast<int>((raw[1] >> (4 * (j & 1))) & 0x0F0F0F0Fu),
-                                      static_cast<int>((raw[2] >> (4 * (j & 1))) & 0x0F0F0F0Fu),
-                                      static_cast<int>((raw[3] >> (4 * (j & 1))) & 0x0F0F0F0Fu)};
-                    const int mb = mj * 0x01010101;
-                    const i32x4 wm = {mb, mb, mb, mb};
-                    const i32x4 c = *reinterpret_cast<const i32x4*>(codes + (32 * t + (lane & 31)) * kCodeStride +
-                                                                   32 * j + 16 * h);
-                    const i32x16 dj = mfma32(c, wq, i32x16{});
-                    mins = mfma32(c, wm, mins);
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) dot[i] += sj * dj[i];
-                }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float a = pscale[32 * t + 8 * (i >> 2) + 4 * h + (i & 3)];
-                    if (a == 0.0f) continue;  // zero activation block: skipped (QuantizedKAvx2Kernel.cs:86)
-                    const float dA = __fmul_rn(d, a), dminA = __fmul_rn(dmin, a);
-                    const float term = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot[i])),
-                                                 __fmul_rn(dminA, static_cast<float>(mins[i])));
-                    acc[t][i] = __fadd_rn(acc[t][i], term);
-                }
-            }
-        } else {
-            Q6KLane r;
-            q6k_lane_load(w, static_cast<int64_t>(rows) * blocks, static_cast<int64_t>(row_c) * blocks + b, h, r);
-            __syncthreads();  // codes staged
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                int dot[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) dot[i] = 0;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {  // scale group k: weights 16k .. 16k + 15 of the block
-                    const int c = 2 * (k >> 3) + (k & 1), kk = (k & 7) >> 1;
-                    const int sc = static_cast<int8_t>(r.sc[c] >> (8 * kk));
-                    const long wq = static_cast<long>(q6k_form(r.qla[c][0], r.qlb[c][0], r.qh[c][0], kk)) |
-                                    (static_cast<long>(q6k_form(r.qla[c][1], r.qlb[c][1], r.qh[c][1], kk)) << 32);
-                    const long cd = *reinterpret_cast<const long*>(codes + (32 * t + (lane & 31)) * kCodeStride +
-                                                                   16 * k + 8 * h);
-                    const i32x16 dk = mfma16(cd, wq, i32x16{});
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) dot[i] += sc * dk[i];
-                }
-                // Centring: sum_k sc_k * (sum of group k's codes), one chain over the block's 32-weight chunks;
-                // the lane's 16 weights of chunk u are group 2u + h.
-                i32x16 cent = {};
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int k = 2 * u + h;
-                    const int c = 2 * (k >> 3) + (k & 1), kk = (k & 7) >> 1;
-                    const int sb = static_cast<int>(static_cast<uint8_t>(r.sc[c] >> (8 * kk))) * 0x01010101;
-                    const i32x4 ws = {sb, sb, sb, sb};
-                    const i32x4 cq = *reinterpret_cast<const i32x4*>(codes + (32 * t + (lane & 31)) * kCodeStride +
-                                                                    32 * u + 16 * h);
-                    cent = mfma32(cq, ws, cent);
-                }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float a = pscale[32 * t + 8 * (i >> 2) + 4 * h + (i & 3)];
-                    if (a == 0.0f) continue;  // zero activation block: skipped
-                    // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32.
-                    const float term = __fmul_rn(__fmul_rn(a, r.d), static_cast<float>(dot[i] - 32 * cent[i]));
-                    acc[t][i] = __fadd_rn(acc[t][i], term);
-                }
-            }
+        for (int i = 0; i < 16; ++i) dot[i] = mad24(sj, cur[i], dot[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + 1 < 8) {
+            cur = next;
+            sj = sn;
         }
     }
-    if (!row_live) return;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int i = 0; i < 16; ++i) {
+        const float a = r.a[i >> 2][i & 3];
+        const float dA = __fmul_rn(d, a), dminA = __fmul_rn(dmin, a);
+        const float t = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot[i])), __fmul_rn(dminA, static_cast<float>(mins[i])));
+        term[i] = a != 0.0f ? t : 0.0f;
+    }
+}
+
+__device__ __forceinline__ long q6k_weights(const Q6KRegs& r, int k, int& sc, long& sb) {
+    const int c = 2 * (k >> 3) + (k & 1), kk = (k & 7) >> 1;
+    sc = static_cast<int8_t>(r.sc[c] >> (8 * kk));
+    const uint32_t b = static_cast<uint32_t>(static_cast<uint8_t>(r.sc[c] >> (8 * kk))) * 0x01010101u;
+    sb = static_cast<long>(b) | (static_cast<long>(b) << 32);
+    return static_cast<long>(q6k_form(r.qla[c][0], r.qlb[c][0], r.qh[c][0], kk)) |
+           (static_cast<long>(q6k_form(r.qla[c][1], r.qlb[c][1], r.qh[c][1], kk)) << 32);
+}
+
+__device__ __forceinline__ void block_terms(const Q6KRegs& r, float (&term)[16], int64_t index) {
+    const float d = half_bits_to_float(r.dpair >> (16 * static_cast<int>(index & 1)));
+    int dot[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int p = p0 + 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (p < positions) store_f32(y + static_cast<int64_t>(p) * rows + row, acc[t][i]);
+    for (int i = 0; i < 16; ++i) dot[i] = 0;
+    i32x16 cent = {};
+    int sc;
+    long sb;
+    long wq = q6k_weights(r, 0, sc, sb);
+    i32x16 cur = mfma16(r.c[0], wq, i32x16{});
+    cent = mfma16(r.c[0], sb, cent);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {  // group k: weights 16k .. 16k + 15 of the block
+        i32x16 next;
+        int sn = 0;
+        if (k + 1 < 16) {
+            long sbn;
+            const long wn = q6k_weights(r, k + 1, sn, sbn);
+            next = mfma16(r.c[k + 1], wn, i32x16{});
+            cent = mfma16(r.c[k + 1], sbn, cent);
         }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dot[i] = mad24(sc, cur[i], dot[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + 1 < 16) {
+            cur = next;
+            sc = sn;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float a = r.a[i >> 2][i & 3];
+        // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32.
+        const float t = __fmul_rn(__fmul_rn(a, d), static_cast<float>(dot[i] - 32 * cent[i]));
+        term[i] = a != 0.0f ? t : 0.0f;
+    }
+}
+
+// Blocks of one row tile are split over S waves ("ways"): way w computes blocks w, w + S, ... and, per round
+// of S blocks, hands its 16 terms per lane to the others through LDS; the wave that owns an output adds the
+// round's S terms in block order, so every (row, position) sum is formed exactly as the sequential one.
+// A workgroup holds R row tiles x S ways (R = 4 / S, or 1 for S = 3) of one position tile.
+template <int S>
+struct Split {
+    static constexpr int R = S == 3 ? 1 : 4 / S;
+    static constexpr int kWaves = R * S;
+    static constexpr int kOwned = (16 + S - 1) / S;  // outputs per lane each way adds up (the last way fewer)
+};
+
+__device__ __forceinline__ int owned_begin(int way, int S) { return way * ((16 + S - 1) / S); }
+__device__ __forceinline__ int owned_end(int way, int S) {
+    const int e = (way + 1) * ((16 + S - 1) / S);
+    return e < 16 ? e : 16;
+}
+
+// Workgroup u of the padded grid: consecutive units (row groups x position tiles, position tiles fastest)
+// go to one XCD (workgroup ids are dealt to the 8 XCDs round-robin), so the position tiles that share a row
+// group's weights share that XCD's L2.
+template <int FORMAT, int S>
+__global__ __launch_bounds__(64 * Split<S>::kWaves) void kmfma_kernel(const uint8_t* __restrict__ w,
+                                                                     const uint8_t* __restrict__ codes,
+                                                                     const float* __restrict__ scales,
+                                                                     float* __restrict__ y, int rows, int blocks,
+                                                                     int64_t row_bytes, int positions, int tiles,
+                                                                     int units) {
+    using SP = Split<S>;
+    // Terms of one round: [row tile][way][quad q][lane] as float4 (conflict-free 16-byte accesses), twice.
+    __shared__ f32x4 exchange[S > 1 ? 2 * SP::R * S * 4 * 64 : 1];
+
+    const int per_xcd = gridDim.x >> 3;
+    const int u = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (u >= units) return;  // whole workgroup
+    const int group = u / tiles, t = u - group * tiles;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int way = wave % S, rt = wave / S;
+    const int h = lane >> 5;
+    const int row = (group * SP::R + rt) * kTile + (lane & 31);
+    const int row_c = row < rows ? row : rows - 1;  // rows past the last compute on a live row, store nothing
+    const int64_t tile_bytes = static_cast<int64_t>(tiles) * 8192;
+    const int chunk_bytes = FORMAT == kQ4_K ? 16 : 8;
+    const uint8_t* ct = codes + static_cast<int64_t>(t) * 8192 + lane * chunk_bytes;
+    const float* st = scales + t * 32 + 4 * h;
+    const int rounds = (blocks + S - 1) / S;
+
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+    // Adds one round's terms: directly for S = 1, else through the exchange buffer.
+    auto add_round = [&](const float (&term)[16], int round) {
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = __fadd_rn(acc[i], term[i]);
+        } else {
+            f32x4* buf = exchange + (round & 1) * (SP::R * S * 4 * 64) + rt * (S * 4 * 64);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                buf[(way * 4 + q) * 64 + lane] = f32x4{term[4 * q], term[4 * q + 1], term[4 * q + 2], term[4 * q + 3]};
+            __syncthreads();
+            // Way `way` adds outputs [owned_begin, owned_end) of every lane: the round's terms in block order.
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (4 * q + 3 < owned_begin(way, S) || 4 * q >= owned_end(way, S)) continue;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) {
+                    const f32x4 v = buf[(s2 * 4 + q) * 64 + lane];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * q + e >= owned_begin(way, S) && 4 * q + e < owned_end(way, S))
+                            acc[4 * q + e] = __fadd_rn(acc[4 * q + e], v[e]);
+                }
+            }
+        }
+    };
+
+    float term[16];
+    if constexpr (FORMAT == kQ4_K) {
+        const uint8_t* wrow = w + row_c * row_bytes;
+        auto load = [&](int b, Q4KRegs& r) {
+            if (b < blocks) load_block(wrow, b, h, ct + b * tile_bytes, st + b * tiles * 32, r);
+        };
+        auto terms = [&](int b, const Q4KRegs& r) {
+            if (b < blocks) {
+                block_terms(r, term);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) term[i] = 0.0f;
+            }
+        };
+        Q4KRegs ra, rb;
+        load(way, ra);
+        int k = 0;
+        for (; k + 1 < rounds; k += 2) {
+            load(way + (k + 1) * S, rb);
+            terms(way + k * S, ra);
+            add_round(term, k);
+            load(way + (k + 2) * S, ra);
+            terms(way + (k + 1) * S, rb);
+            add_round(term, k + 1);
+        }
+        if (k < rounds) {
+            terms(way + k * S, ra);
+            add_round(term, k);
+        }
+    } else {
+        const int64_t count = static_cast<int64_t>(rows) * blocks;
+        const int64_t base = static_cast<int64_t>(row_c) * blocks;
+        auto load = [&](int b, Q6KRegs& r) {
+            if (b < blocks) load_block(w, count, base + b, h, ct + b * tile_bytes, st + b * tiles * 32, r);
+        };
+        auto terms = [&](int b, const Q6KRegs& r) {
+            if (b < blocks) {
+                block_terms(r, term, base + b);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) term[i] = 0.0f;
+            }
+        };
+        Q6KRegs ra, rb;
+        load(way, ra);
+        int k = 0;
+        for (; k + 1 < rounds; k += 2) {
+            load(way + (k + 1) * S, rb);
+            terms(way + k * S, ra);
+            add_round(term, k);
+            load(way + (k + 2) * S, ra);
+            terms(way + (k + 1) * S, rb);
+            add_round(term, k + 1);
+        }
+        if (k < rounds) {
+            terms(way + k * S, ra);
+            add_round(term, k);
+        }
+    }
+    if (row >= rows) return;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (i < owned_begin(way, S) || i >= owned_end(way, S)) continue;
+        const int p = t * kTile + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (p < positions) store_f32(y + static_cast<int64_t>(p) * rows + row, acc[i]);
+    }
+}
+
+template <int FORMAT, int S>
+void launch_split(const uint8_t* w, const uint8_t* codes, const float* scales, float* y, int rows, int blocks,
+                  int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
+    const int groups = (rows + Split<S>::R * kTile - 1) / (Split<S>::R * kTile);
+    const int units = groups * tiles;
+    const int grid = (units + 7) / 8 * 8;
+    kmfma_kernel<FORMAT, S><<<grid, 64 * Split<S>::kWaves, 0, stream>>>(w, codes, scales, y, rows, blocks, row_bytes,
+                                                                         positions, tiles, units);
+}
+
+// Ways per row tile: enough waves for about two per SIMD (2048), at most 4 and at most the block count, and
+// no more ways than shorten the chain of rounds.
+int choose_split(int rows, int blocks, int tiles) {
+    const long wave_tiles = static_cast<long>((rows + kTile - 1) / kTile) * tiles;
+    int s = 1;
+    while (s < 4 && s < blocks && wave_tiles * s < 2048) ++s;
+    while (s > 1 && (blocks + s - 1) / s == (blocks + s - 2) / (s - 1)) --s;
+    return s;
+}
+
+template <int FORMAT>
+void launch_format(const uint8_t* w, const uint8_t* codes, const float* scales, float* y, int rows, int blocks,
+                   int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
+    switch (choose_split(rows, blocks, tiles)) {
+        case 1: launch_split<FORMAT, 1>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+        case 2: launch_split<FORMAT, 2>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+        case 3: launch_split<FORMAT, 3>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+        default: launch_split<FORMAT, 4>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+    }
 }
 
 }  // namespace
 
 int kmfma_min_positions() { return 16; }
 
-hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const uint8_t* act, float* y, int rows, int blocks,
-                             int64_t row_bytes, int positions, hipStream_t stream) {
-    if (rows <= 0 || positions <= 0) return hipSuccess;
-    const dim3 grid((rows + kRowsPerGroup - 1) / kRowsPerGroup, (positions + kPositions - 1) / kPositions);
+size_t kmfma_workspace_bytes(int blocks, int positions) {
+    const size_t tiles = (static_cast<size_t>(positions) + kTile - 1) / kTile;
+    return static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float));
+}
+
+hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
+                             int blocks, int64_t row_bytes, int positions, hipStream_t stream) {
+    if (rows <= 0 || positions <= 0 || blocks <= 0) return hipSuccess;
+    if (format != kQ4_K && format != kQ6_K) return hipErrorInvalidValue;
+    const int tiles = (positions + kTile - 1) / kTile;
+    uint8_t* codes = workspace;
+    float* scales = reinterpret_cast<float*>(workspace + static_cast<size_t>(blocks) * tiles * 8192);
+    const int chunks = format == kQ4_K ? 8 : 16;
+    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile), 256, 0, stream>>>(x, blocks * 256, positions, tiles,
+                                                                                  chunks, codes, scales);
     if (format == kQ4_K)
-        gemv_kmfma_kernel<kQ4_K><<<grid, kThreads, 0, stream>>>(w, act, y, rows, blocks, row_bytes, positions);
-    else if (format == kQ6_K)
-        gemv_kmfma_kernel<kQ6_K><<<grid, kThreads, 0, stream>>>(w, act, y, rows, blocks, row_bytes, positions);
+        launch_format<kQ4_K>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream);
     else
-        return hipErrorInvalidValue;
+        launch_format<kQ6_K>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream);
     return hipGetLastError();
 }
 

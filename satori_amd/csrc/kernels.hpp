@@ -124,11 +124,12 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape,
                             hipStream_t stream);
 
-// Integer K-format product (Q4_K or Q6_K) over `positions` positions on the matrix cores, against Q8_K
-// activations already quantized ([positions][blocks][292] bytes at `act`); outputs bit-exact with
-// launch_gemv_kint's. Used from kmfma_min_positions() positions on.
-hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const uint8_t* act, float* y, int rows, int blocks,
-                             int64_t row_bytes, int positions, hipStream_t stream);
+// Integer K-format product (Q4_K or Q6_K) over `positions` positions on the matrix cores: quantizes the FP32
+// activations x ([positions][blocks * 256]) to Q8_K into `workspace` (kmfma_workspace_bytes), then the
+// product; outputs bit-exact with launch_gemv_kint's. Used from kmfma_min_positions() positions on.
+hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
+                             int blocks, int64_t row_bytes, int positions, hipStream_t stream);
+size_t kmfma_workspace_bytes(int blocks, int positions);
 int kmfma_min_positions();
 
 // Widest row, in Q8_K blocks, the integer product accepts (its LDS holds the staged activation row and the

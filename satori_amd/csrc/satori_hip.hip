@@ -190,10 +190,9 @@ void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, fl
 void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
     const Shape& s = m->shape;
     if (positions >= kmfma_min_positions()) {
-        m->q8k.reserve(static_cast<size_t>(positions) * s.blocks * kQ8KBlockBytes);
-        uint8_t* act = static_cast<uint8_t*>(m->q8k.ptr);
-        check_hip(launch_q8k_quantize(x, s.columns, positions, act, stream), "Q8_K launch");
-        check_hip(launch_gemv_kmfma(m->payload, s.format, act, y, s.rows, s.blocks, s.row_bytes, positions, stream),
+        m->q8k.reserve(kmfma_workspace_bytes(s.blocks, positions));
+        check_hip(launch_gemv_kmfma(m->payload, s.format, x, static_cast<uint8_t*>(m->q8k.ptr), y, s.rows, s.blocks,
+                                    s.row_bytes, positions, stream),
                   "matrix-core gemv launch");
         return;
     }
