@@ -28,12 +28,13 @@
 extern "C" {
 #endif
 
-#define SATORI_HIP_ABI_VERSION 2
+#define SATORI_HIP_ABI_VERSION 3
 
 typedef struct satori_hip_context satori_hip_context;
 typedef struct satori_hip_matrix satori_hip_matrix;
 typedef struct satori_hip_group satori_hip_group;
 typedef struct satori_hip_step satori_hip_step;
+typedef struct satori_hip_gguf satori_hip_gguf;
 
 typedef enum satori_hip_status {
     SATORI_HIP_OK = 0,
@@ -46,7 +47,9 @@ typedef enum satori_hip_status {
     SATORI_HIP_E_OUT_OF_MEMORY = 7,            /* System.OutOfMemoryException */
     SATORI_HIP_E_DEVICE = 8,                   /* System.InvalidOperationException: HIP runtime failure */
     SATORI_HIP_E_OVERFLOW = 9,                 /* System.OverflowException (checked arithmetic) */
-    SATORI_HIP_E_ARGUMENT_NULL = 10            /* System.ArgumentNullException */
+    SATORI_HIP_E_ARGUMENT_NULL = 10,           /* System.ArgumentNullException */
+    SATORI_HIP_E_KEY_NOT_FOUND = 11,           /* System.Collections.Generic.KeyNotFoundException */
+    SATORI_HIP_E_INVALID_OPERATION = 12        /* System.InvalidOperationException (misuse, not the device) */
 } satori_hip_status;
 
 /* Values of Satori.Core.BlockQuantization (src/Satori.Core/BlockQuantization.cs:3), plus Ternary2. */
@@ -203,6 +206,48 @@ int satori_hip_ternary2_quantize(const float* weights, int rows, int columns, in
  * its decoders (Q4KCodec.GetScaleMin, Q4KCodec.DecodeBlock, Q6KCodec.DecodeBlock). */
 int satori_hip_quantize_weights(int format, const float* weights, int rows, int columns, void* payload,
                                 size_t payload_length);
+
+/* ---- GGUF containers (src/Satori.Formats.Gguf) ----
+ * A GGUF v3 file mapped read-only and its catalogue parsed strictly, with the reference's limits and
+ * failure kinds: GgufFile(path) and GgufFile.Parse (src/Satori.Formats.Gguf/GgufFile.cs:17-35, 78-176),
+ * GgufCursor (src/Satori.Formats.Gguf/GgufCursor.cs:7-56). Corrupt structure fails with
+ * SATORI_HIP_E_INVALID_DATA, files outside the supported profile with SATORI_HIP_E_NOT_SUPPORTED. A file
+ * handle needs no context; after close, calls on it fail with SATORI_HIP_E_OBJECT_DISPOSED. Names and
+ * keys returned by the info calls, and windows, stay valid until the file is closed. */
+int satori_hip_gguf_open(const char* path, satori_hip_gguf** file);
+/* GgufFile.Dispose: idempotent; NULL is accepted. */
+int satori_hip_gguf_close(satori_hip_gguf* file);
+/* GgufFile.DataOffset. */
+int satori_hip_gguf_data_offset(const satori_hip_gguf* file, int64_t* offset);
+/* GgufFile.Tensors: count, lookup by name (SATORI_HIP_E_KEY_NOT_FOUND when absent) and the GgufTensor
+ * record of entry `index` in declaration order (src/Satori.Formats.Gguf/GgufTensor.cs:5-20): dims[0] is
+ * the contiguous dimension; offset is absolute in the file. Any out pointer may be NULL. */
+int satori_hip_gguf_tensor_count(const satori_hip_gguf* file, int64_t* count);
+int satori_hip_gguf_tensor_find(const satori_hip_gguf* file, const char* name, int64_t* index);
+int satori_hip_gguf_tensor_info(const satori_hip_gguf* file, int64_t index, const char** name, int* rank,
+                                int64_t dims[4], uint32_t* type, int64_t* offset, int64_t* byte_length);
+/* GgufFile.ReadTensor (src/Satori.Formats.Gguf/GgufFile.cs:42-49): the window [offset, offset + length) of
+ * the tensor's payload, zero-copy. A window beyond the payload fails with
+ * SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE. */
+int satori_hip_gguf_tensor_window(const satori_hip_gguf* file, int64_t index, int64_t offset, int64_t length,
+                                  const void** bytes);
+/* GgufFile.Metadata: count, lookup by key, and the GgufMetadata record
+ * (src/Satori.Formats.Gguf/GgufMetadata.cs:3-4); element_type and element_count are -1 for scalars. */
+int satori_hip_gguf_metadata_count(const satori_hip_gguf* file, int64_t* count);
+int satori_hip_gguf_metadata_find(const satori_hip_gguf* file, const char* key, int64_t* index);
+int satori_hip_gguf_metadata_info(const satori_hip_gguf* file, int64_t index, const char** key, uint32_t* type,
+                                  int64_t* offset, int64_t* byte_length, int64_t* element_type,
+                                  int64_t* element_count);
+/* GgufFile.ReadMetadata (src/Satori.Formats.Gguf/GgufFile.cs:51-56): the value bytes of entry `index`
+ * (for strings the u64 length comes first, as in the file), zero-copy. */
+int satori_hip_gguf_metadata_window(const satori_hip_gguf* file, int64_t index, const void** bytes, int64_t* length);
+/* new GgufQuantizedMatrix(file, name) + CreateExecution (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:13-36):
+ * a rank-2 Q8_0 / Q4_0 / Q4_K / Q6_K tensor within Int32 limits (else SATORI_HIP_E_NOT_SUPPORTED) as
+ * rows = dims[1], columns = dims[0], uploaded from the mapping straight to a resident device matrix. The
+ * block-scale check of QuantizedMatVec.ValidatePayload (src/Satori.Core/QuantizedMatVec.cs:28-42) runs on
+ * the device over the uploaded copy; a non-finite scale frees it and fails with SATORI_HIP_E_INVALID_DATA. */
+int satori_hip_gguf_matrix_create(satori_hip_context* context, const satori_hip_gguf* file, int64_t index,
+                                  satori_hip_matrix** matrix);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import ctypes
 import enum
+import os
 import threading
 
 import numpy as np
@@ -28,10 +29,11 @@ from . import _ffi
 __all__ = [
     "SatoriError", "ArgumentException", "ArgumentOutOfRangeException", "ArgumentNullException",
     "InvalidDataException", "NotSupportedException", "ObjectDisposedException", "PlatformNotSupportedException",
-    "OutOfMemoryException", "InvalidOperationException", "OverflowException",
+    "OutOfMemoryException", "InvalidOperationException", "OverflowException", "KeyNotFoundException",
     "BlockQuantization", "QuantizedMatrixShape", "Ternary2Matrix", "Ternary2MatVec", "MappedTernary2Matrix",
     "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "HipStep", "Q8KCodec", "TERNARY2",
     "device_count", "default_context", "payload_length", "quantize_weights",
+    "GgufFile", "GgufTensor", "GgufMetadata", "GgufQuantizedMatrix", "GgufWeightStore",
 ]
 
 TERNARY2 = 16
@@ -87,10 +89,18 @@ class ArgumentNullException(ArgumentException):
     status = 10
 
 
+class KeyNotFoundException(SatoriError, KeyError):
+    status = 11
+
+    def __str__(self) -> str:  # KeyError would quote the message
+        return self.message
+
+
 _BY_STATUS = {cls.status: cls for cls in (
     ArgumentException, ArgumentOutOfRangeException, InvalidDataException, NotSupportedException,
     ObjectDisposedException, PlatformNotSupportedException, OutOfMemoryException, InvalidOperationException,
-    OverflowException, ArgumentNullException)}
+    OverflowException, ArgumentNullException, KeyNotFoundException)}
+_BY_STATUS[12] = InvalidOperationException  # misuse (the device failure is status 8)
 
 
 def _check(status: int) -> None:
@@ -483,3 +493,206 @@ class Q8KCodec:
     @staticmethod
     def quantize_row(input, context: HipContext | None = None) -> np.ndarray:
         return (context or default_context()).quantize_q8k(input)
+
+
+# ---- GGUF containers (src/Satori.Formats.Gguf) ----
+
+class GgufTensor:
+    """src/Satori.Formats.Gguf/GgufTensor.cs:5-20: name, dimensions (dims[0] contiguous), type id, absolute
+    payload offset, payload byte length."""
+
+    __slots__ = ("name", "dimensions", "type", "offset", "byte_length")
+
+    def __init__(self, name, dimensions, type_, offset, byte_length):
+        self.name, self.dimensions, self.type = name, tuple(dimensions), type_
+        self.offset, self.byte_length = offset, byte_length
+
+    def __repr__(self) -> str:
+        return (f"GgufTensor({self.name!r}, dims={self.dimensions}, type={self.type}, offset={self.offset}, "
+                f"length={self.byte_length})")
+
+
+class GgufMetadata:
+    """src/Satori.Formats.Gguf/GgufMetadata.cs:3-4; element_type / element_count are None for scalars."""
+
+    __slots__ = ("key", "type", "offset", "byte_length", "element_type", "element_count")
+
+    def __init__(self, key, type_, offset, byte_length, element_type, element_count):
+        self.key, self.type, self.offset, self.byte_length = key, type_, offset, byte_length
+        self.element_type = None if element_type < 0 else element_type
+        self.element_count = None if element_count < 0 else element_count
+
+
+class GgufFile:
+    """src/Satori.Formats.Gguf/GgufFile.cs:10-207: a GGUF v3 file mapped read-only with its catalogue parsed
+    strictly by the library (limits and failure kinds of GgufFile.Parse); windows are read from the mapping."""
+
+    def __init__(self, path: str):
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_gguf_open(os.fsencode(path), ctypes.byref(handle)))
+        self._handle = handle
+        lib = _ffi.lib()
+        offset = ctypes.c_int64()
+        _check(lib.satori_hip_gguf_data_offset(handle, ctypes.byref(offset)))
+        self.data_offset = offset.value
+        count = ctypes.c_int64()
+        _check(lib.satori_hip_gguf_tensor_count(handle, ctypes.byref(count)))
+        self._index = {}
+        self.tensors = {}
+        for i in range(count.value):
+            name, rank, dims = ctypes.c_char_p(), ctypes.c_int(), (ctypes.c_int64 * 4)()
+            type_, off, length = ctypes.c_uint32(), ctypes.c_int64(), ctypes.c_int64()
+            _check(lib.satori_hip_gguf_tensor_info(handle, i, ctypes.byref(name), ctypes.byref(rank), dims,
+                                                   ctypes.byref(type_), ctypes.byref(off), ctypes.byref(length)))
+            key = name.value.decode("utf-8")
+            self._index[key] = i
+            self.tensors[key] = GgufTensor(key, dims[:rank.value], type_.value, off.value, length.value)
+        _check(lib.satori_hip_gguf_metadata_count(handle, ctypes.byref(count)))
+        self._meta_index = {}
+        self.metadata = {}
+        for i in range(count.value):
+            key, type_, off, length = ctypes.c_char_p(), ctypes.c_uint32(), ctypes.c_int64(), ctypes.c_int64()
+            et, ec = ctypes.c_int64(), ctypes.c_int64()
+            _check(lib.satori_hip_gguf_metadata_info(handle, i, ctypes.byref(key), ctypes.byref(type_),
+                                                     ctypes.byref(off), ctypes.byref(length), ctypes.byref(et),
+                                                     ctypes.byref(ec)))
+            k = key.value.decode("utf-8")
+            self._meta_index[k] = i
+            self.metadata[k] = GgufMetadata(k, type_.value, off.value, length.value, et.value, ec.value)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._handle
+
+    def tensor_index(self, name: str) -> int:
+        index = ctypes.c_int64()
+        _check(_ffi.lib().satori_hip_gguf_tensor_find(self._handle, name.encode("utf-8"), ctypes.byref(index)))
+        return index.value
+
+    def read_tensor(self, name: str, offset: int, length: int) -> bytes:
+        """GgufFile.ReadTensor (GgufFile.cs:42-49): a copy of the window [offset, offset + length)."""
+        index = self.tensor_index(name)
+        p = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_gguf_tensor_window(self._handle, index, offset, length, ctypes.byref(p)))
+        return ctypes.string_at(p.value, length) if length else b""
+
+    def read_metadata(self, key: str) -> bytes:
+        """GgufFile.ReadMetadata (GgufFile.cs:51-56): the value bytes as stored."""
+        index = ctypes.c_int64()
+        _check(_ffi.lib().satori_hip_gguf_metadata_find(self._handle, key.encode("utf-8"), ctypes.byref(index)))
+        p, n = ctypes.c_void_p(), ctypes.c_int64()
+        _check(_ffi.lib().satori_hip_gguf_metadata_window(self._handle, index.value, ctypes.byref(p), ctypes.byref(n)))
+        return ctypes.string_at(p.value, n.value) if n.value else b""
+
+    _SCALARS = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 10: "<Q", 11: "<q", 12: "<d"}
+
+    def read_scalar(self, key: str):
+        """GgufFile.ReadScalar (GgufFile.cs:58-76)."""
+        import struct
+        entry = self.metadata.get(key)
+        if entry is None:
+            self.read_metadata(key)  # raises KeyNotFoundException
+        if entry.type == 9:
+            raise InvalidOperationException("Use scoped access for arrays.")
+        raw = self.read_metadata(key)
+        if entry.type == 7:
+            return raw[0] != 0
+        if entry.type == 8:
+            return raw[8:].decode("utf-8")
+        return struct.unpack(self._SCALARS[entry.type], raw)[0]
+
+    def dispose(self) -> None:
+        _check(_ffi.lib().satori_hip_gguf_close(self._handle))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.dispose()
+
+
+_GGUF_FORMATS = {8: 0, 2: 1, 12: 2, 14: 3}  # GGUF type id -> BlockQuantization (GgufQuantizedMatrix.cs:20-26)
+
+
+class GgufQuantizedMatrix:
+    """src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:6-86: a rank-2 Q8_0/Q4_0/Q4_K/Q6_K tensor of a GgufFile.
+    The constructor applies the reference's checks (type, rank, Int32 limits, payload validation);
+    create_execution uploads it to a resident device matrix (block scales checked again on the device)."""
+
+    def __init__(self, file: GgufFile, name: str):
+        tensor = file.tensors[name] if name in file.tensors else None
+        if tensor is None:
+            file.tensor_index(name)  # raises KeyNotFoundException
+        dims = tensor.dimensions
+        if (tensor.type not in _GGUF_FORMATS or len(dims) != 2 or tensor.byte_length > 0x7FFFFFFF
+                or any(d > 0x7FFFFFFF for d in dims)):
+            raise NotSupportedException("MatVec requires a rank-2 Q8_0/Q4_0/Q4_K/Q6_K tensor within Int32 limits.")
+        self.shape = QuantizedMatrixShape(dims[1], dims[0], BlockQuantization(_GGUF_FORMATS[tensor.type]))
+        self.name = name
+        self._file = file
+        self._resident = None
+        QuantizedMatVec.validate_payload(file.read_tensor(name, 0, self.shape.byte_length), self.shape)
+
+    def create_execution(self, context: "HipContext | None" = None) -> "HipQuantizedMatrix":
+        """CreateExecution(factory) (GgufQuantizedMatrix.cs:31-36): a device copy owned by the caller."""
+        ctx = context or default_context()
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_gguf_matrix_create(ctx.handle, self._file.handle, self._file.tensor_index(self.name),
+                                                        ctypes.byref(handle)))
+        return HipQuantizedMatrix(ctx, handle)
+
+    def _device(self) -> "HipQuantizedMatrix":
+        if self._resident is None:
+            self._resident = self.create_execution()
+        return self._resident
+
+    def execute(self, input, output) -> None:
+        self._device().execute(input, output)
+
+    def execute_batch(self, input, positions: int, output, threads: int = 1) -> None:
+        if threads <= 0:
+            raise ArgumentOutOfRangeException("threads must be positive.")
+        self._device().execute_batch(input, positions, output)
+
+    def dispose(self) -> None:
+        if self._resident is not None:
+            self._resident.dispose()
+            self._resident = None
+
+
+class GgufWeightStore:
+    """src/Satori.Formats.Gguf/GgufWeightStore.cs:19-55, projection part: tensors of a GgufFile as resident
+    device matrices, created once per name on first use. The store borrows the file."""
+
+    def __init__(self, file: GgufFile, context: "HipContext | None" = None):
+        if file is None:
+            raise ArgumentNullException("Value cannot be null. (Parameter 'file')")
+        self._file = file
+        self._context = context
+        self._matrices = {}
+        self._lock = threading.Lock()
+
+    def has(self, name: str) -> bool:
+        return name in self._file.tensors
+
+    def matrix(self, name: str) -> "HipQuantizedMatrix":
+        with self._lock:
+            m = self._matrices.get(name)
+            if m is None:
+                m = GgufQuantizedMatrix(self._file, name).create_execution(self._context)
+                self._matrices[name] = m
+            return m
+
+    def project(self, name: str, input, output) -> None:
+        self.matrix(name).execute(input, output)
+
+    def project_batch(self, name: str, input, positions: int, output, threads: int = 1) -> None:
+        if threads <= 0:
+            raise ArgumentOutOfRangeException("threads must be positive.")
+        self.matrix(name).execute_batch(input, positions, output)
+
+    def dispose(self) -> None:
+        with self._lock:
+            for m in self._matrices.values():
+                m.dispose()
+            self._matrices.clear()

@@ -51,6 +51,23 @@ SIGNATURES = {
     "satori_hip_quantized_validate": (I, [I, I, I, P, SZ]),
     "satori_hip_ternary2_quantize": (I, [P, I, I, I, P, SZ]),
     "satori_hip_quantize_weights": (I, [I, P, I, I, P, SZ]),
+    "satori_hip_gguf_open": (I, [ctypes.c_char_p, PP]),
+    "satori_hip_gguf_close": (I, [P]),
+    "satori_hip_gguf_data_offset": (I, [P, ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_tensor_count": (I, [P, ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_tensor_find": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_tensor_info": (I, [P, ctypes.c_int64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(I),
+                                        ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint32),
+                                        ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_tensor_window": (I, [P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, PP]),
+    "satori_hip_gguf_metadata_count": (I, [P, ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_metadata_find": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_metadata_info": (I, [P, ctypes.c_int64, ctypes.POINTER(ctypes.c_char_p),
+                                          ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_int64),
+                                          ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
+                                          ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_metadata_window": (I, [P, ctypes.c_int64, PP, ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_gguf_matrix_create": (I, [P, P, ctypes.c_int64, PP]),
 }
 
 _lib = None

@@ -21,7 +21,8 @@ OUT = os.path.join(HERE, "libsatori_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
-SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "gemv_kmfma.hip", "host_cpu.cpp"]
+SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "gemv_kmfma.hip", "scale_check.hip",
+           "host_cpu.cpp", "gguf.cpp"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]
 HIP_ONLY = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -130,6 +130,10 @@ hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count,
 hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
                              int blocks, int64_t row_bytes, int positions, hipStream_t stream);
 size_t kmfma_workspace_bytes(int blocks, int positions);
+
+// Block-scale finiteness of an uploaded GGUF matrix (device layout; `blocks` = rows * blocks per row): a
+// non-zero *flag afterwards (the caller zeroes it first) means some block has a non-finite scale.
+hipError_t launch_scale_check(const uint8_t* payload, int64_t blocks, int format, uint32_t* flag, hipStream_t stream);
 int kmfma_min_positions();
 
 // Widest row, in Q8_K blocks, the integer product accepts (its LDS holds the staged activation row and the

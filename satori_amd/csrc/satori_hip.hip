@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/satori_hip.h"
+#include "gguf.hpp"
 #include "host_shapes.hpp"
 #include "kernels.hpp"
 
@@ -105,6 +106,11 @@ struct satori_hip_group {
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
     std::vector<satori_hip_matrix*> members;   // distinct member matrices (each counts this group)
     int steps = 0;                             // live steps that replay this group
+    bool live = true;
+};
+
+struct satori_hip_gguf {
+    satori::GgufFile* file = nullptr;  // null once closed (the handle stays as a tombstone)
     bool live = true;
 };
 
@@ -392,6 +398,24 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
     } else {
         check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
     }
+}
+
+const satori::GgufFile& live_file(const satori_hip_gguf* f) {
+    require(f, "file");
+    if (!f->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'GgufFile'.");
+    return *f->file;
+}
+
+const GgufTensorInfo& tensor_at(const GgufFile& file, int64_t index) {
+    if (index < 0 || index >= static_cast<int64_t>(file.tensors().size()))
+        fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Tensor index out of range. (Parameter 'index')");
+    return file.tensors()[static_cast<size_t>(index)];
+}
+
+const GgufMetadataInfo& metadata_at(const GgufFile& file, int64_t index) {
+    if (index < 0 || index >= static_cast<int64_t>(file.metadata().size()))
+        fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Metadata index out of range. (Parameter 'index')");
+    return file.metadata()[static_cast<size_t>(index)];
 }
 
 void require_live(const satori_hip_group* g) {
@@ -912,6 +936,177 @@ int satori_hip_step_destroy(satori_hip_step* s) {
         for (satori_hip_group* g : s->groups) g->steps--;
         s->groups.clear();
         s->live = false;
+    });
+}
+
+// ---- GGUF containers ----
+
+int satori_hip_gguf_open(const char* path, satori_hip_gguf** file) {
+    return guarded([&] {
+        require(file, "file");
+        *file = nullptr;
+        require(path, "path");
+        auto* parsed = new GgufFile(path);
+        *file = new satori_hip_gguf{parsed, true};
+    });
+}
+
+int satori_hip_gguf_close(satori_hip_gguf* file) {
+    return guarded([&] {
+        if (!file || !file->live) return;
+        delete file->file;
+        file->file = nullptr;
+        file->live = false;
+    });
+}
+
+int satori_hip_gguf_data_offset(const satori_hip_gguf* file, int64_t* offset) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        require(offset, "offset");
+        *offset = f.data_offset();
+    });
+}
+
+int satori_hip_gguf_tensor_count(const satori_hip_gguf* file, int64_t* count) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        require(count, "count");
+        *count = static_cast<int64_t>(f.tensors().size());
+    });
+}
+
+int satori_hip_gguf_tensor_find(const satori_hip_gguf* file, const char* name, int64_t* index) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        require(name, "name");
+        require(index, "index");
+        const int64_t k = f.find_tensor(name);
+        if (k < 0) fail(SATORI_HIP_E_KEY_NOT_FOUND, std::string("The given key '") + name + "' was not present in the dictionary.");
+        *index = k;
+    });
+}
+
+int satori_hip_gguf_tensor_info(const satori_hip_gguf* file, int64_t index, const char** name, int* rank,
+                                int64_t dims[4], uint32_t* type, int64_t* offset, int64_t* byte_length) {
+    return guarded([&] {
+        const GgufTensorInfo& t = tensor_at(live_file(file), index);
+        if (name) *name = t.name.c_str();
+        if (rank) *rank = t.rank;
+        if (dims)
+            for (int d = 0; d < 4; ++d) dims[d] = t.dims[d];
+        if (type) *type = t.type;
+        if (offset) *offset = t.offset;
+        if (byte_length) *byte_length = t.byte_length;
+    });
+}
+
+int satori_hip_gguf_tensor_window(const satori_hip_gguf* file, int64_t index, int64_t offset, int64_t length,
+                                  const void** bytes) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        const GgufTensorInfo& t = tensor_at(f, index);
+        require(bytes, "bytes");
+        // GgufFile.cs:44-46.
+        if (offset < 0 || length < 0 || offset > t.byte_length || length > t.byte_length - offset)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Window exceeds tensor payload. (Parameter 'offset')");
+        *bytes = f.bytes() + t.offset + offset;
+    });
+}
+
+int satori_hip_gguf_metadata_count(const satori_hip_gguf* file, int64_t* count) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        require(count, "count");
+        *count = static_cast<int64_t>(f.metadata().size());
+    });
+}
+
+int satori_hip_gguf_metadata_find(const satori_hip_gguf* file, const char* key, int64_t* index) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        require(key, "key");
+        require(index, "index");
+        const int64_t k = f.find_metadata(key);
+        if (k < 0) fail(SATORI_HIP_E_KEY_NOT_FOUND, std::string("The given key '") + key + "' was not present in the dictionary.");
+        *index = k;
+    });
+}
+
+int satori_hip_gguf_metadata_info(const satori_hip_gguf* file, int64_t index, const char** key, uint32_t* type,
+                                  int64_t* offset, int64_t* byte_length, int64_t* element_type,
+                                  int64_t* element_count) {
+    return guarded([&] {
+        const GgufMetadataInfo& m = metadata_at(live_file(file), index);
+        if (key) *key = m.key.c_str();
+        if (type) *type = m.type;
+        if (offset) *offset = m.offset;
+        if (byte_length) *byte_length = m.byte_length;
+        if (element_type) *element_type = m.element_type;
+        if (element_count) *element_count = m.element_count;
+    });
+}
+
+int satori_hip_gguf_metadata_window(const satori_hip_gguf* file, int64_t index, const void** bytes, int64_t* length) {
+    return guarded([&] {
+        const GgufFile& f = live_file(file);
+        const GgufMetadataInfo& m = metadata_at(f, index);
+        require(bytes, "bytes");
+        // GgufFile.cs:54.
+        if (m.byte_length > 0x7FFFFFFF) fail(SATORI_HIP_E_NOT_SUPPORTED, "Metadata window exceeds Int32.");
+        *bytes = f.bytes() + m.offset;
+        if (length) *length = m.byte_length;
+    });
+}
+
+int satori_hip_gguf_matrix_create(satori_hip_context* c, const satori_hip_gguf* file, int64_t index,
+                                  satori_hip_matrix** matrix) {
+    return guarded([&] {
+        require(matrix, "matrix");
+        *matrix = nullptr;
+        require_live(c);
+        const GgufFile& f = live_file(file);
+        const GgufTensorInfo& t = tensor_at(f, index);
+        // GgufQuantizedMatrix.cs:16-26.
+        const bool typed = t.type == 8 || t.type == 2 || t.type == 12 || t.type == 14;
+        if (!typed || t.rank != 2 || t.byte_length > 0x7FFFFFFF || t.dims[0] > 0x7FFFFFFF || t.dims[1] > 0x7FFFFFFF)
+            fail(SATORI_HIP_E_NOT_SUPPORTED,
+                 "MatVec requires a rank-2 Q8_0/Q4_0/Q4_K/Q6_K tensor within Int32 limits.");
+        const int format = t.type == 8 ? SATORI_HIP_Q8_0 : t.type == 2 ? SATORI_HIP_Q4_0
+                           : t.type == 12 ? SATORI_HIP_Q4_K : SATORI_HIP_Q6_K;
+        const Shape s = quantized_shape(static_cast<int>(t.dims[1]), static_cast<int>(t.dims[0]), format);
+        const uint8_t* bytes = f.bytes() + t.offset;  // the whole payload: ReadTensor(name, 0, ByteLength)
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        satori_hip_matrix* m = upload(c, s, bytes);
+        uint32_t bad = 0;
+        DeviceBuffer flag;
+        struct Release {
+            DeviceBuffer& buffer;
+            ~Release() { buffer.release(); }
+        } release_flag{flag};
+        try {
+            flag.reserve(sizeof(uint32_t));
+            check_hip(hipMemsetAsync(flag.ptr, 0, sizeof(uint32_t), c->stream), "scale check");
+            check_hip(launch_scale_check(m->payload, static_cast<int64_t>(s.rows) * s.blocks, format,
+                                         static_cast<uint32_t*>(flag.ptr), c->stream),
+                      "scale check");
+            check_hip(hipMemcpyAsync(&bad, flag.ptr, sizeof(bad), hipMemcpyDeviceToHost, c->stream), "scale check");
+            check_hip(hipStreamSynchronize(c->stream), "scale check");
+        } catch (...) {
+            free_matrix(m);
+            delete m;
+            c->matrices--;
+            throw;
+        }
+        if (bad != 0) {
+            free_matrix(m);
+            delete m;
+            c->matrices--;
+            validate_quantized(s, bytes);  // names the first bad block, as the host check does
+            fail(SATORI_HIP_E_INVALID_DATA, "Nonfinite block scale.");
+        }
+        *matrix = m;
     });
 }
 

@@ -659,3 +659,122 @@ def test_step_graph_replays_match_eager_groups(context):
         context.free(p)
     for m in mats:
         m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# GGUF containers to resident matrices (satori_hip_gguf_matrix_create)
+# ---------------------------------------------------------------------------------------------
+
+def _gguf_with(tmp_path, tensors):
+    """A canonical GGUF v3 file holding `tensors` = [(name, rows, columns, type id, payload)]."""
+    import struct
+
+    def s(v):
+        raw = v.encode()
+        return struct.pack("<Q", len(raw)) + raw
+
+    out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 3))
+    out += s("general.architecture") + struct.pack("<I", 8) + s("qwen2")
+    out += s("general.alignment") + struct.pack("<II", 4, 32)
+    out += s("general.quantization_version") + struct.pack("<II", 4, 2)
+    offset, blobs = 0, []
+    for name, rows, columns, type_, payload in tensors:
+        out += s(name) + struct.pack("<IQQIQ", 2, columns, rows, type_, offset)
+        padded = bytes(payload) + bytes(-len(payload) % 32)
+        blobs.append(padded)
+        offset += len(padded)
+    out += bytes(-len(out) % 32)
+    path = str(tmp_path / "model.gguf")
+    with open(path, "wb") as f:
+        f.write(bytes(out) + b"".join(blobs))
+    return path
+
+
+def test_gguf_tensors_upload_to_resident_matrices(context, tmp_path):
+    # GgufQuantizedMatrix.CreateExecution (GgufQuantizedMatrix.cs:31-36): the device matrix made from the
+    # mapped tensor equals the one made from the same bytes through the factory, for every format, on the
+    # FP32 path and on the integer K path (single position and the matrix-core batch).
+    g = rng(99)
+    specs = [("blk.0.attn_q.weight", 300, 512, BQ.Q4_K, 12), ("blk.0.ffn_down.weight", 129, 768, BQ.Q6_K, 14),
+             ("blk.0.attn_k.weight", 70, 256, BQ.Q8_0, 8), ("blk.0.attn_v.weight", 33, 320, BQ.Q4_0, 2)]
+    tensors, payloads = [], {}
+    for name, rows, columns, fmt, type_ in specs:
+        data = S.quantize_weights((g.standard_normal((rows, columns)) * 0.05).astype(np.float32), rows, columns, fmt)
+        payloads[name] = data
+        tensors.append((name, rows, columns, type_, data))
+    path = _gguf_with(tmp_path, tensors)
+    with S.GgufFile(path) as f:
+        store = S.GgufWeightStore(f, context)
+        for name, rows, columns, fmt, _ in specs:
+            assert store.has(name)
+            m = store.matrix(name)
+            ref = context.create(payloads[name], S.QuantizedMatrixShape(rows, columns, fmt))
+            x = g.standard_normal(columns).astype(np.float32)
+            y, y_ref = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+            m.execute(x, y)
+            ref.execute(x, y_ref)
+            assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), name
+            if fmt in (BQ.Q4_K, BQ.Q6_K):
+                for positions in (1, 20):
+                    xb = g.standard_normal(positions * columns).astype(np.float32)
+                    yb, yb_ref = np.zeros(positions * rows, np.float32), np.zeros(positions * rows, np.float32)
+                    store.project_batch(name, xb, positions, yb)
+                    ref.execute_batch(xb, positions, yb_ref)
+                    assert np.array_equal(yb.view(np.uint32), yb_ref.view(np.uint32)), (name, positions)
+            ref.dispose()
+        store.dispose()
+
+
+@pytest.mark.parametrize("fmt,type_,byte", [(BQ.Q4_K, 12, 2), (BQ.Q6_K, 14, 208), (BQ.Q8_0, 8, 0), (BQ.Q4_0, 2, 0)])
+def test_gguf_device_scale_check_rejects_nonfinite_scales(context, tmp_path, fmt, type_, byte):
+    # QuantizedMatVec.ValidatePayload (QuantizedMatVec.cs:28-42) run on the device copy: a NaN scale in the
+    # last block of the last row (Q4_K's dmin, Q6_K's d at byte 208) fails with InvalidData naming its
+    # offset, and a clean tensor of the same file still uploads.
+    g = rng(7)
+    rows, columns = 37, 512
+    data = S.quantize_weights((g.standard_normal((rows, columns)) * 0.05).astype(np.float32), rows, columns, fmt)
+    bad = data.copy()
+    block_bytes = {BQ.Q4_K: 144, BQ.Q6_K: 210, BQ.Q8_0: 34, BQ.Q4_0: 18}[fmt]
+    last = bad.size - block_bytes
+    bad[last + byte:last + byte + 2] = [0x00, 0x7E]  # FP16 NaN
+    path = _gguf_with(tmp_path, [("bad", rows, columns, type_, bad), ("good", rows, columns, type_, data)])
+    with S.GgufFile(path) as f:
+        handle = ctypes_matrix_from_gguf(context, f, "bad")
+        assert handle[0] == S.InvalidDataException.status and str(last) in handle[1]
+        m = S.GgufQuantizedMatrix(f, "good").create_execution(context)
+        x = g.standard_normal(columns).astype(np.float32)
+        y, y_ref = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+        m.execute(x, y)
+        with context.create(data, S.QuantizedMatrixShape(rows, columns, fmt)) as ref:
+            ref.execute(x, y_ref)
+        assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+        m.dispose()
+
+
+def ctypes_matrix_from_gguf(context, f, name):
+    """Raw C-ABI call (the Python binding would check the payload on the host first): status and message."""
+    import ctypes
+    from satori_amd import _ffi
+    handle = ctypes.c_void_p()
+    status = _ffi.lib().satori_hip_gguf_matrix_create(context.handle, f.handle, f.tensor_index(name),
+                                                       ctypes.byref(handle))
+    message = _ffi.lib().satori_hip_last_error().decode()
+    assert not handle.value or status == 0
+    return status, message
+
+
+def test_golden_gguf_file_through_the_container(context):
+    # The reference's q8_0.gguf / q4_0.gguf tensors opened as containers: ones-dot = -8 per row, as the
+    # manifest's FP64 decode gives (test_golden_gguf_ones_dot reads the same bytes by offset).
+    import os
+    from helpers import GOLDEN
+    for name in ("q8_0.gguf", "q4_0.gguf"):
+        with S.GgufFile(os.path.join(GOLDEN, name)) as f:
+            m = S.GgufQuantizedMatrix(f, "weights")
+            y = np.zeros(m.shape.rows, np.float32)
+            m.execute(np.ones(m.shape.columns, np.float32), y)
+            data, _ = gguf_tensor(name)
+            expected = O.q_matvec_scalar(data, m.shape.rows, m.shape.columns, int(m.shape.format),
+                                         np.ones(m.shape.columns, np.float32))
+            assert np.array_equal(y, expected) and y.tolist() == [-8.0], name
+            m.dispose()
