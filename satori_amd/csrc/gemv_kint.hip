@@ -170,37 +170,40 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
             q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * nb, static_cast<int64_t>(row_begin) * nb + p, c, r);
         }
     };
-    int p0 = threadIdx.x / G;
-    Raw cur, nxt;
-    if (p0 < pairs) load_pair(p0, cur);  // in flight while the activations are quantized
+    // This slot's pairs are p0, p0 + kPairsPerStep, ...; up to kDepth of them are loaded before the
+    // activations are quantized, and each processed pair's registers are refilled with the pair kDepth
+    // further on, so kDepth loads stay in flight.
+    constexpr int kDepth = 3;
+    const int p0 = threadIdx.x / G;
+    const int mine = p0 < pairs ? (pairs - 1 - p0) / kPairsPerStep + 1 : 0;
+    Raw buf[kDepth];
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i)
+        if (i < mine) load_pair(p0 + i * kPairsPerStep, buf[i]);
 
-    // Q8_K of the position's activations: each wave quantizes four blocks per pass, their loads in flight
-    // together.
+    // Q8_K of the position's activations: one 16-lane row per block, sixteen blocks per pass.
     const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
     {
-        constexpr int kBatch = 4;
-        const int wave = threadIdx.x >> 6;
-        for (int b0 = kBatch * wave; b0 < nb; b0 += kBatch * (kThreads / 64)) {
-            float v[kBatch][4];
+        const int j = threadIdx.x & 15;
+        for (int b = threadIdx.x >> 4; b < nb; b += kThreads / 16) {
+            float v[16];
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(xrow + 256 * b + 16 * j);
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j)
-                if (b0 + j < nb) q8k_load_values(xrow + 256 * (b0 + j), lane, v[j]);
+            for (int q = 0; q < 4; ++q) {
+                const u32x4 raw = load16_a4(src + 16 * q);
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const int b = b0 + j;
-                if (b >= nb) break;
-                const Q8KLane q = q8k_quantize_values(v[j], lane);
-                act.codes[kCodeStride * b + lane] = q.packed;  // zero block: all codes, sums and the scale are 0
-                if ((lane & 3) == 0) act.sums[16 * b + (lane >> 2)] = static_cast<int16_t>(q.group_sum);
-                if (lane == 0) act.scales[b] = q.scale;
+                for (int e = 0; e < 4; ++e) v[4 * q + e] = __uint_as_float(raw[e]);
             }
+            const Q8KRow16 q = q8k_quantize_row16(v, lane);
+            *reinterpret_cast<u32x4*>(act.codes + kCodeStride * b + 4 * j) =
+                u32x4{q.packed[0], q.packed[1], q.packed[2], q.packed[3]};
+            act.sums[16 * b + j] = static_cast<int16_t>(q.group_sum);
+            if (j == 0) act.scales[b] = q.scale;
         }
     }
     __syncthreads();  // activations staged
-    for (; p0 < pairs; p0 += kPairsPerStep) {
-        const int pn = p0 + kPairsPerStep;
-        if (pn < pairs) load_pair(pn, nxt);
-        const int b = p0 % nb;
+    auto process = [&](const Raw& cur, int p) {
+        const int b = p % nb;
         float term = 0.0f;
         if constexpr (FORMAT == kQ4_K) {
             int dot, min_part;
@@ -219,8 +222,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
             const float a = act.scales[b];
             if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, cur.d), static_cast<float>(dot));
         }
-        if (c == G - 1) terms[p0] = term;  // p0 = r * nb + b
-        cur = nxt;
+        if (c == G - 1) terms[p] = term;  // p = r * nb + b
+    };
+    for (int base = 0; base < mine; base += kDepth) {
+#pragma unroll
+        for (int i = 0; i < kDepth; ++i) {
+            const int k = base + i;
+            if (k < mine) {
+                process(buf[i], p0 + k * kPairsPerStep);
+                if (k + kDepth < mine) load_pair(p0 + (k + kDepth) * kPairsPerStep, buf[i]);
+            }
+        }
     }
     __syncthreads();
     if (threadIdx.x < rows) {
@@ -251,12 +263,14 @@ int kint_max_blocks() { return static_cast<int>((64 * 1024) / ((kActDwords + kTi
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
                             hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
-    // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and a
-    // workgroup keeps more than 128 (row, block) pairs, so the small projections of a decode step spread
-    // over the chip without each workgroup's activation quantization outweighing its share of the product.
+    // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and either a
+    // thread slot would hold more than three (row, block) pairs (the pairs it prefetches before quantizing)
+    // or the grid has fewer than 192 workgroups. Measured on the decode step's groups: q/k/v and o take 8-16
+    // rows, gate/up 32, down (35 blocks) 4; large grouped launches keep 64.
     const int64_t members = static_cast<int64_t>(count) * s.positions;
+    auto groups_for = [&](int t) { return members * ((s.rows_max + t - 1) / t); };
     int tile = kTileRows;
-    while (tile > 4 && tile * s.blocks > 128 && members * ((s.rows_max + tile - 1) / tile) < 1024) tile /= 2;
+    while (tile > 4 && groups_for(tile) < 1024 && (tile * s.blocks > 192 || groups_for(tile) < 192)) tile /= 2;
     s.rows_per_wg = tile;
     dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
     const size_t lds = kint_lds_bytes(s.blocks);

@@ -59,3 +59,66 @@ __device__ __forceinline__ void q8k_load_values(const float* __restrict__ src, i
 }
 
 }  // namespace satori
+
+namespace satori {
+
+// The same quantization with 16 lanes per block (one DPP row), sixteen elements per lane: lane j of the
+// row holds elements 16j .. 16j + 15, which are exactly Q8_K group j, so its group sum needs no cross-lane
+// step. The row maximum of the magnitude keys is an all-reduce by rotation within the row (row_ror 1, 2,
+// 4, 8); the first index holding it is the lowest row lane whose own first maximal element has the key
+// (ballot), and that element's signed value is read from its lane (bpermute). Four blocks per wave.
+struct Q8KRow16 {
+    uint32_t packed[4];  // codes 16j .. 16j + 15
+    int group_sum;       // sum of those 16 codes
+    float scale;         // 1 / inverse, or 0 for an all-zero block
+};
+
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x121, 0xF, 0xF, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x122, 0xF, 0xF, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xF, 0xF, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xF, 0xF, false)));
+    return v;
+}
+
+// `lane` is the lane within the wave (0..63); all 16 lanes of its row must be active together.
+__device__ __forceinline__ Q8KRow16 q8k_quantize_row16(const float (&v)[16], int lane) {
+    uint32_t key = 0;
+    float first = 0.0f;  // the lane's first element of maximal magnitude (strict >: the lowest index wins)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float a = __builtin_fabsf(v[i]);
+        const uint32_t k = a == a ? __float_as_uint(a) : 0u;  // NaN never wins
+        if (k > key) {
+            key = k;
+            first = v[i];
+        }
+    }
+    const uint32_t best = row_max_u32(key);
+    Q8KRow16 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r.packed[w] = 0u;
+    r.group_sum = 0;
+    r.scale = 0.0f;
+    if (best == 0u) return r;  // magnitude 0: the block is all zero bytes (Q8KCodec.cs:59-63)
+    const int base = lane & ~15;
+    const uint64_t holders = __ballot(key == best);
+    const uint32_t row_bits = static_cast<uint32_t>(holders >> base) & 0xFFFFu;
+    const int src = base + __builtin_ctz(row_bits);
+    const float max = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(first)));
+    const float inverse = __fdiv_rn(-127.0f, max);
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float shifted = __fadd_rn(__fmul_rn(inverse, v[i]), 12582912.0f);
+        int n = static_cast<int>(__float_as_uint(shifted) & 0x007FFFFFu) - 0x00400000;  // NearestInteger, :120-125
+        n = n < 127 ? n : 127;
+        sum += static_cast<int8_t>(n);
+        r.packed[i >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(n)) << (8 * (i & 3));
+    }
+    r.group_sum = sum;
+    r.scale = __fdiv_rn(1.0f, inverse);
+    return r;
+}
+
+}  // namespace satori

@@ -425,6 +425,51 @@ def test_k_integer_batch_is_bit_exact(context, fmt, rows, columns):
     m.dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+def test_k_integer_product_quantizer_edge_cases(context, fmt):
+    # Q8KCodec.QuantizeBlock (Q8KCodec.cs:44-76) inside the integer products: ties of the largest magnitude
+    # (the lowest index wins, and its sign sets the scale), the maximum in every lane position of a block,
+    # subnormal and huge blocks, zero blocks; outputs bit-exact against the oracle, for the single-position
+    # kernel (which quantizes in-kernel) and the matrix-core batch (which quantizes in its pack kernel).
+    g = rng(4711)
+    rows, columns = 70, 4096
+    w = (g.standard_normal((rows, columns)) * 0.05).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    cases = []
+    x = np.sign(g.standard_normal(columns)).astype(np.float32)  # all |x| equal: every element ties
+    cases.append(x)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    for b in range(16):  # block b: maximum magnitude 3 at element 17b (each lane slot), a later -3 tie
+        x[256 * b + 17 * b % 256] = 3.0
+        x[256 * b + (17 * b + 100) % 256] = -3.0
+    cases.append(x)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    for b in range(16):  # negative maximum first, positive tie later, and a last-element maximum
+        x[256 * b + 5] = -2.5
+        x[256 * b + 250] = 2.5 if b % 2 else 1.0
+        x[256 * b + 255] = 4.0 if b % 3 == 0 else x[256 * b + 255]
+    cases.append(x)
+    x = (g.standard_normal(columns) * 1e-40).astype(np.float32)  # subnormal blocks
+    x[:256] = 0.0
+    x[512:768] = np.float32(1e-45)
+    cases.append(x)
+    x = (g.standard_normal(columns) * 1e30).astype(np.float32)
+    x[1024:1280] = 0.0
+    cases.append(x)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    for i, x in enumerate(cases):
+        y = np.zeros(rows, np.float32)
+        m.execute_batch(x, 1, y)
+        expected = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x))
+        assert np.array_equal(y.view(np.uint32), expected.view(np.uint32)), f"case {i}"
+    xs = np.stack(cases * 4).astype(np.float32)  # 20 positions: the matrix-core path
+    y = np.zeros(xs.shape[0] * rows, np.float32)
+    m.execute_batch(xs.reshape(-1), xs.shape[0], y)
+    expected = O.q_matvec_batch(data, rows, columns, int(fmt), xs.reshape(-1), xs.shape[0])
+    assert np.array_equal(y.view(np.uint32), expected.view(np.uint32))
+    m.dispose()
+
+
 @pytest.mark.parametrize("fmt,fixture", [(BQ.Q4_K, "q4k-v1.json"), (BQ.Q6_K, "q6k-v1.json")])
 def test_k_integer_batch_multi_position_on_fixture_blocks(context, fmt, fixture):
     # BatchedMatVecTests.cs:45-113: payloads tiled from the fixture blocks, several positions.
