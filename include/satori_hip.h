@@ -98,6 +98,29 @@ int satori_hip_quantized_create(satori_hip_context* context, int rows, int colum
  * validates header and payload, uploads; corrupt files fail with SATORI_HIP_E_INVALID_DATA. */
 int satori_hip_ternary2_open(satori_hip_context* context, const char* path, satori_hip_matrix** matrix);
 
+/* ---- ternary bitplane layout (src/Satori.Core/TernaryBitplaneMatrix.cs) ----
+ * Blocks of the FP32 scale, B/8 bytes of positive-plane bits, B/8 bytes of negative-plane bits; same shape
+ * and byte length as Ternary2. The device copy is the lossless Ternary2 equivalent, so execution is the
+ * Ternary2 MatVec (TernaryBitplaneMatVec.Execute, src/Satori.Core/TernaryBitplaneMatVec.cs:8-12) and the
+ * matrix reports format SATORI_HIP_TERNARY2. */
+/* TernaryBitplaneMatrix.FromPacked (TernaryBitplaneMatrix.cs:56-62) + Validate (:64-85), then upload. */
+int satori_hip_bitplane_create(satori_hip_context* context, int rows, int columns, int block_size,
+                               const void* payload, size_t payload_length, satori_hip_matrix** matrix);
+/* TernaryBitplaneMatrix.Load (TernaryBitplaneMatrix.cs:98-117) of an STB1 file, then upload; every file
+ * defect fails with SATORI_HIP_E_INVALID_DATA. */
+int satori_hip_bitplane_open(satori_hip_context* context, const char* path, satori_hip_matrix** matrix);
+/* TernaryBitplaneMatrix.Load on the host: shape and payload of a valid STB1 file. With payload NULL only
+ * the shape and length are returned; otherwise capacity must be at least the payload length. */
+int satori_hip_bitplane_load(const char* path, int* rows, int* columns, int* block_size, void* payload,
+                             size_t capacity, int64_t* length);
+/* Host conversions and validation: TernaryBitplaneMatrix.FromTernary2 (:19-36, the Ternary2 payload is
+ * validated first), ToTernary2 (:38-54, the bitplane payload is validated first) and Validate. */
+int satori_hip_bitplane_from_ternary2(int rows, int columns, int block_size, const void* ternary2,
+                                      size_t ternary2_length, void* bitplane, size_t bitplane_length);
+int satori_hip_bitplane_to_ternary2(int rows, int columns, int block_size, const void* bitplane,
+                                    size_t bitplane_length, void* ternary2, size_t ternary2_length);
+int satori_hip_bitplane_validate(int rows, int columns, int block_size, const void* payload, size_t payload_length);
+
 /* A second resident copy of already validated weights (device-to-device; no reference counterpart):
  * distinct copies for rotating-buffer measurements or for use from several streams. */
 int satori_hip_matrix_clone(satori_hip_matrix* source, satori_hip_matrix** clone);

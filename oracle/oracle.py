@@ -70,6 +70,10 @@ def _declare(l):
         "or_t2_matvec_avx2": (None, [P, I, I, I, P, P]),
         "or_stq2_write_header": (None, [P, I, I, I]),
         "or_stq2_read_header": (I, [P, P, P, P]),
+        "or_tb_validate": (I, [P, SZ, I, I, I]),
+        "or_tb_from_t2": (None, [P, I, I, I, P]),
+        "or_tb_to_t2": (None, [P, I, I, I, P]),
+        "or_tb_matvec_scalar": (None, [P, I, I, I, P, P]),
         "or_q_byte_length": (ctypes.c_int64, [I, I, I]),
         "or_q_validate": (I, [P, SZ, I, I, I]),
         "or_q_matvec_scalar": (None, [P, I, I, I, P, P]),
@@ -139,6 +143,32 @@ def t2_quantize(weights, rows: int, columns: int, block: int = 64) -> np.ndarray
 def t2_validate(data, rows: int, columns: int, block: int) -> None:
     d = _u8(data)
     _check(lib().or_t2_validate(_ptr(d), d.size, rows, columns, block))
+
+
+def tb_validate(data, rows: int, columns: int, block: int) -> None:
+    d = _u8(data)
+    _check(lib().or_tb_validate(_ptr(d), d.size, rows, columns, block))
+
+
+def tb_from_t2(t2, rows: int, columns: int, block: int) -> np.ndarray:
+    d = _u8(t2)
+    out = np.zeros(d.size, dtype=np.uint8)
+    lib().or_tb_from_t2(_ptr(d), rows, columns, block, _ptr(out))
+    return out
+
+
+def tb_to_t2(tb, rows: int, columns: int, block: int) -> np.ndarray:
+    d = _u8(tb)
+    out = np.zeros(d.size, dtype=np.uint8)
+    lib().or_tb_to_t2(_ptr(d), rows, columns, block, _ptr(out))
+    return out
+
+
+def tb_matvec_scalar(data, rows: int, columns: int, block: int, x) -> np.ndarray:
+    d, xv = _u8(data), _f32(x)
+    y = np.zeros(rows, dtype=np.float32)
+    lib().or_tb_matvec_scalar(_ptr(d), rows, columns, block, _ptr(xv), _ptr(y))
+    return y
 
 
 def t2_dequantize(data, rows: int, columns: int, block: int) -> np.ndarray:

@@ -113,6 +113,87 @@ int or_t2_validate(const uint8_t* data, size_t len, int rows, int columns, int b
     return OR_OK;
 }
 
+/* TernaryBitplaneMatrix.Validate (src/Satori.Core/TernaryBitplaneMatrix.cs:64-85): scale finite, >= 0 and
+ * not -0; no weight in both planes; no bit past the last column; no bit in a zero-scale block. */
+int or_tb_validate(const uint8_t* data, size_t len, int rows, int columns, int block_size) {
+    int64_t length = or_t2_byte_length(rows, columns, block_size);
+    if (length < 0) return (int)-length;
+    if ((int64_t)len != length) return OR_ARGUMENT;
+    int blocks = (int)(((int64_t)columns + block_size - 1) / block_size);
+    int stride = 4 + block_size / 4, plane = block_size / 8;
+    for (int row = 0; row < rows; row++)
+        for (int block = 0; block < blocks; block++) {
+            const uint8_t* bytes = data + ((int64_t)row * blocks + block) * stride;
+            float scale = rdf32(bytes);
+            uint32_t bits = (uint32_t)rd32(bytes);
+            if (!isfinite(scale) || scale < 0 || bits == 0x80000000u) return OR_ARGUMENT;
+            int count = block_size < columns - block * block_size ? block_size : columns - block * block_size;
+            for (int i = 0; i < plane; i++) {
+                int positive = bytes[4 + i], negative = bytes[4 + plane + i];
+                int valid = count - i * 8;
+                valid = valid < 0 ? 0 : valid > 8 ? 8 : valid;
+                int padding = ~((1 << valid) - 1);
+                if ((positive & negative) != 0 || ((positive | negative) & padding) != 0 ||
+                    (scale == 0 && (positive | negative) != 0))
+                    return OR_ARGUMENT;
+            }
+        }
+    return OR_OK;
+}
+
+/* TernaryBitplaneMatrix.FromTernary2 (TernaryBitplaneMatrix.cs:19-36): code 1 sets the positive bit, code 2
+ * the negative bit. */
+void or_tb_from_t2(const uint8_t* t2, int rows, int columns, int block_size, uint8_t* out) {
+    int64_t length = or_t2_byte_length(rows, columns, block_size);
+    int stride = 4 + block_size / 4, plane = block_size / 8;
+    memset(out, 0, (size_t)length);
+    for (int64_t offset = 0; offset < length; offset += stride) {
+        memcpy(out + offset, t2 + offset, 4);
+        for (int i = 0; i < block_size; i++) {
+            int code = (t2[offset + 4 + i / 4] >> (2 * (i % 4))) & 3;
+            if (code != 0) out[offset + 4 + (code == 2 ? plane : 0) + i / 8] |= (uint8_t)(1 << (i % 8));
+        }
+    }
+}
+
+/* TernaryBitplaneMatrix.ToTernary2 (TernaryBitplaneMatrix.cs:38-54). */
+void or_tb_to_t2(const uint8_t* tb, int rows, int columns, int block_size, uint8_t* out) {
+    int64_t length = or_t2_byte_length(rows, columns, block_size);
+    int stride = 4 + block_size / 4, plane = block_size / 8;
+    memset(out, 0, (size_t)length);
+    for (int64_t offset = 0; offset < length; offset += stride) {
+        memcpy(out + offset, tb + offset, 4);
+        for (int i = 0; i < block_size; i++) {
+            int positive = (tb[offset + 4 + i / 8] >> (i % 8)) & 1;
+            int negative = (tb[offset + 4 + plane + i / 8] >> (i % 8)) & 1;
+            out[offset + 4 + i / 4] |= (uint8_t)((positive | negative << 1) << (2 * (i % 4)));
+        }
+    }
+}
+
+/* TernaryBitplaneMatVec.ExecuteScalar (src/Satori.Core/TernaryBitplaneMatVec.cs:24-46): per block a sequential
+ * FP32 sum of +x (positive bit) or -x (negative bit), then total += scale * sum. */
+void or_tb_matvec_scalar(const uint8_t* data, int rows, int columns, int block_size, const float* x, float* y) {
+    int blocks = (int)(((int64_t)columns + block_size - 1) / block_size);
+    int stride = 4 + block_size / 4, plane = block_size / 8;
+    for (int row = 0; row < rows; row++) {
+        float total = 0;
+        for (int block = 0; block < blocks; block++) {
+            const uint8_t* bytes = data + ((int64_t)row * blocks + block) * stride;
+            int column = block * block_size;
+            int count = block_size < columns - column ? block_size : columns - column;
+            float sum = 0;
+            for (int i = 0; i < count; i++) {
+                int mask = 1 << (i % 8);
+                if (bytes[4 + i / 8] & mask) sum += x[column + i];
+                else if (bytes[4 + plane + i / 8] & mask) sum -= x[column + i];
+            }
+            total += rdf32(bytes) * sum;
+        }
+        y[row] = total;
+    }
+}
+
 /* Ternary2Matrix.Dequantize (src/Satori.Core/Ternary2Matrix.cs:103-120). */
 void or_t2_dequantize(const uint8_t* data, int rows, int columns, int block_size, float* out) {
     int blocks = (int)(((int64_t)columns + block_size - 1) / block_size);

@@ -42,6 +42,14 @@ void or_t2_matvec_avx2(const uint8_t* data, int rows, int columns, int block_siz
 void or_stq2_write_header(uint8_t header[32], int rows, int columns, int block_size);
 int or_stq2_read_header(const uint8_t header[32], int* rows, int* columns, int* block_size);
 
+/* Ternary bitplane layout (src/Satori.Core/TernaryBitplaneMatrix.cs, TernaryBitplaneMatVec.cs): each
+ * block is the FP32 scale, then B/8 bytes of positive-plane bits, then B/8 bytes of negative-plane bits
+ * (bit i % 8 of byte i / 8 is weight i). */
+int or_tb_validate(const uint8_t* data, size_t len, int rows, int columns, int block_size);
+void or_tb_from_t2(const uint8_t* t2, int rows, int columns, int block_size, uint8_t* out);
+void or_tb_to_t2(const uint8_t* tb, int rows, int columns, int block_size, uint8_t* out);
+void or_tb_matvec_scalar(const uint8_t* data, int rows, int columns, int block_size, const float* x, float* y);
+
 /* ---- GGUF block formats ---- */
 int64_t or_q_byte_length(int rows, int columns, int format);
 int or_q_validate(const uint8_t* data, size_t len, int rows, int columns, int format);

@@ -34,6 +34,7 @@ __all__ = [
     "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "HipStep", "Q8KCodec", "TERNARY2",
     "device_count", "default_context", "payload_length", "quantize_weights",
     "GgufFile", "GgufTensor", "GgufMetadata", "GgufQuantizedMatrix", "GgufWeightStore",
+    "TernaryBitplaneMatrix", "TernaryBitplaneMatVec",
 ]
 
 TERNARY2 = 16
@@ -220,6 +221,18 @@ class HipContext:
     def open_ternary2(self, path: str) -> "HipQuantizedMatrix":
         handle = ctypes.c_void_p()
         _check(_ffi.lib().satori_hip_ternary2_open(self._handle, str(path).encode(), ctypes.byref(handle)))
+        return HipQuantizedMatrix(self, handle)
+
+    def create_bitplane(self, rows: int, columns: int, block_size: int, payload) -> "HipQuantizedMatrix":
+        data = _as_u8(payload)
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_bitplane_create(self._handle, rows, columns, block_size, _ptr(data), data.size,
+                                                     ctypes.byref(handle)))
+        return HipQuantizedMatrix(self, handle)
+
+    def open_bitplane(self, path: str) -> "HipQuantizedMatrix":
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_bitplane_open(self._handle, str(path).encode(), ctypes.byref(handle)))
         return HipQuantizedMatrix(self, handle)
 
     def quantize_q8k(self, x) -> np.ndarray:
@@ -433,6 +446,91 @@ class Ternary2MatVec:
 
     @staticmethod
     def execute(matrix: Ternary2Matrix, input, output, context: HipContext | None = None) -> None:
+        if matrix is None:
+            raise ArgumentNullException("Value cannot be null. (Parameter 'matrix')")
+        matrix.device(context).execute(input, output)
+
+
+class TernaryBitplaneMatrix:
+    """src/Satori.Core/TernaryBitplaneMatrix.cs:6-118: ternary weights as separate positive and negative
+    bitplanes (same shape and byte length as Ternary2). Conversions and validation run in the library; the
+    device copy (made on first execution) is the lossless Ternary2 equivalent."""
+
+    def __init__(self, rows: int, columns: int, block_size: int, data: np.ndarray):
+        self.rows, self.columns, self.block_size = rows, columns, block_size
+        self._data = data
+        self._device: HipQuantizedMatrix | None = None
+
+    @property
+    def byte_length(self) -> int:
+        return self._data.size
+
+    @property
+    def data(self) -> np.ndarray:
+        return self._data
+
+    def copy_data_to(self, destination: np.ndarray) -> None:
+        destination[: self._data.size] = self._data
+
+    @staticmethod
+    def from_ternary2(matrix: Ternary2Matrix) -> "TernaryBitplaneMatrix":
+        """FromTernary2 (TernaryBitplaneMatrix.cs:19-36)."""
+        out = np.zeros(matrix.byte_length, dtype=np.uint8)
+        _check(_ffi.lib().satori_hip_bitplane_from_ternary2(matrix.rows, matrix.columns, matrix.block_size,
+                                                            _ptr(matrix.data), matrix.byte_length, _ptr(out), out.size))
+        return TernaryBitplaneMatrix(matrix.rows, matrix.columns, matrix.block_size, out)
+
+    def to_ternary2(self) -> Ternary2Matrix:
+        """ToTernary2 (TernaryBitplaneMatrix.cs:38-54)."""
+        out = np.zeros(self.byte_length, dtype=np.uint8)
+        _check(_ffi.lib().satori_hip_bitplane_to_ternary2(self.rows, self.columns, self.block_size, _ptr(self._data),
+                                                          self.byte_length, _ptr(out), out.size))
+        return Ternary2Matrix.from_packed(self.rows, self.columns, self.block_size, out)
+
+    @staticmethod
+    def from_packed(rows: int, columns: int, block_size: int, payload) -> "TernaryBitplaneMatrix":
+        """FromPacked (TernaryBitplaneMatrix.cs:56-62): copies and validates."""
+        owned = _as_u8(payload).copy()
+        _check(_ffi.lib().satori_hip_bitplane_validate(rows, columns, block_size, _ptr(owned), owned.size))
+        return TernaryBitplaneMatrix(rows, columns, block_size, owned)
+
+    def save(self, path: str) -> None:
+        """Save (TernaryBitplaneMatrix.cs:87-96): the STQ2 header with magic "STB1", then the payload."""
+        header = bytearray(32)
+        header[0:4] = b"STB1"
+        header[4:6] = (1).to_bytes(2, "little")
+        header[6:8] = (32).to_bytes(2, "little")
+        header[8:12] = self.rows.to_bytes(4, "little", signed=True)
+        header[12:16] = self.columns.to_bytes(4, "little", signed=True)
+        header[16:20] = self.block_size.to_bytes(4, "little", signed=True)
+        header[24:32] = self.byte_length.to_bytes(8, "little", signed=True)
+        with open(path, "xb") as f:
+            f.write(bytes(header))
+            f.write(self._data.tobytes())
+
+    @staticmethod
+    def load(path: str) -> "TernaryBitplaneMatrix":
+        """Load (TernaryBitplaneMatrix.cs:98-117): every file defect raises InvalidDataException."""
+        rows, columns, block, length = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+        p = os.fsencode(path)
+        _check(_ffi.lib().satori_hip_bitplane_load(p, ctypes.byref(rows), ctypes.byref(columns), ctypes.byref(block),
+                                                   None, 0, ctypes.byref(length)))
+        out = np.zeros(length.value, dtype=np.uint8)
+        _check(_ffi.lib().satori_hip_bitplane_load(p, None, None, None, _ptr(out), out.size, ctypes.byref(length)))
+        return TernaryBitplaneMatrix(rows.value, columns.value, block.value, out)
+
+    def device(self, context: HipContext | None = None) -> HipQuantizedMatrix:
+        if self._device is None:
+            ctx = context or default_context()
+            self._device = ctx.create_bitplane(self.rows, self.columns, self.block_size, self._data)
+        return self._device
+
+
+class TernaryBitplaneMatVec:
+    """src/Satori.Core/TernaryBitplaneMatVec.cs:6-54 with the HIP backend."""
+
+    @staticmethod
+    def execute(matrix: TernaryBitplaneMatrix, input, output, context: HipContext | None = None) -> None:
         if matrix is None:
             raise ArgumentNullException("Value cannot be null. (Parameter 'matrix')")
         matrix.device(context).execute(input, output)

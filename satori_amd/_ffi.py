@@ -51,6 +51,13 @@ SIGNATURES = {
     "satori_hip_quantized_validate": (I, [I, I, I, P, SZ]),
     "satori_hip_ternary2_quantize": (I, [P, I, I, I, P, SZ]),
     "satori_hip_quantize_weights": (I, [I, P, I, I, P, SZ]),
+    "satori_hip_bitplane_create": (I, [P, I, I, I, P, SZ, PP]),
+    "satori_hip_bitplane_open": (I, [P, ctypes.c_char_p, PP]),
+    "satori_hip_bitplane_load": (I, [ctypes.c_char_p, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I), P, SZ,
+                                     ctypes.POINTER(ctypes.c_int64)]),
+    "satori_hip_bitplane_from_ternary2": (I, [I, I, I, P, SZ, P, SZ]),
+    "satori_hip_bitplane_to_ternary2": (I, [I, I, I, P, SZ, P, SZ]),
+    "satori_hip_bitplane_validate": (I, [I, I, I, P, SZ]),
     "satori_hip_gguf_open": (I, [ctypes.c_char_p, PP]),
     "satori_hip_gguf_close": (I, [P]),
     "satori_hip_gguf_data_offset": (I, [P, ctypes.POINTER(ctypes.c_int64)]),

@@ -204,6 +204,7 @@ extern "C" int satori_hip_ternary2_quantize(const float* weights, int rows, int 
             }
         return SATORI_HIP_OK;
     } catch (const Failure& f) {
+        record_error(f.message);
         return f.status;
     }
 }
@@ -232,6 +233,7 @@ extern "C" int satori_hip_quantize_weights(int format, const float* weights, int
             }
         return SATORI_HIP_OK;
     } catch (const Failure& f) {
+        record_error(f.message);
         return f.status;
     }
 }
@@ -245,6 +247,7 @@ extern "C" int satori_hip_payload_length(int format, int rows, int columns, int 
         *length = s.byte_length;
         return SATORI_HIP_OK;
     } catch (const Failure& f) {
+        record_error(f.message);
         return f.status;
     }
 }
@@ -260,6 +263,7 @@ extern "C" int satori_hip_ternary2_validate(int rows, int columns, int block_siz
         validate_ternary2(s, static_cast<const uint8_t*>(payload));
         return SATORI_HIP_OK;
     } catch (const Failure& f) {
+        record_error(f.message);
         return f.status;
     }
 }
@@ -275,6 +279,56 @@ extern "C" int satori_hip_quantized_validate(int rows, int columns, int format, 
         validate_quantized(s, static_cast<const uint8_t*>(payload));
         return SATORI_HIP_OK;
     } catch (const Failure& f) {
+        record_error(f.message);
+        return f.status;
+    }
+}
+
+// ---- Ternary bitplane host utilities (src/Satori.Core/TernaryBitplaneMatrix.cs) ----
+
+extern "C" int satori_hip_bitplane_validate(int rows, int columns, int block_size, const void* payload,
+                                            size_t payload_length) {
+    try {
+        const Shape s = ternary2_shape(rows, columns, block_size);
+        if (!payload) fail(SATORI_HIP_E_ARGUMENT_NULL, "Value cannot be null.");
+        if (static_cast<int64_t>(payload_length) != s.byte_length)
+            fail(SATORI_HIP_E_ARGUMENT, "Incorrect bitplane payload length. (Parameter 'payload')");
+        validate_bitplane(s, static_cast<const uint8_t*>(payload));
+        return SATORI_HIP_OK;
+    } catch (const Failure& f) {
+        record_error(f.message);
+        return f.status;
+    }
+}
+
+extern "C" int satori_hip_bitplane_from_ternary2(int rows, int columns, int block_size, const void* ternary2,
+                                                 size_t ternary2_length, void* bitplane, size_t bitplane_length) {
+    try {
+        const Shape s = ternary2_shape(rows, columns, block_size);
+        if (!ternary2 || !bitplane) fail(SATORI_HIP_E_ARGUMENT_NULL, "Value cannot be null.");
+        if (static_cast<int64_t>(ternary2_length) != s.byte_length || static_cast<int64_t>(bitplane_length) != s.byte_length)
+            fail(SATORI_HIP_E_ARGUMENT, "Payload length must match matrix dimensions.");
+        validate_ternary2(s, static_cast<const uint8_t*>(ternary2));
+        bitplane_from_ternary2(s, static_cast<const uint8_t*>(ternary2), static_cast<uint8_t*>(bitplane));
+        return SATORI_HIP_OK;
+    } catch (const Failure& f) {
+        record_error(f.message);
+        return f.status;
+    }
+}
+
+extern "C" int satori_hip_bitplane_to_ternary2(int rows, int columns, int block_size, const void* bitplane,
+                                               size_t bitplane_length, void* ternary2, size_t ternary2_length) {
+    try {
+        const Shape s = ternary2_shape(rows, columns, block_size);
+        if (!ternary2 || !bitplane) fail(SATORI_HIP_E_ARGUMENT_NULL, "Value cannot be null.");
+        if (static_cast<int64_t>(ternary2_length) != s.byte_length || static_cast<int64_t>(bitplane_length) != s.byte_length)
+            fail(SATORI_HIP_E_ARGUMENT, "Payload length must match matrix dimensions.");
+        validate_bitplane(s, static_cast<const uint8_t*>(bitplane));
+        bitplane_to_ternary2(s, static_cast<const uint8_t*>(bitplane), static_cast<uint8_t*>(ternary2));
+        return SATORI_HIP_OK;
+    } catch (const Failure& f) {
+        record_error(f.message);
         return f.status;
     }
 }

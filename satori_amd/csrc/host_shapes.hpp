@@ -20,6 +20,9 @@ struct Failure {
 
 [[noreturn]] inline void fail(int status, std::string message) { throw Failure{status, std::move(message)}; }
 
+// Sets the calling thread's satori_hip_last_error() message (defined with the runtime).
+void record_error(const std::string& message);
+
 inline float f32_at(const uint8_t* p) {
     float f;
     std::memcpy(&f, p, 4);
@@ -80,6 +83,62 @@ inline Shape ternary2_shape(int rows, int columns, int block_size) {
     s.byte_length = static_cast<int64_t>(rows) * s.row_bytes;
     if (s.byte_length > INT32_MAX) fail(SATORI_HIP_E_OVERFLOW, "Arithmetic operation resulted in an overflow.");
     return s;
+}
+
+// Ternary bitplane blocks (src/Satori.Core/TernaryBitplaneMatrix.cs): the FP32 scale, then B/8 bytes of
+// positive-plane bits and B/8 bytes of negative-plane bits (bit i % 8 of byte i / 8 is weight i). Same shape
+// and byte length as Ternary2.
+
+// TernaryBitplaneMatrix.Validate (TernaryBitplaneMatrix.cs:64-85).
+inline void validate_bitplane(const Shape& s, const uint8_t* data) {
+    const int plane = s.block_size / 8;
+    for (int row = 0; row < s.rows; ++row)
+        for (int block = 0; block < s.blocks; ++block) {
+            const uint8_t* bytes = data + row * s.row_bytes + static_cast<int64_t>(block) * s.block_bytes;
+            float scale;
+            std::memcpy(&scale, bytes, 4);
+            uint32_t bits;
+            std::memcpy(&bits, bytes, 4);
+            if (!std::isfinite(scale) || scale < 0 || bits == 0x80000000u)
+                fail(SATORI_HIP_E_ARGUMENT, "Invalid bitplane scale. (Parameter 'data')");
+            const int count = std::min(s.block_size, s.columns - block * s.block_size);
+            for (int i = 0; i < plane; ++i) {
+                const int positive = bytes[4 + i], negative = bytes[4 + plane + i];
+                const int valid = std::clamp(count - i * 8, 0, 8);
+                const int padding = ~((1 << valid) - 1);
+                if ((positive & negative) != 0 || ((positive | negative) & padding) != 0 ||
+                    (scale == 0 && (positive | negative) != 0))
+                    fail(SATORI_HIP_E_ARGUMENT,
+                         "Overlapping bits, invalid padding or noncanonical zero. (Parameter 'data')");
+            }
+        }
+}
+
+// TernaryBitplaneMatrix.FromTernary2 (TernaryBitplaneMatrix.cs:19-36), on a validated Ternary2 payload.
+inline void bitplane_from_ternary2(const Shape& s, const uint8_t* t2, uint8_t* out) {
+    const int plane = s.block_size / 8;
+    std::memset(out, 0, static_cast<size_t>(s.byte_length));
+    for (int64_t offset = 0; offset < s.byte_length; offset += s.block_bytes) {
+        std::memcpy(out + offset, t2 + offset, 4);
+        for (int i = 0; i < s.block_size; ++i) {
+            const int code = (t2[offset + 4 + i / 4] >> (2 * (i % 4))) & 3;
+            if (code != 0) out[offset + 4 + (code == 2 ? plane : 0) + i / 8] |= static_cast<uint8_t>(1 << (i % 8));
+        }
+    }
+}
+
+// TernaryBitplaneMatrix.ToTernary2 (TernaryBitplaneMatrix.cs:38-54), on a validated bitplane payload.
+inline void bitplane_to_ternary2(const Shape& s, const uint8_t* tb, uint8_t* out) {
+    const int plane = s.block_size / 8;
+    std::memset(out, 0, static_cast<size_t>(s.byte_length));
+    for (int64_t offset = 0; offset < s.byte_length; offset += s.block_bytes) {
+        std::memcpy(out + offset, tb + offset, 4);
+        for (int i = 0; i < s.block_size; ++i) {
+            const int positive = (tb[offset + 4 + i / 8] >> (i % 8)) & 1;
+            const int negative = (tb[offset + 4 + plane + i / 8] >> (i % 8)) & 1;
+            out[offset + 4 + i / 4] |= static_cast<uint8_t>((positive | negative << 1) << (2 * (i % 4)));
+        }
+    }
 }
 
 // QuantizedMatrixShape (src/Satori.Core/QuantizedMatrixShape.cs:5-22).

@@ -24,6 +24,12 @@ namespace {
 
 thread_local std::string g_last_error;
 
+}  // namespace
+
+void record_error(const std::string& message) { g_last_error = message; }
+
+namespace {
+
 // Slack after every payload: the misaligned-block loaders read up to 4 bytes past a block.
 constexpr size_t kPayloadSlack = 256;
 
@@ -400,6 +406,73 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
     }
 }
 
+// A whole file mapped read-only for the duration of a call.
+struct MappedFile {
+    const uint8_t* bytes = nullptr;
+    size_t length = 0;
+    explicit MappedFile(const char* path) {
+        const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+        if (fd < 0) fail(SATORI_HIP_E_ARGUMENT, std::string("Cannot open ") + path + ".");
+        struct stat st;
+        if (::fstat(fd, &st) != 0) {
+            ::close(fd);
+            fail(SATORI_HIP_E_ARGUMENT, std::string("Cannot stat ") + path + ".");
+        }
+        length = static_cast<size_t>(st.st_size);
+        if (length > 0) {
+            void* map = ::mmap(nullptr, length, PROT_READ, MAP_PRIVATE, fd, 0);
+            if (map == MAP_FAILED) {
+                ::close(fd);
+                fail(SATORI_HIP_E_ARGUMENT, std::string("Cannot map ") + path + ".");
+            }
+            bytes = static_cast<const uint8_t*>(map);
+        }
+        ::close(fd);
+    }
+    ~MappedFile() {
+        if (bytes) ::munmap(const_cast<uint8_t*>(bytes), length);
+    }
+};
+
+// TernaryBitplaneMatrix.Load (src/Satori.Core/TernaryBitplaneMatrix.cs:98-117) with
+// TernaryBitplaneFileFormat.ReadHeader (src/Satori.Core/TernaryBitplaneFileFormat.cs:13-19): the STQ2 header
+// with magic "STB1"; every failure is InvalidDataException. Returns the shape of a valid file.
+Shape read_bitplane_file(const MappedFile& f) {
+    if (f.length < 32) fail(SATORI_HIP_E_INVALID_DATA, "Truncated bitplane header.");
+    const uint8_t* h = f.bytes;
+    if (std::memcmp(h, "STB1", 4) != 0) fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane magic.");
+    int32_t rows, columns, block, reserved;
+    int64_t declared;
+    std::memcpy(&rows, h + 8, 4);
+    std::memcpy(&columns, h + 12, 4);
+    std::memcpy(&block, h + 16, 4);
+    std::memcpy(&reserved, h + 20, 4);
+    std::memcpy(&declared, h + 24, 8);
+    if (u16_at(h + 4) != 1 || u16_at(h + 6) != 32 || reserved != 0)
+        fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane header fields.");
+    Shape s;
+    try {
+        s = ternary2_shape(rows, columns, block);
+        if (declared != s.byte_length) fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane header fields.");
+        if (static_cast<int64_t>(f.length) != 32 + s.byte_length)
+            fail(SATORI_HIP_E_INVALID_DATA, "Incorrect bitplane file length.");
+        validate_bitplane(s, h + 32);
+    } catch (const Failure& e) {
+        if (e.status == SATORI_HIP_E_ARGUMENT || e.status == SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE ||
+            e.status == SATORI_HIP_E_OVERFLOW)
+            fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane file.");
+        throw;
+    }
+    return s;
+}
+
+// A bitplane payload executes as its lossless Ternary2 equivalent (same bytes per block, same scales).
+satori_hip_matrix* upload_bitplane(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
+    std::vector<uint8_t> ternary(static_cast<size_t>(s.byte_length));
+    bitplane_to_ternary2(s, payload, ternary.data());
+    return upload(c, s, ternary.data());
+}
+
 const satori::GgufFile& live_file(const satori_hip_gguf* f) {
     require(f, "file");
     if (!f->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'GgufFile'.");
@@ -590,6 +663,55 @@ int satori_hip_ternary2_open(satori_hip_context* c, const char* path, satori_hip
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(c);
         *matrix = upload(c, s, h + 32);
+    });
+}
+
+int satori_hip_bitplane_create(satori_hip_context* c, int rows, int columns, int block_size, const void* payload,
+                               size_t payload_length, satori_hip_matrix** matrix) {
+    return guarded([&] {
+        require(matrix, "matrix");
+        *matrix = nullptr;
+        require_live(c);
+        const Shape s = ternary2_shape(rows, columns, block_size);
+        require(payload, "payload");
+        if (static_cast<int64_t>(payload_length) != s.byte_length)
+            fail(SATORI_HIP_E_ARGUMENT, "Incorrect bitplane payload length. (Parameter 'payload')");
+        validate_bitplane(s, static_cast<const uint8_t*>(payload));
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        *matrix = upload_bitplane(c, s, static_cast<const uint8_t*>(payload));
+    });
+}
+
+int satori_hip_bitplane_open(satori_hip_context* c, const char* path, satori_hip_matrix** matrix) {
+    return guarded([&] {
+        require(matrix, "matrix");
+        *matrix = nullptr;
+        require_live(c);
+        require(path, "path");
+        MappedFile f(path);
+        const Shape s = read_bitplane_file(f);
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        *matrix = upload_bitplane(c, s, f.bytes + 32);
+    });
+}
+
+int satori_hip_bitplane_load(const char* path, int* rows, int* columns, int* block_size, void* payload,
+                             size_t capacity, int64_t* length) {
+    return guarded([&] {
+        require(path, "path");
+        MappedFile f(path);
+        const Shape s = read_bitplane_file(f);
+        if (rows) *rows = s.rows;
+        if (columns) *columns = s.columns;
+        if (block_size) *block_size = s.block_size;
+        if (length) *length = s.byte_length;
+        if (payload) {
+            if (static_cast<int64_t>(capacity) < s.byte_length)
+                fail(SATORI_HIP_E_ARGUMENT, "Destination is too short. (Parameter 'payload')");
+            std::memcpy(payload, f.bytes + 32, static_cast<size_t>(s.byte_length));
+        }
     });
 }
 

@@ -823,3 +823,58 @@ def test_golden_gguf_file_through_the_container(context):
                                          np.ones(m.shape.columns, np.float32))
             assert np.array_equal(y, expected) and y.tolist() == [-8.0], name
             m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# Ternary bitplane layout (executes as its lossless Ternary2 equivalent)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_bitplane_same_corpus_and_results_as_ternary2_including_tails(context, block):
+    # TernaryBitplaneAvx2Tests.cs:7-47: the bitplane product equals the Ternary2 product of the same weights
+    # (here bit for bit on the device) and stays within the NumericalValidation bound of the FP64 product;
+    # corpus cases plus column tails 1..17, 31..33, 63..65, 127..129, 255..257.
+    cases = [(name, w, x) for name, w, x in _critical_cases(block)]
+    for columns in list(range(1, 18)) + [31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257]:
+        w, x = O.corpus_random_matrix(3, columns)
+        cases.append((f"C={columns}", w, x))
+    for name, w, x in cases:
+        rows, columns = w.shape
+        t2 = S.Ternary2Matrix.quantize(w, rows, columns, block)
+        tb = S.TernaryBitplaneMatrix.from_ternary2(t2)
+        y_t2, y_tb = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+        with context.create_ternary2(rows, columns, block, t2.data) as m:
+            m.execute(x, y_t2)
+        S.TernaryBitplaneMatVec.execute(tb, x, y_tb, context)
+        assert np.array_equal(y_t2.view(np.uint32), y_tb.view(np.uint32)), name
+        wq = O.t2_dequantize(t2.data, rows, columns, block).reshape(rows, columns)
+        assert_within(y_tb, fp64_matvec(wq, x), ternary2_bound(wq, x, block), f"{name} B{block}")
+        scalar = O.tb_matvec_scalar(tb.data, rows, columns, block, x)
+        assert_within(y_tb, scalar, relative_bound(wq, x) + (columns + 8) * TINY, f"{name} B{block} vs scalar")
+        tb.device(context).dispose()
+
+
+def test_bitplane_file_opens_to_the_same_device_matrix(context, tmp_path):
+    # TernaryBitplaneMatrix.Load (TernaryBitplaneMatrix.cs:98-117) then execution: the STB1 file, opened on
+    # the device, gives the same outputs as the owned matrix; a corrupt file is InvalidData.
+    g = rng(1234)
+    rows, columns, block = 4099, 1000, 128
+    w = g.standard_normal((rows, columns)).astype(np.float32)
+    tb = S.TernaryBitplaneMatrix.from_ternary2(S.Ternary2Matrix.quantize(w, rows, columns, block))
+    path = str(tmp_path / "w.stb1")
+    tb.save(path)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    y_owned, y_file = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+    S.TernaryBitplaneMatVec.execute(tb, x, y_owned, context)
+    with context.open_bitplane(path) as m:
+        assert (m.rows, m.columns, m.byte_length) == (rows, columns, tb.byte_length)
+        m.execute(x, y_file)
+    assert np.array_equal(y_owned.view(np.uint32), y_file.view(np.uint32))
+    with open(path, "r+b") as f:
+        f.seek(32 + 4)  # first block: set a bit in both planes
+        f.write(bytes([0xFF]))
+        f.seek(32 + 4 + block // 8)
+        f.write(bytes([0xFF]))
+    with pytest.raises(S.InvalidDataException):
+        context.open_bitplane(path)
+    tb.device(context).dispose()
