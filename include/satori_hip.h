@@ -230,6 +230,36 @@ int satori_hip_ternary2_quantize(const float* weights, int rows, int columns, in
 int satori_hip_quantize_weights(int format, const float* weights, int rows, int columns, void* payload,
                                 size_t payload_length);
 
+/* ---- decode-step operators (src/Satori.Core/TransformerOps.cs), device pointers ----
+ * Enqueued on `stream` (NULL: the context stream), like the *_device MatVec calls. Each computes in FP64 as
+ * the reference does and rounds its outputs to FP32 once; outputs agree with the reference's to about one
+ * unit in the last place (Add exactly). Argument checks and their exceptions follow the reference. */
+/* RmsNorm (TransformerOps.cs:13-21) over `count` consecutive vectors of `length`; output == input allowed. */
+int satori_hip_rms_norm(satori_hip_context* context, const float* input, const float* weights, float epsilon,
+                        int length, int count, float* output, void* stream);
+/* RmsNormHeads (TransformerOps.cs:117-130), in place. */
+int satori_hip_rms_norm_heads(satori_hip_context* context, float* vector, const float* weights, float epsilon,
+                              int head_dim, int length, void* stream);
+/* Rope (TransformerOps.cs:23-38, pairs (j, j + 1), base 10000) and RopeHalf (:94-114), in place. */
+int satori_hip_rope(satori_hip_context* context, float* vector, int length, int head_dim, int position, void* stream);
+int satori_hip_rope_half(satori_hip_context* context, float* vector, int length, int head_dim, int position,
+                         double frequency_base, int rotary_dimensions, void* stream);
+/* SwiGlu (TransformerOps.cs:40-50) and Add (:52-57); output may equal an input. */
+int satori_hip_swiglu(satori_hip_context* context, const float* gate, const float* up, int length, float* output,
+                      void* stream);
+int satori_hip_add(satori_hip_context* context, const float* left, const float* right, int length, float* output,
+                   void* stream);
+/* GroupedAttention (TransformerOps.cs:135-179; Attention :61-91 is query_heads == kv_heads): keys/values
+ * token-major [tokens][kv_heads * head_dim]. The scores live on the device (no scratch argument); at most
+ * 8192 tokens per call (SATORI_HIP_E_NOT_SUPPORTED beyond). */
+int satori_hip_grouped_attention(satori_hip_context* context, const float* query, const float* keys,
+                                 const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
+                                 float* output, void* stream);
+/* GgufQuantizedMatrix.ReadRow (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:54-61): row `row` of a resident
+ * Q8_0 / Q4_K / Q6_K matrix decoded to FP32 `columns` floats (QuantizedRow.DecodeRow), bit-identical to the
+ * reference's decode. Q4_0 and Ternary2 fail with SATORI_HIP_E_NOT_SUPPORTED. */
+int satori_hip_matrix_decode_row(satori_hip_matrix* matrix, int row, float* output, void* stream);
+
 /* ---- GGUF containers (src/Satori.Formats.Gguf) ----
  * A GGUF v3 file mapped read-only and its catalogue parsed strictly, with the reference's limits and
  * failure kinds: GgufFile(path) and GgufFile.Parse (src/Satori.Formats.Gguf/GgufFile.cs:17-35, 78-176),

@@ -71,6 +71,14 @@ def _declare(l):
         "or_stq2_write_header": (None, [P, I, I, I]),
         "or_stq2_read_header": (I, [P, P, P, P]),
         "or_tb_validate": (I, [P, SZ, I, I, I]),
+        "or_rms_norm": (None, [P, P, ctypes.c_float, I, P]),
+        "or_rms_norm_heads": (None, [P, P, ctypes.c_float, I, I]),
+        "or_rope": (None, [P, I, I, I]),
+        "or_rope_half": (None, [P, I, I, I, ctypes.c_double, I]),
+        "or_swiglu": (None, [P, P, I, P]),
+        "or_add": (None, [P, P, I, P]),
+        "or_grouped_attention": (None, [P, P, P, I, I, I, I, P, P]),
+        "or_q_decode_row": (None, [P, I, I, P]),
         "or_tb_from_t2": (None, [P, I, I, I, P]),
         "or_tb_to_t2": (None, [P, I, I, I, P]),
         "or_tb_matvec_scalar": (None, [P, I, I, I, P, P]),
@@ -329,3 +337,60 @@ def corpus_random_matrix(rows: int, columns: int):
     x = np.zeros(columns, dtype=np.float32)
     lib().or_corpus_random_matrix(rows, columns, _ptr(w), _ptr(x))
     return w.reshape(rows, columns), x
+
+
+# ---- TransformerOps (FP64 restatements) ----
+
+def rms_norm(x, weights, epsilon: float) -> np.ndarray:
+    xv, wv = _f32(x), _f32(weights)
+    out = np.zeros(xv.size, dtype=np.float32)
+    lib().or_rms_norm(_ptr(xv), _ptr(wv), epsilon, xv.size, _ptr(out))
+    return out
+
+
+def rms_norm_heads(vector, weights, epsilon: float, head_dim: int) -> np.ndarray:
+    v = _f32(vector).copy()
+    wv = _f32(weights)
+    lib().or_rms_norm_heads(_ptr(v), _ptr(wv), epsilon, head_dim, v.size)
+    return v
+
+
+def rope(vector, head_dim: int, position: int) -> np.ndarray:
+    v = _f32(vector).copy()
+    lib().or_rope(_ptr(v), v.size, head_dim, position)
+    return v
+
+
+def rope_half(vector, head_dim: int, position: int, base: float, rotary: int) -> np.ndarray:
+    v = _f32(vector).copy()
+    lib().or_rope_half(_ptr(v), v.size, head_dim, position, base, rotary)
+    return v
+
+
+def swiglu(gate, up) -> np.ndarray:
+    g, u = _f32(gate), _f32(up)
+    out = np.zeros(g.size, dtype=np.float32)
+    lib().or_swiglu(_ptr(g), _ptr(u), g.size, _ptr(out))
+    return out
+
+
+def add(left, right) -> np.ndarray:
+    a, b = _f32(left), _f32(right)
+    out = np.zeros(a.size, dtype=np.float32)
+    lib().or_add(_ptr(a), _ptr(b), a.size, _ptr(out))
+    return out
+
+
+def grouped_attention(query, keys, values, query_heads: int, kv_heads: int, head_dim: int, tokens: int) -> np.ndarray:
+    q, k, v = _f32(query), _f32(keys), _f32(values)
+    scores = np.zeros(max(tokens, 1), dtype=np.float64)
+    out = np.zeros(q.size, dtype=np.float32)
+    lib().or_grouped_attention(_ptr(q), _ptr(k), _ptr(v), query_heads, kv_heads, head_dim, tokens, _ptr(scores), _ptr(out))
+    return out
+
+
+def q_decode_row(row, columns: int, fmt: int) -> np.ndarray:
+    r = _u8(row)
+    out = np.zeros(columns, dtype=np.float32)
+    lib().or_q_decode_row(_ptr(r), columns, fmt, _ptr(out))
+    return out

@@ -673,3 +673,97 @@ void or_corpus_random_matrix(int rows, int columns, float* weights, float* input
     for (int64_t i = 0; i < n; i++) weights[i] = corpus_next(&state) * 2;
     for (int i = 0; i < columns; i++) input[i] = corpus_next(&state);
 }
+
+/* ---- TransformerOps (src/Satori.Core/TransformerOps.cs) ---- */
+
+/* RmsNorm (TransformerOps.cs:13-21). */
+void or_rms_norm(const float* input, const float* weights, float epsilon, int length, float* output) {
+    double sum = 0;
+    for (int i = 0; i < length; i++) sum += (double)input[i] * input[i];
+    double scale = 1 / sqrt(sum / length + epsilon);
+    for (int i = 0; i < length; i++) output[i] = (float)(input[i] * scale * weights[i]);
+}
+
+/* RmsNormHeads (TransformerOps.cs:117-130). */
+void or_rms_norm_heads(float* vector, const float* weights, float epsilon, int head_dim, int length) {
+    for (int start = 0; start < length; start += head_dim) {
+        double sum = 0;
+        for (int i = 0; i < head_dim; i++) sum += (double)vector[start + i] * vector[start + i];
+        double scale = 1 / sqrt(sum / head_dim + epsilon);
+        for (int i = 0; i < head_dim; i++) vector[start + i] = (float)(vector[start + i] * scale * weights[i]);
+    }
+}
+
+/* Rope (TransformerOps.cs:23-38): interleaved pairs (j, j + 1). */
+void or_rope(float* vector, int length, int head_dim, int position) {
+    for (int j = 0; j < head_dim; j += 2) {
+        double angle = position / pow(10000, (double)j / head_dim);
+        double sn = sin(angle), cs = cos(angle);
+        for (int start = 0; start < length; start += head_dim) {
+            double x = vector[start + j], y = vector[start + j + 1];
+            vector[start + j] = (float)(x * cs - y * sn);
+            vector[start + j + 1] = (float)(x * sn + y * cs);
+        }
+    }
+}
+
+/* RopeHalf (TransformerOps.cs:94-114): pairs (k, k + half) of the first `rotary` lanes of each head. */
+void or_rope_half(float* vector, int length, int head_dim, int position, double base, int rotary) {
+    int half = rotary / 2;
+    for (int k = 0; k < half; k++) {
+        double angle = position / pow(base, 2.0 * k / rotary);
+        double sn = sin(angle), cs = cos(angle);
+        for (int start = 0; start < length; start += head_dim) {
+            double x = vector[start + k], y = vector[start + k + half];
+            vector[start + k] = (float)(x * cs - y * sn);
+            vector[start + k + half] = (float)(x * sn + y * cs);
+        }
+    }
+}
+
+/* SwiGlu (TransformerOps.cs:40-50): the sigmoid branch keeps exp's argument non-positive. */
+void or_swiglu(const float* gate, const float* up, int length, float* output) {
+    for (int i = 0; i < length; i++) {
+        double x = gate[i];
+        double sigmoid = x >= 0 ? 1 / (1 + exp(-x)) : exp(x) / (1 + exp(x));
+        output[i] = (float)(x * sigmoid * up[i]);
+    }
+}
+
+/* Add (TransformerOps.cs:52-57): FP32 sums. */
+void or_add(const float* left, const float* right, int length, float* output) {
+    for (int i = 0; i < length; i++) output[i] = left[i] + right[i];
+}
+
+/* GroupedAttention (TransformerOps.cs:135-179); Attention (:61-91) is the case query_heads == kv_heads. */
+void or_grouped_attention(const float* query, const float* keys, const float* values, int query_heads,
+                          int kv_heads, int head_dim, int tokens, double* scores, float* output) {
+    int kv_width = kv_heads * head_dim, group = query_heads / kv_heads;
+    double scale = 1 / sqrt(head_dim);
+    for (int head = 0; head < query_heads; head++) {
+        int kv_head = head / group, q_offset = head * head_dim;
+        double max = -INFINITY;
+        for (int token = 0; token < tokens; token++) {
+            int k_offset = token * kv_width + kv_head * head_dim;
+            double dot = 0;
+            for (int j = 0; j < head_dim; j++) dot += (double)query[q_offset + j] * keys[k_offset + j];
+            scores[token] = dot * scale;
+            max = max > scores[token] ? max : scores[token];
+        }
+        double total = 0;
+        for (int token = 0; token < tokens; token++) total += scores[token] = exp(scores[token] - max);
+        for (int j = 0; j < head_dim; j++) {
+            double sum = 0;
+            for (int token = 0; token < tokens; token++)
+                sum += scores[token] / total * values[token * kv_width + kv_head * head_dim + j];
+            output[q_offset + j] = (float)sum;
+        }
+    }
+}
+
+/* QuantizedRow.DecodeRow (src/Satori.Core/QuantizedRow.cs:59-70) through the block decoders. */
+void or_q_decode_row(const uint8_t* row, int columns, int format, float* output) {
+    int elements = format == 2 || format == 3 ? 256 : 32;
+    int bytes = format == 0 ? 34 : format == 1 ? 18 : format == 2 ? 144 : 210;
+    for (int b = 0; b < columns / elements; b++) or_q_decode_block(row + (int64_t)b * bytes, format, output + (int64_t)b * elements);
+}

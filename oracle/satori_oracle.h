@@ -81,6 +81,18 @@ void or_qk_matvec_quantized_avx2(const uint8_t* weights, int rows, int columns, 
                                  const uint8_t* activations, float* y);
 
 /* NumericalCorpus.RandomMatrix: xorshift32 seed 1729 corpus (weights then input). */
+/* TransformerOps (src/Satori.Core/TransformerOps.cs): FP64 arithmetic in the reference's order, FP32 out. */
+void or_rms_norm(const float* input, const float* weights, float epsilon, int length, float* output);
+void or_rms_norm_heads(float* vector, const float* weights, float epsilon, int head_dim, int length);
+void or_rope(float* vector, int length, int head_dim, int position);
+void or_rope_half(float* vector, int length, int head_dim, int position, double base, int rotary);
+void or_swiglu(const float* gate, const float* up, int length, float* output);
+void or_add(const float* left, const float* right, int length, float* output);
+void or_grouped_attention(const float* query, const float* keys, const float* values, int query_heads,
+                          int kv_heads, int head_dim, int tokens, double* scores, float* output);
+/* QuantizedRow.DecodeRow (src/Satori.Core/QuantizedRow.cs:59-70). */
+void or_q_decode_row(const uint8_t* row, int columns, int format, float* output);
+
 void or_corpus_random_matrix(int rows, int columns, float* weights, float* input);
 
 #ifdef __cplusplus

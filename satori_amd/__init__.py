@@ -34,7 +34,7 @@ __all__ = [
     "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "HipStep", "Q8KCodec", "TERNARY2",
     "device_count", "default_context", "payload_length", "quantize_weights",
     "GgufFile", "GgufTensor", "GgufMetadata", "GgufQuantizedMatrix", "GgufWeightStore",
-    "TernaryBitplaneMatrix", "TernaryBitplaneMatVec",
+    "TernaryBitplaneMatrix", "TernaryBitplaneMatVec", "TransformerOps",
 ]
 
 TERNARY2 = 16
@@ -313,6 +313,20 @@ class HipQuantizedMatrix:
     def execute_batch_device(self, input_ptr: int, positions: int, output_ptr: int, stream: int = 0) -> None:
         _check(_ffi.lib().satori_hip_matvec_batch_device(self._handle, ctypes.c_void_p(input_ptr), positions,
                                                          ctypes.c_void_p(output_ptr), ctypes.c_void_p(stream)))
+
+    def decode_row_device(self, row: int, output_ptr: int, stream: int = 0) -> None:
+        """GgufQuantizedMatrix.ReadRow on the device: row `row` decoded to FP32 at output_ptr (columns floats)."""
+        _check(_ffi.lib().satori_hip_matrix_decode_row(self._handle, row, ctypes.c_void_p(output_ptr),
+                                                       ctypes.c_void_p(stream)))
+
+    def read_row(self, row: int, output) -> None:
+        """GgufQuantizedMatrix.ReadRow (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:54-61)."""
+        out = _as_f32(output)
+        if out.size != self.columns:
+            raise ArgumentOutOfRangeException("Specified argument was out of the range of valid values. (Parameter 'row')")
+        with _DeviceArrays(self.context, out) as (dy,):
+            self.decode_row_device(row, dy)
+            self.context.download(out, dy)
 
     def clone(self) -> "HipQuantizedMatrix":
         handle = ctypes.c_void_p()
@@ -794,3 +808,124 @@ class GgufWeightStore:
             for m in self._matrices.values():
                 m.dispose()
             self._matrices.clear()
+
+
+# ---- decode-step operators (src/Satori.Core/TransformerOps.cs) ----
+
+class _DeviceArrays:
+    """Device copies of host float arrays for one operator call (freed on exit)."""
+
+    def __init__(self, context: "HipContext", *arrays):
+        self.context, self.arrays, self.ptrs = context, arrays, []
+
+    def __enter__(self):
+        for a in self.arrays:
+            p = self.context.alloc(max(a.nbytes, 4))
+            self.ptrs.append(p)
+            if a.nbytes:
+                self.context.upload(p, a)
+        return self.ptrs
+
+    def __exit__(self, *exc):
+        self.context.synchronize()
+        for p in self.ptrs:
+            self.context.free(p)
+
+
+class TransformerOps:
+    """src/Satori.Core/TransformerOps.cs:5-180 on the device, over host float32 arrays (each call copies in,
+    runs on the context stream and copies out). The *_device entry points of the library take device pointers
+    for resident pipelines."""
+
+    @staticmethod
+    def _ctx(context):
+        return context or default_context()
+
+    @staticmethod
+    def rms_norm(input, weights, epsilon: float, output, context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        x, w, y = _as_f32(input).reshape(-1), _as_f32(weights).reshape(-1), _as_f32(output).reshape(-1)
+        if x.size != y.size or w.size != y.size:
+            raise ArgumentException("Lengths differ.")
+        with _DeviceArrays(ctx, x, w) as (dx, dw):
+            _check(_ffi.lib().satori_hip_rms_norm(ctx.handle, ctypes.c_void_p(dx), ctypes.c_void_p(dw), float(epsilon),
+                                                  x.size, 1, ctypes.c_void_p(dx), None))
+            ctx.download(y, dx)
+
+    @staticmethod
+    def rms_norm_heads(vector, weights, epsilon: float, head_dimension: int, context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        v, w = _as_f32(vector).reshape(-1), _as_f32(weights).reshape(-1)
+        if w.size != head_dimension and head_dimension > 0 and v.size % head_dimension == 0:
+            raise ArgumentException("Per-head weights must match the head dimension.")
+        with _DeviceArrays(ctx, v, w) as (dv, dw):
+            _check(_ffi.lib().satori_hip_rms_norm_heads(ctx.handle, ctypes.c_void_p(dv), ctypes.c_void_p(dw),
+                                                        float(epsilon), head_dimension, v.size, None))
+            ctx.download(v, dv)
+
+    @staticmethod
+    def rope(vector, head_dimension: int, position: int, context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        v = _as_f32(vector).reshape(-1)
+        with _DeviceArrays(ctx, v) as (dv,):
+            _check(_ffi.lib().satori_hip_rope(ctx.handle, ctypes.c_void_p(dv), v.size, head_dimension, position, None))
+            ctx.download(v, dv)
+
+    @staticmethod
+    def rope_half(vector, head_dimension: int, position: int, frequency_base: float, rotary_dimensions: int,
+                  context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        v = _as_f32(vector).reshape(-1)
+        with _DeviceArrays(ctx, v) as (dv,):
+            _check(_ffi.lib().satori_hip_rope_half(ctx.handle, ctypes.c_void_p(dv), v.size, head_dimension, position,
+                                                   float(frequency_base), rotary_dimensions, None))
+            ctx.download(v, dv)
+
+    @staticmethod
+    def swiglu(gate, up, output, context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        g, u, y = _as_f32(gate).reshape(-1), _as_f32(up).reshape(-1), _as_f32(output).reshape(-1)
+        if g.size != y.size or u.size != y.size:
+            raise ArgumentException("Lengths differ.")
+        with _DeviceArrays(ctx, g, u) as (dg, du):
+            _check(_ffi.lib().satori_hip_swiglu(ctx.handle, ctypes.c_void_p(dg), ctypes.c_void_p(du), g.size,
+                                                ctypes.c_void_p(dg), None))
+            ctx.download(y, dg)
+
+    @staticmethod
+    def add(left, right, output, context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        a, b, y = _as_f32(left).reshape(-1), _as_f32(right).reshape(-1), _as_f32(output).reshape(-1)
+        if a.size != y.size or b.size != y.size:
+            raise ArgumentException("Lengths differ.")
+        with _DeviceArrays(ctx, a, b) as (da, db):
+            _check(_ffi.lib().satori_hip_add(ctx.handle, ctypes.c_void_p(da), ctypes.c_void_p(db), a.size,
+                                             ctypes.c_void_p(da), None))
+            ctx.download(y, da)
+
+    @staticmethod
+    def grouped_attention(query, keys, values, query_heads: int, kv_heads: int, head_dimension: int, token_count: int,
+                          output, context: "HipContext | None" = None) -> None:
+        ctx = TransformerOps._ctx(context)
+        q, k, v, y = (_as_f32(a).reshape(-1) for a in (query, keys, values, output))
+        if head_dimension <= 0 or query_heads <= 0 or kv_heads <= 0 or query_heads % kv_heads or token_count <= 0:
+            raise ArgumentException("Invalid grouped-attention dimensions.")
+        if q.size != query_heads * head_dimension or y.size != q.size:
+            raise ArgumentException("Query or output width does not match the head count.")
+        if k.size != token_count * kv_heads * head_dimension or v.size != k.size:
+            raise ArgumentException("Key/value width does not match the KV head count.")
+        with _DeviceArrays(ctx, q, k, v, y) as (dq, dk, dv, dy):
+            _check(_ffi.lib().satori_hip_grouped_attention(ctx.handle, ctypes.c_void_p(dq), ctypes.c_void_p(dk),
+                                                           ctypes.c_void_p(dv), query_heads, kv_heads, head_dimension,
+                                                           token_count, ctypes.c_void_p(dy), None))
+            ctx.download(y, dy)
+
+    @staticmethod
+    def attention(query, keys, values, head_dimension: int, token_count: int, output,
+                  context: "HipContext | None" = None) -> None:
+        """Attention (TransformerOps.cs:61-91): equal query and key/value heads."""
+        q = _as_f32(query).reshape(-1)
+        if head_dimension <= 0 or q.size == 0 or q.size % head_dimension:
+            raise ArgumentException("Invalid attention dimensions.")
+        heads = q.size // head_dimension
+        TransformerOps.grouped_attention(q, keys, values, heads, heads, head_dimension, token_count, output, context)

@@ -22,6 +22,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "gemv_kmfma.hip", "scale_check.hip",
+           "transformer_ops.hip",
            "host_cpu.cpp", "gguf.cpp"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]

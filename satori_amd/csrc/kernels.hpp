@@ -131,6 +131,21 @@ hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8
                              int blocks, int64_t row_bytes, int positions, hipStream_t stream);
 size_t kmfma_workspace_bytes(int blocks, int positions);
 
+// Decode-step operators (transformer_ops.hip): TransformerOps in FP64 with FP32 outputs, and the embedding row
+// decode of a resident Q8_0 / Q4_K / Q6_K matrix.
+hipError_t launch_rms_norm(const float* x, const float* w, float epsilon, int length, int count, float* y,
+                           hipStream_t stream);
+hipError_t launch_rms_norm_heads(float* v, const float* w, float epsilon, int head_dim, int heads, hipStream_t stream);
+hipError_t launch_rope(float* v, int heads, int head_dim, int position, double base, int rotary, bool half_split,
+                       hipStream_t stream);
+hipError_t launch_swiglu(const float* gate, const float* up, int length, float* out, hipStream_t stream);
+hipError_t launch_add(const float* left, const float* right, int length, float* out, hipStream_t stream);
+int attention_max_tokens();
+hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
+                            int head_dim, int tokens, float* out, hipStream_t stream);
+hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns, int row, float* out,
+                             hipStream_t stream);
+
 // Block-scale finiteness of an uploaded GGUF matrix (device layout; `blocks` = rows * blocks per row): a
 // non-zero *flag afterwards (the caller zeroes it first) means some block has a non-finite scale.
 hipError_t launch_scale_check(const uint8_t* payload, int64_t blocks, int format, uint32_t* flag, hipStream_t stream);

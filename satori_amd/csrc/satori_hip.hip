@@ -1232,4 +1232,169 @@ int satori_hip_gguf_matrix_create(satori_hip_context* c, const satori_hip_gguf* 
     });
 }
 
+// ---- decode-step operators (TransformerOps, src/Satori.Core/TransformerOps.cs), device pointers ----
+
+}  // extern "C"
+
+namespace {
+
+// Ranges [a, a + n) and [b, b + m) of floats overlap without starting at the same element.
+bool partial_overlap(const void* a, int64_t n, const void* b, int64_t m) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    const bool overlap = x < y + static_cast<uintptr_t>(m) * 4 && y < x + static_cast<uintptr_t>(n) * 4;
+    return overlap && x != y;
+}
+
+bool any_overlap(const void* a, int64_t n, const void* b, int64_t m) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return n > 0 && m > 0 && x < y + static_cast<uintptr_t>(m) * 4 && y < x + static_cast<uintptr_t>(n) * 4;
+}
+
+hipStream_t op_stream(satori_hip_context* c, void* stream) {
+    return stream ? static_cast<hipStream_t>(stream) : c->stream;
+}
+
+// Entry-point frame of the operators: context checks and lock, device current, status from the launch.
+template <class F>
+int op_call(satori_hip_context* c, F&& body) {
+    return guarded([&] {
+        require_live(c);
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        set_device(c);
+        body();
+    });
+}
+
+void check_epsilon(float epsilon) {
+    if (!std::isfinite(epsilon) || epsilon <= 0)
+        fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'epsilon')");
+}
+
+}  // namespace
+
+extern "C" {
+
+int satori_hip_rms_norm(satori_hip_context* c, const float* input, const float* weights, float epsilon, int length,
+                        int count, float* output, void* stream) {
+    return op_call(c, [&] {
+        require(input, "input");
+        require(weights, "weights");
+        require(output, "output");
+        if (length <= 0 || count <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'epsilon')");
+        check_epsilon(epsilon);
+        const int64_t n = static_cast<int64_t>(length) * count;
+        if (partial_overlap(input, n, output, n) || any_overlap(weights, length, output, n))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_rms_norm(input, weights, epsilon, length, count, output, op_stream(c, stream)), "rms_norm launch");
+    });
+}
+
+int satori_hip_rms_norm_heads(satori_hip_context* c, float* vector, const float* weights, float epsilon, int head_dim,
+                              int length, void* stream) {
+    return op_call(c, [&] {
+        require(vector, "vector");
+        require(weights, "weights");
+        if (head_dim <= 0 || length <= 0 || length % head_dim != 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'headDimension')");
+        check_epsilon(epsilon);
+        if (any_overlap(weights, head_dim, vector, length)) fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_rms_norm_heads(vector, weights, epsilon, head_dim, length / head_dim, op_stream(c, stream)),
+                  "rms_norm_heads launch");
+    });
+}
+
+int satori_hip_rope(satori_hip_context* c, float* vector, int length, int head_dim, int position, void* stream) {
+    return op_call(c, [&] {
+        require(vector, "vector");
+        if (head_dim <= 0 || head_dim % 2 != 0 || length <= 0 || length % head_dim != 0 || position < 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'headDimension')");
+        check_hip(launch_rope(vector, length / head_dim, head_dim, position, 10000.0, head_dim, false, op_stream(c, stream)),
+                  "rope launch");
+    });
+}
+
+int satori_hip_rope_half(satori_hip_context* c, float* vector, int length, int head_dim, int position,
+                         double frequency_base, int rotary_dimensions, void* stream) {
+    return op_call(c, [&] {
+        require(vector, "vector");
+        if (head_dim <= 0 || length <= 0 || length % head_dim != 0 || position < 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'headDimension')");
+        if (!std::isfinite(frequency_base) || frequency_base <= 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'frequencyBase')");
+        if (rotary_dimensions <= 0 || rotary_dimensions > head_dim || rotary_dimensions % 2 != 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'rotaryDimensions')");
+        check_hip(launch_rope(vector, length / head_dim, head_dim, position, frequency_base, rotary_dimensions, true,
+                              op_stream(c, stream)),
+                  "rope_half launch");
+    });
+}
+
+int satori_hip_swiglu(satori_hip_context* c, const float* gate, const float* up, int length, float* output,
+                      void* stream) {
+    return op_call(c, [&] {
+        require(gate, "gate");
+        require(up, "up");
+        require(output, "output");
+        if (length < 0) fail(SATORI_HIP_E_ARGUMENT, "Lengths differ.");
+        if (partial_overlap(gate, length, output, length) || partial_overlap(up, length, output, length))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        if (length > 0) check_hip(launch_swiglu(gate, up, length, output, op_stream(c, stream)), "swiglu launch");
+    });
+}
+
+int satori_hip_add(satori_hip_context* c, const float* left, const float* right, int length, float* output,
+                   void* stream) {
+    return op_call(c, [&] {
+        require(left, "left");
+        require(right, "right");
+        require(output, "output");
+        if (length < 0) fail(SATORI_HIP_E_ARGUMENT, "Lengths differ.");
+        if (partial_overlap(left, length, output, length) || partial_overlap(right, length, output, length))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        if (length > 0) check_hip(launch_add(left, right, length, output, op_stream(c, stream)), "add launch");
+    });
+}
+
+int satori_hip_grouped_attention(satori_hip_context* c, const float* query, const float* keys, const float* values,
+                                 int query_heads, int kv_heads, int head_dim, int tokens, float* output, void* stream) {
+    return op_call(c, [&] {
+        require(query, "query");
+        require(keys, "keys");
+        require(values, "values");
+        require(output, "output");
+        if (head_dim <= 0 || query_heads <= 0 || kv_heads <= 0 || query_heads % kv_heads != 0 || tokens <= 0)
+            fail(SATORI_HIP_E_ARGUMENT, "Invalid grouped-attention dimensions.");
+        const int64_t width = static_cast<int64_t>(query_heads) * head_dim;
+        const int64_t kv = static_cast<int64_t>(tokens) * kv_heads * head_dim;
+        if (width > INT32_MAX || kv > INT32_MAX) fail(SATORI_HIP_E_OVERFLOW, "Arithmetic operation resulted in an overflow.");
+        if (any_overlap(query, width, output, width) || any_overlap(keys, kv, output, width) ||
+            any_overlap(values, kv, output, width))
+            fail(SATORI_HIP_E_ARGUMENT, "Attention output overlaps input.");
+        if (tokens > attention_max_tokens())
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "At most " + std::to_string(attention_max_tokens()) + " tokens per call.");
+        check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output,
+                                   op_stream(c, stream)),
+                  "attention launch");
+    });
+}
+
+int satori_hip_matrix_decode_row(satori_hip_matrix* m, int row, float* output, void* stream) {
+    return guarded([&] {
+        require(m, "matrix");
+        satori_hip_context* c = m->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(m);
+        require(output, "output");
+        const Shape& s = m->shape;
+        if (s.format == SATORI_HIP_Q4_0) fail(SATORI_HIP_E_NOT_SUPPORTED, "Q4_0 embedding rows are not supported.");
+        if (s.format == SATORI_HIP_TERNARY2) fail(SATORI_HIP_E_NOT_SUPPORTED, "Embedding rows are defined for the GGUF block formats.");
+        if (row < 0 || row >= s.rows)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'row')");
+        set_device(c);
+        check_hip(launch_decode_row(m->payload, s.format, s.rows, s.columns, row, output, op_stream(c, stream)),
+                  "decode_row launch");
+    });
+}
+
 }  // extern "C"

@@ -1,0 +1,249 @@
+// Decode-step operators around the projections, on the device: TransformerOps (src/Satori.Core/TransformerOps.cs)
+// and the embedding-row decode of GgufQuantizedMatrix.ReadRow (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:54-61,
+// QuantizedRow.DecodeRow, src/Satori.Core/QuantizedRow.cs:59-70).
+//
+// The reference computes these in FP64 and rounds each output to FP32 once; the kernels do the same, with
+// every FP64 operation written as the reference writes it (no contraction: the library is compiled with
+// -ffp-contract=off). Where the reference sums sequentially and a kernel reduces in a tree (the RMS sums of
+// squares, the softmax denominator), or where exp / sin / cos / pow come from the device math library, the
+// FP64 intermediate can differ in its last bits; the FP32 outputs then agree to about one unit in the last
+// place. The row decode and Add are FP32 expressions of the reference and agree bit for bit.
+#include <cmath>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace satori {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Sum of one double per thread over the workgroup (tree in LDS, fixed order: deterministic).
+__device__ __forceinline__ double block_sum(double v, double* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ double block_max(double v, double* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = fmax(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+// RmsNorm (TransformerOps.cs:13-21), one workgroup per vector of `length`; output may equal input.
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, const float* __restrict__ w, float epsilon,
+                                                            int length, float* y) {
+    __shared__ double red[kThreads];
+    const float* xv = x + static_cast<int64_t>(blockIdx.x) * length;
+    float* yv = y + static_cast<int64_t>(blockIdx.x) * length;
+    double part = 0;
+    for (int i = threadIdx.x; i < length; i += kThreads) {
+        const double v = xv[i];
+        part = part + v * v;
+    }
+    const double sum = block_sum(part, red);
+    const double scale = 1.0 / __dsqrt_rn(sum / length + static_cast<double>(epsilon));
+    for (int i = threadIdx.x; i < length; i += kThreads)
+        yv[i] = static_cast<float>(static_cast<double>(xv[i]) * scale * static_cast<double>(w[i]));
+}
+
+// RmsNormHeads (TransformerOps.cs:117-130): one workgroup per head, in place.
+__global__ __launch_bounds__(kThreads) void rms_norm_heads_kernel(float* v, const float* __restrict__ w, float epsilon,
+                                                                  int head_dim) {
+    __shared__ double red[kThreads];
+    float* hv = v + static_cast<int64_t>(blockIdx.x) * head_dim;
+    double part = 0;
+    for (int i = threadIdx.x; i < head_dim; i += kThreads) {
+        const double e = hv[i];
+        part = part + e * e;
+    }
+    const double sum = block_sum(part, red);
+    const double scale = 1.0 / __dsqrt_rn(sum / head_dim + static_cast<double>(epsilon));
+    for (int i = threadIdx.x; i < head_dim; i += kThreads)
+        hv[i] = static_cast<float>(static_cast<double>(hv[i]) * scale * static_cast<double>(w[i]));
+}
+
+// Rope (TransformerOps.cs:23-38, pairs (j, j + 1)) and RopeHalf (:94-114, pairs (k, k + half) of the first
+// `rotary` lanes): one thread per (head, pair).
+__global__ __launch_bounds__(kThreads) void rope_kernel(float* v, int heads, int head_dim, int position, double base,
+                                                        int rotary, int half_split) {
+    const int pairs = rotary / 2;
+    const int64_t index = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (index >= static_cast<int64_t>(heads) * pairs) return;
+    const int head = static_cast<int>(index / pairs), k = static_cast<int>(index % pairs);
+    double angle;
+    int a, b;
+    if (half_split) {
+        angle = position / pow(base, 2.0 * k / rotary);
+        a = k;
+        b = k + pairs;
+    } else {
+        const int j = 2 * k;
+        angle = position / pow(10000.0, static_cast<double>(j) / head_dim);
+        a = j;
+        b = j + 1;
+    }
+    const double sn = sin(angle), cs = cos(angle);
+    float* hv = v + static_cast<int64_t>(head) * head_dim;
+    const double x = hv[a], y = hv[b];
+    hv[a] = static_cast<float>(x * cs - y * sn);
+    hv[b] = static_cast<float>(x * sn + y * cs);
+}
+
+// SwiGlu (TransformerOps.cs:40-50) and Add (:52-57), elementwise; output may equal an input.
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(const float* gate, const float* up, int length, float* out) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= length) return;
+    const double x = gate[i];
+    const double sigmoid = x >= 0 ? 1.0 / (1.0 + exp(-x)) : exp(x) / (1.0 + exp(x));
+    out[i] = static_cast<float>(x * sigmoid * static_cast<double>(up[i]));
+}
+
+__global__ __launch_bounds__(kThreads) void add_kernel(const float* left, const float* right, int length, float* out) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= length) return;
+    out[i] = __fadd_rn(left[i], right[i]);
+}
+
+// GroupedAttention (TransformerOps.cs:135-179): one workgroup per query head. The head's scores live in LDS
+// (`tokens` doubles); each dot product runs over the head lanes in order as the reference's, the maximum is
+// exact, the exponentials and their total are FP64, and each output lane sums its tokens in order.
+__global__ __launch_bounds__(kThreads) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                             const float* __restrict__ v, int query_heads, int kv_heads,
+                                                             int head_dim, int tokens, float* __restrict__ out) {
+    extern __shared__ double scores[];  // tokens
+    __shared__ double red[kThreads];
+    const int head = blockIdx.x;
+    const int kv_head = head / (query_heads / kv_heads);
+    const int kv_width = kv_heads * head_dim;
+    const float* qh = q + static_cast<int64_t>(head) * head_dim;
+    const double scale = 1.0 / __dsqrt_rn(static_cast<double>(head_dim));
+    double local_max = -INFINITY;
+    for (int t = threadIdx.x; t < tokens; t += kThreads) {
+        const float* kt = k + static_cast<int64_t>(t) * kv_width + kv_head * head_dim;
+        double dot = 0;
+        for (int j = 0; j < head_dim; ++j) dot = dot + static_cast<double>(qh[j]) * static_cast<double>(kt[j]);
+        const double s = dot * scale;
+        scores[t] = s;
+        local_max = fmax(local_max, s);
+    }
+    const double max = block_max(local_max, red);
+    double part = 0;
+    for (int t = threadIdx.x; t < tokens; t += kThreads) {
+        const double e = exp(scores[t] - max);
+        scores[t] = e;
+        part = part + e;
+    }
+    const double total = block_sum(part, red);  // also orders the exponentials before their use below
+    for (int j = threadIdx.x; j < head_dim; j += kThreads) {
+        double sum = 0;
+        for (int t = 0; t < tokens; ++t)
+            sum = sum + scores[t] / total * static_cast<double>(v[static_cast<int64_t>(t) * kv_width + kv_head * head_dim + j]);
+        out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(sum);
+    }
+}
+
+__device__ __forceinline__ uint32_t byte_at(const uint8_t* p) { return *(const SATORI_GLOBAL uint8_t*)(p); }
+__device__ __forceinline__ uint32_t half_bits_at(const uint8_t* p) { return byte_at(p) | (byte_at(p + 1) << 8); }
+
+// One row of a resident Q8_0 / Q4_K / Q6_K matrix decoded to FP32 (QuantizedRow.DecodeQ8Block,
+// Q4KCodec.DecodeBlock, Q6KCodec.DecodeBlock), one thread per element, reading the device layout (Q6_K
+// regrouped as at upload).
+__global__ __launch_bounds__(kThreads) void decode_row_kernel(const uint8_t* __restrict__ w, int format, int rows,
+                                                              int columns, int row, float* __restrict__ out) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= columns) return;
+    float value;
+    if (format == kQ8_0) {
+        const uint8_t* block = w + (static_cast<int64_t>(row) * (columns / 32) + i / 32) * 34;
+        const float scale = half_bits_to_float(half_bits_at(block));
+        value = scale * static_cast<float>(static_cast<int8_t>(byte_at(block + 2 + i % 32)));
+    } else if (format == kQ4_K) {
+        const uint8_t* block = w + (static_cast<int64_t>(row) * (columns / 256) + i / 256) * 144;
+        const int e = i % 256, group = e / 64, high = (e % 64) / 32, l = e % 32;
+        const u32x4 head = load16_a4(block);
+        int s, m;
+        q4k_scale_min(2 * group + high, head, s, m);
+        const float d = half_bits_to_float(head[0] & 0xFFFFu), dmin = half_bits_to_float(head[0] >> 16);
+        const uint32_t q = (byte_at(block + 16 + 32 * group + l) >> (4 * high)) & 0xF;
+        value = __fsub_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(s)), static_cast<float>(q)),
+                          __fmul_rn(dmin, static_cast<float>(m)));
+    } else {  // Q6_K, regrouped: records of 192 bytes, then 16 scale bytes per block, then the FP16 d values
+        const int64_t count = static_cast<int64_t>(rows) * (columns / 256);
+        const int64_t index = static_cast<int64_t>(row) * (columns / 256) + i / 256;
+        const int e = i % 256, hh = e / 128, kk = (e % 128) / 32, t = (e % 32) / 16, x = e % 16;
+        const int c = 2 * hh + t;
+        const uint8_t* q = w + index * 192 + 48 * c;
+        const uint32_t low = kk & 1 ? byte_at(q + 16 + x) : byte_at(q + x);
+        const uint32_t nib = kk < 2 ? (low & 0xF) : (low >> 4);
+        const uint32_t hb = (byte_at(q + 32 + x) >> (2 * kk)) & 3;
+        const int code = static_cast<int>(nib | (hb << 4)) - 32;
+        const int sc = static_cast<int8_t>(byte_at(w + count * 192 + index * 16 + 4 * c + kk));
+        const float d = half_bits_to_float(half_bits_at(w + count * 208 + index * 2));
+        value = __fmul_rn(__fmul_rn(d, static_cast<float>(sc)), static_cast<float>(code));
+    }
+    out[i] = value;
+}
+
+int grid_for(int64_t n) { return static_cast<int>((n + kThreads - 1) / kThreads); }
+
+}  // namespace
+
+hipError_t launch_rms_norm(const float* x, const float* w, float epsilon, int length, int count, float* y,
+                           hipStream_t stream) {
+    rms_norm_kernel<<<count, kThreads, 0, stream>>>(x, w, epsilon, length, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_heads(float* v, const float* w, float epsilon, int head_dim, int heads, hipStream_t stream) {
+    rms_norm_heads_kernel<<<heads, kThreads, 0, stream>>>(v, w, epsilon, head_dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float* v, int heads, int head_dim, int position, double base, int rotary, bool half_split,
+                       hipStream_t stream) {
+    rope_kernel<<<grid_for(static_cast<int64_t>(heads) * (rotary / 2)), kThreads, 0, stream>>>(
+        v, heads, head_dim, position, base, rotary, half_split ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* gate, const float* up, int length, float* out, hipStream_t stream) {
+    swiglu_kernel<<<grid_for(length), kThreads, 0, stream>>>(gate, up, length, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const float* left, const float* right, int length, float* out, hipStream_t stream) {
+    add_kernel<<<grid_for(length), kThreads, 0, stream>>>(left, right, length, out);
+    return hipGetLastError();
+}
+
+int attention_max_tokens() { return 8192; }  // 64 KB of FP64 scores in LDS
+
+hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
+                            int head_dim, int tokens, float* out, hipStream_t stream) {
+    if (tokens > attention_max_tokens()) return hipErrorInvalidValue;
+    attention_kernel<<<query_heads, kThreads, static_cast<size_t>(tokens) * sizeof(double), stream>>>(
+        q, k, v, query_heads, kv_heads, head_dim, tokens, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns, int row, float* out,
+                             hipStream_t stream) {
+    decode_row_kernel<<<grid_for(columns), kThreads, 0, stream>>>(w, format, rows, columns, row, out);
+    return hipGetLastError();
+}
+
+}  // namespace satori

@@ -878,3 +878,158 @@ def test_bitplane_file_opens_to_the_same_device_matrix(context, tmp_path):
     with pytest.raises(S.InvalidDataException):
         context.open_bitplane(path)
     tb.device(context).dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# Decode-step operators (TransformerOps on the device) and embedding-row decode
+# ---------------------------------------------------------------------------------------------
+
+def _within_fixture(actual, expected, name):
+    # TransformerOpsTests.cs:13-16 / QwenOperatorTests.cs:19-26: |a - e| <= 2e-6 + 2e-6 |e|.
+    actual, expected = np.asarray(actual, np.float64), np.asarray(expected, np.float64)
+    assert np.all(np.isfinite(actual)), name
+    err = np.abs(actual - expected)
+    assert np.all(err <= 2e-6 + 2e-6 * np.abs(expected)), f"{name}: max err {err.max()}"
+
+
+def _within_ulp(actual, expected, name, ulps=1):
+    # FP64 intermediates that differ only in their last bits (tree sums, device exp/sin/cos/pow) round to
+    # FP32 outputs at most one unit in the last place apart.
+    a, e = np.asarray(actual, np.float32), np.asarray(expected, np.float32)
+    spacing = np.spacing(np.maximum(np.abs(a), np.abs(e)).astype(np.float32)).astype(np.float64)
+    err = np.abs(a.astype(np.float64) - e.astype(np.float64))
+    assert np.all(err <= ulps * spacing), f"{name}: max err {err.max()} at {np.argmax(err - ulps * spacing)}"
+
+
+def test_operators_match_reference_fixtures(context):
+    # TransformerOpsTests.cs:8-25 and QwenOperatorTests.cs:28-112 on the device.
+    T = S.TransformerOps
+    d = load_json("transformer-v1.json")
+    f = lambda k: np.array(d[k], np.float32)
+    out = np.zeros(96, np.float32)
+    T.rms_norm(f("x"), f("weights"), 1e-5, out, context)
+    _within_fixture(out, d["rms"], "rms")
+    x = f("x")
+    T.rope(x, 48, 37, context)
+    _within_fixture(x, d["rope"], "rope")
+    out = np.zeros(8, np.float32)
+    T.swiglu(f("gate"), f("up"), out, context)
+    _within_fixture(out, d["swiglu"], "swiglu")
+    out = np.zeros(96, np.float32)
+    T.attention(f("query"), f("keys"), f("values"), 48, 7, out, context)
+    _within_fixture(out, d["attention"], "attention")
+    d2 = load_json("transformer-v2.json")
+    F = lambda v: np.array(v, np.float32)
+    g = d2["gqa"]
+    out = np.zeros(len(g["query"]), np.float32)
+    T.grouped_attention(F(g["query"]), F(g["keys"]), F(g["values"]), g["query_heads"], g["kv_heads"], g["head_dim"],
+                        g["tokens"], out, context)
+    _within_fixture(out, g["output"], "gqa")
+    for key in ("rope_full", "rope_partial"):
+        r = d2[key]
+        v = F(r["input"])
+        T.rope_half(v, r["head_dim"], r["position"], r["base"], r["rotary"], context)
+        _within_fixture(v, r["output"], key)
+    n = d2["qk_norm"]
+    v = F(n["input"])
+    T.rms_norm_heads(v, F(n["weights"]), np.float32(n["epsilon"]), len(n["weights"]), context)
+    _within_fixture(v, n["output"], "qk_norm")
+    b = d2["bias"]
+    out = np.zeros(len(b["base"]), np.float32)
+    T.add(F(b["base"]), F(b["bias"]), out, context)
+    _within_fixture(out, b["output"], "bias")
+
+
+def test_operators_match_oracle_at_decode_sizes(context):
+    # Qwen-1.5B-shaped decode vectors: hidden 1536, FFN 8960, 12 query heads / 2 KV heads of 128 lanes, a KV
+    # prefix of 1 .. 2048 tokens, RoPE base 1e6 at a large position. FP32 outputs within one unit in the
+    # last place of the oracle's; Add exactly.
+    T = S.TransformerOps
+    g = rng(808)
+    x = (g.standard_normal(1536) * 3).astype(np.float32)
+    w = g.uniform(0.5, 1.5, 1536).astype(np.float32)
+    out = np.zeros(1536, np.float32)
+    T.rms_norm(x, w, 1e-6, out, context)
+    _within_ulp(out, O.rms_norm(x, w, np.float32(1e-6)), "rms_norm")
+    q = g.standard_normal(12 * 128).astype(np.float32)
+    for position in (0, 1, 4095, 100000):
+        v = q.copy()
+        T.rope_half(v, 128, position, 1e6, 128, context)
+        _within_ulp(v, O.rope_half(q, 128, position, 1e6, 128), f"rope_half {position}")
+        v = q.copy()
+        T.rope(v, 128, position, context)
+        _within_ulp(v, O.rope(q, 128, position), f"rope {position}")
+    v = q.copy()
+    T.rms_norm_heads(v, w[:128], 1e-6, 128, context)
+    _within_ulp(v, O.rms_norm_heads(q, w[:128], np.float32(1e-6), 128), "rms_norm_heads")
+    gate = (g.standard_normal(8960) * 6).astype(np.float32)
+    up = g.standard_normal(8960).astype(np.float32)
+    out = np.zeros(8960, np.float32)
+    T.swiglu(gate, up, out, context)
+    _within_ulp(out, O.swiglu(gate, up), "swiglu")
+    T.add(gate, up, out, context)
+    assert np.array_equal(out, O.add(gate, up))
+    for tokens in (1, 2, 33, 257, 2048):
+        keys = g.standard_normal(tokens * 256).astype(np.float32)
+        values = g.standard_normal(tokens * 256).astype(np.float32)
+        out = np.zeros(12 * 128, np.float32)
+        T.grouped_attention(q, keys, values, 12, 2, 128, tokens, out, context)
+        _within_ulp(out, O.grouped_attention(q, keys, values, 12, 2, 128, tokens), f"attention {tokens}")
+
+
+def test_operator_extremes_and_argument_errors(context):
+    # TransformerOpsTests.cs:27-53 and QwenOperatorTests.cs:138-144.
+    T = S.TransformerOps
+    fmax = np.finfo(np.float32).max
+    x = np.array([fmax, -fmax], np.float32)
+    out = np.zeros(2, np.float32)
+    T.rms_norm(x, np.ones(2, np.float32), 1e-5, out, context)
+    assert out.tolist() == [1.0, -1.0]
+    out = np.zeros(2, np.float32)
+    T.attention(np.array([fmax, fmax], np.float32), np.array([fmax, fmax, -fmax, -fmax], np.float32),
+                np.array([3, 4, 100, 200], np.float32), 2, 2, out, context)
+    assert out.tolist() == [3.0, 4.0]
+    with pytest.raises(S.ArgumentOutOfRangeException):
+        T.rope(np.zeros(8, np.float32), 3, 0, context)
+    with pytest.raises(S.ArgumentOutOfRangeException):
+        T.rope_half(np.zeros(8, np.float32), 8, 0, 10000, 5, context)
+    with pytest.raises(S.ArgumentOutOfRangeException):
+        T.rms_norm(np.ones(4, np.float32), np.ones(4, np.float32), 0.0, np.zeros(4, np.float32), context)
+    with pytest.raises(S.ArgumentException):
+        T.grouped_attention(np.zeros(32, np.float32), np.zeros(48, np.float32), np.zeros(48, np.float32), 4, 3, 8, 3,
+                            np.zeros(32, np.float32), context)
+    with pytest.raises(S.NotSupportedException):
+        T.attention(np.zeros(2, np.float32), np.zeros(2 * 8193, np.float32), np.zeros(2 * 8193, np.float32), 2, 8193,
+                    np.zeros(2, np.float32), context)
+    # Partial overlap of device ranges is rejected before anything runs (TransformerOps.cs:7-11).
+    import ctypes
+    from satori_amd import _ffi
+    buf = context.alloc(64)
+    status = _ffi.lib().satori_hip_add(context.handle, ctypes.c_void_p(buf), ctypes.c_void_p(buf), 4,
+                                       ctypes.c_void_p(buf + 4), None)
+    assert status == S.ArgumentException.status
+    context.free(buf)
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_K, BQ.Q6_K, BQ.Q4_0])
+def test_embedding_rows_decode_like_the_reference(context, fmt):
+    # GgufQuantizedMatrix.ReadRow (GgufQuantizedMatrix.cs:54-61) / QuantizedRow.DecodeRow: every decoded row
+    # equals the oracle's decode bit for bit (Q6_K from its regrouped device layout); Q4_0 is not supported.
+    g = rng(55)
+    rows, columns = 37, 768
+    w = (g.standard_normal((rows, columns)) * 0.1).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    row_bytes = data.size // rows
+    out = np.zeros(columns, np.float32)
+    if fmt == BQ.Q4_0:
+        with pytest.raises(S.NotSupportedException):
+            m.read_row(0, out)
+    else:
+        for r in (0, 1, 17, rows - 1):
+            m.read_row(r, out)
+            expected = O.q_decode_row(data[r * row_bytes:(r + 1) * row_bytes], columns, int(fmt))
+            assert np.array_equal(out.view(np.uint32), expected.view(np.uint32)), r
+        with pytest.raises(S.ArgumentOutOfRangeException):
+            m.read_row(rows, out)
+    m.dispose()
