@@ -38,12 +38,17 @@ struct Q8_0Chunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
+    // Regrouped device layout: 32-byte code records, then the FP16 scales.
     __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
-        const uint8_t* block = m.w + row * s.row_bytes + chunk * 34;
-        uint32_t head[1];
-        load_unaligned<1>(block, head);
-        r.scale = half_bits_to_float(head[0] & 0xFFFFu);
-        load_unaligned<8>(block + 2, r.q);
+        const int64_t count = static_cast<int64_t>(m.rows) * s.blocks;
+        const int64_t index = static_cast<int64_t>(row) * s.blocks + chunk;
+        const u32x4 a = load16_a4(m.w + index * 32), b = load16_a4(m.w + index * 32 + 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.q[i] = a[i];
+            r.q[4 + i] = b[i];
+        }
+        r.scale = half_bits_to_float(load4_a4(m.w + count * 32 + (index & ~int64_t(1)) * 2) >> (16 * (index & 1)));
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -81,12 +86,14 @@ struct Q4_0Chunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
+    // Regrouped device layout: 16-byte code records, then the FP16 scales.
     __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
-        const uint8_t* block = m.w + row * s.row_bytes + chunk * 18;
-        uint32_t head[1];
-        load_unaligned<1>(block, head);
-        r.scale = half_bits_to_float(head[0] & 0xFFFFu);
-        load_unaligned<4>(block + 2, r.q);
+        const int64_t count = static_cast<int64_t>(m.rows) * s.blocks;
+        const int64_t index = static_cast<int64_t>(row) * s.blocks + chunk;
+        const u32x4 a = load16_a4(m.w + index * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.q[i] = a[i];
+        r.scale = half_bits_to_float(load4_a4(m.w + count * 16 + (index & ~int64_t(1)) * 2) >> (16 * (index & 1)));
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {

@@ -79,6 +79,11 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
 // 48c: ql[64h + 16t, +16), ql[64h + 32 + 16t, +16), qh[32h + 16t, +16)), then n records of 16 scale bytes
 // (quarter c's sc[8h + 2k + t] at 4c + k), then n FP16 d values.
 
+// ---- Q8_0 / Q4_0 device layout ----
+// The same bytes regrouped so that code loads are aligned: for the n = rows * blocks blocks in row-major
+// order, n code records (Q8_0: the 32 signed bytes; Q4_0: the 16 nibble bytes), then the n FP16 scales.
+constexpr int legacy_record_bytes(int format) { return format == kQ8_0 ? 32 : 16; }
+
 // How a Ternary2 launch is cut: workgroups of `waves` waves (one 64-row panel each) take equal ranges of
 // the launch's (panel group, tile) units; items cut between two ranges are finished by a second kernel.
 // The launch needs a device scratch buffer of `scratch_bytes` whose start holds the plan's tables (range

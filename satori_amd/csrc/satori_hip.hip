@@ -290,6 +290,22 @@ std::vector<uint8_t> q6k_regroup(const Shape& s, const uint8_t* packed) {
     return out;
 }
 
+// Regroups a validated Q8_0 / Q4_0 payload into the device layout of kernels.hpp: aligned code records, then
+// the FP16 scales.
+std::vector<uint8_t> legacy_regroup(const Shape& s, const uint8_t* packed) {
+    const int64_t n = static_cast<int64_t>(s.rows) * s.blocks;
+    const int record = legacy_record_bytes(s.format);
+    std::vector<uint8_t> out(static_cast<size_t>(n) * s.block_bytes);
+    uint8_t* codes = out.data();
+    uint8_t* scales = codes + n * record;
+    for (int64_t i = 0; i < n; ++i) {
+        const uint8_t* block = packed + i * s.block_bytes;
+        std::memcpy(scales + i * 2, block, 2);
+        std::memcpy(codes + i * record, block + 2, static_cast<size_t>(record));
+    }
+    return out;
+}
+
 // Device allocations of one matrix: the weights (+ slack) and, for a split Ternary2 plan, its scratch.
 // Executions of one matrix that overlap in time (device entry points on different streams) share that
 // scratch and must be serialised by the caller.
@@ -320,6 +336,8 @@ satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* 
         regrouped = ternary2_panels(s, payload);
     else if (s.format == SATORI_HIP_Q6_K)
         regrouped = q6k_regroup(s, payload);
+    else if (s.format == SATORI_HIP_Q8_0 || s.format == SATORI_HIP_Q4_0)
+        regrouped = legacy_regroup(s, payload);
     if (!regrouped.empty()) {
         source = regrouped.data();
         bytes = static_cast<int64_t>(regrouped.size());

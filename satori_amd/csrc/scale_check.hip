@@ -14,8 +14,8 @@ __device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
     return *(const SATORI_GLOBAL uint16_t*)(p);
 }
 
-// Blocks of the device layout: Q8_0 (34 B), Q4_0 (18 B) and Q4_K (144 B) as uploaded; Q6_K regrouped, with
-// the FP16 d of every block in one array after the codes and scales. A block with a non-finite scale
+// Blocks of the device layout: Q4_K (144 B) as uploaded; Q6_K, Q8_0 and Q4_0 regrouped, with the FP16 scale
+// of every block in one array after the codes (and, for Q6_K, the sub-block scales). A block with a non-finite scale
 // stores its index + 1 into *flag (any one of them: the caller reports the first from the host copy).
 __global__ __launch_bounds__(256) void scale_check_kernel(const uint8_t* __restrict__ payload, int64_t blocks,
                                                           int format, uint32_t* __restrict__ flag) {
@@ -27,8 +27,8 @@ __global__ __launch_bounds__(256) void scale_check_kernel(const uint8_t* __restr
         } else if (format == kQ4_K) {
             const uint8_t* b = payload + 144 * i;
             bad = half_nonfinite(load_u16(b)) || half_nonfinite(load_u16(b + 2));
-        } else {
-            bad = half_nonfinite(load_u16(payload + (format == kQ8_0 ? 34 : 18) * i));
+        } else {  // Q8_0 / Q4_0 regrouped: the FP16 scales follow the code records
+            bad = half_nonfinite(load_u16(payload + blocks * legacy_record_bytes(format) + 2 * i));
         }
         if (bad) *(SATORI_GLOBAL uint32_t*)(flag) = static_cast<uint32_t>(i) + 1u;
     }

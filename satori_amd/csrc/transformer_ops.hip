@@ -160,17 +160,18 @@ __device__ __forceinline__ uint32_t byte_at(const uint8_t* p) { return *(const S
 __device__ __forceinline__ uint32_t half_bits_at(const uint8_t* p) { return byte_at(p) | (byte_at(p + 1) << 8); }
 
 // One row of a resident Q8_0 / Q4_K / Q6_K matrix decoded to FP32 (QuantizedRow.DecodeQ8Block,
-// Q4KCodec.DecodeBlock, Q6KCodec.DecodeBlock), one thread per element, reading the device layout (Q6_K
-// regrouped as at upload).
+// Q4KCodec.DecodeBlock, Q6KCodec.DecodeBlock), one thread per element, reading the device layout (Q8_0 and
+// Q6_K regrouped as at upload).
 __global__ __launch_bounds__(kThreads) void decode_row_kernel(const uint8_t* __restrict__ w, int format, int rows,
                                                               int columns, int row, float* __restrict__ out) {
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= columns) return;
     float value;
-    if (format == kQ8_0) {
-        const uint8_t* block = w + (static_cast<int64_t>(row) * (columns / 32) + i / 32) * 34;
-        const float scale = half_bits_to_float(half_bits_at(block));
-        value = scale * static_cast<float>(static_cast<int8_t>(byte_at(block + 2 + i % 32)));
+    if (format == kQ8_0) {  // regrouped: 32-byte code records, then the FP16 scales
+        const int64_t count = static_cast<int64_t>(rows) * (columns / 32);
+        const int64_t index = static_cast<int64_t>(row) * (columns / 32) + i / 32;
+        const float scale = half_bits_to_float(half_bits_at(w + count * 32 + index * 2));
+        value = scale * static_cast<float>(static_cast<int8_t>(byte_at(w + index * 32 + i % 32)));
     } else if (format == kQ4_K) {
         const uint8_t* block = w + (static_cast<int64_t>(row) * (columns / 256) + i / 256) * 144;
         const int e = i % 256, group = e / 64, high = (e % 64) / 32, l = e % 32;
