@@ -22,6 +22,8 @@
 // groups of 16 weights: one 32x32x16 MFMA per group and a multiply-add by sc_k; the centring sum is an
 // MFMA chain whose weight operand is sc_k repeated over the group. All magnitudes stay below 2^23 before
 // the int24 multiply (|D_j| <= 32 * 15 * 127, |D_k| <= 16 * 63 * 127) and below 2^31 after.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "q8k_device.hpp"
@@ -84,47 +86,26 @@ __global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict
     if (lane == 0) store_f32(scales + (static_cast<int64_t>(b) * tiles + t) * 32 + r, q.scale);
 }
 
-// The data one lane needs for one block: the weights of its row (its k half of every chunk) and the codes
-// and scales of the tile's positions.
+// The weights one lane needs for one block: its row's data for its k half of every chunk.
 struct Q4KRegs {
     u32x4 head;   // d, dmin, packed 6-bit scales and mins
     u32x4 qs[4];  // qs[32g + 16h, +16) for g = 0..3
-    i32x4 c[8];   // codes of sub-block j, this lane's half
-    f32x4 a[4];   // scales of positions 8q + 4h .. + 3
 };
 
 struct Q6KRegs {
     uint32_t qla[4][2], qlb[4][2], qh[4][2];  // this lane's 8 bytes of each quarter's arrays
     u32x4 sc;                                 // quarter c's scale of form kk at byte 4c + kk
     uint32_t dpair;                           // the FP16 d of this block (and its neighbour)
-    long c[16];                               // codes of group k, this lane's half
-    f32x4 a[4];
 };
 
-__device__ __forceinline__ void load_codes_scales(const uint8_t* ct, const float* st, i32x4 (&c)[8], f32x4 (&a)[4]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const u32x4 v = load16_a4(ct + 1024 * j);
-        c[j] = i32x4{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]), static_cast<int>(v[3])};
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(st + 8 * q));
-        a[q] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
-    }
-}
-
-__device__ __forceinline__ void load_block(const uint8_t* wrow, int b, int h, const uint8_t* ct, const float* st,
-                                           Q4KRegs& r) {
+__device__ __forceinline__ void load_weights(const uint8_t* wrow, int b, int h, Q4KRegs& r) {
     const uint8_t* block = wrow + static_cast<int64_t>(b) * 144;
     r.head = load16_a4(block);
 #pragma unroll
     for (int g = 0; g < 4; ++g) r.qs[g] = load16_a4(block + 16 + 32 * g + 16 * h);
-    load_codes_scales(ct, st, r.c, r.a);
 }
 
-__device__ __forceinline__ void load_block(const uint8_t* w, int64_t count, int64_t index, int h, const uint8_t* ct,
-                                           const float* st, Q6KRegs& r) {
+__device__ __forceinline__ void load_weights(const uint8_t* w, int64_t count, int64_t index, int h, Q6KRegs& r) {
     const uint8_t* record = w + index * 192;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -138,15 +119,6 @@ __device__ __forceinline__ void load_block(const uint8_t* w, int64_t count, int6
     }
     r.sc = load16_a4(w + count * 192 + index * 16);
     r.dpair = load4_a4(w + count * 208 + (index & ~int64_t(1)) * 2);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        r.c[k] = static_cast<long>(load8_a8(ct + 512 * k));
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(st + 8 * q));
-        r.a[q] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
-    }
 }
 
 __device__ __forceinline__ uint32_t q6k_form(uint32_t a, uint32_t b, uint32_t hb, int kk) {
@@ -158,11 +130,23 @@ __device__ __forceinline__ uint32_t q6k_form(uint32_t a, uint32_t b, uint32_t hb
     }
 }
 
-// The block's FP32 terms of the lane's 16 (row, position) outputs. A zero activation block contributes +0
-// (the reference skips it, QuantizedKAvx2Kernel.cs:86; adding +0 is the same, since a sum that starts at +0
-// is never -0). The sub-block (group) products are software-pipelined: the MFMA of sub-block j + 1 is issued
-// before the results of j are scaled, and a scheduling barrier per step keeps the compiler from hoisting
-// every MFMA of the block (which would hold all their result tiles in registers at once).
+// A block's packed codes and scales staged in LDS: the 8 KB of codes in operand order, then the tile's 32
+// position scales.
+struct StagedBlock {
+    uint8_t codes[8192];
+    float scales[32];
+};
+
+__device__ __forceinline__ f32x4 staged_scales(const StagedBlock& sb, int q, int h) {
+    return *reinterpret_cast<const f32x4*>(sb.scales + 8 * q + 4 * h);
+}
+
+// The block's FP32 terms of the lane's 16 (row, position) outputs, from the staged codes. A zero activation
+// block contributes +0 or -0 (the reference skips it, QuantizedKAvx2Kernel.cs:86): its scale is 0 and every
+// resident block scale is finite (checked at upload), and adding a zero to a sum that starts at +0 never
+// changes it, since such a sum is never -0. The sub-block (group) products are software-pipelined: the MFMA
+// of sub-block j + 1 is issued before the results of j are scaled, and a scheduling barrier per step keeps
+// the compiler from hoisting every MFMA of the block (which would hold all their result tiles in registers).
 __device__ __forceinline__ i32x4 q4k_weights(const Q4KRegs& r, int j) {
     const u32x4 raw = r.qs[j >> 1];
     const int shift = 4 * (j & 1);
@@ -170,7 +154,12 @@ __device__ __forceinline__ i32x4 q4k_weights(const Q4KRegs& r, int j) {
                  static_cast<int>((raw[2] >> shift) & 0x0F0F0F0Fu), static_cast<int>((raw[3] >> shift) & 0x0F0F0F0Fu)};
 }
 
-__device__ __forceinline__ void block_terms(const Q4KRegs& r, float (&term)[16]) {
+__device__ __forceinline__ i32x4 staged_codes16(const StagedBlock& sb, int j, int lane) {
+    return *reinterpret_cast<const i32x4*>(sb.codes + 1024 * j + 16 * lane);
+}
+
+__device__ __forceinline__ void block_terms(const Q4KRegs& r, const StagedBlock& sb, int lane, float (&term)[16]) {
+    const int h = lane >> 5;
     const float d = half_bits_to_float(r.head[0] & 0xFFFFu), dmin = half_bits_to_float(r.head[0] >> 16);
     int dot[16];
 #pragma unroll
@@ -178,16 +167,18 @@ __device__ __forceinline__ void block_terms(const Q4KRegs& r, float (&term)[16])
     i32x16 mins = {};
     int sj, mj;
     q4k_scale_min(0, r.head, sj, mj);
-    i32x16 cur = mfma32(r.c[0], q4k_weights(r, 0), i32x16{});
-    mins = mfma32(r.c[0], i32x4{mj * 0x01010101, mj * 0x01010101, mj * 0x01010101, mj * 0x01010101}, mins);
+    i32x4 c = staged_codes16(sb, 0, lane);
+    i32x16 cur = mfma32(c, q4k_weights(r, 0), i32x16{});
+    mins = mfma32(c, i32x4{mj * 0x01010101, mj * 0x01010101, mj * 0x01010101, mj * 0x01010101}, mins);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         i32x16 next;
         int sn = 0, mn = 0;
         if (j + 1 < 8) {
             q4k_scale_min(j + 1, r.head, sn, mn);
-            next = mfma32(r.c[j + 1], q4k_weights(r, j + 1), i32x16{});
-            mins = mfma32(r.c[j + 1], i32x4{mn * 0x01010101, mn * 0x01010101, mn * 0x01010101, mn * 0x01010101}, mins);
+            const i32x4 cn = staged_codes16(sb, j + 1, lane);
+            next = mfma32(cn, q4k_weights(r, j + 1), i32x16{});
+            mins = mfma32(cn, i32x4{mn * 0x01010101, mn * 0x01010101, mn * 0x01010101, mn * 0x01010101}, mins);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) dot[i] = mad24(sj, cur[i], dot[i]);
@@ -198,11 +189,14 @@ __device__ __forceinline__ void block_terms(const Q4KRegs& r, float (&term)[16])
         }
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float a = r.a[i >> 2][i & 3];
-        const float dA = __fmul_rn(d, a), dminA = __fmul_rn(dmin, a);
-        const float t = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot[i])), __fmul_rn(dminA, static_cast<float>(mins[i])));
-        term[i] = a != 0.0f ? t : 0.0f;
+    for (int q = 0; q < 4; ++q) {
+        const f32x4 a4 = staged_scales(sb, q, h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q + e;
+            const float dA = __fmul_rn(d, a4[e]), dminA = __fmul_rn(dmin, a4[e]);
+            term[i] = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot[i])), __fmul_rn(dminA, static_cast<float>(mins[i])));
+        }
     }
 }
 
@@ -215,7 +209,13 @@ __device__ __forceinline__ long q6k_weights(const Q6KRegs& r, int k, int& sc, lo
            (static_cast<long>(q6k_form(r.qla[c][1], r.qlb[c][1], r.qh[c][1], kk)) << 32);
 }
 
-__device__ __forceinline__ void block_terms(const Q6KRegs& r, float (&term)[16], int64_t index) {
+__device__ __forceinline__ long staged_codes8(const StagedBlock& sb, int k, int lane) {
+    return *reinterpret_cast<const long*>(sb.codes + 512 * k + 8 * lane);
+}
+
+__device__ __forceinline__ void block_terms(const Q6KRegs& r, const StagedBlock& stage, int lane, int64_t index,
+                                            float (&term)[16]) {
+    const int h = lane >> 5;
     const float d = half_bits_to_float(r.dpair >> (16 * static_cast<int>(index & 1)));
     int dot[16];
 #pragma unroll
@@ -224,8 +224,9 @@ __device__ __forceinline__ void block_terms(const Q6KRegs& r, float (&term)[16],
     int sc;
     long sb;
     long wq = q6k_weights(r, 0, sc, sb);
-    i32x16 cur = mfma16(r.c[0], wq, i32x16{});
-    cent = mfma16(r.c[0], sb, cent);
+    long c = staged_codes8(stage, 0, lane);
+    i32x16 cur = mfma16(c, wq, i32x16{});
+    cent = mfma16(c, sb, cent);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {  // group k: weights 16k .. 16k + 15 of the block
         i32x16 next;
@@ -233,8 +234,9 @@ __device__ __forceinline__ void block_terms(const Q6KRegs& r, float (&term)[16],
         if (k + 1 < 16) {
             long sbn;
             const long wn = q6k_weights(r, k + 1, sn, sbn);
-            next = mfma16(r.c[k + 1], wn, i32x16{});
-            cent = mfma16(r.c[k + 1], sbn, cent);
+            const long cn = staged_codes8(stage, k + 1, lane);
+            next = mfma16(cn, wn, i32x16{});
+            cent = mfma16(cn, sbn, cent);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) dot[i] = mad24(sc, cur[i], dot[i]);
@@ -245,44 +247,41 @@ __device__ __forceinline__ void block_terms(const Q6KRegs& r, float (&term)[16],
         }
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float a = r.a[i >> 2][i & 3];
-        // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32.
-        const float t = __fmul_rn(__fmul_rn(a, d), static_cast<float>(dot[i] - 32 * cent[i]));
-        term[i] = a != 0.0f ? t : 0.0f;
+    for (int q = 0; q < 4; ++q) {
+        const f32x4 a4 = staged_scales(stage, q, h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q + e;
+            // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32.
+            term[i] = __fmul_rn(__fmul_rn(a4[e], d), static_cast<float>(dot[i] - 32 * cent[i]));
+        }
     }
 }
 
 // Blocks of one row tile are split over S waves ("ways"): way w computes blocks w, w + S, ... and, per round
 // of S blocks, hands its 16 terms per lane to the others through LDS; the wave that owns an output adds the
 // round's S terms in block order, so every (row, position) sum is formed exactly as the sequential one.
-// A workgroup holds R row tiles x S ways (R = 4 / S, or 1 for S = 3) of one position tile.
+// A workgroup holds R = 4 / S row tiles x S ways of one position tile; the S blocks of a round are staged
+// once in LDS for all of them: each thread loads its 32 S bytes of the next round's codes (and a few threads
+// the scales) into registers while the current round is computed, and writes them to LDS after it.
 template <int S>
 struct Split {
-    static constexpr int R = S == 3 ? 1 : 4 / S;
-    static constexpr int kWaves = R * S;
-    static constexpr int kOwned = (16 + S - 1) / S;  // outputs per lane each way adds up (the last way fewer)
+    static constexpr int R = 4 / S;
+    static constexpr int kOwned = 16 / S;  // outputs per lane each way adds up (whole quads)
 };
-
-__device__ __forceinline__ int owned_begin(int way, int S) { return way * ((16 + S - 1) / S); }
-__device__ __forceinline__ int owned_end(int way, int S) {
-    const int e = (way + 1) * ((16 + S - 1) / S);
-    return e < 16 ? e : 16;
-}
 
 // Workgroup u of the padded grid: consecutive units (row groups x position tiles, position tiles fastest)
 // go to one XCD (workgroup ids are dealt to the 8 XCDs round-robin), so the position tiles that share a row
 // group's weights share that XCD's L2.
 template <int FORMAT, int S>
-__global__ __launch_bounds__(64 * Split<S>::kWaves) void kmfma_kernel(const uint8_t* __restrict__ w,
-                                                                     const uint8_t* __restrict__ codes,
-                                                                     const float* __restrict__ scales,
-                                                                     float* __restrict__ y, int rows, int blocks,
-                                                                     int64_t row_bytes, int positions, int tiles,
-                                                                     int units) {
+__global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ codes,
+                                                    const float* __restrict__ scales, float* __restrict__ y, int rows,
+                                                    int blocks, int64_t row_bytes, int positions, int tiles,
+                                                    int units) {
     using SP = Split<S>;
-    // Terms of one round: [row tile][way][quad q][lane] as float4 (conflict-free 16-byte accesses), twice.
-    __shared__ f32x4 exchange[S > 1 ? 2 * SP::R * S * 4 * 64 : 1];
+    __shared__ StagedBlock stage[S];
+    // Terms of one round: [row tile][way][quad q][lane] as float4 (conflict-free 16-byte accesses).
+    __shared__ f32x4 exchange[S > 1 ? SP::R * S * 4 * 64 : 1];
 
     const int per_xcd = gridDim.x >> 3;
     const int u = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
@@ -293,108 +292,123 @@ __global__ __launch_bounds__(64 * Split<S>::kWaves) void kmfma_kernel(const uint
     const int h = lane >> 5;
     const int row = (group * SP::R + rt) * kTile + (lane & 31);
     const int row_c = row < rows ? row : rows - 1;  // rows past the last compute on a live row, store nothing
-    const int64_t tile_bytes = static_cast<int64_t>(tiles) * 8192;
-    const int chunk_bytes = FORMAT == kQ4_K ? 16 : 8;
-    const uint8_t* ct = codes + static_cast<int64_t>(t) * 8192 + lane * chunk_bytes;
-    const float* st = scales + t * 32 + 4 * h;
     const int rounds = (blocks + S - 1) / S;
 
-    float acc[16];
+    // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [32i, 32i + 32) of each block's codes
+    // and, for i < 8 S, four scales.
+    u32x4 sc0[S], sc1[S];
+    u32x4 sscale = {0u, 0u, 0u, 0u};
+    auto stage_load = [&](int k) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+        for (int s = 0; s < S; ++s) {
+            const int b = k * S + s;
+            if (b < blocks) {
+                const uint8_t* src = codes + (static_cast<int64_t>(b) * tiles + t) * 8192 + 32 * threadIdx.x;
+                sc0[s] = load16_a4(src);
+                sc1[s] = load16_a4(src + 16);
+            }
+        }
+        if (threadIdx.x < 8 * S) {
+            const int s = threadIdx.x >> 3, b = k * S + s;
+            if (b < blocks)
+                sscale = load16_a4(reinterpret_cast<const uint8_t*>(scales + (static_cast<int64_t>(b) * tiles + t) * 32 +
+                                                                    4 * (threadIdx.x & 7)));
+        }
+    };
+    auto stage_store = [&](int k) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (k * S + s < blocks) {
+                *reinterpret_cast<u32x4*>(stage[s].codes + 32 * threadIdx.x) = sc0[s];
+                *reinterpret_cast<u32x4*>(stage[s].codes + 32 * threadIdx.x + 16) = sc1[s];
+            }
+        }
+        if (threadIdx.x < 8 * S)
+            *reinterpret_cast<u32x4*>(stage[threadIdx.x >> 3].scales + 4 * (threadIdx.x & 7)) = sscale;
+    };
+
+    // This way's accumulators: outputs way * kOwned + o of the lane (all 16 for S = 1), quads
+    // q = way * (4 / S) + qq.
+    float acc[SP::kOwned];
+#pragma unroll
+    for (int o = 0; o < SP::kOwned; ++o) acc[o] = 0.0f;
 
     // Adds one round's terms: directly for S = 1, else through the exchange buffer.
-    auto add_round = [&](const float (&term)[16], int round) {
+    auto add_round = [&](const float (&term)[16]) {
         if constexpr (S == 1) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = __fadd_rn(acc[i], term[i]);
         } else {
-            f32x4* buf = exchange + (round & 1) * (SP::R * S * 4 * 64) + rt * (S * 4 * 64);
+            f32x4* buf = exchange + rt * (S * 4 * 64);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 buf[(way * 4 + q) * 64 + lane] = f32x4{term[4 * q], term[4 * q + 1], term[4 * q + 2], term[4 * q + 3]};
             __syncthreads();
-            // Way `way` adds outputs [owned_begin, owned_end) of every lane: the round's terms in block order.
+            // The round's S terms of each owned output, added in block order. The next round's first barrier
+            // orders these reads before the buffer is written again.
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (4 * q + 3 < owned_begin(way, S) || 4 * q >= owned_end(way, S)) continue;
+            for (int qq = 0; qq < 4 / S; ++qq) {
+                const int q = way * (4 / S) + qq;
 #pragma unroll
                 for (int s2 = 0; s2 < S; ++s2) {
                     const f32x4 v = buf[(s2 * 4 + q) * 64 + lane];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (4 * q + e >= owned_begin(way, S) && 4 * q + e < owned_end(way, S))
-                            acc[4 * q + e] = __fadd_rn(acc[4 * q + e], v[e]);
+                    for (int e = 0; e < 4; ++e) acc[4 * qq + e] = __fadd_rn(acc[4 * qq + e], v[e]);
                 }
             }
         }
     };
 
-    float term[16];
-    if constexpr (FORMAT == kQ4_K) {
-        const uint8_t* wrow = w + row_c * row_bytes;
-        auto load = [&](int b, Q4KRegs& r) {
-            if (b < blocks) load_block(wrow, b, h, ct + b * tile_bytes, st + b * tiles * 32, r);
-        };
-        auto terms = [&](int b, const Q4KRegs& r) {
-            if (b < blocks) {
-                block_terms(r, term);
-            } else {
+    using Regs = typename std::conditional<FORMAT == kQ4_K, Q4KRegs, Q6KRegs>::type;
+    const uint8_t* wrow = w + row_c * row_bytes;
+    const int64_t count = static_cast<int64_t>(rows) * blocks;
+    const int64_t base = static_cast<int64_t>(row_c) * blocks;
+    auto load_w = [&](int b, Regs& r) {
+        if (b < blocks) {
+            if constexpr (FORMAT == kQ4_K)
+                load_weights(wrow, b, h, r);
+            else
+                load_weights(w, count, base + b, h, r);
+        }
+    };
+    auto round = [&](int k, Regs& cur, Regs& nxt) {
+        __syncthreads();  // the previous round's staged blocks (and exchanged terms) are no longer read
+        stage_store(k);
+        if (k + 1 < rounds) {
+            stage_load(k + 1);
+            load_w((k + 1) * S + way, nxt);
+        }
+        __syncthreads();  // round k staged
+        const int b = k * S + way;
+        float term[16];
+        if (b < blocks) {
+            if constexpr (FORMAT == kQ4_K)
+                block_terms(cur, stage[way], lane, term);
+            else
+                block_terms(cur, stage[way], lane, base + b, term);
+        } else {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) term[i] = 0.0f;
-            }
-        };
-        Q4KRegs ra, rb;
-        load(way, ra);
-        int k = 0;
-        for (; k + 1 < rounds; k += 2) {
-            load(way + (k + 1) * S, rb);
-            terms(way + k * S, ra);
-            add_round(term, k);
-            load(way + (k + 2) * S, ra);
-            terms(way + (k + 1) * S, rb);
-            add_round(term, k + 1);
+            for (int i = 0; i < 16; ++i) term[i] = 0.0f;
         }
-        if (k < rounds) {
-            terms(way + k * S, ra);
-            add_round(term, k);
-        }
-    } else {
-        const int64_t count = static_cast<int64_t>(rows) * blocks;
-        const int64_t base = static_cast<int64_t>(row_c) * blocks;
-        auto load = [&](int b, Q6KRegs& r) {
-            if (b < blocks) load_block(w, count, base + b, h, ct + b * tile_bytes, st + b * tiles * 32, r);
-        };
-        auto terms = [&](int b, const Q6KRegs& r) {
-            if (b < blocks) {
-                block_terms(r, term, base + b);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) term[i] = 0.0f;
-            }
-        };
-        Q6KRegs ra, rb;
-        load(way, ra);
-        int k = 0;
-        for (; k + 1 < rounds; k += 2) {
-            load(way + (k + 1) * S, rb);
-            terms(way + k * S, ra);
-            add_round(term, k);
-            load(way + (k + 2) * S, ra);
-            terms(way + (k + 1) * S, rb);
-            add_round(term, k + 1);
-        }
-        if (k < rounds) {
-            terms(way + k * S, ra);
-            add_round(term, k);
-        }
+        add_round(term);
+    };
+
+    Regs ra, rb;
+    stage_load(0);
+    load_w(way, ra);
+    int k = 0;
+    for (; k + 1 < rounds; k += 2) {
+        round(k, ra, rb);
+        round(k + 1, rb, ra);
     }
+    if (k < rounds) round(k, ra, rb);
+
     if (row >= rows) return;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        if (i < owned_begin(way, S) || i >= owned_end(way, S)) continue;
+    for (int o = 0; o < SP::kOwned; ++o) {
+        const int i = way * SP::kOwned + o;
         const int p = t * kTile + 8 * (i >> 2) + 4 * h + (i & 3);
-        if (p < positions) store_f32(y + static_cast<int64_t>(p) * rows + row, acc[i]);
+        if (p < positions) store_f32(y + static_cast<int64_t>(p) * rows + row, acc[o]);
     }
 }
 
@@ -404,17 +418,17 @@ void launch_split(const uint8_t* w, const uint8_t* codes, const float* scales, f
     const int groups = (rows + Split<S>::R * kTile - 1) / (Split<S>::R * kTile);
     const int units = groups * tiles;
     const int grid = (units + 7) / 8 * 8;
-    kmfma_kernel<FORMAT, S><<<grid, 64 * Split<S>::kWaves, 0, stream>>>(w, codes, scales, y, rows, blocks, row_bytes,
-                                                                         positions, tiles, units);
+    kmfma_kernel<FORMAT, S><<<grid, 256, 0, stream>>>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles,
+                                                      units);
 }
 
-// Ways per row tile: enough waves for about two per SIMD (2048), at most 4 and at most the block count, and
-// no more ways than shorten the chain of rounds.
+// Ways per row tile (1, 2 or 4): enough waves for about two per SIMD (2048), at most the block count, and no
+// more ways than shorten the chain of rounds.
 int choose_split(int rows, int blocks, int tiles) {
     const long wave_tiles = static_cast<long>((rows + kTile - 1) / kTile) * tiles;
     int s = 1;
-    while (s < 4 && s < blocks && wave_tiles * s < 2048) ++s;
-    while (s > 1 && (blocks + s - 1) / s == (blocks + s - 2) / (s - 1)) --s;
+    while (s < 4 && 2 * s <= blocks && wave_tiles * s < 2048) s *= 2;
+    while (s > 1 && (blocks + s - 1) / s == (blocks + s / 2 - 1) / (s / 2)) s /= 2;
     return s;
 }
 
@@ -424,7 +438,6 @@ void launch_format(const uint8_t* w, const uint8_t* codes, const float* scales, 
     switch (choose_split(rows, blocks, tiles)) {
         case 1: launch_split<FORMAT, 1>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
         case 2: launch_split<FORMAT, 2>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
-        case 3: launch_split<FORMAT, 3>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
         default: launch_split<FORMAT, 4>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
     }
 }
