@@ -16,6 +16,8 @@ The same line carries, labelled:
   cache:     the grouped launch over G references to ONE copy (cache resident, not an HBM figure);
   decode_step: the 197 projections of one decode token of a Qwen-1.5B-shaped model (Q4_K/Q6_K on the Q8_K
              integer path, 1.03 GB per token), replayed as one graph; tokens/s and GB/s;
+  decode_token: a whole token of that model on the device (operators, attention over a 511-token KV prefix,
+             projections), captured once and replayed;
   prefill:   the same model's projections over 512 positions (ExecuteBatch in 256-position chunks);
              tokens/s and int8 TOP/s;
   roofline:  for the headline kernel, from HIP events on the launch stream;
@@ -269,6 +271,53 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int) -> dic
     }
 
 
+def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, position: int = 511) -> dict:
+    """A whole decode token on the device (satori_amd.decode.DeviceDecoder): embedding-row decode, per layer
+    RmsNorm, q/k/v, bias adds, RoPE, grouped attention over a `position`-token key/value prefix (random),
+    o, residual, RmsNorm, gate/up, SwiGLU, down, residual; then the final norm and the output projection
+    (tied to the embedding, as Qwen2.5-1.5B). Captured once as one step and replayed; also timed eagerly."""
+    from satori_amd.decode import DecoderConfig, DeviceDecoder
+    g = rng(2029)
+    cfg = DecoderConfig(hidden=model.D, heads=12, kv_heads=2, head_dim=128, ffn=model.FFN, epsilon=1e-6,
+                        rope_base=1e6, max_tokens=position + 1)
+    vectors = []
+    for _ in model.layers:
+        vectors.append({
+            "attn_norm": model.device(g.uniform(0.5, 1.5, model.D).astype(np.float32)),
+            "ffn_norm": model.device(g.uniform(0.5, 1.5, model.D).astype(np.float32)),
+            "q_bias": model.device((g.standard_normal(model.D) * 0.1).astype(np.float32)),
+            "k_bias": model.device((g.standard_normal(model.KV) * 0.1).astype(np.float32)),
+            "v_bias": model.device((g.standard_normal(model.KV) * 0.1).astype(np.float32)),
+        })
+    out_norm = model.device(g.uniform(0.5, 1.5, model.D).astype(np.float32))
+    dec = DeviceDecoder(ctx, cfg, model.layers, vectors, out_norm, model.output, model.output)
+    for layer in range(len(model.layers)):
+        prefix = (g.standard_normal((cfg.max_tokens, model.KV)) * 0.5).astype(np.float32)
+        ctx.upload(dec.keys[layer], prefix)
+        ctx.upload(dec.values[layer], prefix[::-1].copy())
+    step = dec.capture(151, position)
+    warm_up(ctx, step.execute, 0.5)
+    graph_ms = time_launches(ctx, events, step.execute, steps, warmup)
+    eager_ms = time_launches(ctx, events, lambda: dec.enqueue(151, position), max(5, steps // 4), 2)
+    unfused = dec.capture(151, position, fused=False)
+    unfused_ms = time_launches(ctx, events, unfused.execute, max(5, steps // 2), 2)
+    unfused.dispose()
+    finite = bool(np.all(np.isfinite(dec.read_logits())))
+    step.dispose()
+    dec.dispose()
+    return {
+        "model": "Qwen-1.5B-shaped whole decode token on the device (random-init weights and KV prefix)",
+        "position": position,
+        "kernel_launches_per_token": dec.launches_per_token(),
+        "us_per_token": graph_ms * 1e3,
+        "tokens_per_s": 1e3 / graph_ms,
+        "eager_us_per_token": eager_ms * 1e3,
+        "unfused_us_per_token": unfused_ms * 1e3,
+        "unfused_launches_per_token": dec.launches_per_token(fused=False),
+        "finite_logits": finite,
+    }
+
+
 def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions: int = 512) -> dict:
     """The projections of a 512-token prefill: every layer projection over all positions through
     ExecuteBatch in chunks of 256 positions (the reference's chunk, and the ABI's limit for K formats),
@@ -438,11 +487,13 @@ def main() -> int:
             formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
             c.close()
 
-    decode = pre = None
+    decode = pre = token = None
     if not args.quick:
         progress("decode step (197 projections per token)")
         model = DecodeModel(ctx)
         decode = decode_step(ctx, events, model, 50, 5)
+        progress("whole decode token (operators + projections, position 511)")
+        token = decode_token(ctx, events, model, 30, 3)
         progress("prefill (512 positions)")
         pre = prefill(ctx, events, model, 3, 1)
         model.close()
@@ -487,6 +538,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_step": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode.items()}
                         if decode else None),
+        "decode_token": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in token.items()}
+                         if token else None),
         "prefill": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in pre.items()} if pre else None),
         "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in formats.items()},

@@ -230,6 +230,16 @@ int satori_hip_ternary2_quantize(const float* weights, int rows, int columns, in
 int satori_hip_quantize_weights(int format, const float* weights, int rows, int columns, void* payload,
                                 size_t payload_length);
 
+/* Stream capture (no reference counterpart; for resident decode loops): everything the calls between begin
+ * and end enqueue on the context stream (stream argument NULL) -- group launches, *_device MatVecs, the
+ * decode-step operators, row decodes -- is recorded into one graph, which capture_end turns into a step
+ * replayed by satori_hip_step_execute and freed by satori_hip_step_destroy. The step keeps the matrices and
+ * groups it launches from being destroyed. While capturing, calls that synchronise, allocate or copy
+ * through the host fail with SATORI_HIP_E_INVALID_OPERATION (a many-position K product must have run once
+ * before, so its workspace exists), and no other thread may use the context. */
+int satori_hip_capture_begin(satori_hip_context* context);
+int satori_hip_capture_end(satori_hip_context* context, satori_hip_step** step);
+
 /* ---- decode-step operators (src/Satori.Core/TransformerOps.cs), device pointers ----
  * Enqueued on `stream` (NULL: the context stream), like the *_device MatVec calls. Each computes in FP64 as
  * the reference does and rounds its outputs to FP32 once; outputs agree with the reference's to about one
@@ -249,9 +259,20 @@ int satori_hip_swiglu(satori_hip_context* context, const float* gate, const floa
                       void* stream);
 int satori_hip_add(satori_hip_context* context, const float* left, const float* right, int length, float* output,
                    void* stream);
+/* Fused steps of DenseForward.Step, bit-identical to the separate calls: Add then RmsNorm
+ * (DenseForward.cs:156-158: residual += addend, normed = RmsNorm(residual)), and the attention inputs of one
+ * position (DenseForward.cs:128-151: the q/k/v bias adds when biases are given (NULL: none), RopeHalf of the
+ * query in place and of the key into key_out, the value into value_out -- key_out / value_out being the
+ * cache slots). */
+int satori_hip_add_rms_norm(satori_hip_context* context, float* residual, const float* addend, const float* weights,
+                            float epsilon, int length, float* normed, void* stream);
+int satori_hip_attention_inputs(satori_hip_context* context, float* query, const float* query_bias, const float* key,
+                                const float* key_bias, float* key_out, const float* value, const float* value_bias,
+                                float* value_out, int query_heads, int kv_heads, int head_dim, int position,
+                                double frequency_base, int rotary_dimensions, void* stream);
 /* GroupedAttention (TransformerOps.cs:135-179; Attention :61-91 is query_heads == kv_heads): keys/values
  * token-major [tokens][kv_heads * head_dim]. The scores live on the device (no scratch argument); at most
- * 8192 tokens per call (SATORI_HIP_E_NOT_SUPPORTED beyond). */
+ * 6912 tokens per call (SATORI_HIP_E_NOT_SUPPORTED beyond). */
 int satori_hip_grouped_attention(satori_hip_context* context, const float* query, const float* keys,
                                  const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
                                  float* output, void* stream);

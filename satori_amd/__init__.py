@@ -34,7 +34,7 @@ __all__ = [
     "QuantizedMatVec", "HipContext", "HipQuantizedMatrix", "HipGroup", "HipStep", "Q8KCodec", "TERNARY2",
     "device_count", "default_context", "payload_length", "quantize_weights",
     "GgufFile", "GgufTensor", "GgufMetadata", "GgufQuantizedMatrix", "GgufWeightStore",
-    "TernaryBitplaneMatrix", "TernaryBitplaneMatVec", "TransformerOps",
+    "TernaryBitplaneMatrix", "TernaryBitplaneMatVec", "TransformerOps", "DeviceOps",
 ]
 
 TERNARY2 = 16
@@ -235,6 +235,16 @@ class HipContext:
         _check(_ffi.lib().satori_hip_bitplane_open(self._handle, str(path).encode(), ctypes.byref(handle)))
         return HipQuantizedMatrix(self, handle)
 
+    def capture_begin(self) -> None:
+        """Starts recording the work enqueued on the context stream (satori_hip_capture_begin)."""
+        _check(_ffi.lib().satori_hip_capture_begin(self._handle))
+
+    def capture_end(self) -> "HipStep":
+        """Ends the recording; the recorded work becomes a replayable step (satori_hip_capture_end)."""
+        handle = ctypes.c_void_p()
+        _check(_ffi.lib().satori_hip_capture_end(self._handle, ctypes.byref(handle)))
+        return HipStep(self, handle=handle)
+
     def quantize_q8k(self, x) -> np.ndarray:
         """Q8KCodec.QuantizeRow on the device (src/Satori.Core/Q8KCodec.cs:85-93)."""
         xv = _as_f32(x).reshape(-1)
@@ -367,11 +377,12 @@ class HipStep:
     """An ordered list of groups captured once and replayed as one HIP graph (the projection sequence of a
     decode step). The groups must stay alive while the step exists."""
 
-    def __init__(self, context: HipContext, groups):
-        n = len(groups)
-        handles = (ctypes.c_void_p * n)(*[g._handle.value for g in groups])
-        handle = ctypes.c_void_p()
-        _check(_ffi.lib().satori_hip_step_create(context.handle, handles, n, ctypes.byref(handle)))
+    def __init__(self, context: HipContext, groups=None, handle: ctypes.c_void_p | None = None):
+        if handle is None:
+            n = len(groups)
+            handles = (ctypes.c_void_p * n)(*[g._handle.value for g in groups])
+            handle = ctypes.c_void_p()
+            _check(_ffi.lib().satori_hip_step_create(context.handle, handles, n, ctypes.byref(handle)))
         self._handle = handle
 
     def execute(self, stream: int = 0) -> None:
@@ -929,3 +940,50 @@ class TransformerOps:
             raise ArgumentException("Invalid attention dimensions.")
         heads = q.size // head_dimension
         TransformerOps.grouped_attention(q, keys, values, heads, heads, head_dimension, token_count, output, context)
+
+
+class DeviceOps:
+    """The decode-step operators over device pointers (ints), enqueued on the context stream (so they can be
+    captured with HipContext.capture_begin / capture_end). Argument meaning as TransformerOps."""
+
+    def __init__(self, context: "HipContext"):
+        self.context = context
+        self._h = context.handle
+
+    @staticmethod
+    def _p(v: int) -> ctypes.c_void_p:
+        return ctypes.c_void_p(v)
+
+    def rms_norm(self, x: int, weights: int, epsilon: float, length: int, y: int, count: int = 1) -> None:
+        _check(_ffi.lib().satori_hip_rms_norm(self._h, self._p(x), self._p(weights), float(epsilon), length, count,
+                                              self._p(y), None))
+
+    def rms_norm_heads(self, v: int, weights: int, epsilon: float, head_dim: int, length: int) -> None:
+        _check(_ffi.lib().satori_hip_rms_norm_heads(self._h, self._p(v), self._p(weights), float(epsilon), head_dim,
+                                                    length, None))
+
+    def rope_half(self, v: int, length: int, head_dim: int, position: int, base: float, rotary: int) -> None:
+        _check(_ffi.lib().satori_hip_rope_half(self._h, self._p(v), length, head_dim, position, float(base), rotary,
+                                               None))
+
+    def swiglu(self, gate: int, up: int, length: int, out: int) -> None:
+        _check(_ffi.lib().satori_hip_swiglu(self._h, self._p(gate), self._p(up), length, self._p(out), None))
+
+    def add(self, left: int, right: int, length: int, out: int) -> None:
+        _check(_ffi.lib().satori_hip_add(self._h, self._p(left), self._p(right), length, self._p(out), None))
+
+    def add_rms_norm(self, residual: int, addend: int, weights: int, epsilon: float, length: int, normed: int) -> None:
+        _check(_ffi.lib().satori_hip_add_rms_norm(self._h, self._p(residual), self._p(addend), self._p(weights),
+                                                  float(epsilon), length, self._p(normed), None))
+
+    def attention_inputs(self, q: int, q_bias: int, k: int, k_bias: int, k_out: int, v: int, v_bias: int, v_out: int,
+                         heads: int, kv_heads: int, head_dim: int, position: int, base: float, rotary: int) -> None:
+        """Biases may be 0 (none)."""
+        _check(_ffi.lib().satori_hip_attention_inputs(self._h, self._p(q), self._p(q_bias), self._p(k), self._p(k_bias),
+                                                      self._p(k_out), self._p(v), self._p(v_bias), self._p(v_out), heads,
+                                                      kv_heads, head_dim, position, float(base), rotary, None))
+
+    def grouped_attention(self, q: int, k: int, v: int, query_heads: int, kv_heads: int, head_dim: int, tokens: int,
+                          out: int) -> None:
+        _check(_ffi.lib().satori_hip_grouped_attention(self._h, self._p(q), self._p(k), self._p(v), query_heads,
+                                                       kv_heads, head_dim, tokens, self._p(out), None))

@@ -58,6 +58,8 @@ SIGNATURES = {
     "satori_hip_bitplane_from_ternary2": (I, [I, I, I, P, SZ, P, SZ]),
     "satori_hip_bitplane_to_ternary2": (I, [I, I, I, P, SZ, P, SZ]),
     "satori_hip_bitplane_validate": (I, [I, I, I, P, SZ]),
+    "satori_hip_capture_begin": (I, [P]),
+    "satori_hip_capture_end": (I, [P, PP]),
     "satori_hip_rms_norm": (I, [P, P, P, ctypes.c_float, I, I, P, P]),
     "satori_hip_rms_norm_heads": (I, [P, P, P, ctypes.c_float, I, I, P]),
     "satori_hip_rope": (I, [P, P, I, I, I, P]),
@@ -65,6 +67,8 @@ SIGNATURES = {
     "satori_hip_swiglu": (I, [P, P, P, I, P, P]),
     "satori_hip_add": (I, [P, P, P, I, P, P]),
     "satori_hip_grouped_attention": (I, [P, P, P, P, I, I, I, I, P, P]),
+    "satori_hip_add_rms_norm": (I, [P, P, P, P, ctypes.c_float, I, P, P]),
+    "satori_hip_attention_inputs": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, ctypes.c_double, I, P]),
     "satori_hip_matrix_decode_row": (I, [P, I, P, P]),
     "satori_hip_gguf_open": (I, [ctypes.c_char_p, PP]),
     "satori_hip_gguf_close": (I, [P]),

@@ -145,6 +145,11 @@ hipError_t launch_rope(float* v, int heads, int head_dim, int position, double b
                        hipStream_t stream);
 hipError_t launch_swiglu(const float* gate, const float* up, int length, float* out, hipStream_t stream);
 hipError_t launch_add(const float* left, const float* right, int length, float* out, hipStream_t stream);
+hipError_t launch_add_rms_norm(float* residual, const float* addend, const float* w, float epsilon, int length,
+                               float* normed, hipStream_t stream);
+hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k, const float* k_bias, float* k_out,
+                                   const float* v, const float* v_bias, float* v_out, int heads, int kv_heads,
+                                   int head_dim, int position, double base, int rotary, hipStream_t stream);
 int attention_max_tokens();
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
                             int head_dim, int tokens, float* out, hipStream_t stream);

@@ -87,6 +87,11 @@ struct satori_hip_context {
     int matrices = 0;
     satori::DeviceBuffer x, y, q8k;
     satori::PinnedBuffer host_x, host_y;
+    // Stream capture (satori_hip_capture_begin / _end): the matrices and groups launched on the context
+    // stream while capturing, referenced by the step the capture becomes.
+    bool capturing = false;
+    std::vector<satori_hip_matrix*> captured_matrices;
+    std::vector<satori_hip_group*> captured_groups;
 };
 
 struct satori_hip_matrix {
@@ -97,7 +102,7 @@ struct satori_hip_matrix {
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
     satori::DeviceBuffer q8k;    // K formats: Q8_K activations of the last many-position product
-    int groups = 0;              // live groups that launch this matrix
+    int groups = 0;              // live groups and captured steps that launch this matrix
     bool live = true;
 };
 
@@ -122,7 +127,8 @@ struct satori_hip_gguf {
 
 struct satori_hip_step {
     satori_hip_context* context = nullptr;
-    std::vector<satori_hip_group*> groups;  // in launch order (each counts this step)
+    std::vector<satori_hip_group*> groups;     // in launch order (each counts this step)
+    std::vector<satori_hip_matrix*> matrices;  // launched directly in a captured step (each counts it)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool live = true;
@@ -170,6 +176,17 @@ void require_live(const satori_hip_matrix* m) {
 
 void set_device(const satori_hip_context* c) { check_hip(hipSetDevice(c->device), "hipSetDevice"); }
 
+// Calls that synchronise, allocate or copy through the host cannot be recorded into a graph.
+void require_not_capturing(const satori_hip_context* c) {
+    if (c->capturing)
+        fail(SATORI_HIP_E_INVALID_OPERATION, "Not allowed while the context stream is being captured.");
+}
+
+// Work enqueued on the context stream while capturing becomes part of the step: keep what it launches alive.
+void note_launch(satori_hip_context* c, satori_hip_matrix* m, hipStream_t stream) {
+    if (c->capturing && stream == c->stream) c->captured_matrices.push_back(m);
+}
+
 LaunchShape launch_shape(const Shape& s, int positions, int rows_max) {
     LaunchShape l{};
     l.format = s.format == SATORI_HIP_TERNARY2 ? kTernary2 : s.format;
@@ -202,7 +219,11 @@ void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, fl
 void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
     const Shape& s = m->shape;
     if (positions >= kmfma_min_positions()) {
-        m->q8k.reserve(kmfma_workspace_bytes(s.blocks, positions));
+        const size_t need = kmfma_workspace_bytes(s.blocks, positions);
+        if (m->context->capturing && m->q8k.bytes < need)
+            fail(SATORI_HIP_E_INVALID_OPERATION,
+                 "Run this many-position product once before capturing it (its workspace is allocated on first use).");
+        m->q8k.reserve(need);
         check_hip(launch_gemv_kmfma(m->payload, s.format, x, static_cast<uint8_t*>(m->q8k.ptr), y, s.rows, s.blocks,
                                     s.row_bytes, positions, stream),
                   "matrix-core gemv launch");
@@ -328,6 +349,7 @@ void free_matrix(satori_hip_matrix* m) {
 }
 
 satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
+    require_not_capturing(c);
     set_device(c);
     std::vector<uint8_t> regrouped;
     const uint8_t* source = payload;
@@ -365,6 +387,7 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     satori_hip_context* c = m->context;
     std::lock_guard<std::mutex> guard(c->lock);
     require_live(m);
+    require_not_capturing(c);
     require(input, "input");
     require(output, "output");
     const Shape& s = m->shape;
@@ -569,6 +592,7 @@ int satori_hip_context_destroy(satori_hip_context* c) {
     return guarded([&] {
         if (!c) return;
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (!c->live) return;
         if (c->matrices > 0)
             fail(SATORI_HIP_E_ARGUMENT, "Matrices created on the context must be destroyed first.");
@@ -740,6 +764,7 @@ int satori_hip_matrix_clone(satori_hip_matrix* source, satori_hip_matrix** clone
         require(source, "source");
         satori_hip_context* c = source->context;
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         require_live(source);
         set_device(c);
         auto* m = new satori_hip_matrix();
@@ -766,6 +791,7 @@ int satori_hip_matrix_destroy(satori_hip_matrix* m) {
         if (!m) return;
         satori_hip_context* c = m->context;
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (!m->live) return;
         if (m->groups > 0) fail(SATORI_HIP_E_ARGUMENT, "Groups that launch the matrix must be destroyed first.");
         if (c->live) {
@@ -812,6 +838,7 @@ int satori_hip_quantize_q8k(satori_hip_context* c, const float* input, int colum
         if (output_length != out_bytes) fail(SATORI_HIP_E_ARGUMENT, "Invalid Q8_K row dimensions.");
         const size_t in_bytes = static_cast<size_t>(columns) * sizeof(float);
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         require_live(c);
         set_device(c);
         c->x.reserve(in_bytes);
@@ -838,7 +865,9 @@ int satori_hip_matvec_device(satori_hip_matrix* m, const float* input, float* ou
         require(input, "input");
         require(output, "output");
         set_device(m->context);
-        enqueue_float(m, input, 1, output, stream ? static_cast<hipStream_t>(stream) : m->context->stream);
+        const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : m->context->stream;
+        enqueue_float(m, input, 1, output, st);
+        note_launch(m->context, m, st);
     });
 }
 
@@ -863,6 +892,7 @@ int satori_hip_matvec_batch_device(satori_hip_matrix* m, const float* input, int
         } else {
             enqueue_float(m, input, positions, output, st);
         }
+        note_launch(c, m, st);
     });
 }
 
@@ -872,6 +902,7 @@ int satori_hip_device_alloc(satori_hip_context* c, size_t bytes, void** device_p
         *device_ptr = nullptr;
         require_live(c);
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (bytes == 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "bytes must be positive.");
         set_device(c);
         check_hip(hipMalloc(device_ptr, bytes), "hipMalloc");
@@ -882,6 +913,7 @@ int satori_hip_device_free(satori_hip_context* c, void* device_ptr) {
     return guarded([&] {
         require_live(c);
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (!device_ptr) return;
         set_device(c);
         check_hip(hipStreamSynchronize(c->stream), "stream");
@@ -902,6 +934,7 @@ int satori_hip_copy(satori_hip_context* c, void* destination, const void* source
             default: fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "kind must be 1, 2 or 3.");
         }
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         set_device(c);
         check_hip(hipMemcpyAsync(destination, source, bytes, k, c->stream), "hipMemcpyAsync");
         check_hip(hipStreamSynchronize(c->stream), "stream");
@@ -912,6 +945,7 @@ int satori_hip_synchronize(satori_hip_context* c) {
     return guarded([&] {
         require_live(c);
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         set_device(c);
         check_hip(hipStreamSynchronize(c->stream), "stream");
     });
@@ -929,6 +963,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
         require(outputs, "outputs");
         if (count <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "count must be positive.");
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         const Shape& first = matrices[0] ? matrices[0]->shape : Shape{};
         std::vector<MatDesc> host(count);
         auto* g = new satori_hip_group();
@@ -980,7 +1015,9 @@ int satori_hip_group_execute(satori_hip_group* g, void* stream) {
         std::lock_guard<std::mutex> guard(c->lock);
         if (!g->live || !c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
         set_device(c);
-        enqueue_group(g, stream ? static_cast<hipStream_t>(stream) : c->stream);
+        const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        enqueue_group(g, st);
+        if (c->capturing && st == c->stream) c->captured_groups.push_back(g);
     });
 }
 
@@ -989,6 +1026,7 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         if (!g) return;
         satori_hip_context* c = g->context;
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (!g->live) return;
         if (g->steps > 0) fail(SATORI_HIP_E_ARGUMENT, "Steps that replay the group must be destroyed first.");
         if (c->live) {
@@ -1014,6 +1052,7 @@ int satori_hip_step_create(satori_hip_context* c, satori_hip_group* const* group
         require(groups, "groups");
         if (count <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "count must be positive.");
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         for (int i = 0; i < count; ++i) {
             require_live(groups[i]);
             if (groups[i]->context != c) fail(SATORI_HIP_E_ARGUMENT, "Every group must belong to the context.");
@@ -1052,6 +1091,7 @@ int satori_hip_step_execute(satori_hip_step* s, void* stream) {
         require(s, "step");
         satori_hip_context* c = s->context;
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (!s->live || !c->live)
             fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_step'.");
         set_device(c);
@@ -1064,6 +1104,7 @@ int satori_hip_step_destroy(satori_hip_step* s) {
         if (!s) return;
         satori_hip_context* c = s->context;
         std::lock_guard<std::mutex> guard(c->lock);
+        require_not_capturing(c);
         if (!s->live) return;
         if (c->live) {
             (void)hipSetDevice(c->device);
@@ -1074,8 +1115,68 @@ int satori_hip_step_destroy(satori_hip_step* s) {
         s->exec = nullptr;
         s->graph = nullptr;
         for (satori_hip_group* g : s->groups) g->steps--;
+        for (satori_hip_matrix* m : s->matrices) m->groups--;
         s->groups.clear();
+        s->matrices.clear();
         s->live = false;
+    });
+}
+
+int satori_hip_capture_begin(satori_hip_context* c) {
+    return guarded([&] {
+        require_live(c);
+        std::lock_guard<std::mutex> guard(c->lock);
+        require_live(c);
+        require_not_capturing(c);
+        set_device(c);
+        // Everything enqueued on the context stream before the capture must not be part of the graph.
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+        check_hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph capture");
+        c->capturing = true;
+        c->captured_matrices.clear();
+        c->captured_groups.clear();
+    });
+}
+
+int satori_hip_capture_end(satori_hip_context* c, satori_hip_step** step) {
+    return guarded([&] {
+        require(step, "step");
+        *step = nullptr;
+        require_live(c);
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!c->capturing) fail(SATORI_HIP_E_INVALID_OPERATION, "The context stream is not being captured.");
+        set_device(c);
+        c->capturing = false;
+        std::vector<satori_hip_matrix*> matrices;
+        std::vector<satori_hip_group*> groups;
+        matrices.swap(c->captured_matrices);
+        groups.swap(c->captured_groups);
+        hipGraph_t graph = nullptr;
+        check_hip(hipStreamEndCapture(c->stream, &graph), "graph capture");
+        if (!graph) fail(SATORI_HIP_E_DEVICE, "The capture produced no graph.");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            check_hip(e, "graph instantiation");
+        }
+        auto* st = new satori_hip_step();
+        st->context = c;
+        st->graph = graph;
+        st->exec = exec;
+        for (satori_hip_group* g : groups) {
+            if (std::find(st->groups.begin(), st->groups.end(), g) == st->groups.end()) {
+                st->groups.push_back(g);
+                g->steps++;
+            }
+        }
+        for (satori_hip_matrix* m : matrices) {
+            if (std::find(st->matrices.begin(), st->matrices.end(), m) == st->matrices.end()) {
+                st->matrices.push_back(m);
+                m->groups++;
+            }
+        }
+        *step = st;
     });
 }
 
@@ -1374,6 +1475,52 @@ int satori_hip_add(satori_hip_context* c, const float* left, const float* right,
     });
 }
 
+int satori_hip_add_rms_norm(satori_hip_context* c, float* residual, const float* addend, const float* weights,
+                            float epsilon, int length, float* normed, void* stream) {
+    return op_call(c, [&] {
+        require(residual, "residual");
+        require(addend, "addend");
+        require(weights, "weights");
+        require(normed, "normed");
+        if (length <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'epsilon')");
+        check_epsilon(epsilon);
+        if (partial_overlap(addend, length, residual, length) || any_overlap(normed, length, residual, length) ||
+            any_overlap(weights, length, normed, length) || any_overlap(addend, length, normed, length))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_add_rms_norm(residual, addend, weights, epsilon, length, normed, op_stream(c, stream)),
+                  "add_rms_norm launch");
+    });
+}
+
+int satori_hip_attention_inputs(satori_hip_context* c, float* query, const float* query_bias, const float* key,
+                                const float* key_bias, float* key_out, const float* value, const float* value_bias,
+                                float* value_out, int query_heads, int kv_heads, int head_dim, int position,
+                                double frequency_base, int rotary_dimensions, void* stream) {
+    return op_call(c, [&] {
+        require(query, "query");
+        require(key, "key");
+        require(key_out, "keyOut");
+        require(value, "value");
+        require(value_out, "valueOut");
+        if (head_dim <= 0 || query_heads <= 0 || kv_heads <= 0 || position < 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'headDimension')");
+        if (!std::isfinite(frequency_base) || frequency_base <= 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'frequencyBase')");
+        if (rotary_dimensions <= 0 || rotary_dimensions > head_dim || rotary_dimensions % 2 != 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'rotaryDimensions')");
+        const int64_t qw = static_cast<int64_t>(query_heads) * head_dim, kw = static_cast<int64_t>(kv_heads) * head_dim;
+        if (any_overlap(key, kw, key_out, kw) && key != key_out) fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        if (any_overlap(value, kw, value_out, kw) && value != value_out) fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        if (any_overlap(query, qw, key_out, kw) || any_overlap(query, qw, value_out, kw) ||
+            any_overlap(key_out, kw, value_out, kw))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_attention_inputs(query, query_bias, key, key_bias, key_out, value, value_bias, value_out,
+                                          query_heads, kv_heads, head_dim, position, frequency_base, rotary_dimensions,
+                                          op_stream(c, stream)),
+                  "attention_inputs launch");
+    });
+}
+
 int satori_hip_grouped_attention(satori_hip_context* c, const float* query, const float* keys, const float* values,
                                  int query_heads, int kv_heads, int head_dim, int tokens, float* output, void* stream) {
     return op_call(c, [&] {
@@ -1412,6 +1559,7 @@ int satori_hip_matrix_decode_row(satori_hip_matrix* m, int row, float* output, v
         set_device(c);
         check_hip(launch_decode_row(m->payload, s.format, s.rows, s.columns, row, output, op_stream(c, stream)),
                   "decode_row launch");
+        note_launch(c, m, op_stream(c, stream));
     });
 }
 

@@ -60,6 +60,74 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, cons
         yv[i] = static_cast<float>(static_cast<double>(xv[i]) * scale * static_cast<double>(w[i]));
 }
 
+// Add then RmsNorm (DenseForward.cs:156-158 and :149 of the next layer): residual += addend in FP32, then the
+// RmsNorm of the new residual into `normed`. The per-thread partition and the reduction tree are those of
+// rms_norm_kernel, so the outputs equal the two separate calls bit for bit.
+__global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(float* residual, const float* addend,
+                                                                const float* __restrict__ w, float epsilon, int length,
+                                                                float* normed) {
+    __shared__ double red[kThreads];
+    double part = 0;
+    for (int i = threadIdx.x; i < length; i += kThreads) {
+        const float r = __fadd_rn(residual[i], addend[i]);
+        residual[i] = r;
+        const double v = r;
+        part = part + v * v;
+    }
+    const double sum = block_sum(part, red);
+    const double scale = 1.0 / __dsqrt_rn(sum / length + static_cast<double>(epsilon));
+    for (int i = threadIdx.x; i < length; i += kThreads)
+        normed[i] = static_cast<float>(static_cast<double>(residual[i]) * scale * static_cast<double>(w[i]));
+}
+
+// The attention inputs of one decode position (DenseForward.cs:128-151): q += q_bias and k + k_bias,
+// v + v_bias (when the biases are given), then RopeHalf of q and of the key, the key and value written to
+// their cache slots. Same per-element operations as Add and RopeHalf, so the outputs equal the separate
+// calls bit for bit. Threads: q pairs, key pairs, then the unrotated q and key lanes, then the values.
+__device__ __forceinline__ float biased(const float* x, const float* bias, int i) {
+    return bias ? __fadd_rn(x[i], bias[i]) : x[i];
+}
+
+__global__ __launch_bounds__(kThreads) void attention_inputs_kernel(float* q, const float* q_bias, const float* k,
+                                                                    const float* k_bias, float* k_out, const float* v,
+                                                                    const float* v_bias, float* v_out, int heads,
+                                                                    int kv_heads, int head_dim, int position,
+                                                                    double base, int rotary) {
+    const int pairs = rotary / 2, pass = head_dim - rotary;
+    const int64_t qp = static_cast<int64_t>(heads) * pairs, kp = static_cast<int64_t>(kv_heads) * pairs;
+    const int64_t qr = static_cast<int64_t>(heads) * pass, kr = static_cast<int64_t>(kv_heads) * pass;
+    const int64_t vw = static_cast<int64_t>(kv_heads) * head_dim;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < qp + kp) {
+        const bool is_q = i < qp;
+        const int64_t index = is_q ? i : i - qp;
+        const int head = static_cast<int>(index / pairs), kk = static_cast<int>(index % pairs);
+        const int a = head * head_dim + kk, b = a + pairs;
+        const double angle = position / pow(base, 2.0 * kk / rotary);
+        const double sn = sin(angle), cs = cos(angle);
+        const double x = is_q ? biased(q, q_bias, a) : biased(k, k_bias, a);
+        const double y = is_q ? biased(q, q_bias, b) : biased(k, k_bias, b);
+        float* dst = is_q ? q : k_out;
+        dst[a] = static_cast<float>(x * cs - y * sn);
+        dst[b] = static_cast<float>(x * sn + y * cs);
+        return;
+    }
+    i -= qp + kp;
+    if (i < qr + kr) {  // lanes past the rotary dimensions pass through (biased)
+        const bool is_q = i < qr;
+        const int64_t index = is_q ? i : i - qr;
+        const int head = static_cast<int>(index / pass), lane = rotary + static_cast<int>(index % pass);
+        const int e = head * head_dim + lane;
+        if (is_q)
+            q[e] = biased(q, q_bias, e);
+        else
+            k_out[e] = biased(k, k_bias, e);
+        return;
+    }
+    i -= qr + kr;
+    if (i < vw) v_out[i] = biased(v, v_bias, static_cast<int>(i));
+}
+
 // RmsNormHeads (TransformerOps.cs:117-130): one workgroup per head, in place.
 __global__ __launch_bounds__(kThreads) void rms_norm_heads_kernel(float* v, const float* __restrict__ w, float epsilon,
                                                                   int head_dim) {
@@ -118,41 +186,110 @@ __global__ __launch_bounds__(kThreads) void add_kernel(const float* left, const 
     out[i] = __fadd_rn(left[i], right[i]);
 }
 
-// GroupedAttention (TransformerOps.cs:135-179): one workgroup per query head. The head's scores live in LDS
-// (`tokens` doubles); each dot product runs over the head lanes in order as the reference's, the maximum is
-// exact, the exponentials and their total are FP64, and each output lane sums its tokens in order.
-__global__ __launch_bounds__(kThreads) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                             const float* __restrict__ v, int query_heads, int kv_heads,
-                                                             int head_dim, int tokens, float* __restrict__ out) {
+// GroupedAttention (TransformerOps.cs:135-179): one workgroup of 1024 threads per query head. Scores: one
+// thread per token, the dot product over the head lanes in the reference's order (the query staged in LDS,
+// the key row read in 16-byte loads). The maximum is exact; the exponentials and their total are FP64, and the reference's
+// weight of token t, scores[t] / total, is formed once per token. Output: lane j of the head is summed over
+// eight token groups (threads j + 128 g), whose FP64 partial sums are added in group order. The FP64
+// reassociations stay far below the FP32 output's last place.
+constexpr int kAttnThreads = 1024;
+constexpr int kAttnGroups = kAttnThreads / 128;  // token groups of the output sums (head_dim <= 128 per pass)
+
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                                 const float* __restrict__ v, int query_heads,
+                                                                 int kv_heads, int head_dim, int tokens,
+                                                                 float* __restrict__ out) {
     extern __shared__ double scores[];  // tokens
-    __shared__ double red[kThreads];
+    __shared__ double red[kAttnThreads];
     const int head = blockIdx.x;
     const int kv_head = head / (query_heads / kv_heads);
     const int kv_width = kv_heads * head_dim;
     const float* qh = q + static_cast<int64_t>(head) * head_dim;
     const double scale = 1.0 / __dsqrt_rn(static_cast<double>(head_dim));
-    double local_max = -INFINITY;
-    for (int t = threadIdx.x; t < tokens; t += kThreads) {
+    __shared__ float qs[512];  // the head's query lanes (head_dim <= 512 staged; wider heads read global)
+    for (int j = threadIdx.x; j < head_dim && j < 512; j += kAttnThreads) qs[j] = qh[j];
+    __syncthreads();
+    const bool staged = head_dim <= 512 && (head_dim & 3) == 0;  // 16-byte loads need 4-byte alignment only
+    for (int t = threadIdx.x; t < tokens; t += kAttnThreads) {
         const float* kt = k + static_cast<int64_t>(t) * kv_width + kv_head * head_dim;
         double dot = 0;
-        for (int j = 0; j < head_dim; ++j) dot = dot + static_cast<double>(qh[j]) * static_cast<double>(kt[j]);
-        const double s = dot * scale;
-        scores[t] = s;
-        local_max = fmax(local_max, s);
+        if (staged) {
+            // The token's key row in 16-byte loads, eight in flight; the dot product in lane order.
+            for (int j0 = 0; j0 < head_dim; j0 += 32) {
+                f32x4 kv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (j0 + 4 * i < head_dim) {
+                        const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(kt + j0 + 4 * i));
+                        kv[i] = f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                      __uint_as_float(raw[3])};
+                    }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (j0 + 4 * i >= head_dim) break;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        dot = dot + static_cast<double>(qs[j0 + 4 * i + e]) * static_cast<double>(kv[i][e]);
+                }
+            }
+        } else {
+            for (int j = 0; j < head_dim; ++j) dot = dot + static_cast<double>(qh[j]) * static_cast<double>(kt[j]);
+        }
+        scores[t] = dot * scale;
     }
-    const double max = block_max(local_max, red);
+    __syncthreads();
+    double local_max = -INFINITY;
+    for (int t = threadIdx.x; t < tokens; t += kAttnThreads) local_max = fmax(local_max, scores[t]);
+    red[threadIdx.x] = local_max;
+    __syncthreads();
+    for (int s = kAttnThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = fmax(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const double max = red[0];
+    __syncthreads();
     double part = 0;
-    for (int t = threadIdx.x; t < tokens; t += kThreads) {
+    for (int t = threadIdx.x; t < tokens; t += kAttnThreads) {
         const double e = exp(scores[t] - max);
         scores[t] = e;
         part = part + e;
     }
-    const double total = block_sum(part, red);  // also orders the exponentials before their use below
-    for (int j = threadIdx.x; j < head_dim; j += kThreads) {
+    red[threadIdx.x] = part;
+    __syncthreads();
+    for (int s = kAttnThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
+        __syncthreads();
+    }
+    const double total = red[0];
+    __syncthreads();
+    for (int t = threadIdx.x; t < tokens; t += kAttnThreads) scores[t] = scores[t] / total;
+    __syncthreads();
+    const int per_group = (tokens + kAttnGroups - 1) / kAttnGroups;
+    for (int j0 = 0; j0 < head_dim; j0 += 128) {
+        const int j = j0 + (threadIdx.x & 127), group = threadIdx.x >> 7;
         double sum = 0;
-        for (int t = 0; t < tokens; ++t)
-            sum = sum + scores[t] / total * static_cast<double>(v[static_cast<int64_t>(t) * kv_width + kv_head * head_dim + j]);
-        out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(sum);
+        if (j < head_dim) {
+            const int t_end = min(tokens, (group + 1) * per_group);
+            const float* vj = v + kv_head * head_dim + j;
+            int t = group * per_group;
+            for (; t + 8 <= t_end; t += 8) {  // eight loads in flight, then the sums in token order
+                float vt[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) vt[i] = vj[static_cast<int64_t>(t + i) * kv_width];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sum = sum + scores[t + i] * static_cast<double>(vt[i]);
+            }
+            for (; t < t_end; ++t) sum = sum + scores[t] * static_cast<double>(vj[static_cast<int64_t>(t) * kv_width]);
+        }
+        red[threadIdx.x] = sum;
+        __syncthreads();
+        if (threadIdx.x < 128 && j < head_dim) {
+            double total_j = 0;
+#pragma unroll
+            for (int g = 0; g < kAttnGroups; ++g) total_j = total_j + red[threadIdx.x + 128 * g];
+            out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(total_j);
+        }
+        __syncthreads();
     }
 }
 
@@ -231,12 +368,29 @@ hipError_t launch_add(const float* left, const float* right, int length, float* 
     return hipGetLastError();
 }
 
-int attention_max_tokens() { return 8192; }  // 64 KB of FP64 scores in LDS
+hipError_t launch_add_rms_norm(float* residual, const float* addend, const float* w, float epsilon, int length,
+                               float* normed, hipStream_t stream) {
+    add_rms_norm_kernel<<<1, kThreads, 0, stream>>>(residual, addend, w, epsilon, length, normed);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k, const float* k_bias, float* k_out,
+                                   const float* v, const float* v_bias, float* v_out, int heads, int kv_heads,
+                                   int head_dim, int position, double base, int rotary, hipStream_t stream) {
+    const int64_t items = static_cast<int64_t>(heads + kv_heads) * (rotary / 2) +
+                          static_cast<int64_t>(heads + kv_heads) * (head_dim - rotary) +
+                          static_cast<int64_t>(kv_heads) * head_dim;
+    attention_inputs_kernel<<<grid_for(items), kThreads, 0, stream>>>(q, q_bias, k, k_bias, k_out, v, v_bias, v_out,
+                                                                     heads, kv_heads, head_dim, position, base, rotary);
+    return hipGetLastError();
+}
+
+int attention_max_tokens() { return 6912; }  // FP64 scores in LDS: 54 KB, with the 8 KB reduction buffer and the 2 KB query 64 KB
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
                             int head_dim, int tokens, float* out, hipStream_t stream) {
     if (tokens > attention_max_tokens()) return hipErrorInvalidValue;
-    attention_kernel<<<query_heads, kThreads, static_cast<size_t>(tokens) * sizeof(double), stream>>>(
+    attention_kernel<<<query_heads, kAttnThreads, static_cast<size_t>(tokens) * sizeof(double), stream>>>(
         q, k, v, query_heads, kv_heads, head_dim, tokens, out);
     return hipGetLastError();
 }

@@ -1,0 +1,152 @@
+"""One decode token on the device: the projection sequence of DenseForward.Step and Final
+(src/Satori.Core/Model/DenseForward.cs:100-162, 298-306) over resident quantized matrices, with the operators
+of TransformerOps (src/Satori.Core/TransformerOps.cs) between the projections, the key/value cache on the
+device, and the whole token recordable as one replayable step (HipContext.capture_begin / capture_end).
+
+Per layer: RmsNorm -> q/k/v projections (one group launch) -> bias adds (k and v written straight into the
+cache slot) -> half-split RoPE of q and the new key -> grouped attention over the cached prefix -> o projection
+-> residual add -> RmsNorm -> gate/up projections (one group launch) -> SwiGLU -> down projection -> residual
+add. Then the final RmsNorm and the output projection. The K-format projections quantize their input to Q8_K
+inside their own launch, so no separate quantization runs. By default the attention inputs (bias adds, RoPE,
+cache writes) are one launch and each residual add shares a launch with the RmsNorm after it: 9 launches per
+layer instead of 14, with bit-identical results.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import DeviceOps, HipContext, HipGroup, HipQuantizedMatrix, HipStep
+
+
+@dataclass
+class DecoderConfig:
+    hidden: int          # embedding width
+    heads: int           # query heads
+    kv_heads: int        # key/value heads
+    head_dim: int
+    ffn: int             # feed-forward width
+    epsilon: float       # RMS norm epsilon
+    rope_base: float     # RoPE frequency base
+    max_tokens: int      # key/value cache capacity (positions)
+
+
+class DeviceDecoder:
+    """Resident decode loop. `layers[i]` maps "q", "k", "v", "o", "gate", "up", "down" to resident matrices;
+    `vectors[i]` maps "attn_norm", "ffn_norm" (and optionally "q_bias", "k_bias", "v_bias") to device
+    pointers of FP32 vectors; `output_norm` is a device pointer, `output` the output projection and
+    `embedding` the token-embedding matrix (its rows are decoded on the device, GgufQuantizedMatrix.ReadRow)."""
+
+    def __init__(self, context: HipContext, config: DecoderConfig, layers: list[dict], vectors: list[dict],
+                 output_norm: int, output: HipQuantizedMatrix, embedding: HipQuantizedMatrix):
+        self.ctx, self.cfg = context, config
+        self.layers, self.vectors = layers, vectors
+        self.output_norm, self.output, self.embedding = output_norm, output, embedding
+        self.ops = DeviceOps(context)
+        c = config
+        self.q_width = c.heads * c.head_dim
+        self.kv_width = c.kv_heads * c.head_dim
+        self._buffers = []
+
+        def buf(n):
+            p = context.alloc(4 * n)
+            context.upload(p, np.zeros(n, np.float32))
+            self._buffers.append(p)
+            return p
+
+        self.residual, self.normed = buf(c.hidden), buf(c.hidden)
+        self.q, self.k, self.v = buf(self.q_width), buf(self.kv_width), buf(self.kv_width)
+        self.context_vec, self.projected = buf(self.q_width), buf(c.hidden)
+        self.gate, self.up, self.activated = buf(c.ffn), buf(c.ffn), buf(c.ffn)
+        self.logits = buf(output.rows)
+        self.zero_kv = buf(self.kv_width)
+        self.keys = [buf(c.max_tokens * self.kv_width) for _ in layers]
+        self.values = [buf(c.max_tokens * self.kv_width) for _ in layers]
+        self.groups = []
+        for m in layers:
+            self.groups.append({
+                "qkv": HipGroup(context, [m["q"], m["k"], m["v"]], [self.normed] * 3, [self.q, self.k, self.v], True),
+                "o": HipGroup(context, [m["o"]], [self.context_vec], [self.projected], True),
+                "gateup": HipGroup(context, [m["gate"], m["up"]], [self.normed] * 2, [self.gate, self.up], True),
+                "down": HipGroup(context, [m["down"]], [self.activated], [self.projected], True),
+            })
+        self.final = HipGroup(context, [output], [self.normed], [self.logits], True)
+
+    def enqueue(self, token: int, position: int, fused: bool = True) -> None:
+        """Enqueues one token at `position` (keys/values of positions < position are in the cache). Fused:
+        the bias adds, RoPE and cache writes of a layer's attention inputs are one launch, and every residual
+        add shares its launch with the RmsNorm that follows (bit-identical to the unfused sequence)."""
+        c, ops = self.cfg, self.ops
+        if not 0 <= position < c.max_tokens:
+            raise ValueError("position outside the key/value cache")
+        self.embedding.decode_row_device(token, self.residual)
+        if fused:
+            ops.rms_norm(self.residual, self.vectors[0]["attn_norm"], c.epsilon, c.hidden, self.normed)
+        for layer, (g, vec) in enumerate(zip(self.groups, self.vectors)):
+            k_slot = self.keys[layer] + 4 * position * self.kv_width
+            v_slot = self.values[layer] + 4 * position * self.kv_width
+            if not fused:
+                ops.rms_norm(self.residual, vec["attn_norm"], c.epsilon, c.hidden, self.normed)
+            g["qkv"].execute()
+            if fused:
+                ops.attention_inputs(self.q, vec.get("q_bias", 0), self.k, vec.get("k_bias", 0), k_slot, self.v,
+                                     vec.get("v_bias", 0), v_slot, c.heads, c.kv_heads, c.head_dim, position,
+                                     c.rope_base, c.head_dim)
+            else:
+                if "q_bias" in vec:
+                    ops.add(self.q, vec["q_bias"], self.q_width, self.q)
+                ops.add(self.k, vec.get("k_bias", self.zero_kv), self.kv_width, k_slot)
+                ops.add(self.v, vec.get("v_bias", self.zero_kv), self.kv_width, v_slot)
+                ops.rope_half(self.q, self.q_width, c.head_dim, position, c.rope_base, c.head_dim)
+                ops.rope_half(k_slot, self.kv_width, c.head_dim, position, c.rope_base, c.head_dim)
+            ops.grouped_attention(self.q, self.keys[layer], self.values[layer], c.heads, c.kv_heads, c.head_dim,
+                                  position + 1, self.context_vec)
+            g["o"].execute()
+            if fused:
+                ops.add_rms_norm(self.residual, self.projected, vec["ffn_norm"], c.epsilon, c.hidden, self.normed)
+            else:
+                ops.add(self.residual, self.projected, c.hidden, self.residual)
+                ops.rms_norm(self.residual, vec["ffn_norm"], c.epsilon, c.hidden, self.normed)
+            g["gateup"].execute()
+            ops.swiglu(self.gate, self.up, c.ffn, self.activated)
+            g["down"].execute()
+            if fused:
+                following = (self.vectors[layer + 1]["attn_norm"] if layer + 1 < len(self.groups)
+                             else self.output_norm)
+                ops.add_rms_norm(self.residual, self.projected, following, c.epsilon, c.hidden, self.normed)
+            else:
+                ops.add(self.residual, self.projected, c.hidden, self.residual)
+        if not fused:
+            ops.rms_norm(self.residual, self.output_norm, c.epsilon, c.hidden, self.normed)
+        self.final.execute()
+
+    def launches_per_token(self, fused: bool = True) -> int:
+        if fused:
+            return 2 + 9 * len(self.layers) + 1
+        per_layer = 14 if all("q_bias" in v for v in self.vectors) else 13
+        return 1 + per_layer * len(self.layers) + 2
+
+    def capture(self, token: int, position: int, fused: bool = True) -> HipStep:
+        """The token at `position` recorded as one replayable step."""
+        self.ctx.capture_begin()
+        try:
+            self.enqueue(token, position, fused)
+        except BaseException:
+            self.ctx.capture_end().dispose()
+            raise
+        return self.ctx.capture_end()
+
+    def read_logits(self) -> np.ndarray:
+        out = np.zeros(self.output.rows, np.float32)
+        self.ctx.synchronize()
+        return self.ctx.download(out, self.logits)
+
+    def dispose(self) -> None:
+        for g in self.groups:
+            for gr in g.values():
+                gr.dispose()
+        self.final.dispose()
+        for p in self._buffers:
+            self.ctx.free(p)
+        self._buffers = []

@@ -969,7 +969,7 @@ def test_operators_match_oracle_at_decode_sizes(context):
     _within_ulp(out, O.swiglu(gate, up), "swiglu")
     T.add(gate, up, out, context)
     assert np.array_equal(out, O.add(gate, up))
-    for tokens in (1, 2, 33, 257, 2048):
+    for tokens in (1, 2, 33, 257, 2048, 6912):
         keys = g.standard_normal(tokens * 256).astype(np.float32)
         values = g.standard_normal(tokens * 256).astype(np.float32)
         out = np.zeros(12 * 128, np.float32)
@@ -999,7 +999,7 @@ def test_operator_extremes_and_argument_errors(context):
         T.grouped_attention(np.zeros(32, np.float32), np.zeros(48, np.float32), np.zeros(48, np.float32), 4, 3, 8, 3,
                             np.zeros(32, np.float32), context)
     with pytest.raises(S.NotSupportedException):
-        T.attention(np.zeros(2, np.float32), np.zeros(2 * 8193, np.float32), np.zeros(2 * 8193, np.float32), 2, 8193,
+        T.attention(np.zeros(2, np.float32), np.zeros(2 * 6913, np.float32), np.zeros(2 * 6913, np.float32), 2, 6913,
                     np.zeros(2, np.float32), context)
     # Partial overlap of device ranges is rejected before anything runs (TransformerOps.cs:7-11).
     import ctypes
@@ -1033,3 +1033,107 @@ def test_embedding_rows_decode_like_the_reference(context, fmt):
         with pytest.raises(S.ArgumentOutOfRangeException):
             m.read_row(rows, out)
     m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# A whole decode token on the device (DenseForward.Step + Final), eager and captured
+# ---------------------------------------------------------------------------------------------
+
+def test_device_decode_token_matches_host_composition(context):
+    # DenseForward.Step / Final (DenseForward.cs:100-162, 298-306) on a small random model: the device token
+    # (eager, and captured then replayed three times with eager work in between) against the same sequence
+    # composed on the host from the oracle's operators and integer projections. Eager and replayed logits
+    # are bit-identical; against the host they agree to 1e-3 of the largest logit (operator outputs within
+    # one unit in the last place can move a Q8_K code of a later projection by one step).
+    from satori_amd.decode import DecoderConfig, DeviceDecoder
+    g = rng(2718)
+    cfg = DecoderConfig(hidden=512, heads=4, kv_heads=2, head_dim=128, ffn=1024, epsilon=1e-6, rope_base=1e6,
+                        max_tokens=64)
+    vocab, n_layers, position, token = 300, 2, 37, 123
+    qw, kvw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+
+    def quant(rows, cols, fmt, scale=0.05):
+        return S.quantize_weights((g.standard_normal((rows, cols)) * scale).astype(np.float32), rows, cols, fmt)
+
+    shapes = {"q": (qw, cfg.hidden, BQ.Q4_K), "k": (kvw, cfg.hidden, BQ.Q4_K), "v": (kvw, cfg.hidden, BQ.Q4_K),
+              "o": (cfg.hidden, qw, BQ.Q4_K), "gate": (cfg.ffn, cfg.hidden, BQ.Q4_K),
+              "up": (cfg.ffn, cfg.hidden, BQ.Q4_K), "down": (cfg.hidden, cfg.ffn, BQ.Q6_K)}
+    host_layers, dev_layers, host_vecs, dev_vecs, buffers = [], [], [], [], []
+
+    def dev_vec(a):
+        p = context.alloc(a.nbytes)
+        context.upload(p, a)
+        buffers.append(p)
+        return p
+
+    for _ in range(n_layers):
+        data = {n: quant(r, c, f) for n, (r, c, f) in shapes.items()}
+        host_layers.append(data)
+        dev_layers.append({n: context.create(d, S.QuantizedMatrixShape(*shapes[n])) for n, d in data.items()})
+        vec = {"attn_norm": g.uniform(0.5, 1.5, cfg.hidden).astype(np.float32),
+               "ffn_norm": g.uniform(0.5, 1.5, cfg.hidden).astype(np.float32),
+               "q_bias": (g.standard_normal(qw) * 0.1).astype(np.float32),
+               "k_bias": (g.standard_normal(kvw) * 0.1).astype(np.float32),
+               "v_bias": (g.standard_normal(kvw) * 0.1).astype(np.float32)}
+        host_vecs.append(vec)
+        dev_vecs.append({k: dev_vec(v) for k, v in vec.items()})
+    out_norm = g.uniform(0.5, 1.5, cfg.hidden).astype(np.float32)
+    out_data = quant(vocab, cfg.hidden, BQ.Q6_K, 0.1)
+    output = context.create(out_data, S.QuantizedMatrixShape(vocab, cfg.hidden, BQ.Q6_K))
+    dec = DeviceDecoder(context, cfg, dev_layers, dev_vecs, dev_vec(out_norm), output, output)  # tied embedding
+    # A random key/value prefix for positions < `position`, the same on both sides.
+    prefix_k = [(g.standard_normal((cfg.max_tokens, kvw)) * 0.5).astype(np.float32) for _ in range(n_layers)]
+    prefix_v = [(g.standard_normal((cfg.max_tokens, kvw)) * 0.5).astype(np.float32) for _ in range(n_layers)]
+    for layer in range(n_layers):
+        context.upload(dec.keys[layer], prefix_k[layer])
+        context.upload(dec.values[layer], prefix_v[layer])
+
+    def proj(data, rows, cols, fmt, x):
+        return O.qk_matvec_quantized_avx2(data, rows, cols, int(fmt), O.q8k_quantize_row(x))
+
+    row_bytes = out_data.size // vocab
+    x = O.q_decode_row(out_data[token * row_bytes:(token + 1) * row_bytes], cfg.hidden, int(BQ.Q6_K))
+    for layer in range(n_layers):
+        d, vec = host_layers[layer], host_vecs[layer]
+        normed = O.rms_norm(x, vec["attn_norm"], np.float32(cfg.epsilon))
+        q = O.add(proj(d["q"], qw, cfg.hidden, BQ.Q4_K, normed), vec["q_bias"])
+        k = O.add(proj(d["k"], kvw, cfg.hidden, BQ.Q4_K, normed), vec["k_bias"])
+        v = O.add(proj(d["v"], kvw, cfg.hidden, BQ.Q4_K, normed), vec["v_bias"])
+        q = O.rope_half(q, cfg.head_dim, position, cfg.rope_base, cfg.head_dim)
+        k = O.rope_half(k, cfg.head_dim, position, cfg.rope_base, cfg.head_dim)
+        keys, values = prefix_k[layer].copy(), prefix_v[layer].copy()
+        keys[position], values[position] = k, v
+        ctx_vec = O.grouped_attention(q, keys[:position + 1].reshape(-1), values[:position + 1].reshape(-1),
+                                      cfg.heads, cfg.kv_heads, cfg.head_dim, position + 1)
+        x = O.add(x, proj(d["o"], cfg.hidden, qw, BQ.Q4_K, ctx_vec))
+        normed = O.rms_norm(x, vec["ffn_norm"], np.float32(cfg.epsilon))
+        act = O.swiglu(proj(d["gate"], cfg.ffn, cfg.hidden, BQ.Q4_K, normed),
+                       proj(d["up"], cfg.ffn, cfg.hidden, BQ.Q4_K, normed))
+        x = O.add(x, proj(d["down"], cfg.hidden, cfg.ffn, BQ.Q6_K, act))
+    expected = proj(out_data, vocab, cfg.hidden, BQ.Q6_K, O.rms_norm(x, out_norm, np.float32(cfg.epsilon)))
+
+    dec.enqueue(token, position)
+    eager = dec.read_logits()
+    assert np.all(np.isfinite(eager))
+    err = np.abs(eager.astype(np.float64) - expected)
+    assert err.max() <= 1e-3 * np.abs(expected).max(), f"max err {err.max()} of {np.abs(expected).max()}"
+    dec.enqueue(token, position, fused=False)  # the unfused operator sequence gives the same bits
+    assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32))
+    step = dec.capture(token, position)
+    for replay in range(3):
+        context.upload(dec.logits, np.zeros(vocab, np.float32))
+        dec.enqueue(5, 40)  # eager work between replays: another token, a cache slot the step does not read
+        step.execute()
+        assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), replay
+    with pytest.raises(S.ArgumentException):
+        dev_layers[0]["q"].dispose()  # held by the decoder's group
+    with pytest.raises(S.InvalidOperationException):
+        context.capture_end()          # nothing is being captured
+    step.dispose()
+    dec.dispose()
+    for layer in dev_layers:
+        for m in layer.values():
+            m.dispose()
+    output.dispose()
+    for p in buffers:
+        context.free(p)
