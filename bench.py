@@ -21,7 +21,8 @@ The same line carries, labelled:
   prefill:   the same model's projections over 512 positions (ExecuteBatch in 256-position chunks);
              tokens/s and int8 TOP/s;
   roofline:  for the headline kernel, from HIP events on the launch stream;
-  cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core.
+  cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core; each format's
+             entry also carries its own restated reference AVX2 path timed on one core (cpu_gbs).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 """
@@ -368,15 +369,46 @@ def profiled_traffic(name: str):
     return None, None
 
 
+def pin_one_core():
+    """Pins this process to its first allowed core (the CPU baselines run on one thread, as the reference's
+    own measurements do); returns the core, or None where affinity cannot be set."""
+    try:
+        core = sorted(os.sched_getaffinity(0))[0]
+        os.sched_setaffinity(0, {core})
+        return core
+    except (AttributeError, OSError):
+        return None
+
+
+def cpu_format(data, rows, columns, fmt, x, quantized, seconds) -> dict:
+    """Restated reference AVX2 path of one format (oracle) on one host core, warm payload, bounded sample:
+    Ternary2Avx2Kernel for Ternary2, QuantizedAvx2Kernel for Q8_0 / Q4_0, and for the K formats the decode
+    path (Q8KCodec.QuantizeRow of x, then QuantizedKAvx2Kernel.ExecuteQuantizedTiled at one position)."""
+    from oracle import oracle as O
+
+    y = np.zeros(rows, np.float32)
+    if fmt is None:  # Ternary2, block size in `quantized`
+        run = lambda: O.t2_matvec_avx2(data, rows, columns, quantized, x, y)
+    elif quantized:
+        run = lambda: O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x), y)
+    else:
+        run = lambda: O.q_matvec_avx2(data, rows, columns, int(fmt), x, y)
+    run()  # warm
+    samples, start = [], time.perf_counter()
+    while time.perf_counter() - start < seconds or len(samples) < 3:
+        t0 = time.perf_counter()
+        run()
+        samples.append(time.perf_counter() - t0)
+    best = min(samples)
+    return {"cpu_gbs": data.size / best / 1e9, "cpu_ms_min": best * 1e3,
+            "cpu_ms_median": sorted(samples)[len(samples) // 2] * 1e3, "cpu_runs": len(samples)}
+
+
 def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
     """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample."""
     from oracle import oracle as O
 
-    try:
-        core = sorted(os.sched_getaffinity(0))[0]
-        os.sched_setaffinity(0, {core})
-    except (AttributeError, OSError):
-        core = None
+    core = pin_one_core()
     y = np.zeros(rows, np.float32)
     O.t2_matvec_avx2(payload, rows, columns, block, x, y)  # warm
     iterations, start = 0, time.perf_counter()
@@ -411,6 +443,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-format-seconds", type=float, default=1.0,
+                    help="CPU sample per format (restated reference AVX2 path, one core)")
     ap.add_argument("--warmup-seconds", type=float, default=1.5,
                     help="untimed headline launches before the first timed region (steady-state clocks)")
     ap.add_argument("--quick", action="store_true", help="headline workload only, no other formats")
@@ -466,12 +500,14 @@ def main() -> int:
     head.close()
 
     formats = {"ternary2-4096-b128": headline}
+    cpu_cases = {"ternary2-4096-b128": (payload, rows, columns, None, x, block)}
     if not args.quick:
         for b in (64, 256):
             p, xb = make_ternary2(rows, columns, b)
             c = Case(ctx, f"ternary2-4096-b{b}", lambda: ctx.create_ternary2(rows, columns, b, p), p.size, rows,
                      columns, xb, False)
             formats[c.name] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
+            cpu_cases[c.name] = (p, rows, columns, None, xb, b)
             c.close()
         for fmt, r, cc, quantized, label in (
                 (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
@@ -485,6 +521,7 @@ def main() -> int:
             shape = S.QuantizedMatrixShape(r, cc, fmt)
             c = Case(ctx, label, lambda: ctx.create(data, shape), data.size, r, cc, xf, quantized)
             formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
+            cpu_cases[label] = (data, r, cc, fmt, xf, quantized)
             c.close()
 
     decode = pre = token = None
@@ -500,6 +537,11 @@ def main() -> int:
 
     progress("cpu baseline")
     cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
+    if not args.quick:
+        progress("cpu baseline per format")
+        for label, case in cpu_cases.items():
+            formats[label].update(cpu_format(*case, args.cpu_format_seconds))
+            formats[label]["gpu_over_cpu"] = formats[label]["gbs"] / formats[label]["cpu_gbs"]
     value = headline["gbs"]
     traffic, traffic_source = profiled_traffic("ternary2_4096_b128_grouped.md")
     line = {

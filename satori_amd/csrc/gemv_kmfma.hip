@@ -8,8 +8,8 @@
 // single-position integer kernel's bit for bit.
 //
 // Two launches. The pack kernel quantizes every (position, block) to Q8_K (the same bytes as the reference
-// quantizer) and stores the codes in the order the MFMA operands are read, with the block scales in a
-// separate array; the product kernel then needs no LDS and no barriers.
+// quantizer) and stores the codes in the order the MFMA operands are read, with the block scales and the
+// group sums (as FP16) in separate arrays; the product kernel stages each round's blocks in LDS.
 //
 // Product orientation: D = C x W^T with the positions' codes as the first operand (M = 32 positions) and the
 // weights as the second (N = 32 rows). Lane l = 32h + r then holds the 16 outputs of row r at positions
@@ -17,11 +17,12 @@
 // 32-position tile and walks its blocks in order, loading block b+1 while it computes block b.
 //
 // Q4_K: Dot = sum_j s_j * D_j with D_j = sum over sub-block j (32 weights) of q * c: one 32x32x32 MFMA per
-// sub-block and an int24 multiply-add by s_j; Min = sum_j m_j * sum_j c is an MFMA chain whose weight
-// operand is m_j repeated over the sub-block. Q6_K: Dot = sum_k sc_k * (D_k - 32 * sum_k c) over the 16
-// groups of 16 weights: one 32x32x16 MFMA per group and a multiply-add by sc_k; the centring sum is an
-// MFMA chain whose weight operand is sc_k repeated over the group. All magnitudes stay below 2^23 before
-// the int24 multiply (|D_j| <= 32 * 15 * 127, |D_k| <= 16 * 63 * 127) and below 2^31 after.
+// sub-block and an int24 multiply-add by s_j; Min = sum_j m_j * (bsum_2j + bsum_2j+1) is one 32x32x16 FP16
+// product of the 16 group sums with m_(g/2). Q6_K: Dot = sum_k sc_k * D_k - 32 * sum_k sc_k * bsum_k over
+// the 16 groups of 16 weights: one 32x32x16 MFMA per group and a multiply-add by sc_k, and one FP16 product
+// of the group sums with sc_k. All magnitudes stay below 2^23 before the int24 multiply
+// (|D_j| <= 32 * 15 * 127, |D_k| <= 16 * 63 * 127) and below 2^31 after; the FP16 products are exact
+// (operands of at most 11 significant bits, sums below 2^24).
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -33,6 +34,8 @@ namespace {
 
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTile = 32;      // rows and positions per wave tile
 
@@ -42,6 +45,14 @@ __device__ __forceinline__ i32x16 mfma32(const i32x4& c, const i32x4& w, const i
 
 __device__ __forceinline__ i32x16 mfma16(long c, long w, const i32x16& acc) {
     return __builtin_amdgcn_mfma_i32_32x32x16_i8(c, w, acc, 0, 0, 0);
+}
+
+// One 32x32x16 FP16 product into FP32 (lane l holds k = 8 (l / 32) .. + 8 of row / column l % 32, the same
+// output layout as the int8 products). Used for the block's group-sum terms, whose operands are integers of
+// at most 11 significant bits (exact in FP16) and whose products and sums stay below 2^24, so the FP32
+// result is the exact integer.
+__device__ __forceinline__ f32x16 mfma_f16(const f16x8& a, const f16x8& b) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, f32x16{}, 0, 0, 0);
 }
 
 // Signed 24-bit multiply-add (v_mad_i32_i24): both factors must fit in 24 bits. The empty asm makes the
@@ -59,7 +70,9 @@ __device__ __forceinline__ int mad24(int a, int b, int c) {
 // at (b * tiles + t) * 8192, split into `chunks` chunks of 256 / chunks codes (8 for Q4_K: the 32x32x32
 // operand, 16 for Q6_K: the 32x32x16 operand); chunk j's lane l = 32h + r holds the codes
 // j * (256 / chunks) + h * (128 / chunks) .. + 128 / chunks of position 32t + r, at byte l * (128 / chunks).
-// Scales: float at (b * tiles + t) * 32 + r. Positions past the last are zero codes and scale 0.
+// Scales: float at (b * tiles + t) * 32 + r. Group sums (the 16 Q8_K sums of 16 codes, |sum| <= 2032) as FP16
+// in the first operand order of the 32x32x16 FP16 product: 1 KB per (block, tile), lane l = 32h + r holding
+// sums 8h .. 8h + 7 of position 32t + r. Positions past the last are zero codes, sums and scale 0.
 __device__ __forceinline__ int64_t pack_code_offset(int b, int t, int tiles, int chunks, int k, int r) {
     const int per = 256 / chunks, half = per / 2;
     const int j = k / per, h = (k % per) / half;
@@ -69,7 +82,7 @@ __device__ __forceinline__ int64_t pack_code_offset(int b, int t, int tiles, int
 // One wave per (position, block): four blocks of one position per workgroup.
 __global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict__ x, int columns, int positions,
                                                          int tiles, int chunks, uint8_t* __restrict__ codes,
-                                                         float* __restrict__ scales) {
+                                                         float* __restrict__ scales, _Float16* __restrict__ sums) {
     const int blocks = columns / 256;
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= blocks) return;
@@ -84,6 +97,11 @@ __global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict
     }
     store_u32(reinterpret_cast<uint32_t*>(codes + pack_code_offset(b, t, tiles, chunks, 4 * lane, r)), q.packed);
     if (lane == 0) store_f32(scales + (static_cast<int64_t>(b) * tiles + t) * 32 + r, q.scale);
+    if ((lane & 3) == 0) {  // lane 4g holds the sum of group g (codes 16g .. 16g + 15)
+        const int g = lane >> 2;
+        sums[(static_cast<int64_t>(b) * tiles + t) * 512 + (32 * (g >> 3) + r) * 8 + (g & 7)] =
+            static_cast<_Float16>(static_cast<float>(q.group_sum));
+    }
 }
 
 // The weights one lane needs for one block: its row's data for its k half of every chunk.
@@ -94,7 +112,7 @@ struct Q4KRegs {
 
 struct Q6KRegs {
     uint32_t qla[4][2], qlb[4][2], qh[4][2];  // this lane's 8 bytes of each quarter's arrays
-    u32x4 sc;                                 // quarter c's scale of form kk at byte 4c + kk
+    u32x4 sc;                                 // quarter c's scale of form kk at byte 4c + kk (group 32c' + ...)
     uint32_t dpair;                           // the FP16 d of this block (and its neighbour)
 };
 
@@ -130,12 +148,17 @@ __device__ __forceinline__ uint32_t q6k_form(uint32_t a, uint32_t b, uint32_t hb
     }
 }
 
-// A block's packed codes and scales staged in LDS: the 8 KB of codes in operand order, then the tile's 32
-// position scales.
+// A block's packed codes, group sums and scales staged in LDS: the 8 KB of codes in operand order, the 1 KB of
+// FP16 group sums in operand order, then the tile's 32 position scales.
 struct StagedBlock {
     uint8_t codes[8192];
+    uint8_t sums[1024];
     float scales[32];
 };
+
+__device__ __forceinline__ f16x8 staged_sums(const StagedBlock& sb, int lane) {
+    return *reinterpret_cast<const f16x8*>(sb.sums + 16 * lane);
+}
 
 __device__ __forceinline__ f32x4 staged_scales(const StagedBlock& sb, int q, int h) {
     return *reinterpret_cast<const f32x4*>(sb.scales + 8 * q + 4 * h);
@@ -161,33 +184,28 @@ __device__ __forceinline__ i32x4 staged_codes16(const StagedBlock& sb, int j, in
 __device__ __forceinline__ void block_terms(const Q4KRegs& r, const StagedBlock& sb, int lane, float (&term)[16]) {
     const int h = lane >> 5;
     const float d = half_bits_to_float(r.head[0] & 0xFFFFu), dmin = half_bits_to_float(r.head[0] >> 16);
+    int sc[8], mn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q4k_scale_min(j, r.head, sc[j], mn[j]);
     int dot[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) dot[i] = 0;
-    i32x16 mins = {};
-    int sj, mj;
-    q4k_scale_min(0, r.head, sj, mj);
-    i32x4 c = staged_codes16(sb, 0, lane);
-    i32x16 cur = mfma32(c, q4k_weights(r, 0), i32x16{});
-    mins = mfma32(c, i32x4{mj * 0x01010101, mj * 0x01010101, mj * 0x01010101, mj * 0x01010101}, mins);
+    i32x16 cur = mfma32(staged_codes16(sb, 0, lane), q4k_weights(r, 0), i32x16{});
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         i32x16 next;
-        int sn = 0, mn = 0;
-        if (j + 1 < 8) {
-            q4k_scale_min(j + 1, r.head, sn, mn);
-            const i32x4 cn = staged_codes16(sb, j + 1, lane);
-            next = mfma32(cn, q4k_weights(r, j + 1), i32x16{});
-            mins = mfma32(cn, i32x4{mn * 0x01010101, mn * 0x01010101, mn * 0x01010101, mn * 0x01010101}, mins);
-        }
+        if (j + 1 < 8) next = mfma32(staged_codes16(sb, j + 1, lane), q4k_weights(r, j + 1), i32x16{});
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dot[i] = mad24(sj, cur[i], dot[i]);
+        for (int i = 0; i < 16; ++i) dot[i] = mad24(sc[j], cur[i], dot[i]);
         __builtin_amdgcn_sched_barrier(0);
-        if (j + 1 < 8) {
-            cur = next;
-            sj = sn;
-        }
+        if (j + 1 < 8) cur = next;
     }
+    // MinProduct = sum over the 16 group sums g of m_(g / 2) * sum_g: one FP16 product (|sum_g| <= 2032,
+    // m <= 63, |total| < 2^21).
+    f16x8 mw;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mw[e] = static_cast<_Float16>(static_cast<float>(h ? mn[4 + e / 2] : mn[e / 2]));
+    const f32x16 mins = mfma_f16(staged_sums(sb, lane), mw);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const f32x4 a4 = staged_scales(sb, q, h);
@@ -195,16 +213,15 @@ __device__ __forceinline__ void block_terms(const Q4KRegs& r, const StagedBlock&
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
             const float dA = __fmul_rn(d, a4[e]), dminA = __fmul_rn(dmin, a4[e]);
-            term[i] = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot[i])), __fmul_rn(dminA, static_cast<float>(mins[i])));
+            // mins[i] is the exact integer MinProduct, i.e. its float conversion.
+            term[i] = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot[i])), __fmul_rn(dminA, mins[i]));
         }
     }
 }
 
-__device__ __forceinline__ long q6k_weights(const Q6KRegs& r, int k, int& sc, long& sb) {
+__device__ __forceinline__ long q6k_weights(const Q6KRegs& r, int k, int& sc) {
     const int c = 2 * (k >> 3) + (k & 1), kk = (k & 7) >> 1;
     sc = static_cast<int8_t>(r.sc[c] >> (8 * kk));
-    const uint32_t b = static_cast<uint32_t>(static_cast<uint8_t>(r.sc[c] >> (8 * kk))) * 0x01010101u;
-    sb = static_cast<long>(b) | (static_cast<long>(b) << 32);
     return static_cast<long>(q6k_form(r.qla[c][0], r.qlb[c][0], r.qh[c][0], kk)) |
            (static_cast<long>(q6k_form(r.qla[c][1], r.qlb[c][1], r.qh[c][1], kk)) << 32);
 }
@@ -220,24 +237,13 @@ __device__ __forceinline__ void block_terms(const Q6KRegs& r, const StagedBlock&
     int dot[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) dot[i] = 0;
-    i32x16 cent = {};
     int sc;
-    long sb;
-    long wq = q6k_weights(r, 0, sc, sb);
-    long c = staged_codes8(stage, 0, lane);
-    i32x16 cur = mfma16(c, wq, i32x16{});
-    cent = mfma16(c, sb, cent);
+    i32x16 cur = mfma16(staged_codes8(stage, 0, lane), q6k_weights(r, 0, sc), i32x16{});
 #pragma unroll
     for (int k = 0; k < 16; ++k) {  // group k: weights 16k .. 16k + 15 of the block
         i32x16 next;
         int sn = 0;
-        if (k + 1 < 16) {
-            long sbn;
-            const long wn = q6k_weights(r, k + 1, sn, sbn);
-            const long cn = staged_codes8(stage, k + 1, lane);
-            next = mfma16(cn, wn, i32x16{});
-            cent = mfma16(cn, sbn, cent);
-        }
+        if (k + 1 < 16) next = mfma16(staged_codes8(stage, k + 1, lane), q6k_weights(r, k + 1, sn), i32x16{});
 #pragma unroll
         for (int i = 0; i < 16; ++i) dot[i] = mad24(sc, cur[i], dot[i]);
         __builtin_amdgcn_sched_barrier(0);
@@ -246,14 +252,22 @@ __device__ __forceinline__ void block_terms(const Q6KRegs& r, const StagedBlock&
             sc = sn;
         }
     }
+    // Centring sum = sum over the 16 groups k of sc_k * sum_k: one FP16 product (|sum_k| <= 2032,
+    // |sc_k| <= 128, |total| < 2^23). Group 8h + e's scale is byte e / 2 of dword 2h + e % 2.
+    const uint32_t s0 = h ? r.sc[2] : r.sc[0], s1 = h ? r.sc[3] : r.sc[1];
+    f16x8 sw;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        sw[e] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((e & 1 ? s1 : s0) >> (8 * (e >> 1)))));
+    const f32x16 cent = mfma_f16(staged_sums(stage, lane), sw);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const f32x4 a4 = staged_scales(stage, q, h);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
-            // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32.
-            term[i] = __fmul_rn(__fmul_rn(a4[e], d), static_cast<float>(dot[i] - 32 * cent[i]));
+            // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32 (cent[i] is an exact integer).
+            term[i] = __fmul_rn(__fmul_rn(a4[e], d), static_cast<float>(dot[i] - 32 * static_cast<int>(cent[i])));
         }
     }
 }
@@ -275,7 +289,8 @@ struct Split {
 // group's weights share that XCD's L2.
 template <int FORMAT, int S>
 __global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ codes,
-                                                    const float* __restrict__ scales, float* __restrict__ y, int rows,
+                                                    const float* __restrict__ scales, const uint8_t* __restrict__ sums,
+                                                    float* __restrict__ y, int rows,
                                                     int blocks, int64_t row_bytes, int positions, int tiles,
                                                     int units) {
     using SP = Split<S>;
@@ -294,9 +309,10 @@ __global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ 
     const int row_c = row < rows ? row : rows - 1;  // rows past the last compute on a live row, store nothing
     const int rounds = (blocks + S - 1) / S;
 
-    // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [32i, 32i + 32) of each block's codes
-    // and, for i < 8 S, four scales.
+    // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [32i, 32i + 32) of each block's codes,
+    // bytes [4i, 4i + 4) of its group sums and, for i < 8 S, four scales.
     u32x4 sc0[S], sc1[S];
+    uint32_t ssum[S];
     u32x4 sscale = {0u, 0u, 0u, 0u};
     auto stage_load = [&](int k) {
 #pragma unroll
@@ -306,6 +322,7 @@ __global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ 
                 const uint8_t* src = codes + (static_cast<int64_t>(b) * tiles + t) * 8192 + 32 * threadIdx.x;
                 sc0[s] = load16_a4(src);
                 sc1[s] = load16_a4(src + 16);
+                ssum[s] = load4_a4(sums + (static_cast<int64_t>(b) * tiles + t) * 1024 + 4 * threadIdx.x);
             }
         }
         if (threadIdx.x < 8 * S) {
@@ -321,6 +338,7 @@ __global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ 
             if (k * S + s < blocks) {
                 *reinterpret_cast<u32x4*>(stage[s].codes + 32 * threadIdx.x) = sc0[s];
                 *reinterpret_cast<u32x4*>(stage[s].codes + 32 * threadIdx.x + 16) = sc1[s];
+                *reinterpret_cast<uint32_t*>(stage[s].sums + 4 * threadIdx.x) = ssum[s];
             }
         }
         if (threadIdx.x < 8 * S)
@@ -413,13 +431,13 @@ __global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ 
 }
 
 template <int FORMAT, int S>
-void launch_split(const uint8_t* w, const uint8_t* codes, const float* scales, float* y, int rows, int blocks,
-                  int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
+void launch_split(const uint8_t* w, const uint8_t* codes, const float* scales, const uint8_t* sums, float* y,
+                  int rows, int blocks, int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
     const int groups = (rows + Split<S>::R * kTile - 1) / (Split<S>::R * kTile);
     const int units = groups * tiles;
     const int grid = (units + 7) / 8 * 8;
-    kmfma_kernel<FORMAT, S><<<grid, 256, 0, stream>>>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles,
-                                                      units);
+    kmfma_kernel<FORMAT, S><<<grid, 256, 0, stream>>>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions,
+                                                      tiles, units);
 }
 
 // Ways per row tile (1, 2 or 4): enough waves for about two per SIMD (2048), at most the block count, and no
@@ -433,12 +451,12 @@ int choose_split(int rows, int blocks, int tiles) {
 }
 
 template <int FORMAT>
-void launch_format(const uint8_t* w, const uint8_t* codes, const float* scales, float* y, int rows, int blocks,
-                   int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
+void launch_format(const uint8_t* w, const uint8_t* codes, const float* scales, const uint8_t* sums, float* y,
+                   int rows, int blocks, int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
     switch (choose_split(rows, blocks, tiles)) {
-        case 1: launch_split<FORMAT, 1>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
-        case 2: launch_split<FORMAT, 2>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
-        default: launch_split<FORMAT, 4>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+        case 1: launch_split<FORMAT, 1>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+        case 2: launch_split<FORMAT, 2>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+        default: launch_split<FORMAT, 4>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream); break;
     }
 }
 
@@ -448,7 +466,7 @@ int kmfma_min_positions() { return 16; }
 
 size_t kmfma_workspace_bytes(int blocks, int positions) {
     const size_t tiles = (static_cast<size_t>(positions) + kTile - 1) / kTile;
-    return static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float));
+    return static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float) + 1024);
 }
 
 hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
@@ -458,13 +476,14 @@ hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8
     const int tiles = (positions + kTile - 1) / kTile;
     uint8_t* codes = workspace;
     float* scales = reinterpret_cast<float*>(workspace + static_cast<size_t>(blocks) * tiles * 8192);
+    uint8_t* sums = workspace + static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float));
     const int chunks = format == kQ4_K ? 8 : 16;
-    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile), 256, 0, stream>>>(x, blocks * 256, positions, tiles,
-                                                                                  chunks, codes, scales);
+    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile), 256, 0, stream>>>(
+        x, blocks * 256, positions, tiles, chunks, codes, scales, reinterpret_cast<_Float16*>(sums));
     if (format == kQ4_K)
-        launch_format<kQ4_K>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream);
+        launch_format<kQ4_K>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream);
     else
-        launch_format<kQ6_K>(w, codes, scales, y, rows, blocks, row_bytes, positions, tiles, stream);
+        launch_format<kQ6_K>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream);
     return hipGetLastError();
 }
 
