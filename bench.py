@@ -320,8 +320,9 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
 
 
 def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions: int = 512) -> dict:
-    """The projections of a 512-token prefill: every layer projection over all positions through
-    ExecuteBatch in chunks of 256 positions (the reference's chunk, and the ABI's limit for K formats),
+    """The projections of a 512-token prefill: every layer projection over all positions in chunks of 256
+    positions (the reference's chunk, and the ABI's limit for K formats), q/k/v and gate/up each as one
+    grouped product over their shared input (DenseForward.LayerBatch), o and down through ExecuteBatch,
     and the output projection for the last position only (DenseSession.cs:156-159). The FLOP-based rate
     counts 2 int8 operations per weight per position."""
     d, ffn = model.D, model.FFN
@@ -332,18 +333,36 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     logits = model.device(np.zeros(model.VOCAB, np.float32))
     inputs = {"q": h, "k": h, "v": h, "o": attn, "gate": h2, "up": h2, "down": act}
     chunk = 256
+    chunks = [(p0, min(chunk, positions - p0)) for p0 in range(0, positions, chunk)]
+
+    def group(m, names, p0):
+        # Projections of one chunk that read one input (q/k/v, gate/up): one grouped many-position product.
+        return S.HipGroup(ctx, [m[n] for n in names],
+                          [inputs[n] + 4 * p0 * model.roles[n][1] for n in names],
+                          [out[n] + 4 * p0 * model.roles[n][0] for n in names], True)
+
+    plan = []  # per layer and chunk: the q/k/v group, o, the gate/up group, down
+    for m in model.layers:
+        for p0, n in chunks:
+            plan.append((group(m, ("q", "k", "v"), p0), group(m, ("gate", "up"), p0), m, p0, n))
+
+    def single(m, name, p0, n):
+        r, c, _ = model.roles[name]
+        m[name].execute_batch_device(inputs[name] + 4 * p0 * c, n, out[name] + 4 * p0 * r)
 
     def run():
-        for m in model.layers:
-            for name, mat in m.items():
-                r, c, _ = model.roles[name]
-                for p0 in range(0, positions, chunk):
-                    n = min(chunk, positions - p0)
-                    mat.execute_batch_device(inputs[name] + 4 * p0 * c, n, out[name] + 4 * p0 * r)
+        for qkv, gateup, m, p0, n in plan:
+            qkv.execute_batch(n)
+            single(m, "o", p0, n)
+            gateup.execute_batch(n)
+            single(m, "down", p0, n)
         model.output.execute_batch_device(h + 4 * (positions - 1) * d, 1, logits)
 
     run()
     ms = time_launches(ctx, events, run, steps, warmup)
+    for qkv, gateup, *_ in plan:
+        qkv.dispose()
+        gateup.dispose()
     weights = sum(r * c for r, c, _ in model.roles.values()) * model.LAYERS
     ops = 2.0 * weights * positions + 2.0 * model.VOCAB * d
     return {

@@ -189,6 +189,14 @@ int satori_hip_group_create(satori_hip_context* context, satori_hip_matrix* cons
                             const float* const* inputs, float* const* outputs, int quantized_activations,
                             satori_hip_group** group);
 int satori_hip_group_execute(satori_hip_group* group, void* stream);
+/* The group's members over `positions` (1..256) positions: member i reads inputs[i] as [positions][columns]
+ * and writes outputs[i] as [positions][rows_i] (the creation pointers), exactly as
+ * satori_hip_matvec_batch_device per member. K-format groups with quantized activations only
+ * (SATORI_HIP_E_NOT_SUPPORTED otherwise); members sharing an input pointer share its Q8_K quantization. The
+ * prefill counterpart of the group launch: the q/k/v projections of DenseForward.LayerBatch
+ * (src/Satori.Core/Model/DenseForward.cs:187-196) read one input, and so do gate/up (:243-248). The first call at a position count allocates the group's workspace (not while
+ * capturing: SATORI_HIP_E_INVALID_OPERATION). */
+int satori_hip_group_execute_batch(satori_hip_group* group, int positions, void* stream);
 /* Fails with SATORI_HIP_E_ARGUMENT while a step replays the group. A matrix cannot be destroyed while a
  * group launches it (same status). */
 int satori_hip_group_destroy(satori_hip_group* group);

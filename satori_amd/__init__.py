@@ -369,6 +369,12 @@ class HipGroup:
     def execute(self, stream: int = 0) -> None:
         _check(_ffi.lib().satori_hip_group_execute(self._handle, ctypes.c_void_p(stream)))
 
+    def execute_batch(self, positions: int, stream: int = 0) -> None:
+        """Every member over `positions` positions (inputs [positions][columns], outputs [positions][rows]),
+        as ExecuteBatch per member; K-format groups with quantized activations only. Members that share an
+        input share its Q8_K quantization (the prefill's q/k/v and gate/up, DenseForward.LayerBatch)."""
+        _check(_ffi.lib().satori_hip_group_execute_batch(self._handle, int(positions), ctypes.c_void_p(stream)))
+
     def dispose(self) -> None:
         _check(_ffi.lib().satori_hip_group_destroy(self._handle))
 

@@ -38,6 +38,7 @@ SIGNATURES = {
     "satori_hip_matvec_batch_device": (I, [P, P, I, P, P]),
     "satori_hip_group_create": (I, [P, P, I, P, P, I, PP]),
     "satori_hip_group_execute": (I, [P, P]),
+    "satori_hip_group_execute_batch": (I, [P, I, P]),
     "satori_hip_group_destroy": (I, [P]),
     "satori_hip_step_create": (I, [P, P, I, PP]),
     "satori_hip_step_execute": (I, [P, P]),

@@ -288,19 +288,28 @@ struct Split {
 // go to one XCD (workgroup ids are dealt to the 8 XCDs round-robin), so the position tiles that share a row
 // group's weights share that XCD's L2.
 template <int FORMAT, int S>
-__global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ codes,
-                                                    const float* __restrict__ scales, const uint8_t* __restrict__ sums,
-                                                    float* __restrict__ y, int rows,
-                                                    int blocks, int64_t row_bytes, int positions, int tiles,
-                                                    int units) {
+__global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a) {
     using SP = Split<S>;
     __shared__ StagedBlock stage[S];
     // Terms of one round: [row tile][way][quad q][lane] as float4 (conflict-free 16-byte accesses).
     __shared__ f32x4 exchange[S > 1 ? SP::R * S * 4 * 64 : 1];
 
+    // Unit u of the launch (members one after the other, each (row group, position tile) with position tiles
+    // fastest) -> member and unit within it.
     const int per_xcd = gridDim.x >> 3;
-    const int u = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (u >= units) return;  // whole workgroup
+    int u = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    int mi = 0;
+    while (mi + 1 < a.count && u >= a.units[mi]) u -= a.units[mi++];
+    if (u >= a.units[mi]) return;  // whole workgroup
+    const KmfmaMember& m = a.m[mi];
+    const uint8_t* __restrict__ w = m.w;
+    const int rows = m.rows, blocks = a.blocks, tiles = a.tiles;
+    const int64_t row_bytes = m.row_bytes;
+    const uint8_t* __restrict__ codes = m.workspace;
+    const uint8_t* __restrict__ sums = m.workspace + kmfma_sums_offset(blocks, tiles);
+    const float* __restrict__ scales = reinterpret_cast<const float*>(m.workspace + kmfma_scales_offset(blocks, tiles));
+    float* __restrict__ y = m.y;
+    const int positions = a.positions;
     const int group = u / tiles, t = u - group * tiles;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int way = wave % S, rt = wave / S;
@@ -431,19 +440,20 @@ __global__ __launch_bounds__(256) void kmfma_kernel(const uint8_t* __restrict__ 
 }
 
 template <int FORMAT, int S>
-void launch_split(const uint8_t* w, const uint8_t* codes, const float* scales, const uint8_t* sums, float* y,
-                  int rows, int blocks, int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
-    const int groups = (rows + Split<S>::R * kTile - 1) / (Split<S>::R * kTile);
-    const int units = groups * tiles;
-    const int grid = (units + 7) / 8 * 8;
-    kmfma_kernel<FORMAT, S><<<grid, 256, 0, stream>>>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions,
-                                                      tiles, units);
+void launch_split(KmfmaArgs& a, hipStream_t stream) {
+    int total = 0;
+    for (int i = 0; i < a.count; ++i) {
+        const int groups = (a.m[i].rows + Split<S>::R * kTile - 1) / (Split<S>::R * kTile);
+        a.units[i] = groups * a.tiles;
+        total += a.units[i];
+    }
+    const int grid = (total + 7) / 8 * 8;
+    kmfma_kernel<FORMAT, S><<<grid, 256, 0, stream>>>(a);
 }
 
 // Ways per row tile (1, 2 or 4): enough waves for about two per SIMD (2048), at most the block count, and no
 // more ways than shorten the chain of rounds.
-int choose_split(int rows, int blocks, int tiles) {
-    const long wave_tiles = static_cast<long>((rows + kTile - 1) / kTile) * tiles;
+int choose_split(long wave_tiles, int blocks) {
     int s = 1;
     while (s < 4 && 2 * s <= blocks && wave_tiles * s < 2048) s *= 2;
     while (s > 1 && (blocks + s - 1) / s == (blocks + s / 2 - 1) / (s / 2)) s /= 2;
@@ -451,12 +461,13 @@ int choose_split(int rows, int blocks, int tiles) {
 }
 
 template <int FORMAT>
-void launch_format(const uint8_t* w, const uint8_t* codes, const float* scales, const uint8_t* sums, float* y,
-                   int rows, int blocks, int64_t row_bytes, int positions, int tiles, hipStream_t stream) {
-    switch (choose_split(rows, blocks, tiles)) {
-        case 1: launch_split<FORMAT, 1>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream); break;
-        case 2: launch_split<FORMAT, 2>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream); break;
-        default: launch_split<FORMAT, 4>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream); break;
+void launch_format(KmfmaArgs& a, hipStream_t stream) {
+    long wave_tiles = 0;
+    for (int i = 0; i < a.count; ++i) wave_tiles += static_cast<long>((a.m[i].rows + kTile - 1) / kTile) * a.tiles;
+    switch (choose_split(wave_tiles, a.blocks)) {
+        case 1: launch_split<FORMAT, 1>(a, stream); break;
+        case 2: launch_split<FORMAT, 2>(a, stream); break;
+        default: launch_split<FORMAT, 4>(a, stream); break;
     }
 }
 
@@ -465,26 +476,50 @@ void launch_format(const uint8_t* w, const uint8_t* codes, const float* scales, 
 int kmfma_min_positions() { return 16; }
 
 size_t kmfma_workspace_bytes(int blocks, int positions) {
-    const size_t tiles = (static_cast<size_t>(positions) + kTile - 1) / kTile;
-    return static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float) + 1024);
+    const int tiles = (positions + kTile - 1) / kTile;
+    return kmfma_sums_offset(blocks, tiles) + static_cast<size_t>(blocks) * tiles * 1024;
+}
+
+hipError_t launch_kmfma_pack(int format, const float* x, int blocks, int positions, uint8_t* workspace,
+                             hipStream_t stream) {
+    if (positions <= 0 || blocks <= 0) return hipSuccess;
+    if (format != kQ4_K && format != kQ6_K) return hipErrorInvalidValue;
+    const int tiles = (positions + kTile - 1) / kTile;
+    const int chunks = format == kQ4_K ? 8 : 16;
+    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile), 256, 0, stream>>>(
+        x, blocks * 256, positions, tiles, chunks, workspace,
+        reinterpret_cast<float*>(workspace + kmfma_scales_offset(blocks, tiles)),
+        reinterpret_cast<_Float16*>(workspace + kmfma_sums_offset(blocks, tiles)));
+    return hipGetLastError();
+}
+
+hipError_t launch_kmfma_product(int format, const KmfmaMember* members, int count, int blocks, int positions,
+                                hipStream_t stream) {
+    if (count <= 0 || positions <= 0 || blocks <= 0) return hipSuccess;
+    if (count > kKmfmaMaxMembers || (format != kQ4_K && format != kQ6_K)) return hipErrorInvalidValue;
+    KmfmaArgs a{};
+    for (int i = 0; i < count; ++i) {
+        if (members[i].rows <= 0) return hipErrorInvalidValue;
+        a.m[i] = members[i];
+    }
+    a.count = count;
+    a.blocks = blocks;
+    a.positions = positions;
+    a.tiles = (positions + kTile - 1) / kTile;
+    if (format == kQ4_K)
+        launch_format<kQ4_K>(a, stream);
+    else
+        launch_format<kQ6_K>(a, stream);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
                              int blocks, int64_t row_bytes, int positions, hipStream_t stream) {
     if (rows <= 0 || positions <= 0 || blocks <= 0) return hipSuccess;
-    if (format != kQ4_K && format != kQ6_K) return hipErrorInvalidValue;
-    const int tiles = (positions + kTile - 1) / kTile;
-    uint8_t* codes = workspace;
-    float* scales = reinterpret_cast<float*>(workspace + static_cast<size_t>(blocks) * tiles * 8192);
-    uint8_t* sums = workspace + static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float));
-    const int chunks = format == kQ4_K ? 8 : 16;
-    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile), 256, 0, stream>>>(
-        x, blocks * 256, positions, tiles, chunks, codes, scales, reinterpret_cast<_Float16*>(sums));
-    if (format == kQ4_K)
-        launch_format<kQ4_K>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream);
-    else
-        launch_format<kQ6_K>(w, codes, scales, sums, y, rows, blocks, row_bytes, positions, tiles, stream);
-    return hipGetLastError();
+    hipError_t e = launch_kmfma_pack(format, x, blocks, positions, workspace, stream);
+    if (e != hipSuccess) return e;
+    const KmfmaMember one{w, workspace, y, rows, 0, row_bytes};
+    return launch_kmfma_product(format, &one, 1, blocks, positions, stream);
 }
 
 }  // namespace satori

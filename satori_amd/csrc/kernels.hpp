@@ -136,6 +136,36 @@ hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8
                              int blocks, int64_t row_bytes, int positions, hipStream_t stream);
 size_t kmfma_workspace_bytes(int blocks, int positions);
 
+// The same product in two steps, for several matrices of one format and width: launch_kmfma_pack quantizes
+// one activation array into a workspace, and launch_kmfma_product runs up to kKmfmaMaxMembers products in one
+// launch, member i reading the workspace packed from its input (members may share one).
+constexpr int kKmfmaMaxMembers = 4;
+struct KmfmaMember {
+    const uint8_t* w;          // resident payload (Q4_K) or its regrouped device layout (Q6_K)
+    const uint8_t* workspace;  // packed activations (launch_kmfma_pack, kmfma_workspace_bytes)
+    float* y;                  // output [positions][rows]
+    int rows;
+    int pad_;
+    int64_t row_bytes;
+};
+struct KmfmaArgs {
+    KmfmaMember m[kKmfmaMaxMembers];
+    int units[kKmfmaMaxMembers];
+    int count, blocks, positions, tiles;
+};
+// Workspace layout for `tiles` 32-position tiles: codes (8 KB per block and tile), then FP32 scales (32 per
+// block and tile), then FP16 group sums (1 KB per block and tile).
+__host__ __device__ inline size_t kmfma_scales_offset(int blocks, int tiles) {
+    return static_cast<size_t>(blocks) * tiles * 8192;
+}
+__host__ __device__ inline size_t kmfma_sums_offset(int blocks, int tiles) {
+    return static_cast<size_t>(blocks) * tiles * (8192 + 32 * sizeof(float));
+}
+hipError_t launch_kmfma_pack(int format, const float* x, int blocks, int positions, uint8_t* workspace,
+                             hipStream_t stream);
+hipError_t launch_kmfma_product(int format, const KmfmaMember* members, int count, int blocks, int positions,
+                                hipStream_t stream);
+
 // Decode-step operators (transformer_ops.hip): TransformerOps in FP64 with FP32 outputs, and the embedding row
 // decode of a resident Q8_0 / Q4_K / Q6_K matrix.
 hipError_t launch_rms_norm(const float* x, const float* w, float epsilon, int length, int count, float* y,

@@ -113,6 +113,8 @@ struct satori_hip_group {
     bool quantized = false;
     int rows_max = 0;
     satori::MatDesc* descriptors = nullptr;   // device
+    std::vector<satori::MatDesc> host;         // the same descriptors on the host
+    satori::DeviceBuffer batch;                // K groups: packed Q8_K activations of many-position calls
     satori::T2Plan plan{};                     // Ternary2 groups
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
     std::vector<satori_hip_matrix*> members;   // distinct member matrices (each counts this group)
@@ -444,6 +446,42 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
         check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
     } else {
         check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
+    }
+}
+
+// Enqueues one K-format group over `positions` positions (inputs [positions][columns], outputs
+// [positions][rows]): the integer kernel below kmfma_min_positions(), else the matrix-core product, with the
+// Q8_K pack of each distinct input pointer done once and up to kKmfmaMaxMembers members per launch.
+void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
+    const Shape& s = g->shape;
+    if (positions < kmfma_min_positions()) {
+        check_hip(launch_gemv_kint(MatDesc{}, g->descriptors, g->count, launch_shape(s, positions, g->rows_max), st),
+                  "integer gemv launch");
+        return;
+    }
+    std::vector<const float*> inputs;
+    std::vector<size_t> slot(g->count);
+    for (int i = 0; i < g->count; ++i) {
+        auto it = std::find(inputs.begin(), inputs.end(), g->host[i].x);
+        slot[i] = static_cast<size_t>(it - inputs.begin());
+        if (it == inputs.end()) inputs.push_back(g->host[i].x);
+    }
+    const size_t per = kmfma_workspace_bytes(s.blocks, positions);
+    if (g->context->capturing && g->batch.bytes < per * inputs.size())
+        fail(SATORI_HIP_E_INVALID_OPERATION,
+             "Run this many-position product once before capturing it (its workspace is allocated on first use).");
+    g->batch.reserve(per * inputs.size());
+    uint8_t* ws = static_cast<uint8_t*>(g->batch.ptr);
+    for (size_t k = 0; k < inputs.size(); ++k)
+        check_hip(launch_kmfma_pack(s.format, inputs[k], s.blocks, positions, ws + k * per, st), "Q8_K pack launch");
+    for (int i0 = 0; i0 < g->count; i0 += kKmfmaMaxMembers) {
+        const int n = std::min(kKmfmaMaxMembers, g->count - i0);
+        KmfmaMember members[kKmfmaMaxMembers];
+        for (int j = 0; j < n; ++j) {
+            const MatDesc& d = g->host[i0 + j];
+            members[j] = KmfmaMember{d.w, ws + slot[i0 + j] * per, d.y, d.rows, 0, s.row_bytes};
+        }
+        check_hip(launch_kmfma_product(s.format, members, n, s.blocks, positions, st), "matrix-core gemv launch");
     }
 }
 
@@ -993,6 +1031,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
             check_hip(hipMalloc(reinterpret_cast<void**>(&g->descriptors), sizeof(MatDesc) * count), "hipMalloc");
             check_hip(hipMemcpy(g->descriptors, host.data(), sizeof(MatDesc) * count, hipMemcpyHostToDevice),
                       "descriptor upload");
+            g->host = host;
         } catch (...) {
             if (g->descriptors) (void)hipFree(g->descriptors);
             if (g->scratch) (void)hipFree(g->scratch);
@@ -1021,6 +1060,23 @@ int satori_hip_group_execute(satori_hip_group* g, void* stream) {
     });
 }
 
+int satori_hip_group_execute_batch(satori_hip_group* g, int positions, void* stream) {
+    return guarded([&] {
+        require(g, "group");
+        satori_hip_context* c = g->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!g->live || !c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
+        if (!g->quantized)
+            fail(SATORI_HIP_E_NOT_SUPPORTED,
+                 "The many-position group product is defined for K-format groups with quantized activations.");
+        if (positions <= 0 || positions > 256) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "positions must be 1..256.");
+        set_device(c);
+        const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        enqueue_group_batch(g, positions, st);
+        if (c->capturing && st == c->stream) c->captured_groups.push_back(g);
+    });
+}
+
 int satori_hip_group_destroy(satori_hip_group* g) {
     return guarded([&] {
         if (!g) return;
@@ -1039,6 +1095,7 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         g->descriptors = nullptr;
         if (g->scratch) (void)hipFree(g->scratch);
         g->scratch = nullptr;
+        g->batch.release();
         g->live = false;
     });
 }

@@ -515,6 +515,69 @@ def test_k_matrix_core_batch_equals_per_position(context, fmt, rows, columns, po
     m.dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("positions", [1, 9, 16, 77, 256])
+def test_k_group_batch_equals_member_batches(context, fmt, positions):
+    # DenseForward.LayerBatch (DenseForward.cs:187-196): q/k/v read one normalized batch. The grouped
+    # many-position product (shared Q8_K pack, several members per launch) must equal each member's own
+    # ExecuteBatch bit for bit: five members (more than one launch holds), ragged row counts, two inputs
+    # (members 0, 1, 3, 4 share one), and zero / huge positions inside the batch.
+    columns = 768
+    g = rng(100 + positions + int(fmt))
+    row_counts = [200, 33, 64, 300, 1]
+    x = [g.standard_normal((positions, columns), dtype=np.float32) for _ in range(2)]
+    x[0][positions // 2] = 0.0
+    x[1][positions - 1] *= 1e15
+    mats, datas = [], []
+    for r in row_counts:
+        w = (g.standard_normal((r, columns), dtype=np.float32) * 0.02).astype(np.float32)
+        datas.append(S.quantize_weights(w, r, columns, fmt))
+        mats.append(context.create(datas[-1], S.QuantizedMatrixShape(r, columns, fmt)))
+    which = [0, 0, 1, 0, 0]
+    dx = [context.alloc(4 * a.size) for a in x]
+    for p, a in zip(dx, x):
+        context.upload(p, a.reshape(-1))
+    dy = [context.alloc(4 * positions * r) for r in row_counts]
+    group = S.HipGroup(context, mats, [dx[i] for i in which], dy, True)
+    try:
+        for repeat in range(2):  # the second call reuses the group's workspace
+            for p, r in zip(dy, row_counts):
+                context.upload(p, np.full(positions * r, np.nan, np.float32))
+            group.execute_batch(positions)
+            for i, (m, r) in enumerate(zip(mats, row_counts)):
+                got = context.download(np.zeros(positions * r, np.float32), dy[i])
+                want = np.zeros(positions * r, np.float32)
+                m.execute_batch(x[which[i]].reshape(-1), positions, want)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (repeat, i, r)
+    finally:
+        group.dispose()
+        for p in dx + dy:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
+def test_k_group_batch_errors(context):
+    g = rng(5)
+    w = (g.standard_normal((64, 512), dtype=np.float32) * 0.02).astype(np.float32)
+    m = context.create(S.quantize_weights(w, 64, 512, BQ.Q4_K), S.QuantizedMatrixShape(64, 512, BQ.Q4_K))
+    x, y = context.alloc(4 * 512 * 256), context.alloc(4 * 64 * 256)
+    float_group = S.HipGroup(context, [m], [x], [y], False)
+    group = S.HipGroup(context, [m], [x], [y], True)
+    try:
+        with pytest.raises(S.NotSupportedException):
+            float_group.execute_batch(16)
+        for bad in (0, 257):
+            with pytest.raises(S.ArgumentOutOfRangeException):
+                group.execute_batch(bad)
+    finally:
+        float_group.dispose()
+        group.dispose()
+        context.free(x)
+        context.free(y)
+        m.dispose()
+
+
 @pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
 def test_legacy_batch_matches_per_position(context, fmt):
     # BatchedMatVecTests.cs:61-88 (float path): each position within 1e-5 * sum|w x| of the scalar product.
