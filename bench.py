@@ -229,7 +229,7 @@ class DecodeModel:
             self.ctx.free(p)
 
 
-def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int) -> dict:
+def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_only: bool = False) -> dict:
     """The projection sequence of one decode token (197 projections, batch 1) on the Q8_K integer path.
     Projections that share an input form one group (q/k/v, gate/up); the 113 groups of a token are
     captured once as a graph (satori_hip_step) and replayed. Attention, norms and SwiGLU are not part of
@@ -247,16 +247,20 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int) -> dic
         groups.append(S.HipGroup(ctx, [m["gate"], m["up"]], [h2] * 2, [out["gate"], out["up"]], True))
         groups.append(S.HipGroup(ctx, [m["down"]], [act], [out["down"]], True))
     groups.append(S.HipGroup(ctx, [model.output], [h], [logits], True))
-    step = S.HipStep(ctx, groups)
-    warm_up(ctx, step.execute, 0.5)
-    graph_ms = time_launches(ctx, events, step.execute, steps, warmup)
 
     def eager():
         for grp in groups:
             grp.execute()
 
-    eager_ms = time_launches(ctx, events, eager, max(5, steps // 4), 2)
-    step.dispose()
+    if eager_only:  # for kernel statistics: the same launches without the graph
+        warm_up(ctx, eager, 0.5)
+        graph_ms = eager_ms = time_launches(ctx, events, eager, steps, warmup)
+    else:
+        step = S.HipStep(ctx, groups)
+        warm_up(ctx, step.execute, 0.5)
+        graph_ms = time_launches(ctx, events, step.execute, steps, warmup)
+        eager_ms = time_launches(ctx, events, eager, max(5, steps // 4), 2)
+        step.dispose()
     for grp in groups:
         grp.dispose()
     return {
@@ -456,6 +460,36 @@ def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
     }
 
 
+def other_formats(ctx):
+    """(label, make) for the Ternary2 block sizes besides 128 and the GGUF formats at their configurations;
+    make() returns the grouped Case and the CPU baseline's arguments (payload, rows, columns, format or None
+    for Ternary2, x, block size or quantized flag)."""
+    rows = columns = 4096
+    out = []
+    for b in (64, 256):
+        def make(b=b):
+            p, xb = make_ternary2(rows, columns, b)
+            c = Case(ctx, f"ternary2-4096-b{b}", lambda: ctx.create_ternary2(rows, columns, b, p), p.size, rows,
+                     columns, xb, False)
+            return c, (p, rows, columns, None, xb, b)
+        out.append((f"ternary2-4096-b{b}", make))
+    for fmt, r, cc, quantized, label in (
+            (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
+            (BQ.Q4_0, 11008, 4096, False, "q4_0-11008x4096"),
+            (BQ.Q4_0, 4096, 11008, False, "q4_0-4096x11008"),
+            (BQ.Q4_K, 8960, 1536, True, "q4_k-8960x1536-q8k"),
+            (BQ.Q4_K, 1536, 8960, True, "q4_k-1536x8960-q8k"),
+            (BQ.Q6_K, 8960, 1536, True, "q6_k-8960x1536-q8k"),
+            (BQ.Q6_K, 1536, 8960, True, "q6_k-1536x8960-q8k")):
+        def make(fmt=fmt, r=r, cc=cc, quantized=quantized, label=label):
+            data, xf = make_gguf(fmt, r, cc)
+            shape = S.QuantizedMatrixShape(r, cc, fmt)
+            c = Case(ctx, label, lambda: ctx.create(data, shape), data.size, r, cc, xf, quantized)
+            return c, (data, r, cc, fmt, xf, quantized)
+        out.append((label, make))
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -472,7 +506,9 @@ def main() -> int:
     ap.add_argument("--profile-prefill", action="store_true",
                     help="only the 512-position prefill (steps and warmup as given), for rocprofv3")
     ap.add_argument("--profile-decode", action="store_true",
-                    help="only the decode step (steps and warmup as given), for rocprofv3")
+                    help="only the decode step, launched eagerly (steps and warmup as given), for rocprofv3")
+    ap.add_argument("--profile-formats", action="store_true",
+                    help="only the grouped launches of every format (steps and warmup as given), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the MatVec on a single MI355X "
@@ -487,9 +523,29 @@ def main() -> int:
         if args.profile_prefill:
             result = {"profile": "prefill", **prefill(ctx, events, model, args.steps, args.warmup)}
         else:
-            result = {"profile": "decode step", **decode_step(ctx, events, model, args.steps, args.warmup)}
+            result = {"profile": "decode step (eager)",
+                      **decode_step(ctx, events, model, args.steps, args.warmup, eager_only=True)}
         model.close()
         print(json.dumps(result))
+        return 0
+
+    if args.profile_formats:
+        lines = {}
+        for label, make in other_formats(ctx):
+            c, _ = make()
+            warm_up(ctx, c.run_group, 0.25)
+            ms = time_launches(ctx, events, c.run_group, args.steps, args.warmup)
+            lines[label] = {"copies": c.copies, "launch_us": round(ms * 1e3, 2),
+                            "gbs": round(c.copies * c.payload_bytes / (ms * 1e-3) / 1e9, 1),
+                            "algorithmic_bytes_per_launch": c.copies * c.payload_bytes}
+            progress(f"{label}: {lines[label]}")
+            c.close()
+        src, dst = ctx.alloc(CALIBRATION_BYTES), ctx.alloc(CALIBRATION_BYTES)
+        ctx.copy_device(dst, src, CALIBRATION_BYTES)
+        ctx.free(src)
+        ctx.free(dst)
+        print(json.dumps({"profile": "formats grouped", "launches": args.steps + args.warmup, "formats": lines,
+                          "calibration_copy_bytes": CALIBRATION_BYTES}))
         return 0
 
     rows = columns = 4096
@@ -521,26 +577,10 @@ def main() -> int:
     formats = {"ternary2-4096-b128": headline}
     cpu_cases = {"ternary2-4096-b128": (payload, rows, columns, None, x, block)}
     if not args.quick:
-        for b in (64, 256):
-            p, xb = make_ternary2(rows, columns, b)
-            c = Case(ctx, f"ternary2-4096-b{b}", lambda: ctx.create_ternary2(rows, columns, b, p), p.size, rows,
-                     columns, xb, False)
-            formats[c.name] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
-            cpu_cases[c.name] = (p, rows, columns, None, xb, b)
-            c.close()
-        for fmt, r, cc, quantized, label in (
-                (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
-                (BQ.Q4_0, 11008, 4096, False, "q4_0-11008x4096"),
-                (BQ.Q4_0, 4096, 11008, False, "q4_0-4096x11008"),
-                (BQ.Q4_K, 8960, 1536, True, "q4_k-8960x1536-q8k"),
-                (BQ.Q4_K, 1536, 8960, True, "q4_k-1536x8960-q8k"),
-                (BQ.Q6_K, 8960, 1536, True, "q6_k-8960x1536-q8k"),
-                (BQ.Q6_K, 1536, 8960, True, "q6_k-1536x8960-q8k")):
-            data, xf = make_gguf(fmt, r, cc)
-            shape = S.QuantizedMatrixShape(r, cc, fmt)
-            c = Case(ctx, label, lambda: ctx.create(data, shape), data.size, r, cc, xf, quantized)
+        for label, make in other_formats(ctx):
+            c, cpu_case = make()
             formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
-            cpu_cases[label] = (data, r, cc, fmt, xf, quantized)
+            cpu_cases[label] = cpu_case
             c.close()
 
     decode = pre = token = None
