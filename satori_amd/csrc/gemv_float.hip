@@ -53,7 +53,7 @@ struct Q8_0Chunk {
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
 #pragma unroll
-        for (int j = 0; j < kWeights; ++j) x[j] = xf(32 * chunk + j);
+        for (int j = 0; j < kWeights; j += 4) xf.quad(32 * chunk + j, x + j);
     }
     __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
         float acc0 = 0.0f, acc1 = 0.0f;
@@ -98,7 +98,7 @@ struct Q4_0Chunk {
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
 #pragma unroll
-        for (int j = 0; j < kWeights; ++j) x[j] = xf(32 * chunk + j);
+        for (int j = 0; j < kWeights; j += 4) xf.quad(32 * chunk + j, x + j);
     }
     __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
         float acc0 = 0.0f, acc1 = 0.0f;
@@ -148,9 +148,9 @@ struct Q4_KChunk {
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
         const int base = (chunk >> 3) * 256 + 64 * ((chunk & 7) >> 1) + 16 * (chunk & 1);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            x[i] = xf(base + i);
-            x[16 + i] = xf(base + 32 + i);
+        for (int i = 0; i < 16; i += 4) {
+            xf.quad(base + i, x + i);
+            xf.quad(base + 32 + i, x + 16 + i);
         }
     }
     __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
@@ -202,7 +202,7 @@ struct Q6_KChunk {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) x[16 * k + i] = xf(base + 32 * k + i);
+            for (int i = 0; i < 16; i += 4) xf.quad(base + 32 * k + i, x + 16 * k + i);
     }
     __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
         float ds[4], bias[4];
@@ -237,6 +237,30 @@ struct Q6_KChunk {
     }
 };
 
+// Reads of the activations by aligned quads (i % 4 == 0): one 16-byte LDS read of the staged copy (element i
+// at i + 4 * (i >> PAD), so a quad stays contiguous and the quads of neighbouring lanes, 32, 64 or 128
+// elements apart plus the padding, start on different banks), or of global memory, zero past the end.
+template <int PAD, bool XLDS>
+struct XReader {
+    const float* xs;
+    const float* x;
+    int columns;
+    __device__ __forceinline__ void quad(int i, float* out) const {
+        if constexpr (XLDS) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xs + i + ((i >> PAD) << 2));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[e] = v[e];
+        } else if (i + 3 < columns) {
+            const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(x + i));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[e] = __uint_as_float(v[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[e] = i + e < columns ? load_f32(x + i + e) : 0.0f;
+        }
+    }
+};
+
 // ------------------------------------------------------------------------------------------------
 // The kernel. Grid: x = row tiles of s.rows_per_wg rows, y = group member, z = position.
 // ONE: every row has at most L chunks, so a lane's activations are loaded once per workgroup.
@@ -263,12 +287,7 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
             xs[i + ((i >> F::kPadShift) << 2)] = i < columns ? load_f32(x + i) : 0.0f;
         __syncthreads();
     }
-    auto xf = [&](int i) -> float {
-        if constexpr (XLDS)
-            return xs[i + ((i >> F::kPadShift) << 2)];
-        else
-            return i < columns ? load_f32(x + i) : 0.0f;
-    };
+    const XReader<F::kPadShift, XLDS> xf{xs, x, columns};
 
     constexpr int kRowsPerPass = 64 / L;
     constexpr int kStride = kWaves * kRowsPerPass;  // rows between a lane's consecutive rows
