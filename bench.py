@@ -17,7 +17,8 @@ The same line carries, labelled:
   decode_step: the 197 projections of one decode token of a Qwen-1.5B-shaped model (Q4_K/Q6_K on the Q8_K
              integer path, 1.03 GB per token), replayed as one graph; tokens/s and GB/s;
   decode_token: a whole token of that model on the device (operators, attention over a 511-token KV prefix,
-             projections), captured once and replayed;
+             projections; the residual adds and RmsNorms folded into the projection launches),
+             captured once and replayed, with the fused and unfused operator sequences beside it;
   prefill:   the same model's projections over 512 positions (ExecuteBatch in 256-position chunks);
              tokens/s and int8 TOP/s;
   roofline:  for the headline kernel, from HIP events on the launch stream;
@@ -300,25 +301,33 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
         prefix = (g.standard_normal((cfg.max_tokens, model.KV)) * 0.5).astype(np.float32)
         ctx.upload(dec.keys[layer], prefix)
         ctx.upload(dec.values[layer], prefix[::-1].copy())
-    step = dec.capture(151, position)
+    # Folded (add + RmsNorm inside the projection launches), the default; fused and unfused for comparison.
+    step = dec.capture(151, position, folded=True)
     warm_up(ctx, step.execute, 0.5)
     graph_ms = time_launches(ctx, events, step.execute, steps, warmup)
-    eager_ms = time_launches(ctx, events, lambda: dec.enqueue(151, position), max(5, steps // 4), 2)
-    unfused = dec.capture(151, position, fused=False)
-    unfused_ms = time_launches(ctx, events, unfused.execute, max(5, steps // 2), 2)
-    unfused.dispose()
-    finite = bool(np.all(np.isfinite(dec.read_logits())))
+    eager_ms = time_launches(ctx, events, lambda: dec.enqueue(151, position, folded=True), max(5, steps // 4), 2)
+    folded_logits = dec.read_logits()
+    timed = {}
+    for name, fused in (("fused", True), ("unfused", False)):
+        other = dec.capture(151, position, fused=fused)
+        timed[name] = time_launches(ctx, events, other.execute, max(5, steps // 2), 2)
+        other.dispose()
+    same = bool(np.array_equal(dec.read_logits().view(np.uint32), folded_logits.view(np.uint32)))
+    finite = bool(np.all(np.isfinite(folded_logits)))
     step.dispose()
     dec.dispose()
     return {
         "model": "Qwen-1.5B-shaped whole decode token on the device (random-init weights and KV prefix)",
         "position": position,
-        "kernel_launches_per_token": dec.launches_per_token(),
+        "kernel_launches_per_token": dec.launches_per_token(folded=True),
         "us_per_token": graph_ms * 1e3,
         "tokens_per_s": 1e3 / graph_ms,
         "eager_us_per_token": eager_ms * 1e3,
-        "unfused_us_per_token": unfused_ms * 1e3,
+        "fused_us_per_token": timed["fused"] * 1e3,
+        "fused_launches_per_token": dec.launches_per_token(),
+        "unfused_us_per_token": timed["unfused"] * 1e3,
         "unfused_launches_per_token": dec.launches_per_token(fused=False),
+        "same_logits_all_modes": same,
         "finite_logits": finite,
     }
 

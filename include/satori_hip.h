@@ -197,6 +197,24 @@ int satori_hip_group_execute(satori_hip_group* group, void* stream);
  * (src/Satori.Core/Model/DenseForward.cs:187-196) read one input, and so do gate/up (:243-248). The first call at a position count allocates the group's workspace (not while
  * capturing: SATORI_HIP_E_INVALID_OPERATION). */
 int satori_hip_group_execute_batch(satori_hip_group* group, int positions, void* stream);
+/* Input transforms: a K-format group with quantized activations can compute its (shared) input inside its
+ * own launch from the operands of the decode-step operator that would produce it, instead of reading
+ * inputs[i]; the operator's launch then disappears. The values are those of the operator bit for bit.
+ *  SATORI_HIP_INPUT_ADD_RMS_NORM: input = RmsNorm(a + b, weights, epsilon) (b may be NULL: RmsNorm(a)),
+ *    as satori_hip_add_rms_norm / satori_hip_rms_norm compute it; when residual_out is not NULL the launch
+ *    also writes a + b there (it must not overlap a or b);
+ *  SATORI_HIP_INPUT_SWIGLU: input = SwiGlu(a, b), as satori_hip_swiglu;
+ *  SATORI_HIP_INPUT_PLAIN: back to reading inputs[i].
+ * Vectors have the members' column count. One-position launches only (satori_hip_group_execute_batch
+ * fails with SATORI_HIP_E_NOT_SUPPORTED). Not while steps replay the group (SATORI_HIP_E_ARGUMENT) or while
+ * capturing. No counterpart in the reference, whose DenseForward.Step (src/Satori.Core/Model/
+ * DenseForward.cs:100-162) runs RmsNorm (:107, :151), Add (:148, :160) and SwiGlu (:156) as separate
+ * TransformerOps calls between its projections. */
+#define SATORI_HIP_INPUT_PLAIN 0
+#define SATORI_HIP_INPUT_ADD_RMS_NORM 1
+#define SATORI_HIP_INPUT_SWIGLU 2
+int satori_hip_group_set_input(satori_hip_group* group, int kind, const float* a, const float* b,
+                               const float* weights, float epsilon, float* residual_out);
 /* Fails with SATORI_HIP_E_ARGUMENT while a step replays the group. A matrix cannot be destroyed while a
  * group launches it (same status). */
 int satori_hip_group_destroy(satori_hip_group* group);

@@ -375,6 +375,24 @@ class HipGroup:
         input share its Q8_K quantization (the prefill's q/k/v and gate/up, DenseForward.LayerBatch)."""
         _check(_ffi.lib().satori_hip_group_execute_batch(self._handle, int(positions), ctypes.c_void_p(stream)))
 
+    def set_input_add_rms_norm(self, residual: int, addend: int, weights: int, epsilon: float,
+                               residual_out: int = 0) -> None:
+        """The group's input becomes RmsNorm(residual + addend, weights, epsilon) computed inside its launch
+        (addend 0: RmsNorm(residual)); residual + addend is also written to residual_out when given. Device
+        pointers; bit-identical to the separate add / RmsNorm operators."""
+        _check(_ffi.lib().satori_hip_group_set_input(self._handle, 1, ctypes.c_void_p(residual),
+                                                     ctypes.c_void_p(addend or None), ctypes.c_void_p(weights),
+                                                     float(epsilon), ctypes.c_void_p(residual_out or None)))
+
+    def set_input_swiglu(self, gate: int, up: int) -> None:
+        """The group's input becomes SwiGlu(gate, up) computed inside its launch (device pointers)."""
+        _check(_ffi.lib().satori_hip_group_set_input(self._handle, 2, ctypes.c_void_p(gate), ctypes.c_void_p(up),
+                                                     None, 0.0, None))
+
+    def set_input_plain(self) -> None:
+        """The group reads its creation inputs again."""
+        _check(_ffi.lib().satori_hip_group_set_input(self._handle, 0, None, None, None, 0.0, None))
+
     def dispose(self) -> None:
         _check(_ffi.lib().satori_hip_group_destroy(self._handle))
 

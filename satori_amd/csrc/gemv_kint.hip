@@ -12,6 +12,7 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "ops_device.hpp"
 #include "q8k_device.hpp"
 
 namespace satori {
@@ -133,9 +134,17 @@ __device__ __forceinline__ int q6k_dot(const Q6KRaw& r, const ActTile& act, int 
     return total;
 }
 
-template <int FORMAT>
+// LDS: staged activations, the row terms, then (input transforms) 256 doubles for the RmsNorm reduction at an
+// 8-byte aligned dword offset. Sized for the largest tile so one bound serves every launch.
+__host__ __device__ inline int kint_red_offset(int blocks, int tile_rows) {
+    return ((kActDwords + tile_rows) * blocks + 1) & ~1;
+}
+
+static_assert(kThreads == kOpsThreads, "the RmsNorm reduction is the operators' 256-thread tree");
+
+template <int FORMAT, int XF>
 __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const MatDesc* __restrict__ group,
-                                                              LaunchShape s) {
+                                                              LaunchShape s, InputTransform xf) {
     constexpr int G = 4;  // lanes per (row, block) pair
     constexpr int kBlockBytes = FORMAT == kQ4_K ? 144 : 210;
     constexpr int kPairsPerStep = kThreads / G;
@@ -181,18 +190,51 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     for (int i = 0; i < kDepth; ++i)
         if (i < mine) load_pair(p0 + i * kPairsPerStep, buf[i]);
 
-    // Q8_K of the position's activations: one 16-lane row per block, sixteen blocks per pass.
+    // Q8_K of the position's activations: one 16-lane row per block, sixteen blocks per pass. With an input
+    // transform the activations are computed here from the operator's operands, in the operator's own
+    // arithmetic (the RmsNorm sum of squares over the same 256-thread partition and tree).
     const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
+    double scale = 0.0;
+    if constexpr (XF == kInputAddRmsNorm) {
+        double* red = reinterpret_cast<double*>(smem + kint_red_offset(nb, tile_rows));
+        const bool writer = xf.residual_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+        double part = 0;
+        for (int i = threadIdx.x; i < s.columns; i += kThreads) {
+            const float r = xf.b ? __fadd_rn(xf.a[i], xf.b[i]) : xf.a[i];
+            if (writer) xf.residual_out[i] = r;
+            const double v = r;
+            part = part + v * v;
+        }
+        scale = rms_scale(block_sum_256(part, red), s.columns, xf.epsilon);
+    }
     {
         const int j = threadIdx.x & 15;
         for (int b = threadIdx.x >> 4; b < nb; b += kThreads / 16) {
             float v[16];
-            const uint8_t* src = reinterpret_cast<const uint8_t*>(xrow + 256 * b + 16 * j);
+            const int i0 = 256 * b + 16 * j;
+            auto quad = [&](const float* p, int q) {
+                const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(p + i0 + 4 * q));
+                return f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                             __uint_as_float(raw[3])};
+            };
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const u32x4 raw = load16_a4(src + 16 * q);
+                if constexpr (XF == kInputPlain) {
+                    const f32x4 x4 = quad(xrow, q);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[4 * q + e] = __uint_as_float(raw[e]);
+                    for (int e = 0; e < 4; ++e) v[4 * q + e] = x4[e];
+                } else if constexpr (XF == kInputAddRmsNorm) {
+                    const f32x4 a4 = quad(xf.a, q), w4 = quad(xf.w, q);
+                    f32x4 b4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if (xf.b) b4 = quad(xf.b, q);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[4 * q + e] = rms_value(xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e], scale, w4[e]);
+                } else {
+                    const f32x4 g4 = quad(xf.a, q), u4 = quad(xf.b, q);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[4 * q + e] = swiglu_value(g4[e], u4[e]);
+                }
             }
             const Q8KRow16 q = q8k_quantize_row16(v, lane);
             *reinterpret_cast<u32x4*>(act.codes + kCodeStride * b + 4 * j) =
@@ -255,13 +297,18 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
 }
 
 size_t kint_lds_bytes(int blocks) {
-    return static_cast<size_t>(kActDwords + kTileRows) * blocks * sizeof(uint32_t);
+    return static_cast<size_t>(kint_red_offset(blocks, kTileRows)) * sizeof(uint32_t) + kThreads * sizeof(double);
 }
 
-int kint_max_blocks() { return static_cast<int>((64 * 1024) / ((kActDwords + kTileRows) * sizeof(uint32_t))); }
+int kint_max_blocks() {
+    return static_cast<int>((64 * 1024 - kThreads * sizeof(double) - 4) / ((kActDwords + kTileRows) * sizeof(uint32_t)));
+}
 
-hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
-                            hipStream_t stream) {
+namespace {
+
+template <int XF>
+hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, const InputTransform& xf,
+                       hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
     // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and either a
     // thread slot would hold more than three (row, block) pairs (the pairs it prefetches before quantizing)
@@ -276,12 +323,34 @@ hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count,
     const size_t lds = kint_lds_bytes(s.blocks);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     if (s.format == kQ4_K)
-        gemv_kint_kernel<kQ4_K><<<grid, kThreads, lds, stream>>>(one, group, s);
+        gemv_kint_kernel<kQ4_K, XF><<<grid, kThreads, lds, stream>>>(one, group, s, xf);
     else if (s.format == kQ6_K)
-        gemv_kint_kernel<kQ6_K><<<grid, kThreads, lds, stream>>>(one, group, s);
+        gemv_kint_kernel<kQ6_K, XF><<<grid, kThreads, lds, stream>>>(one, group, s, xf);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
+                            hipStream_t stream) {
+    return launch_kint<kInputPlain>(one, group, count, s, InputTransform{}, stream);
+}
+
+hipError_t launch_gemv_kint_transformed(const MatDesc* group, int count, LaunchShape s, const InputTransform& xf,
+                                        hipStream_t stream) {
+    if (s.positions != 1 || !xf.a) return hipErrorInvalidValue;
+    switch (xf.kind) {
+        case kInputPlain: return launch_kint<kInputPlain>(MatDesc{}, group, count, s, xf, stream);
+        case kInputAddRmsNorm:
+            if (!xf.w) return hipErrorInvalidValue;
+            return launch_kint<kInputAddRmsNorm>(MatDesc{}, group, count, s, xf, stream);
+        case kInputSwiGlu:
+            if (!xf.b) return hipErrorInvalidValue;
+            return launch_kint<kInputSwiGlu>(MatDesc{}, group, count, s, xf, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace satori

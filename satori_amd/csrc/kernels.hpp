@@ -129,6 +129,23 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
 hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape,
                             hipStream_t stream);
 
+// The shared input of a one-position K-format launch computed inside it from the decode step's operands
+// instead of read from `x` (every workgroup computes it; the operator's launch disappears):
+//  kInputAddRmsNorm: input = RmsNorm(a + b, w, epsilon) as add_rms_norm_kernel computes it (b may be null:
+//    RmsNorm(a)); a + b is written to residual_out (if not null) by one workgroup;
+//  kInputSwiGlu: input = SwiGlu(a, b) as swiglu_kernel computes it.
+constexpr int kInputPlain = 0, kInputAddRmsNorm = 1, kInputSwiGlu = 2;
+struct InputTransform {
+    int kind;
+    float epsilon;
+    const float* a;
+    const float* b;
+    const float* w;
+    float* residual_out;
+};
+hipError_t launch_gemv_kint_transformed(const MatDesc* group, int count, LaunchShape shape,
+                                        const InputTransform& input, hipStream_t stream);
+
 // Integer K-format product (Q4_K or Q6_K) over `positions` positions on the matrix cores: quantizes the FP32
 // activations x ([positions][blocks * 256]) to Q8_K into `workspace` (kmfma_workspace_bytes), then the
 // product; outputs bit-exact with launch_gemv_kint's. Used from kmfma_min_positions() positions on.

@@ -115,6 +115,7 @@ struct satori_hip_group {
     satori::MatDesc* descriptors = nullptr;   // device
     std::vector<satori::MatDesc> host;         // the same descriptors on the host
     satori::DeviceBuffer batch;                // K groups: packed Q8_K activations of many-position calls
+    satori::InputTransform input{};            // K groups: input computed in the launch (kInputPlain: read x)
     satori::T2Plan plan{};                     // Ternary2 groups
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
     std::vector<satori_hip_matrix*> members;   // distinct member matrices (each counts this group)
@@ -440,7 +441,9 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
 void enqueue_group(satori_hip_group* g, hipStream_t st) {
     const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
     const MatDesc none{};
-    if (g->quantized) {
+    if (g->quantized && g->input.kind != kInputPlain) {
+        check_hip(launch_gemv_kint_transformed(g->descriptors, g->count, l, g->input, st), "integer gemv launch");
+    } else if (g->quantized) {
         check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
     } else if (g->shape.format == SATORI_HIP_TERNARY2) {
         check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
@@ -454,6 +457,8 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
 // Q8_K pack of each distinct input pointer done once and up to kKmfmaMaxMembers members per launch.
 void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
     const Shape& s = g->shape;
+    if (g->input.kind != kInputPlain)
+        fail(SATORI_HIP_E_NOT_SUPPORTED, "An input transform applies to one-position group launches only.");
     if (positions < kmfma_min_positions()) {
         check_hip(launch_gemv_kint(MatDesc{}, g->descriptors, g->count, launch_shape(s, positions, g->rows_max), st),
                   "integer gemv launch");
@@ -1074,6 +1079,47 @@ int satori_hip_group_execute_batch(satori_hip_group* g, int positions, void* str
         const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
         enqueue_group_batch(g, positions, st);
         if (c->capturing && st == c->stream) c->captured_groups.push_back(g);
+    });
+}
+
+int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, const float* b, const float* weights,
+                               float epsilon, float* residual_out) {
+    return guarded([&] {
+        require(g, "group");
+        satori_hip_context* c = g->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!g->live || !c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
+        require_not_capturing(c);
+        if (g->steps > 0) fail(SATORI_HIP_E_ARGUMENT, "Steps that replay the group must be destroyed first.");
+        if (!g->quantized)
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "Input transforms apply to K-format groups with quantized activations.");
+        InputTransform t{};
+        t.kind = kind;
+        switch (kind) {
+            case SATORI_HIP_INPUT_PLAIN: break;
+            case SATORI_HIP_INPUT_ADD_RMS_NORM:
+                require(a, "a");
+                require(weights, "weights");
+                if (!std::isfinite(epsilon) || epsilon < 0.0f)
+                    fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "epsilon must be finite and non-negative.");
+                break;
+            case SATORI_HIP_INPUT_SWIGLU:
+                require(a, "a");
+                require(b, "b");
+                break;
+            default: fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Unknown input transform.");
+        }
+        if (kind != SATORI_HIP_INPUT_PLAIN) {
+            t.a = a;
+            t.b = b;
+            t.w = kind == SATORI_HIP_INPUT_ADD_RMS_NORM ? weights : nullptr;
+            t.epsilon = epsilon;
+            t.residual_out = kind == SATORI_HIP_INPUT_ADD_RMS_NORM ? residual_out : nullptr;
+            const size_t n = static_cast<size_t>(g->shape.columns) * sizeof(float);
+            if (t.residual_out && (overlaps(t.residual_out, n, a, n) || (b && overlaps(t.residual_out, n, b, n))))
+                fail(SATORI_HIP_E_ARGUMENT, "residual_out must not overlap the operands.");
+        }
+        g->input = t;
     });
 }
 

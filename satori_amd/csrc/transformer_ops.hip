@@ -12,24 +12,14 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "ops_device.hpp"
 
 namespace satori {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = kOpsThreads;
 
-// Sum of one double per thread over the workgroup (tree in LDS, fixed order: deterministic).
-__device__ __forceinline__ double block_sum(double v, double* red) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int s = kThreads / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
-        __syncthreads();
-    }
-    const double r = red[0];
-    __syncthreads();
-    return r;
-}
+__device__ __forceinline__ double block_sum(double v, double* red) { return block_sum_256(v, red); }
 
 __device__ __forceinline__ double block_max(double v, double* red) {
     red[threadIdx.x] = v;
@@ -54,10 +44,8 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, cons
         const double v = xv[i];
         part = part + v * v;
     }
-    const double sum = block_sum(part, red);
-    const double scale = 1.0 / __dsqrt_rn(sum / length + static_cast<double>(epsilon));
-    for (int i = threadIdx.x; i < length; i += kThreads)
-        yv[i] = static_cast<float>(static_cast<double>(xv[i]) * scale * static_cast<double>(w[i]));
+    const double scale = rms_scale(block_sum(part, red), length, epsilon);
+    for (int i = threadIdx.x; i < length; i += kThreads) yv[i] = rms_value(xv[i], scale, w[i]);
 }
 
 // Add then RmsNorm (DenseForward.cs:156-158 and :149 of the next layer): residual += addend in FP32, then the
@@ -74,10 +62,8 @@ __global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(float* residual,
         const double v = r;
         part = part + v * v;
     }
-    const double sum = block_sum(part, red);
-    const double scale = 1.0 / __dsqrt_rn(sum / length + static_cast<double>(epsilon));
-    for (int i = threadIdx.x; i < length; i += kThreads)
-        normed[i] = static_cast<float>(static_cast<double>(residual[i]) * scale * static_cast<double>(w[i]));
+    const double scale = rms_scale(block_sum(part, red), length, epsilon);
+    for (int i = threadIdx.x; i < length; i += kThreads) normed[i] = rms_value(residual[i], scale, w[i]);
 }
 
 // The attention inputs of one decode position (DenseForward.cs:128-151): q += q_bias and k + k_bias,
@@ -175,9 +161,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float* v, int heads, int
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(const float* gate, const float* up, int length, float* out) {
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= length) return;
-    const double x = gate[i];
-    const double sigmoid = x >= 0 ? 1.0 / (1.0 + exp(-x)) : exp(x) / (1.0 + exp(x));
-    out[i] = static_cast<float>(x * sigmoid * static_cast<double>(up[i]));
+    out[i] = swiglu_value(gate[i], up[i]);
 }
 
 __global__ __launch_bounds__(kThreads) void add_kernel(const float* left, const float* right, int length, float* out) {

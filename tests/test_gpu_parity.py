@@ -276,6 +276,68 @@ def test_legacy_critical_cases_within_gamma_bound(context, fmt):
             m.dispose()
 
 
+def test_concurrent_execution_then_disposal_race():
+    # VulkanQ8Tests.cs:119-140: four threads execute one matrix concurrently, each result checked; then an
+    # execution races the disposal of the matrix and its context: it either completes or raises
+    # ObjectDisposedException, and repeated disposal is a no-op. Calls release the GIL in the library,
+    # which serialises them per context.
+    import threading
+
+    rows, columns = 257, 768
+    g = rng(119)
+    w = (g.standard_normal((rows, columns), dtype=np.float32) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, BQ.Q8_0)
+    wq = O.decode_matrix(data, rows, columns, int(BQ.Q8_0))
+    ctx = S.HipContext(0)
+    m = ctx.create(data, S.QuantizedMatrixShape(rows, columns, BQ.Q8_0))
+    errors = []
+
+    def worker(seed):
+        try:
+            x = rng(seed).standard_normal(columns, dtype=np.float32)
+            for _ in range(10):
+                y = np.zeros(rows, np.float32)
+                m.execute(x, y)
+                assert_within(y, fp64_matvec(wq, x), relative_bound(wq, x) + 64 * TINY, f"thread {seed}")
+        except BaseException as e:  # re-raised in the test thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(60)
+    assert not errors, errors
+    start = threading.Barrier(2)
+    outcome = []
+
+    def work():
+        start.wait()
+        try:
+            m.execute(np.ones(columns, np.float32), np.zeros(rows, np.float32))
+            outcome.append("completed")
+        except S.ObjectDisposedException:
+            outcome.append("disposed")
+        except BaseException as e:
+            outcome.append(e)
+
+    def dispose():
+        start.wait()
+        m.dispose()
+        ctx.dispose()
+
+    pair = [threading.Thread(target=work), threading.Thread(target=dispose)]
+    for t in pair:
+        t.start()
+    for t in pair:
+        t.join(60)
+    assert outcome in (["completed"], ["disposed"]), outcome
+    m.dispose()
+    ctx.dispose()
+    with pytest.raises(S.ObjectDisposedException):
+        m.execute(np.ones(columns, np.float32), np.zeros(rows, np.float32))
+
+
 @pytest.mark.parametrize("fmt,rows,columns", [(BQ.Q8_0, 4096, 4096), (BQ.Q4_0, 11008, 4096),
                                               (BQ.Q4_0, 4096, 11008), (BQ.Q8_0, 65, 96)])
 def test_legacy_benchmark_shapes_match_scalar_reference(context, fmt, rows, columns):
@@ -1102,6 +1164,87 @@ def test_embedding_rows_decode_like_the_reference(context, fmt):
 # A whole decode token on the device (DenseForward.Step + Final), eager and captured
 # ---------------------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+def test_group_input_transforms_equal_separate_operators(context, fmt):
+    # A K group computing its input from the operators' operands (RmsNorm(a + b), RmsNorm(a), SwiGlu(a, b))
+    # equals the operator launch followed by the plain group, bit for bit, and writes a + b once.
+    g = rng(31 + int(fmt))
+    columns, rows = 1536, [300, 64]
+    mats = [context.create(S.quantize_weights((g.standard_normal((r, columns)) * 0.02).astype(np.float32), r,
+                                              columns, fmt), S.QuantizedMatrixShape(r, columns, fmt)) for r in rows]
+    a, b, w = (g.standard_normal(columns).astype(np.float32) for _ in range(3))
+    b[7] = -a[7]  # a zero of the sum
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    da, db, dw, dx = dev(a), dev(b), dev(w), dev(np.zeros(columns, np.float32))
+    dres = dev(np.zeros(columns, np.float32))
+    ys = [dev(np.zeros(r, np.float32)) for r in rows]
+    ops = S.DeviceOps(context)
+    plain = S.HipGroup(context, mats, [dx, dx], ys, True)
+    fused = S.HipGroup(context, mats, [dx, dx], [dev(np.zeros(r, np.float32)) for r in rows], True)
+    fused_out = buffers[-2:]
+    try:
+        def compare(tag):
+            for y0, y1, r in zip(ys, fused_out, rows):
+                want = context.download(np.zeros(r, np.float32), y0)
+                got = context.download(np.zeros(r, np.float32), y1)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), tag
+
+        # RmsNorm(a + b): the operator adds into a copy of a and normalises into x.
+        dsum = dev(a.copy())
+        ops.add_rms_norm(dsum, db, dw, 1e-6, columns, dx)
+        plain.execute()
+        fused.set_input_add_rms_norm(da, db, dw, 1e-6, dres)
+        fused.execute()
+        compare("add_rms_norm")
+        assert np.array_equal(context.download(np.zeros(columns, np.float32), dres).view(np.uint32),
+                              context.download(np.zeros(columns, np.float32), dsum).view(np.uint32))
+        # RmsNorm(a) without an addend.
+        ops.rms_norm(da, dw, 1e-6, columns, dx)
+        plain.execute()
+        fused.set_input_add_rms_norm(da, 0, dw, 1e-6)
+        fused.execute()
+        compare("rms_norm")
+        # SwiGlu(a, b).
+        ops.swiglu(da, db, columns, dx)
+        plain.execute()
+        fused.set_input_swiglu(da, db)
+        fused.execute()
+        compare("swiglu")
+        # Errors: many positions, overlapping output, unknown kind, FP32-activation groups.
+        with pytest.raises(S.NotSupportedException):
+            fused.execute_batch(16)
+        with pytest.raises(S.ArgumentException):
+            fused.set_input_add_rms_norm(da, db, dw, 1e-6, da)
+        with pytest.raises(S.ArgumentOutOfRangeException):
+            _check_status(S._ffi.lib().satori_hip_group_set_input(fused._handle, 9, None, None, None, 0.0, None))
+        float_group = S.HipGroup(context, mats[:1], [dx], [ys[0]], False)
+        with pytest.raises(S.NotSupportedException):
+            float_group.set_input_swiglu(da, db)
+        float_group.dispose()
+        fused.set_input_plain()
+        fused.execute()
+        plain.execute()
+        compare("plain again")
+    finally:
+        plain.dispose()
+        fused.dispose()
+        for p in buffers:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
+def _check_status(code):
+    S._check(code)
+
+
 def test_device_decode_token_matches_host_composition(context):
     # DenseForward.Step / Final (DenseForward.cs:100-162, 298-306) on a small random model: the device token
     # (eager, and captured then replayed three times with eager work in between) against the same sequence
@@ -1188,10 +1331,21 @@ def test_device_decode_token_matches_host_composition(context):
         dec.enqueue(5, 40)  # eager work between replays: another token, a cache slot the step does not read
         step.execute()
         assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), replay
+    # Folded: residual add + RmsNorm inside the projections' launches, eager and replayed.
+    dec.enqueue(token, position, folded=True)
+    assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32))
+    folded = dec.capture(token, position, folded=True)
+    for replay in range(3):
+        context.upload(dec.logits, np.zeros(vocab, np.float32))
+        dec.enqueue(7, 41, folded=True)  # eager work between replays
+        folded.execute()
+        assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), ("folded", replay)
+    assert dec.launches_per_token(folded=True) == 2 + 7 * n_layers
     with pytest.raises(S.ArgumentException):
         dev_layers[0]["q"].dispose()  # held by the decoder's group
     with pytest.raises(S.InvalidOperationException):
         context.capture_end()          # nothing is being captured
+    folded.dispose()
     step.dispose()
     dec.dispose()
     for layer in dev_layers:
