@@ -319,14 +319,14 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
     return {
         "model": "Qwen-1.5B-shaped whole decode token on the device (random-init weights and KV prefix)",
         "position": position,
-        "kernel_launches_per_token": dec.launches_per_token(folded=True),
+        "kernel_launches_per_token": dec.launches_per_token(folded=True, position=position),
         "us_per_token": graph_ms * 1e3,
         "tokens_per_s": 1e3 / graph_ms,
         "eager_us_per_token": eager_ms * 1e3,
         "fused_us_per_token": timed["fused"] * 1e3,
-        "fused_launches_per_token": dec.launches_per_token(),
+        "fused_launches_per_token": dec.launches_per_token(position=position),
         "unfused_us_per_token": timed["unfused"] * 1e3,
-        "unfused_launches_per_token": dec.launches_per_token(fused=False),
+        "unfused_launches_per_token": dec.launches_per_token(fused=False, position=position),
         "same_logits_all_modes": same,
         "finite_logits": finite,
     }

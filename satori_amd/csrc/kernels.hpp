@@ -198,8 +198,13 @@ hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k
                                    const float* v, const float* v_bias, float* v_out, int heads, int kv_heads,
                                    int head_dim, int position, double base, int rotary, hipStream_t stream);
 int attention_max_tokens();
+// Grouped attention over `tokens` cached positions. Long prefixes are split over up to 16 workgroups per head
+// (attention_splits) whose FP64 partials go to `scratch` (attention_scratch_bytes, which covers every token
+// count for these heads); a single split needs no scratch.
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
-                            int head_dim, int tokens, float* out, hipStream_t stream);
+                            int head_dim, int tokens, float* out, double* scratch, hipStream_t stream);
+int attention_splits(int tokens, int head_dim);
+size_t attention_scratch_bytes(int query_heads, int head_dim);
 hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns, int row, float* out,
                              hipStream_t stream);
 

@@ -86,6 +86,7 @@ struct satori_hip_context {
     bool live = true;
     int matrices = 0;
     satori::DeviceBuffer x, y, q8k;
+    satori::DeviceBuffer attention;  // split-attention partials (grouped attention over long prefixes)
     satori::PinnedBuffer host_x, host_y;
     // Stream capture (satori_hip_capture_begin / _end): the matrices and groups launched on the context
     // stream while capturing, referenced by the step the capture becomes.
@@ -644,6 +645,7 @@ int satori_hip_context_destroy(satori_hip_context* c) {
         c->x.release();
         c->y.release();
         c->q8k.release();
+        c->attention.release();
         c->host_x.release();
         c->host_y.release();
         (void)hipStreamDestroy(c->stream);
@@ -1641,7 +1643,16 @@ int satori_hip_grouped_attention(satori_hip_context* c, const float* query, cons
             fail(SATORI_HIP_E_ARGUMENT, "Attention output overlaps input.");
         if (tokens > attention_max_tokens())
             fail(SATORI_HIP_E_NOT_SUPPORTED, "At most " + std::to_string(attention_max_tokens()) + " tokens per call.");
-        check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output,
+        double* scratch = nullptr;
+        if (attention_splits(tokens, head_dim) > 1) {
+            const size_t need = attention_scratch_bytes(query_heads, head_dim);
+            if (c->capturing && c->attention.bytes < need)
+                fail(SATORI_HIP_E_INVALID_OPERATION,
+                     "Run an attention of these heads once before capturing it (its workspace is allocated on first use).");
+            c->attention.reserve(need);
+            scratch = static_cast<double*>(c->attention.ptr);
+        }
+        check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output, scratch,
                                    op_stream(c, stream)),
                   "attention launch");
     });

@@ -8,6 +8,7 @@
 // squares, the softmax denominator), or where exp / sin / cos / pow come from the device math library, the
 // FP64 intermediate can differ in its last bits; the FP32 outputs then agree to about one unit in the last
 // place. The row decode and Add are FP32 expressions of the reference and agree bit for bit.
+#include <algorithm>
 #include <cmath>
 
 #include "device_common.hpp"
@@ -277,6 +278,174 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     }
 }
 
+// The same attention split over the key/value tokens (flash-decoding), for the long prefixes a single
+// workgroup per head would stream through one CU: workgroup (head, split) computes its tokens' scores, their
+// maximum m, the exponentials e_t = exp(score_t - m), their total l and the unnormalised sums
+// o_j = sum_t e_t * v_tj, all FP64; the combine kernel rescales each split by exp(m_split - M) with M the
+// head's maximum and divides by the rescaled total. Against the reference's softmax-then-sum this
+// reassociates FP64 operations only (far below the FP32 output's last place).
+constexpr int kSplitThreads = 256;
+constexpr int kMaxSplits = 16;
+
+__device__ __forceinline__ double split_reduce(double v, double* red, bool take_max) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = kSplitThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s)
+            red[threadIdx.x] = take_max ? fmax(red[threadIdx.x], red[threadIdx.x + s]) : red[threadIdx.x] + red[threadIdx.x + s];
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const float* __restrict__ q,
+                                                                        const float* __restrict__ k,
+                                                                        const float* __restrict__ v, int query_heads,
+                                                                        int kv_heads, int head_dim, int tokens,
+                                                                        double* __restrict__ partial) {
+    extern __shared__ double es[];  // this split's exponentials
+    __shared__ double red[kSplitThreads];
+    __shared__ float qs[512];
+    const int head = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+    const int per = (tokens + splits - 1) / splits;
+    const int t0 = split * per, t1 = min(tokens, t0 + per);
+    const int kv_head = head / (query_heads / kv_heads);
+    const int kv_width = kv_heads * head_dim;
+    const double scale = 1.0 / __dsqrt_rn(static_cast<double>(head_dim));
+    // The first 16 values of this thread's output lane and token half are loaded before anything else, so
+    // they arrive while the scores are computed.
+    const int count = t1 - t0, half = (count + 1) / 2;
+    const int vj0 = threadIdx.x & 127, vgroup = threadIdx.x >> 7;
+    const int va = t0 + vgroup * half, vb = min(t1, va + half);
+    float vpre[16];
+    if (vj0 < head_dim) {
+        const float* vj = v + kv_head * head_dim + vj0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) vpre[i] = va + i < vb ? vj[static_cast<int64_t>(va + i) * kv_width] : 0.0f;
+    }
+    for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) qs[j] = q[static_cast<int64_t>(head) * head_dim + j];
+    __syncthreads();
+    // Scores: eight threads per token, thread p summing lanes [p * head_dim / 8, (p + 1) * head_dim / 8) of
+    // the key row in order (16-byte loads, all in flight), the eight partial sums then added in order.
+    double local_max = -INFINITY;
+    const int piece = head_dim / 8, p8 = threadIdx.x & 7;
+    for (int base = t0; base < t1; base += kSplitThreads / 8) {
+        const int t = base + (threadIdx.x >> 3);
+        double dot = 0;
+        if (t < t1) {
+            const float* kt = k + static_cast<int64_t>(t) * kv_width + kv_head * head_dim + p8 * piece;
+            const float* qp = qs + p8 * piece;
+            for (int j0 = 0; j0 < piece; j0 += 16) {
+                f32x4 kv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (j0 + 4 * i < piece) {
+                        const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(kt + j0 + 4 * i));
+                        kv[i] = f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                      __uint_as_float(raw[3])};
+                    }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (j0 + 4 * i >= piece) break;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        dot = dot + static_cast<double>(qp[j0 + 4 * i + e]) * static_cast<double>(kv[i][e]);
+                }
+            }
+        }
+        red[threadIdx.x] = dot;
+        __syncthreads();
+        if (p8 == 0 && t < t1) {
+            double total = red[threadIdx.x];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) total = total + red[threadIdx.x + i];
+            const double sc = total * scale;
+            es[t - t0] = sc;
+            local_max = fmax(local_max, sc);
+        }
+        __syncthreads();
+    }
+    const double m = split_reduce(local_max, red, true);
+    double part = 0;
+    for (int t = t0 + threadIdx.x; t < t1; t += kSplitThreads) {
+        const double e = exp(es[t - t0] - m);
+        es[t - t0] = e;
+        part = part + e;
+    }
+    const double l = split_reduce(part, red, false);
+    double* out = partial + (static_cast<int64_t>(head) * splits + split) * (2 + head_dim);
+    if (threadIdx.x == 0) {
+        out[0] = m;
+        out[1] = l;
+    }
+    // Unnormalised sums: lane j of the head over two token halves (threads j and j + 128), added in order.
+    for (int j0 = 0; j0 < head_dim; j0 += 128) {
+        const int j = j0 + vj0;
+        double sum = 0;
+        if (j < head_dim) {
+            const float* vj = v + kv_head * head_dim + j;
+            int t = va;
+            if (j0 == 0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (va + i < vb) sum = sum + es[va + i - t0] * static_cast<double>(vpre[i]);
+                t = min(vb, va + 16);
+            }
+            for (; t + 16 <= vb; t += 16) {
+                float vt[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) vt[i] = vj[static_cast<int64_t>(t + i) * kv_width];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sum = sum + es[t + i - t0] * static_cast<double>(vt[i]);
+            }
+            for (; t < vb; ++t) sum = sum + es[t - t0] * static_cast<double>(vj[static_cast<int64_t>(t) * kv_width]);
+        }
+        red[threadIdx.x] = sum;
+        __syncthreads();
+        if (threadIdx.x < 128 && j < head_dim) out[2 + j] = red[threadIdx.x] + red[threadIdx.x + 128];
+        __syncthreads();
+    }
+}
+
+// One workgroup per head: the splits' weights exp(m_s - M) once (FP64), then lane j's rescaled sum over the
+// splits in order, divided by the rescaled total.
+__global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(const double* __restrict__ partial,
+                                                                          int splits, int head_dim,
+                                                                          float* __restrict__ out) {
+    __shared__ double weight[kMaxSplits];
+    __shared__ double total;
+    const int head = blockIdx.x;
+    const int stride = 2 + head_dim;
+    const double* p = partial + static_cast<int64_t>(head) * splits * stride;
+    if (threadIdx.x < 64) {
+        double big = -INFINITY;
+        for (int s = 0; s < splits; ++s) big = fmax(big, p[s * stride]);
+        if (threadIdx.x < splits) {
+            const double* ps = p + threadIdx.x * stride;
+            weight[threadIdx.x] = ps[1] > 0 ? exp(ps[0] - big) : 0.0;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0;
+        for (int s = 0; s < splits; ++s) t = t + weight[s] * p[s * stride + 1];
+        total = t;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) {
+        double o[kMaxSplits];
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s) o[s] = s < splits ? p[s * stride + 2 + j] : 0.0;
+        double sum = 0;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s)
+            if (s < splits) sum = sum + weight[s] * o[s];
+        out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(sum / total);
+    }
+}
+
 __device__ __forceinline__ uint32_t byte_at(const uint8_t* p) { return *(const SATORI_GLOBAL uint8_t*)(p); }
 __device__ __forceinline__ uint32_t half_bits_at(const uint8_t* p) { return byte_at(p) | (byte_at(p + 1) << 8); }
 
@@ -371,11 +540,31 @@ hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k
 
 int attention_max_tokens() { return 6912; }  // FP64 scores in LDS: 54 KB, with the 8 KB reduction buffer and the 2 KB query 64 KB
 
+int attention_splits(int tokens, int head_dim) {
+    // At least 32 tokens per split, at most 16 splits; heads wider than the staged query, or whose eighths
+    // are not whole 16-byte quads, stay whole.
+    if (head_dim > 512 || (head_dim & 31) != 0) return 1;
+    return std::max(1, std::min(kMaxSplits, (tokens + 31) / 32));
+}
+
+size_t attention_scratch_bytes(int query_heads, int head_dim) {
+    return static_cast<size_t>(query_heads) * kMaxSplits * (2 + head_dim) * sizeof(double);
+}
+
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
-                            int head_dim, int tokens, float* out, hipStream_t stream) {
+                            int head_dim, int tokens, float* out, double* scratch, hipStream_t stream) {
     if (tokens > attention_max_tokens()) return hipErrorInvalidValue;
-    attention_kernel<<<query_heads, kAttnThreads, static_cast<size_t>(tokens) * sizeof(double), stream>>>(
-        q, k, v, query_heads, kv_heads, head_dim, tokens, out);
+    const int splits = attention_splits(tokens, head_dim);
+    if (splits == 1) {
+        attention_kernel<<<query_heads, kAttnThreads, static_cast<size_t>(tokens) * sizeof(double), stream>>>(
+            q, k, v, query_heads, kv_heads, head_dim, tokens, out);
+        return hipGetLastError();
+    }
+    if (!scratch) return hipErrorInvalidValue;
+    const int per = (tokens + splits - 1) / splits;
+    attention_split_kernel<<<dim3(query_heads, splits), kSplitThreads, static_cast<size_t>(per) * sizeof(double),
+                             stream>>>(q, k, v, query_heads, kv_heads, head_dim, tokens, scratch);
+    attention_combine_kernel<<<query_heads, kSplitThreads, 0, stream>>>(scratch, splits, head_dim, out);
     return hipGetLastError();
 }
 

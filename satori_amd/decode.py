@@ -79,6 +79,10 @@ class DeviceDecoder:
             })
         self.final = HipGroup(context, [output], [self.normed], [self.logits], True)
         self._folded = None  # groups with input transforms, made on first use
+        # The split attention's workspace is allocated by its first call (for every token count of these
+        # heads): make that call now, so that a token can be captured before any has run.
+        self.ops.grouped_attention(self.q, self.keys[0], self.values[0], c.heads, c.kv_heads, c.head_dim,
+                                   c.max_tokens, self.context_vec)
 
     def _folded_groups(self):
         """Per layer the q/k/v group reading RmsNorm(residual + previous down output) (layer 0: RmsNorm of the
@@ -168,13 +172,19 @@ class DeviceDecoder:
             ops.rms_norm(self.residual, self.output_norm, c.epsilon, c.hidden, self.normed)
         self.final.execute()
 
-    def launches_per_token(self, fused: bool = True, folded: bool = False) -> int:
+    def launches_per_token(self, fused: bool = True, folded: bool = False, position: int | None = None) -> int:
+        """Kernel launches of one token. At a `position` whose prefix exceeds 32 tokens the attention is split
+        over several workgroups per head and combined by a second kernel (for head widths that are multiples
+        of 32 up to 512), one more launch per layer."""
+        c = self.cfg
+        split = position is not None and position + 1 > 32 and c.head_dim % 32 == 0 and c.head_dim <= 512
+        extra = len(self.layers) if split else 0
         if folded:
-            return 1 + 7 * len(self.layers) + 1
+            return 1 + 7 * len(self.layers) + 1 + extra
         if fused:
-            return 2 + 9 * len(self.layers) + 1
+            return 2 + 9 * len(self.layers) + 1 + extra
         per_layer = 14 if all("q_bias" in v for v in self.vectors) else 13
-        return 1 + per_layer * len(self.layers) + 2
+        return 1 + per_layer * len(self.layers) + 2 + extra
 
     def capture(self, token: int, position: int, fused: bool = True, folded: bool = False) -> HipStep:
         """The token at `position` recorded as one replayable step."""

@@ -1100,6 +1100,16 @@ def test_operators_match_oracle_at_decode_sizes(context):
         out = np.zeros(12 * 128, np.float32)
         T.grouped_attention(q, keys, values, 12, 2, 128, tokens, out, context)
         _within_ulp(out, O.grouped_attention(q, keys, values, 12, 2, 128, tokens), f"attention {tokens}")
+    # Split prefixes at other head widths: 96 (eighths of 12 lanes), 256, and 80 (not split: rows are not
+    # whole eighths of 16-byte quads), with 7 query heads per key/value head.
+    for head_dim, tokens in ((96, 100), (256, 65), (80, 300)):
+        qq = g.standard_normal(14 * head_dim).astype(np.float32)
+        keys = g.standard_normal(tokens * 2 * head_dim).astype(np.float32)
+        values = g.standard_normal(tokens * 2 * head_dim).astype(np.float32)
+        out = np.zeros(14 * head_dim, np.float32)
+        T.grouped_attention(qq, keys, values, 14, 2, head_dim, tokens, out, context)
+        _within_ulp(out, O.grouped_attention(qq, keys, values, 14, 2, head_dim, tokens),
+                    f"attention {head_dim} x {tokens}")
 
 
 def test_operator_extremes_and_argument_errors(context):
@@ -1340,7 +1350,7 @@ def test_device_decode_token_matches_host_composition(context):
         dec.enqueue(7, 41, folded=True)  # eager work between replays
         folded.execute()
         assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), ("folded", replay)
-    assert dec.launches_per_token(folded=True) == 2 + 7 * n_layers
+    assert dec.launches_per_token(folded=True, position=position) == 2 + 8 * n_layers  # split attention
     with pytest.raises(S.ArgumentException):
         dev_layers[0]["q"].dispose()  # held by the decoder's group
     with pytest.raises(S.InvalidOperationException):
