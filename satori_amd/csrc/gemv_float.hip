@@ -339,7 +339,31 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
             float acc[kRowUnroll];
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) acc[u] = 0.0f;
-            for (int c = lr; c < nchunks; c += L) {
+            int c = lr;
+            for (; c + L < nchunks; c += 2 * L) {  // two chunks per step: both rows' loads of both in flight
+                typename F::Regs ra[kRowUnroll], rb[kRowUnroll];
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int row = base + u * kStride + sub;
+                    if (row < row_end) {
+                        F::load(m, s, row, c, ra[u]);
+                        F::load(m, s, row, c + L, rb[u]);
+                    }
+                }
+                F::load_x(xf, c, xr);
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int row = base + u * kStride + sub;
+                    if (row < row_end) acc[u] += F::dot(ra[u], xr, k);
+                }
+                F::load_x(xf, c + L, xr);
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; ++u) {
+                    const int row = base + u * kStride + sub;
+                    if (row < row_end) acc[u] += F::dot(rb[u], xr, k);
+                }
+            }
+            for (; c < nchunks; c += L) {
                 F::load_x(xf, c, xr);
                 typename F::Regs regs[kRowUnroll];
 #pragma unroll
