@@ -202,7 +202,7 @@ int satori_hip_group_execute_batch(satori_hip_group* group, int positions, void*
  * inputs[i]; the operator's launch then disappears. The values are those of the operator bit for bit.
  *  SATORI_HIP_INPUT_ADD_RMS_NORM: input = RmsNorm(a + b, weights, epsilon) (b may be NULL: RmsNorm(a)),
  *    as satori_hip_add_rms_norm / satori_hip_rms_norm compute it; when residual_out is not NULL the launch
- *    also writes a + b there (it must not overlap a or b);
+ *    also writes a + b there (it must not overlap a, b, the weights or the members' outputs);
  *  SATORI_HIP_INPUT_SWIGLU: input = SwiGlu(a, b), as satori_hip_swiglu;
  *  SATORI_HIP_INPUT_PLAIN: back to reading inputs[i].
  * Vectors have the members' column count. One-position launches only (satori_hip_group_execute_batch

@@ -1118,8 +1118,14 @@ int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, co
             t.epsilon = epsilon;
             t.residual_out = kind == SATORI_HIP_INPUT_ADD_RMS_NORM ? residual_out : nullptr;
             const size_t n = static_cast<size_t>(g->shape.columns) * sizeof(float);
-            if (t.residual_out && (overlaps(t.residual_out, n, a, n) || (b && overlaps(t.residual_out, n, b, n))))
-                fail(SATORI_HIP_E_ARGUMENT, "residual_out must not overlap the operands.");
+            if (t.residual_out) {
+                // One workgroup writes residual_out while the others read the operands and write the outputs.
+                bool clash = overlaps(t.residual_out, n, a, n) || (b && overlaps(t.residual_out, n, b, n)) ||
+                             overlaps(t.residual_out, n, weights, n);
+                for (const MatDesc& d : g->host)
+                    clash = clash || overlaps(t.residual_out, n, d.y, static_cast<size_t>(d.rows) * sizeof(float));
+                if (clash) fail(SATORI_HIP_E_ARGUMENT, "residual_out must not overlap the operands or the outputs.");
+            }
         }
         g->input = t;
     });

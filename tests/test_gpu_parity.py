@@ -1232,6 +1232,8 @@ def test_group_input_transforms_equal_separate_operators(context, fmt):
             fused.execute_batch(16)
         with pytest.raises(S.ArgumentException):
             fused.set_input_add_rms_norm(da, db, dw, 1e-6, da)
+        with pytest.raises(S.ArgumentException):  # an output of the group
+            fused.set_input_add_rms_norm(da, db, dw, 1e-6, fused_out[0])
         with pytest.raises(S.ArgumentOutOfRangeException):
             _check_status(S._ffi.lib().satori_hip_group_set_input(fused._handle, 9, None, None, None, 0.0, None))
         float_group = S.HipGroup(context, mats[:1], [dx], [ys[0]], False)
