@@ -21,6 +21,7 @@ The same line carries, labelled:
              captured once and replayed, with the fused and unfused operator sequences beside it;
   prefill:   the same model's projections over 512 positions (ExecuteBatch in 256-position chunks);
              tokens/s and int8 TOP/s;
+  loading:   upload rates of a GGUF tensor (device scale check), an STQ2 file and an STB1 bitplane file;
   roofline:  for the headline kernel, from HIP events on the launch stream;
   cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core; each format's
              entry also carries its own restated reference AVX2 path timed on one core (cpu_gbs).
@@ -387,6 +388,82 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     }
 
 
+def write_gguf(path: str, tensors) -> None:
+    """A GGUF v3 file (the subset the reader accepts, docs/gguf-subset-v1.md) holding `tensors`:
+    (name, rows, columns, ggml type, payload bytes), 32-byte aligned."""
+    import struct
+
+    def string(v: str) -> bytes:
+        raw = v.encode()
+        return struct.pack("<Q", len(raw)) + raw
+
+    out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 3))
+    out += string("general.architecture") + struct.pack("<I", 8) + string("llama")
+    out += string("general.alignment") + struct.pack("<II", 4, 32)
+    out += string("general.quantization_version") + struct.pack("<II", 4, 2)
+    offset, blobs = 0, []
+    for name, rows, columns, type_, payload in tensors:
+        out += string(name) + struct.pack("<I", 2) + struct.pack("<QQ", columns, rows) + struct.pack("<IQ", type_, offset)
+        blobs.append((offset, payload))
+        offset += (payload.size + 31) // 32 * 32
+    while len(out) % 32:
+        out += b"\0"
+    data = bytearray(offset)
+    for off, payload in blobs:
+        data[off:off + payload.size] = payload.tobytes()
+    with open(path, "wb") as f:
+        f.write(bytes(out) + bytes(data))
+
+
+def loading(ctx, seconds: float = 0.5) -> dict:
+    """Resident upload rates of the on-disk formats (payload bytes / time, files in the page cache):
+    a GGUF tensor bound and uploaded straight from the mapping with its block scales checked on the device
+    (satori_hip_gguf_matrix_create), an STQ2 file opened, validated and uploaded (MappedTernary2Matrix), and
+    the same matrix as an STB1 bitplane file (satori_hip_bitplane_open, converted on upload); beside them the
+    upload of the same payloads from host memory."""
+    import shutil
+    import tempfile
+
+    d = tempfile.mkdtemp(prefix="satori_bench_")
+    out = {}
+
+    def rate(fn, nbytes):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds or n < 3:
+            fn()
+            n += 1
+        return nbytes * n / (time.perf_counter() - t0) / 1e9
+
+    try:
+        q4, _ = make_gguf(BQ.Q4_K, 8960, 1536)
+        q6, _ = make_gguf(BQ.Q6_K, 1536, 8960)
+        path = os.path.join(d, "model.gguf")
+        write_gguf(path, [("blk.0.ffn_gate.weight", 8960, 1536, 12, q4), ("blk.0.ffn_down.weight", 1536, 8960, 14, q6)])
+        with S.GgufFile(path) as f:
+            for name, data, fmt, rows, cols in (("blk.0.ffn_gate.weight", q4, BQ.Q4_K, 8960, 1536),
+                                                ("blk.0.ffn_down.weight", q6, BQ.Q6_K, 1536, 8960)):
+                gm = S.GgufQuantizedMatrix(f, name)
+                label = f"gguf_{fmt.name.lower()}_{rows}x{cols}"
+                out[label + "_gbs"] = rate(lambda: gm.create_execution(ctx).dispose(), data.size)
+                out[label + "_host_gbs"] = rate(lambda: ctx.create(data, S.QuantizedMatrixShape(rows, cols, fmt)).dispose(),
+                                                data.size)
+        payload, _ = make_ternary2(4096, 4096, 128)
+        t2 = S.Ternary2Matrix.from_packed(4096, 4096, 128, payload)
+        stq2 = os.path.join(d, "matrix.stq2")
+        t2.save(stq2)
+        out["stq2_4096_b128_gbs"] = rate(lambda: S.MappedTernary2Matrix(stq2, ctx).dispose(), payload.size)
+        out["ternary2_4096_b128_host_gbs"] = rate(lambda: ctx.create_ternary2(4096, 4096, 128, payload).dispose(),
+                                                  payload.size)
+        bp = S.TernaryBitplaneMatrix.from_ternary2(t2)
+        stb1 = os.path.join(d, "matrix.stb1")
+        bp.save(stb1)
+        out["stb1_bitplane_4096_b128_gbs"] = rate(lambda: ctx.open_bitplane(stb1).dispose(), payload.size)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return out
+
+
 def profiled_traffic(name: str):
     """HBM bytes per launch of the headline kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary (calibrated against a copy of known size); None when the summary is absent."""
@@ -592,7 +669,7 @@ def main() -> int:
             cpu_cases[label] = cpu_case
             c.close()
 
-    decode = pre = token = None
+    decode = pre = token = load = None
     if not args.quick:
         progress("decode step (197 projections per token)")
         model = DecodeModel(ctx)
@@ -602,6 +679,8 @@ def main() -> int:
         progress("prefill (512 positions)")
         pre = prefill(ctx, events, model, 3, 1)
         model.close()
+        progress("loading (GGUF, STQ2, STB1 uploads)")
+        load = loading(ctx)
 
     progress("cpu baseline")
     cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
@@ -651,6 +730,7 @@ def main() -> int:
         "decode_token": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in token.items()}
                          if token else None),
         "prefill": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in pre.items()} if pre else None),
+        "loading": ({k: round(v, 2) for k, v in load.items()} if load else None),
         "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in formats.items()},
     }

@@ -102,6 +102,21 @@ inline void validate_bitplane(const Shape& s, const uint8_t* data) {
             if (!std::isfinite(scale) || scale < 0 || bits == 0x80000000u)
                 fail(SATORI_HIP_E_ARGUMENT, "Invalid bitplane scale. (Parameter 'data')");
             const int count = std::min(s.block_size, s.columns - block * s.block_size);
+            if (scale != 0 && count == s.block_size) {
+                // A whole block with a positive scale: only a weight in both planes is invalid (planes of 8, 16
+                // or 32 bytes: whole 8-byte words).
+                uint64_t overlap = 0;
+                for (int i = 0; i < plane; i += 8) {
+                    uint64_t p, n;
+                    std::memcpy(&p, bytes + 4 + i, 8);
+                    std::memcpy(&n, bytes + 4 + plane + i, 8);
+                    overlap |= p & n;
+                }
+                if (overlap)
+                    fail(SATORI_HIP_E_ARGUMENT,
+                         "Overlapping bits, invalid padding or noncanonical zero. (Parameter 'data')");
+                continue;
+            }
             for (int i = 0; i < plane; ++i) {
                 const int positive = bytes[4 + i], negative = bytes[4 + plane + i];
                 const int valid = std::clamp(count - i * 8, 0, 8);
@@ -114,15 +129,36 @@ inline void validate_bitplane(const Shape& s, const uint8_t* data) {
         }
 }
 
-// TernaryBitplaneMatrix.FromTernary2 (TernaryBitplaneMatrix.cs:19-36), on a validated Ternary2 payload.
+// Bit (de)interleaving of four 2-bit codes and their plane bits, a byte at a time: code i of a Ternary2
+// byte is bits 2i (positive) and 2i + 1 (negative); plane bit i of a nibble is weight i.
+struct CodeTables {
+    uint8_t even[256];    // bits 0, 2, 4, 6 of a byte -> bits 0..3
+    uint16_t spread[256]; // bits 0..7 -> bits 0, 2, ..., 14
+    constexpr CodeTables() : even(), spread() {
+        for (int v = 0; v < 256; ++v) {
+            even[v] = static_cast<uint8_t>((v & 1) | ((v >> 1) & 2) | ((v >> 2) & 4) | ((v >> 3) & 8));
+            uint16_t w = 0;
+            for (int b = 0; b < 8; ++b) w = static_cast<uint16_t>(w | (((v >> b) & 1) << (2 * b)));
+            spread[v] = w;
+        }
+    }
+};
+inline constexpr CodeTables kCodeTables{};
+inline uint8_t even_bits(uint8_t v) { return kCodeTables.even[v]; }
+
+// TernaryBitplaneMatrix.FromTernary2 (TernaryBitplaneMatrix.cs:19-36), on a validated Ternary2 payload:
+// code 1 sets the positive plane bit, code 2 the negative one (code 3 does not occur).
 inline void bitplane_from_ternary2(const Shape& s, const uint8_t* t2, uint8_t* out) {
     const int plane = s.block_size / 8;
-    std::memset(out, 0, static_cast<size_t>(s.byte_length));
     for (int64_t offset = 0; offset < s.byte_length; offset += s.block_bytes) {
         std::memcpy(out + offset, t2 + offset, 4);
-        for (int i = 0; i < s.block_size; ++i) {
-            const int code = (t2[offset + 4 + i / 4] >> (2 * (i % 4))) & 3;
-            if (code != 0) out[offset + 4 + (code == 2 ? plane : 0) + i / 8] |= static_cast<uint8_t>(1 << (i % 8));
+        const uint8_t* codes = t2 + offset + 4;
+        uint8_t* positive = out + offset + 4;
+        uint8_t* negative = positive + plane;
+        for (int j = 0; j < plane; ++j) {  // weights 8j .. 8j + 7: code bytes 2j and 2j + 1
+            const uint8_t lo = codes[2 * j], hi = codes[2 * j + 1];
+            positive[j] = static_cast<uint8_t>(even_bits(lo) | (even_bits(hi) << 4));
+            negative[j] = static_cast<uint8_t>(even_bits(lo >> 1) | (even_bits(hi >> 1) << 4));
         }
     }
 }
@@ -130,13 +166,15 @@ inline void bitplane_from_ternary2(const Shape& s, const uint8_t* t2, uint8_t* o
 // TernaryBitplaneMatrix.ToTernary2 (TernaryBitplaneMatrix.cs:38-54), on a validated bitplane payload.
 inline void bitplane_to_ternary2(const Shape& s, const uint8_t* tb, uint8_t* out) {
     const int plane = s.block_size / 8;
-    std::memset(out, 0, static_cast<size_t>(s.byte_length));
     for (int64_t offset = 0; offset < s.byte_length; offset += s.block_bytes) {
         std::memcpy(out + offset, tb + offset, 4);
-        for (int i = 0; i < s.block_size; ++i) {
-            const int positive = (tb[offset + 4 + i / 8] >> (i % 8)) & 1;
-            const int negative = (tb[offset + 4 + plane + i / 8] >> (i % 8)) & 1;
-            out[offset + 4 + i / 4] |= static_cast<uint8_t>((positive | negative << 1) << (2 * (i % 4)));
+        const uint8_t* positive = tb + offset + 4;
+        const uint8_t* negative = positive + plane;
+        uint8_t* codes = out + offset + 4;
+        for (int j = 0; j < plane; ++j) {
+            const uint16_t w = static_cast<uint16_t>(kCodeTables.spread[positive[j]] | (kCodeTables.spread[negative[j]] << 1));
+            codes[2 * j] = static_cast<uint8_t>(w);
+            codes[2 * j + 1] = static_cast<uint8_t>(w >> 8);
         }
     }
 }
@@ -168,6 +206,7 @@ inline Shape quantized_shape(int rows, int columns, int format) {
 
 // Ternary2Matrix.ValidatePayload (src/Satori.Core/Ternary2Matrix.cs:83-101).
 inline void validate_ternary2(const Shape& s, const uint8_t* data) {
+    const int code_bytes = s.block_size / 4;  // 16, 32 or 64: whole 8-byte words
     for (int row = 0; row < s.rows; ++row)
         for (int block = 0; block < s.blocks; ++block) {
             const uint8_t* bytes = data + row * s.row_bytes + static_cast<int64_t>(block) * s.block_bytes;
@@ -177,6 +216,17 @@ inline void validate_ternary2(const Shape& s, const uint8_t* data) {
             if (!std::isfinite(scale) || scale < 0 || bits == 0x80000000u)
                 fail(SATORI_HIP_E_ARGUMENT, "Invalid block scale.");
             const int count = std::min(s.block_size, s.columns - block * s.block_size);
+            if (scale != 0 && count == s.block_size) {
+                // A whole block with a positive scale: only code 3 (both bits of a field set) is invalid.
+                uint64_t bad = 0;
+                for (int i = 0; i < code_bytes; i += 8) {
+                    uint64_t w;
+                    std::memcpy(&w, bytes + 4 + i, 8);
+                    bad |= w & (w >> 1) & 0x5555555555555555ull;
+                }
+                if (bad) fail(SATORI_HIP_E_ARGUMENT, "Invalid weight code or padding.");
+                continue;
+            }
             for (int i = 0; i < s.block_size; ++i) {
                 const int code = (bytes[4 + i / 4] >> (2 * (i % 4))) & 3;
                 if (code == 3 || ((i >= count || scale == 0) && code != 0))
