@@ -18,8 +18,11 @@
 namespace satori {
 namespace {
 
+// Workgroups are 256 threads, or 512 when the staged activations take more than a third of the LDS (long
+// rows): the LDS then caps the workgroups per CU, and wider workgroups keep more waves resident.
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr int kWideThreads = 512;
+constexpr int kWideLdsBytes = 40 * 1024;
 
 // ------------------------------------------------------------------------------------------------
 // Q8_0: f16 d + 32 int8, w = d * q (docs/gguf-subset-v1.md:94; QuantizedMatVec.ExecuteScalar,
@@ -266,8 +269,8 @@ struct XReader {
 // ONE: every row has at most L chunks, so a lane's activations are loaded once per workgroup.
 // XLDS: the activations fit the LDS budget; otherwise they are read from global memory (L2).
 // ------------------------------------------------------------------------------------------------
-template <class F, int L, bool ONE, bool XLDS>
-__global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const MatDesc* __restrict__ group,
+template <class F, int L, bool ONE, bool XLDS, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const MatDesc* __restrict__ group,
                                                                LaunchShape s) {
     const MatDesc m = group ? group[blockIdx.y] : one;
     const int row_begin = blockIdx.x * s.rows_per_wg;
@@ -283,14 +286,14 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
     extern __shared__ float xs[];
     if constexpr (XLDS) {
         const int padded = F::padded_columns(s);
-        for (int i = threadIdx.x; i < padded; i += kThreads)
+        for (int i = threadIdx.x; i < padded; i += THREADS)
             xs[i + ((i >> F::kPadShift) << 2)] = i < columns ? load_f32(x + i) : 0.0f;
         __syncthreads();
     }
     const XReader<F::kPadShift, XLDS> xf{xs, x, columns};
 
     constexpr int kRowsPerPass = 64 / L;
-    constexpr int kStride = kWaves * kRowsPerPass;  // rows between a lane's consecutive rows
+    constexpr int kStride = THREADS / 64 * kRowsPerPass;  // rows between a lane's consecutive rows
     constexpr int kRowUnroll = F::kRowUnroll;
     constexpr int kStep = kStride * kRowUnroll;      // rows per iteration of the whole workgroup
     const int lane = threadIdx.x & 63;
@@ -390,15 +393,28 @@ __global__ __launch_bounds__(kThreads) void gemv_float_kernel(MatDesc one, const
 // LDS budget for the staged activations.
 constexpr int kMaxLdsBytes = 64 * 1024;
 
-template <class F, int L, bool ONE>
-hipError_t launch_variant(const MatDesc& one, const MatDesc* group, int count, const LaunchShape& s, dim3 grid,
-                          int padded, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(padded + 4 * (padded >> F::kPadShift) + 4) * sizeof(float);
+template <class F>
+size_t staged_lds_bytes(int padded) {
+    return static_cast<size_t>(padded + 4 * (padded >> F::kPadShift) + 4) * sizeof(float);
+}
+
+template <class F, int L, bool ONE, int THREADS>
+hipError_t launch_variant(const MatDesc& one, const MatDesc* group, const LaunchShape& s, dim3 grid, int padded,
+                          hipStream_t stream) {
+    const size_t lds = staged_lds_bytes<F>(padded);
     if (lds <= kMaxLdsBytes)
-        gemv_float_kernel<F, L, ONE, true><<<grid, kThreads, lds, stream>>>(one, group, s);
+        gemv_float_kernel<F, L, ONE, true, THREADS><<<grid, THREADS, lds, stream>>>(one, group, s);
     else
-        gemv_float_kernel<F, L, ONE, false><<<grid, kThreads, 0, stream>>>(one, group, s);
+        gemv_float_kernel<F, L, ONE, false, THREADS><<<grid, THREADS, 0, stream>>>(one, group, s);
     return hipGetLastError();
+}
+
+template <class F, int L>
+hipError_t launch_lanes(const MatDesc& one, const MatDesc* group, const LaunchShape& s, dim3 grid, int padded,
+                        bool one_chunk, bool wide, hipStream_t stream) {
+    if (one_chunk) return launch_variant<F, L, true, kThreads>(one, group, s, grid, padded, stream);
+    if (wide) return launch_variant<F, L, false, kWideThreads>(one, group, s, grid, padded, stream);
+    return launch_variant<F, L, false, kThreads>(one, group, s, grid, padded, stream);
 }
 
 template <class F>
@@ -407,8 +423,12 @@ hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, La
     // Lanes per row: enough for one chunk per lane when the row is short, capped at the wave.
     int lanes = 8;
     while (lanes < 64 && lanes < chunks) lanes <<= 1;
+    const bool one_chunk = chunks <= lanes;
+    const size_t lds = staged_lds_bytes<F>(padded);
+    const bool wide = !one_chunk && lds > kWideLdsBytes && lds <= kMaxLdsBytes;
+    const int waves = (wide ? kWideThreads : kThreads) / 64;
     const int rows_per_pass = 64 / lanes;
-    const int rows_per_iteration = kWaves * rows_per_pass * F::kRowUnroll;
+    const int rows_per_iteration = waves * rows_per_pass * F::kRowUnroll;
     // Rows per workgroup: at least one full iteration; grow while the grid keeps >= 2048 workgroups
     // (8 per CU on 256 CUs), so small matrices still spread over the whole chip.
     int64_t groups_total = static_cast<int64_t>(count) * s.positions;
@@ -418,20 +438,11 @@ hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, La
         rows_per_wg *= 2;
     s.rows_per_wg = rows_per_wg;
     dim3 grid((s.rows_max + rows_per_wg - 1) / rows_per_wg, count, s.positions);
-    const bool one_chunk = chunks <= lanes;
     switch (lanes) {
-        case 8:
-            return one_chunk ? launch_variant<F, 8, true>(one, group, count, s, grid, padded, stream)
-                             : launch_variant<F, 8, false>(one, group, count, s, grid, padded, stream);
-        case 16:
-            return one_chunk ? launch_variant<F, 16, true>(one, group, count, s, grid, padded, stream)
-                             : launch_variant<F, 16, false>(one, group, count, s, grid, padded, stream);
-        case 32:
-            return one_chunk ? launch_variant<F, 32, true>(one, group, count, s, grid, padded, stream)
-                             : launch_variant<F, 32, false>(one, group, count, s, grid, padded, stream);
-        default:
-            return one_chunk ? launch_variant<F, 64, true>(one, group, count, s, grid, padded, stream)
-                             : launch_variant<F, 64, false>(one, group, count, s, grid, padded, stream);
+        case 8: return launch_lanes<F, 8>(one, group, s, grid, padded, one_chunk, wide, stream);
+        case 16: return launch_lanes<F, 16>(one, group, s, grid, padded, one_chunk, wide, stream);
+        case 32: return launch_lanes<F, 32>(one, group, s, grid, padded, one_chunk, wide, stream);
+        default: return launch_lanes<F, 64>(one, group, s, grid, padded, one_chunk, wide, stream);
     }
 }
 
