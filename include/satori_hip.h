@@ -262,7 +262,9 @@ int satori_hip_quantize_weights(int format, const float* weights, int rows, int 
  * replayed by satori_hip_step_execute and freed by satori_hip_step_destroy. The step keeps the matrices and
  * groups it launches from being destroyed. While capturing, calls that synchronise, allocate or copy
  * through the host fail with SATORI_HIP_E_INVALID_OPERATION (a many-position K product must have run once
- * before, so its workspace exists), and no other thread may use the context. */
+ * before, so its workspace exists), and no other thread may use the context. The step records the device
+ * addresses of the workspaces it launches with (a matrix's or group's Q8_K buffer, the split attention's
+ * partials): while it lives, a call that would grow one of them fails with SATORI_HIP_E_INVALID_OPERATION. */
 int satori_hip_capture_begin(satori_hip_context* context);
 int satori_hip_capture_end(satori_hip_context* context, satori_hip_step** step);
 

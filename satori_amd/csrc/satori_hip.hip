@@ -87,6 +87,8 @@ struct satori_hip_context {
     int matrices = 0;
     satori::DeviceBuffer x, y, q8k;
     satori::DeviceBuffer attention;  // split-attention partials (grouped attention over long prefixes)
+    int attention_steps = 0;         // live captured steps whose graph uses `attention`
+    bool captured_attention = false; // the capture in progress enqueued a split attention
     satori::PinnedBuffer host_x, host_y;
     // Stream capture (satori_hip_capture_begin / _end): the matrices and groups launched on the context
     // stream while capturing, referenced by the step the capture becomes.
@@ -104,6 +106,7 @@ struct satori_hip_matrix {
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
     satori::DeviceBuffer q8k;    // K formats: Q8_K activations of the last many-position product
     int groups = 0;              // live groups and captured steps that launch this matrix
+    int steps = 0;               // captured steps that launch this matrix directly (they hold its q8k buffer)
     bool live = true;
 };
 
@@ -133,6 +136,7 @@ struct satori_hip_step {
     satori_hip_context* context = nullptr;
     std::vector<satori_hip_group*> groups;     // in launch order (each counts this step)
     std::vector<satori_hip_matrix*> matrices;  // launched directly in a captured step (each counts it)
+    bool attention = false;                    // the graph uses the context's split-attention workspace
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool live = true;
@@ -227,6 +231,10 @@ void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y,
         if (m->context->capturing && m->q8k.bytes < need)
             fail(SATORI_HIP_E_INVALID_OPERATION,
                  "Run this many-position product once before capturing it (its workspace is allocated on first use).");
+        if (m->steps > 0 && m->q8k.bytes < need)  // a captured step holds the current buffer
+            fail(SATORI_HIP_E_INVALID_OPERATION,
+                 "The workspace of this matrix cannot grow while a captured step launches it: destroy the step, "
+                 "or run the largest product before capturing.");
         m->q8k.reserve(need);
         check_hip(launch_gemv_kmfma(m->payload, s.format, x, static_cast<uint8_t*>(m->q8k.ptr), y, s.rows, s.blocks,
                                     s.row_bytes, positions, stream),
@@ -476,6 +484,10 @@ void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
     if (g->context->capturing && g->batch.bytes < per * inputs.size())
         fail(SATORI_HIP_E_INVALID_OPERATION,
              "Run this many-position product once before capturing it (its workspace is allocated on first use).");
+    if (g->steps > 0 && g->batch.bytes < per * inputs.size())  // a captured step holds the current buffer
+        fail(SATORI_HIP_E_INVALID_OPERATION,
+             "The workspace of this group cannot grow while a captured step replays it: destroy the step, "
+             "or run the largest product before capturing.");
     g->batch.reserve(per * inputs.size());
     uint8_t* ws = static_cast<uint8_t*>(g->batch.ptr);
     for (size_t k = 0; k < inputs.size(); ++k)
@@ -1226,7 +1238,12 @@ int satori_hip_step_destroy(satori_hip_step* s) {
         s->exec = nullptr;
         s->graph = nullptr;
         for (satori_hip_group* g : s->groups) g->steps--;
-        for (satori_hip_matrix* m : s->matrices) m->groups--;
+        for (satori_hip_matrix* m : s->matrices) {
+            m->groups--;
+            m->steps--;
+        }
+        if (s->attention) c->attention_steps--;
+        s->attention = false;
         s->groups.clear();
         s->matrices.clear();
         s->live = false;
@@ -1246,6 +1263,7 @@ int satori_hip_capture_begin(satori_hip_context* c) {
         c->capturing = true;
         c->captured_matrices.clear();
         c->captured_groups.clear();
+        c->captured_attention = false;
     });
 }
 
@@ -1285,8 +1303,12 @@ int satori_hip_capture_end(satori_hip_context* c, satori_hip_step** step) {
             if (std::find(st->matrices.begin(), st->matrices.end(), m) == st->matrices.end()) {
                 st->matrices.push_back(m);
                 m->groups++;
+                m->steps++;
             }
         }
+        st->attention = c->captured_attention;
+        if (st->attention) c->attention_steps++;
+        c->captured_attention = false;
         *step = st;
     });
 }
@@ -1655,7 +1677,12 @@ int satori_hip_grouped_attention(satori_hip_context* c, const float* query, cons
             if (c->capturing && c->attention.bytes < need)
                 fail(SATORI_HIP_E_INVALID_OPERATION,
                      "Run an attention of these heads once before capturing it (its workspace is allocated on first use).");
+            if (c->attention_steps > 0 && c->attention.bytes < need)  // captured steps hold the current buffer
+                fail(SATORI_HIP_E_INVALID_OPERATION,
+                     "The attention workspace cannot grow while captured steps use it: destroy them, or run the "
+                     "widest attention before capturing.");
             c->attention.reserve(need);
+            if (c->capturing && op_stream(c, stream) == c->stream) c->captured_attention = true;
             scratch = static_cast<double*>(c->attention.ptr);
         }
         check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output, scratch,

@@ -619,6 +619,59 @@ def test_k_group_batch_equals_member_batches(context, fmt, positions):
             m.dispose()
 
 
+def test_workspaces_do_not_grow_under_captured_steps():
+    # A captured step records the device address of the workspace it launches with: the matrix's Q8_K
+    # buffer, the group's, the context's split-attention partials. An eager call that would grow (reallocate)
+    # one of them while such a step lives is refused; after the step is destroyed it proceeds.
+    ctx = S.HipContext(0)  # fresh: its workspaces start empty
+    rows, columns = 64, 512
+    g = rng(4242)
+    w = (g.standard_normal((rows, columns)) * 0.1).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, BQ.Q4_K)
+    m = ctx.create(data, S.QuantizedMatrixShape(rows, columns, BQ.Q4_K))
+    x = g.standard_normal((64, columns)).astype(np.float32)
+    dx, dy = ctx.alloc(x.nbytes), ctx.alloc(4 * rows * 64)
+    ctx.upload(dx, x)
+    group = S.HipGroup(ctx, [m], [dx], [dy], True)
+    heads, kv_heads, hd, tokens = 2, 1, 64, 64
+    wide = 8 * 128  # the buffers fit the wider call below (8 query heads of 128, one KV head)
+    dq, dk, dv, do = ctx.alloc(4 * wide), ctx.alloc(4 * tokens * 128), ctx.alloc(4 * tokens * 128), ctx.alloc(4 * wide)
+    for p_, n_ in ((dq, wide), (dk, tokens * 128), (dv, tokens * 128)):
+        ctx.upload(p_, g.standard_normal(n_).astype(np.float32))
+    ops = S.DeviceOps(ctx)
+    m.execute_batch_device(dx, 16, dy)      # allocates the 16-position workspaces
+    group.execute_batch(16)
+    ops.grouped_attention(dq, dk, dv, heads, kv_heads, hd, tokens, do)
+    ctx.capture_begin()
+    m.execute_batch_device(dx, 16, dy)
+    group.execute_batch(16)
+    ops.grouped_attention(dq, dk, dv, heads, kv_heads, hd, tokens, do)
+    step = ctx.capture_end()
+    step.execute()
+    with pytest.raises(S.InvalidOperationException):
+        m.execute_batch_device(dx, 64, dy)
+    with pytest.raises(S.InvalidOperationException):
+        group.execute_batch(64)
+    with pytest.raises(S.InvalidOperationException):
+        ops.grouped_attention(dq, dk, dv, 8, 1, 128, tokens, do)  # wider heads: a larger workspace
+    m.execute_batch_device(dx, 16, dy)      # within the current workspace: allowed
+    step.execute()
+    ctx.synchronize()
+    step.dispose()
+    m.execute_batch_device(dx, 64, dy)      # the step is gone: the workspace may grow
+    group.execute_batch(64)
+    ops.grouped_attention(dq, dk, dv, 8, 1, 128, tokens, do)
+    ctx.synchronize()
+    expected = O.qk_matvec_quantized_avx2(data, rows, columns, int(BQ.Q4_K), O.q8k_quantize_row(x[63]))
+    y = ctx.download(np.empty((64, rows), np.float32), dy)
+    assert np.array_equal(y[63].view(np.uint32), np.asarray(expected, np.float32).view(np.uint32))
+    group.dispose()
+    m.dispose()
+    for p_ in (dx, dy, dq, dk, dv, do):
+        ctx.free(p_)
+    ctx.dispose()
+
+
 def test_k_group_batch_errors(context):
     g = rng(5)
     w = (g.standard_normal((64, 512), dtype=np.float32) * 0.02).astype(np.float32)
