@@ -43,7 +43,7 @@ __global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restric
 }
 
 // ------------------------------------------------------------------------------------------------
-// Integer product. A workgroup owns s.rows_per_wg rows (16, 32 or 64) of one member at one position. It quantizes the
+// Integer product. A workgroup owns s.rows_per_wg rows (4 to 64) of one member at one position. It quantizes the
 // position's FP32 activation row to Q8_K itself (one wave per block, bit-exact as above; every workgroup
 // computes the same bytes) straight into LDS as separate arrays (codes, group sums, scales), so no separate
 // quantization launch precedes the product and code reads are 16-byte aligned.
@@ -313,11 +313,15 @@ hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, Laun
     // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and either a
     // thread slot would hold more than three (row, block) pairs (the pairs it prefetches before quantizing)
     // or the grid has fewer than 192 workgroups. Measured on the decode step's groups: q/k/v and o take 8-16
-    // rows, gate/up 32, down (35 blocks) 4; large grouped launches keep 64.
+    // rows, gate/up 32, down (35 blocks) 4; large grouped launches keep 64. Then halved while a workgroup
+    // would stream more than 256 KB of payload, so long rows leave no long tail of workgroups at the end of
+    // a launch (1536 x 8960 grouped: Q6_K 5.43 -> 5.76 TB/s, Q4_K 5.70 -> 5.86 TB/s at 32 rows; 16 rows
+    // measured slower).
     const int64_t members = static_cast<int64_t>(count) * s.positions;
     auto groups_for = [&](int t) { return members * ((s.rows_max + t - 1) / t); };
     int tile = kTileRows;
     while (tile > 4 && groups_for(tile) < 1024 && (tile * s.blocks > 192 || groups_for(tile) < 192)) tile /= 2;
+    while (tile > 4 && static_cast<int64_t>(tile) * s.row_bytes > 256 * 1024) tile /= 2;
     s.rows_per_wg = tile;
     dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
     const size_t lds = kint_lds_bytes(s.blocks);
