@@ -31,6 +31,10 @@ constexpr int kWideLdsBytes = 40 * 1024;
 // ------------------------------------------------------------------------------------------------
 struct Q8_0Chunk {
     static constexpr int kRowUnroll = 2;
+    // Payload cap per workgroup (0: none): more, smaller workgroups leave a shorter tail at the end of a large
+    // launch (4096x4096 grouped: 5.79 -> 5.96 TB/s); Q4_0 measured slower with the cap (its longer rows make
+    // the per-workgroup activation staging the larger cost).
+    static constexpr int kMaxWorkgroupPayload = 256 * 1024;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 5;
     struct Regs {
@@ -79,6 +83,7 @@ struct Q8_0Chunk {
 // ------------------------------------------------------------------------------------------------
 struct Q4_0Chunk {
     static constexpr int kRowUnroll = 2;
+    static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 5;
     struct Regs {
@@ -130,6 +135,7 @@ struct Q4_0Chunk {
 
 struct Q4_KChunk {
     static constexpr int kRowUnroll = 2;
+    static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 6;
     struct Regs {
@@ -188,6 +194,7 @@ struct Q4_KChunk {
 // ------------------------------------------------------------------------------------------------
 struct Q6_KChunk {
     static constexpr int kRowUnroll = 1;
+    static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 64;
     static constexpr int kPadShift = 7;
     using Regs = Q6KQuarter;
@@ -436,6 +443,10 @@ hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, La
     while (rows_per_wg < 1024 &&
            groups_total * ((s.rows_max + 2 * rows_per_wg - 1) / (2 * rows_per_wg)) >= 2048)
         rows_per_wg *= 2;
+    if (F::kMaxWorkgroupPayload > 0)
+        while (rows_per_wg > rows_per_iteration &&
+               static_cast<int64_t>(rows_per_wg) * s.row_bytes > F::kMaxWorkgroupPayload)
+            rows_per_wg /= 2;
     s.rows_per_wg = rows_per_wg;
     dim3 grid((s.rows_max + rows_per_wg - 1) / rows_per_wg, count, s.positions);
     switch (lanes) {
