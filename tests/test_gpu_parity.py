@@ -619,6 +619,59 @@ def test_k_group_batch_equals_member_batches(context, fmt, positions):
             m.dispose()
 
 
+def test_randomized_shapes_sweep(context):
+    # A seeded sweep over every MatVec path and random shapes (rows 1-3000, so rows end inside panels and
+    # tiles; ragged Ternary2 columns; odd block counts; long and short rows): the FP32 paths within the
+    # 1e-5 * sum|w*x| gate of the oracle's scalar restatement of ExecuteScalarCore / ExecuteScalar, the
+    # integer K path (1-15 positions: in-kernel quantization; 16 and more: the matrix-core product) equal to
+    # the oracle's ExecuteQuantizedTiled bit for bit.
+    g = rng(20261201)
+    for case in range(45):
+        kind = case % 9
+        rows = int(g.integers(1, 3001))
+        what = f"case {case}"
+        if kind < 3:
+            block = (64, 128, 256)[kind]
+            columns = int(g.integers(1, 6001))
+            what += f" Ternary2 B{block} {rows}x{columns}"
+            payload = _t2_random_payload(g, rows, columns, block)
+            m = context.create_ternary2(rows, columns, block, payload)
+            x = g.standard_normal(columns).astype(np.float32)
+            y = run(m, x)
+            wq = O.t2_dequantize(payload, rows, columns, block)
+            scalar = O.t2_matvec_scalar(payload, rows, columns, block, x)
+            assert_within(y, scalar, relative_bound(wq, x) + (columns + 8) * TINY, what)
+        elif kind < 7:
+            fmt = (BQ.Q8_0, BQ.Q4_0, BQ.Q4_K, BQ.Q6_K)[kind - 3]
+            unit = 32 if fmt in (BQ.Q8_0, BQ.Q4_0) else 256
+            columns = unit * int(g.integers(1, 6000 // unit + 2))
+            what += f" {fmt.name} FP32 {rows}x{columns}"
+            w = (g.standard_normal((rows, columns)) * 0.05).astype(np.float32)
+            data = S.quantize_weights(w, rows, columns, fmt)
+            m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+            x = g.standard_normal(columns).astype(np.float32)
+            y = run(m, x)
+            wq = O.decode_matrix(data, rows, columns, int(fmt))
+            scalar = O.q_matvec_scalar(data, rows, columns, int(fmt), x)
+            assert_within(y, scalar, relative_bound(wq, x) + 64 * TINY, what)
+        else:
+            fmt = BQ.Q4_K if kind == 7 else BQ.Q6_K
+            positions = int(g.choice([1, 3, 15, 16, 40]))
+            rows = min(rows, 1500)
+            columns = 256 * int(g.integers(1, 36))
+            what += f" {fmt.name} Q8_K {rows}x{columns} x {positions} positions"
+            w = (g.standard_normal((rows, columns)) * 0.05).astype(np.float32)
+            data = S.quantize_weights(w, rows, columns, fmt)
+            m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+            x = g.standard_normal((positions, columns)).astype(np.float32)
+            y = np.zeros(positions * rows, np.float32)
+            m.execute_batch(x.reshape(-1), positions, y)
+            expected = np.concatenate([O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x[p]))
+                                       for p in range(positions)])
+            assert np.array_equal(y.view(np.uint32), expected.astype(np.float32).view(np.uint32)), what
+        m.dispose()
+
+
 def test_workspaces_do_not_grow_under_captured_steps():
     # A captured step records the device address of the workspace it launches with: the matrix's Q8_K
     # buffer, the group's, the context's split-attention partials. An eager call that would grow (reallocate)
