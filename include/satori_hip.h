@@ -63,6 +63,8 @@ typedef enum satori_hip_format {
 
 /* ---- library ---- */
 
+/* Library plumbing with no counterpart in the reference (it is a managed library): the ABI revision of
+ * this header, the calling thread's last failure message and the visible device count. */
 int satori_hip_abi_version(void);
 
 /* Message of the calling thread's last failure ("" after success). */
@@ -317,13 +319,14 @@ int satori_hip_matrix_decode_row(satori_hip_matrix* matrix, int row, float* outp
  * handle needs no context; after close, calls on it fail with SATORI_HIP_E_OBJECT_DISPOSED. Names and
  * keys returned by the info calls, and windows, stay valid until the file is closed. */
 int satori_hip_gguf_open(const char* path, satori_hip_gguf** file);
-/* GgufFile.Dispose: idempotent; NULL is accepted. */
+/* GgufFile.Dispose (src/Satori.Formats.Gguf/GgufFile.cs:206): idempotent; NULL is accepted. */
 int satori_hip_gguf_close(satori_hip_gguf* file);
-/* GgufFile.DataOffset. */
+/* GgufFile.DataOffset (src/Satori.Formats.Gguf/GgufFile.cs:40). */
 int satori_hip_gguf_data_offset(const satori_hip_gguf* file, int64_t* offset);
-/* GgufFile.Tensors: count, lookup by name (SATORI_HIP_E_KEY_NOT_FOUND when absent) and the GgufTensor
- * record of entry `index` in declaration order (src/Satori.Formats.Gguf/GgufTensor.cs:5-20): dims[0] is
- * the contiguous dimension; offset is absolute in the file. Any out pointer may be NULL. */
+/* GgufFile.Tensors (src/Satori.Formats.Gguf/GgufFile.cs:38): count, lookup by name
+ * (SATORI_HIP_E_KEY_NOT_FOUND when absent) and the GgufTensor record of entry `index` in declaration
+ * order (src/Satori.Formats.Gguf/GgufTensor.cs:5-20): dims[0] is the contiguous dimension; offset is
+ * absolute in the file. Any out pointer may be NULL. */
 int satori_hip_gguf_tensor_count(const satori_hip_gguf* file, int64_t* count);
 int satori_hip_gguf_tensor_find(const satori_hip_gguf* file, const char* name, int64_t* index);
 int satori_hip_gguf_tensor_info(const satori_hip_gguf* file, int64_t index, const char** name, int* rank,
@@ -333,8 +336,9 @@ int satori_hip_gguf_tensor_info(const satori_hip_gguf* file, int64_t index, cons
  * SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE. */
 int satori_hip_gguf_tensor_window(const satori_hip_gguf* file, int64_t index, int64_t offset, int64_t length,
                                   const void** bytes);
-/* GgufFile.Metadata: count, lookup by key, and the GgufMetadata record
- * (src/Satori.Formats.Gguf/GgufMetadata.cs:3-4); element_type and element_count are -1 for scalars. */
+/* GgufFile.Metadata (src/Satori.Formats.Gguf/GgufFile.cs:39): count, lookup by key, and the GgufMetadata
+ * record (src/Satori.Formats.Gguf/GgufMetadata.cs:3-4); element_type and element_count are -1 for
+ * scalars. */
 int satori_hip_gguf_metadata_count(const satori_hip_gguf* file, int64_t* count);
 int satori_hip_gguf_metadata_find(const satori_hip_gguf* file, const char* key, int64_t* index);
 int satori_hip_gguf_metadata_info(const satori_hip_gguf* file, int64_t index, const char** key, uint32_t* type,
