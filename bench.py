@@ -282,7 +282,8 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
     """A whole decode token on the device (satori_amd.decode.DeviceDecoder): embedding-row decode, per layer
     RmsNorm, q/k/v, bias adds, RoPE, grouped attention over a `position`-token key/value prefix (random),
     o, residual, RmsNorm, gate/up, SwiGLU, down, residual; then the final norm and the output projection
-    (tied to the embedding, as Qwen2.5-1.5B). Captured once as one step and replayed; also timed eagerly."""
+    (tied to the embedding, as Qwen2.5-1.5B). Captured once as one step and replayed; also timed eagerly,
+    and replayed once more at the end of a 4096-token context."""
     from satori_amd.decode import DecoderConfig, DeviceDecoder
     g = rng(2029)
     cfg = DecoderConfig(hidden=model.D, heads=12, kv_heads=2, head_dim=128, ffn=model.FFN, epsilon=1e-6,
@@ -317,6 +318,22 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
     finite = bool(np.all(np.isfinite(folded_logits)))
     step.dispose()
     dec.dispose()
+    # The same token at the end of a 4096-token context (FP32 key/value cache of 4096 positions).
+    long_position = 4095
+    long_cfg = DecoderConfig(hidden=model.D, heads=12, kv_heads=2, head_dim=128, ffn=model.FFN, epsilon=1e-6,
+                             rope_base=1e6, max_tokens=long_position + 1)
+    long_dec = DeviceDecoder(ctx, long_cfg, model.layers, vectors, out_norm, model.output, model.output)
+    for layer in range(len(model.layers)):
+        prefix = (g.standard_normal((long_cfg.max_tokens, model.KV)) * 0.5).astype(np.float32)
+        ctx.upload(long_dec.keys[layer], prefix)
+        ctx.upload(long_dec.values[layer], prefix[::-1].copy())
+    long_step = long_dec.capture(151, long_position, folded=True)
+    warm_up(ctx, long_step.execute, 0.3)
+    long_ms = time_launches(ctx, events, long_step.execute, steps, warmup)
+    long_finite = bool(np.all(np.isfinite(long_dec.read_logits())))
+    long_launches = long_dec.launches_per_token(folded=True, position=long_position)
+    long_step.dispose()
+    long_dec.dispose()
     return {
         "model": "Qwen-1.5B-shaped whole decode token on the device (random-init weights and KV prefix)",
         "position": position,
@@ -330,6 +347,8 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
         "unfused_launches_per_token": dec.launches_per_token(fused=False, position=position),
         "same_logits_all_modes": same,
         "finite_logits": finite,
+        "context_4096": {"position": long_position, "us_per_token": long_ms * 1e3, "tokens_per_s": 1e3 / long_ms,
+                         "kernel_launches_per_token": long_launches, "finite_logits": long_finite},
     }
 
 

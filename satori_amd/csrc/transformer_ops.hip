@@ -285,7 +285,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // head's maximum and divides by the rescaled total. Against the reference's softmax-then-sum this
 // reassociates FP64 operations only (far below the FP32 output's last place).
 constexpr int kSplitThreads = 256;
-constexpr int kMaxSplits = 16;
+constexpr int kMaxSplits = 32;
+constexpr int kCombineChunk = 16;  // splits whose values one combine thread loads at a time
 
 __device__ __forceinline__ double split_reduce(double v, double* red, bool take_max) {
     red[threadIdx.x] = v;
@@ -435,13 +436,15 @@ __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(const 
     }
     __syncthreads();
     for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) {
-        double o[kMaxSplits];
-#pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) o[s] = s < splits ? p[s * stride + 2 + j] : 0.0;
         double sum = 0;
+        for (int s0 = 0; s0 < splits; s0 += kCombineChunk) {  // in split order, a chunk of loads in flight
+            double o[kCombineChunk];
 #pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s)
-            if (s < splits) sum = sum + weight[s] * o[s];
+            for (int s = 0; s < kCombineChunk; ++s) o[s] = s0 + s < splits ? p[(s0 + s) * stride + 2 + j] : 0.0;
+#pragma unroll
+            for (int s = 0; s < kCombineChunk; ++s)
+                if (s0 + s < splits) sum = sum + weight[s0 + s] * o[s];
+        }
         out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(sum / total);
     }
 }
@@ -541,8 +544,9 @@ hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k
 int attention_max_tokens() { return 6912; }  // FP64 scores in LDS: 54 KB, with the 8 KB reduction buffer and the 2 KB query 64 KB
 
 int attention_splits(int tokens, int head_dim) {
-    // At least 32 tokens per split, at most 16 splits; heads wider than the staged query, or whose eighths
-    // are not whole 16-byte quads, stay whole.
+    // At least 32 tokens per split, at most 32 splits (a 4096-token context: 128 tokens per split, 384
+    // workgroups for 12 heads; 16 and 64 splits measured slower there); heads wider than the staged query,
+    // or whose eighths are not whole 16-byte quads, stay whole.
     if (head_dim > 512 || (head_dim & 31) != 0) return 1;
     return std::max(1, std::min(kMaxSplits, (tokens + 31) / 32));
 }
