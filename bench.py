@@ -616,7 +616,7 @@ def main() -> int:
                     help="only the grouped launches of every format (steps and warmup as given), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build runs the MatVec on a single MI355X "
+        print("bench.py measures one GPU: the library runs the MatVec on a single MI355X "
               "(multi-GPU row sharding is design-only); run with --gpus 1", file=sys.stderr)
         return 2
 

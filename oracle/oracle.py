@@ -1,6 +1,6 @@
 """ctypes front end for the CPU oracle (oracle/liboracle.so).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` as the checker and by
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` for the expected values and by
 bench.py's ``cpu_baseline`` leg. The product package ``satori_amd`` never imports this module.
 
 Every wrapper takes and returns numpy arrays and raises the exception class the reference raises

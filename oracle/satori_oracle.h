@@ -2,7 +2,7 @@
  * CPU oracle for the quantized MatVec hot path.
  *
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's scalar (and AVX2)
- * kernels, used as the checker by tests/, by __graft_entry__.smoke() and as the timed CPU
+ * kernels, giving the expected values to tests/ and __graft_entry__.smoke() and serving as the timed CPU
  * baseline leg of bench.py. The product (satori_amd/libsatori_hip.so) never links, loads or
  * calls anything in this directory.
  *

@@ -1,6 +1,7 @@
 """Shared test helpers: fixture loading, seeded synthetic data and the reference's error bounds.
 
-The oracle (oracle/oracle.py) is the checker; these helpers only load data and compute bounds in FP64.
+The oracle (oracle/oracle.py) supplies the expected values; these helpers only load data and compute
+bounds in FP64.
 """
 from __future__ import annotations
 

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/) before the GPU tests compare against it.
 
 Every oracle function is checked against at least one of: the reference's golden fixtures
 (tests/golden, copied data), the reference tests' known-answer values, FP64 brute force, or an exact
