@@ -142,8 +142,10 @@ int satori_hip_matrix_shape(const satori_hip_matrix* matrix, int* rows, int* col
  * (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:38) and IQuantizedMatrix.Execute
  * (src/Satori.Core/IQuantizedMatrix.cs:7): FP32 activations for every format (K formats use the
  * float decode of Q4KCodec.DotBlock / Q6KCodec.DotBlock). input_length must equal columns and
- * output_length rows; overlapping buffers and non-finite inputs are rejected (ArgumentException,
- * as src/Satori.Backends.Vulkan/VulkanQ8Matrix.cs:82-83). */
+ * output_length rows; overlapping buffers are rejected (ArgumentException). Non-finite inputs are rejected
+ * for the GGUF formats, whose call is the IQuantizedMatrix.Execute plugin seam of a GPU backend
+ * (src/Satori.Backends.Vulkan/VulkanQ8Matrix.cs:82-83), and accepted and propagated for Ternary2, as
+ * Ternary2MatVec.Execute does (src/Satori.Core/Ternary2MatVec.cs:30-36, 52-76). */
 int satori_hip_matvec(satori_hip_matrix* matrix, const float* input, size_t input_length, float* output,
                       size_t output_length);
 
@@ -151,7 +153,8 @@ int satori_hip_matvec(satori_hip_matrix* matrix, const float* input, size_t inpu
  * GgufQuantizedMatrix.ExecuteBatch (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:43-48):
  * input [positions][columns] -> output [positions][rows]. K formats quantize each position to
  * Q8_K on the device and use the integer product (at most 256 positions, as
- * src/Satori.Core/QuantizedKAvx2Kernel.cs:50-51); Q8_0 / Q4_0 use the FP32 product. Ternary2 is
+ * src/Satori.Core/QuantizedKAvx2Kernel.cs:50-51; any width); Q8_0 / Q4_0 use the FP32 product. Non-finite
+ * inputs are accepted and propagate as in the reference (QuantizedMatVec.cs:104-116). Ternary2 is
  * rejected with SATORI_HIP_E_NOT_SUPPORTED (the reference has no batched Ternary2 product). */
 int satori_hip_matvec_batch(satori_hip_matrix* matrix, const float* input, size_t input_length, int positions,
                             float* output, size_t output_length);
@@ -301,8 +304,11 @@ int satori_hip_attention_inputs(satori_hip_context* context, float* query, const
                                 float* value_out, int query_heads, int kv_heads, int head_dim, int position,
                                 double frequency_base, int rotary_dimensions, void* stream);
 /* GroupedAttention (TransformerOps.cs:135-179; Attention :61-91 is query_heads == kv_heads): keys/values
- * token-major [tokens][kv_heads * head_dim]. The scores live on the device (no scratch argument); at most
- * 6912 tokens per call (SATORI_HIP_E_NOT_SUPPORTED beyond). */
+ * token-major [tokens][kv_heads * head_dim]. The scores live on the device (no scratch argument). Prefixes
+ * longer than 32 tokens are split over several workgroups per head, whose partial sums go to a workspace the
+ * context keeps per stream: it is allocated by the first split attention on that stream and grows with the
+ * prefix; attentions on different streams never share one. While capturing, and while captured steps use the
+ * context stream's workspace, a call that would have to grow it fails with SATORI_HIP_E_INVALID_OPERATION. */
 int satori_hip_grouped_attention(satori_hip_context* context, const float* query, const float* keys,
                                  const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
                                  float* output, void* stream);

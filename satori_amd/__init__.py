@@ -3,7 +3,7 @@
 Host-side mirror of the reference's surfaces over the C ABI of libsatori_hip.so (include/satori_hip.h).
 Names, argument meaning and exceptions follow the reference (src/Satori.Core, src/Satori.Formats.Gguf):
 
-  Ternary2Matrix.quantize / from_packed / dequantize   Ternary2Matrix.cs:38-120
+  Ternary2Matrix.quantize / from_packed              Ternary2Matrix.cs:38-101
   Ternary2MatVec.execute                              Ternary2MatVec.cs:9 (HIP backend)
   MappedTernary2Matrix(path).execute                  MappedTernary2Matrix.cs:9-56 (HIP backend)
   QuantizedMatrixShape, BlockQuantization             QuantizedMatrixShape.cs:5-33, BlockQuantization.cs:3
@@ -1008,6 +1008,8 @@ class DeviceOps:
                                                       kv_heads, head_dim, position, float(base), rotary, None))
 
     def grouped_attention(self, q: int, k: int, v: int, query_heads: int, kv_heads: int, head_dim: int, tokens: int,
-                          out: int) -> None:
+                          out: int, stream: int = 0) -> None:
+        """`stream`: a HIP stream handle (0: the context stream)."""
         _check(_ffi.lib().satori_hip_grouped_attention(self._h, self._p(q), self._p(k), self._p(v), query_heads,
-                                                       kv_heads, head_dim, tokens, self._p(out), None))
+                                                       kv_heads, head_dim, tokens, self._p(out),
+                                                       self._p(stream) if stream else None))

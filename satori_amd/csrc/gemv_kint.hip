@@ -47,8 +47,10 @@ __global__ __launch_bounds__(64) void q8k_quantize_kernel(const float* __restric
 // position's FP32 activation row to Q8_K itself (one wave per block, bit-exact as above; every workgroup
 // computes the same bytes) straight into LDS as separate arrays (codes, group sums, scales), so no separate
 // quantization launch precedes the product and code reads are 16-byte aligned.
-// Work items are (row, block) pairs, 4 lanes of 64 weights each; the G lanes' int32 partials are summed exactly, the pair's leader forms the block's FP32
-// term and stores it in LDS, and finally one thread per row adds its terms in block order.
+// Work items are (row, block) pairs, 4 lanes of 64 weights each; the G lanes' int32 partials are summed
+// exactly, the pair's leader forms the block's FP32 term and stores it in LDS, and finally one thread per row
+// adds its terms in block order. A row wider than the LDS holds (more than kint_max_blocks() blocks) is
+// staged and summed in chunks of blocks, in block order, so the sum is the same sequential one.
 // ------------------------------------------------------------------------------------------------
 constexpr int kThreads = 256;
 constexpr int kTileRows = 64;
@@ -156,27 +158,32 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     const int rows = min(tile_rows, m.rows - row_begin);
     const int position = blockIdx.z;
     const int nb = s.blocks;
+    // Blocks staged at a time: the whole row when it fits the LDS, else chunks of K blocks walked in block
+    // order (each chunk's terms are added to the row sums before the next chunk is staged).
+    const int K = s.chunk_blocks;
 
     extern __shared__ uint32_t smem[];
     ActTile act;
-    act.codes = smem;                                                          // kCodeStride * nb dwords
-    act.scales = reinterpret_cast<float*>(smem + kCodeStride * nb);            // nb
-    act.sums = reinterpret_cast<int16_t*>(smem + (kCodeStride + 1) * nb);      // 16 * nb int16 = 8 * nb dwords
-    float* terms = reinterpret_cast<float*>(smem + kActDwords * nb);           // tile_rows * nb
+    act.codes = smem;                                                          // kCodeStride * K dwords
+    act.scales = reinterpret_cast<float*>(smem + kCodeStride * K);             // K
+    act.sums = reinterpret_cast<int16_t*>(smem + (kCodeStride + 1) * K);       // 16 * K int16 = 8 * K dwords
+    float* terms = reinterpret_cast<float*>(smem + kActDwords * K);            // tile_rows * K
 
-    // Work items are (row, block) pairs in row-major order; the G lanes of a pair share its index, so the
-    // DPP group sums stay inside the pair. The next pair's payload is loaded before the current one is
-    // reduced.
+    // Work items are (row, block) pairs of the chunk in row-major order; the G lanes of a pair share its
+    // index, so the DPP group sums stay inside the pair. The next pair's payload is loaded before the
+    // current one is reduced.
     const int lane = threadIdx.x & 63;
     const int c = lane % G;
-    const int pairs = rows * nb;
     const uint8_t* tile = m.w + static_cast<int64_t>(row_begin) * s.row_bytes;
-    auto load_pair = [&](int p, Raw& r) {
+    // Pair p of the chunk starting at block b0 with kb blocks: row p / kb of the tile, block b0 + p % kb.
+    auto load_pair = [&](int b0, int kb, int p, Raw& r) {
+        const int row = p / kb, b = b0 + p % kb;
         if constexpr (FORMAT == kQ4_K) {
-            q4k_load(tile + (p / nb) * s.row_bytes + (p % nb) * kBlockBytes, c, r);
+            q4k_load(tile + row * s.row_bytes + b * kBlockBytes, c, r);
         } else {
-            // Q6_K: block p of the tile is block row_begin * nb + p of the matrix.
-            q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * nb, static_cast<int64_t>(row_begin) * nb + p, c, r);
+            // Q6_K: block b of tile row `row` is block (row_begin + row) * nb + b of the matrix.
+            q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * nb,
+                             static_cast<int64_t>(row_begin + row) * nb + b, c, r);
         }
     };
     // This slot's pairs are p0, p0 + kPairsPerStep, ...; up to kDepth of them are loaded before the
@@ -184,19 +191,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
     // further on, so kDepth loads stay in flight.
     constexpr int kDepth = 3;
     const int p0 = threadIdx.x / G;
-    const int mine = p0 < pairs ? (pairs - 1 - p0) / kPairsPerStep + 1 : 0;
+    int kb = min(K, nb);
+    int mine = p0 < rows * kb ? (rows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
     Raw buf[kDepth];
 #pragma unroll
     for (int i = 0; i < kDepth; ++i)
-        if (i < mine) load_pair(p0 + i * kPairsPerStep, buf[i]);
+        if (i < mine) load_pair(0, kb, p0 + i * kPairsPerStep, buf[i]);
 
     // Q8_K of the position's activations: one 16-lane row per block, sixteen blocks per pass. With an input
     // transform the activations are computed here from the operator's operands, in the operator's own
-    // arithmetic (the RmsNorm sum of squares over the same 256-thread partition and tree).
+    // arithmetic (the RmsNorm sum of squares over the same 256-thread partition and tree, over the whole row).
     const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
     double scale = 0.0;
     if constexpr (XF == kInputAddRmsNorm) {
-        double* red = reinterpret_cast<double*>(smem + kint_red_offset(nb, tile_rows));
+        double* red = reinterpret_cast<double*>(smem + kint_red_offset(K, tile_rows));
         const bool writer = xf.residual_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
         double part = 0;
         for (int i = threadIdx.x; i < s.columns; i += kThreads) {
@@ -207,84 +215,96 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
         }
         scale = rms_scale(block_sum_256(part, red), s.columns, xf.epsilon);
     }
-    {
-        const int j = threadIdx.x & 15;
-        for (int b = threadIdx.x >> 4; b < nb; b += kThreads / 16) {
-            float v[16];
-            const int i0 = 256 * b + 16 * j;
-            auto quad = [&](const float* p, int q) {
-                const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(p + i0 + 4 * q));
-                return f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
-                             __uint_as_float(raw[3])};
-            };
+    // Block order from +0, as the reference accumulator (QuantizedKAvx2Kernel.cs:63, 90-94). A skipped
+    // block stores +0, and adding +0 to a sum that starts at +0 never changes it.
+    float acc = 0.0f;
+    for (int b0 = 0;;) {
+        {
+            const int j = threadIdx.x & 15;
+            for (int bl = threadIdx.x >> 4; bl < kb; bl += kThreads / 16) {
+                float v[16];
+                const int i0 = 256 * (b0 + bl) + 16 * j;
+                auto quad = [&](const float* p, int q) {
+                    const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(p + i0 + 4 * q));
+                    return f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                 __uint_as_float(raw[3])};
+                };
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if constexpr (XF == kInputPlain) {
-                    const f32x4 x4 = quad(xrow, q);
+                for (int q = 0; q < 4; ++q) {
+                    if constexpr (XF == kInputPlain) {
+                        const f32x4 x4 = quad(xrow, q);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[4 * q + e] = x4[e];
-                } else if constexpr (XF == kInputAddRmsNorm) {
-                    const f32x4 a4 = quad(xf.a, q), w4 = quad(xf.w, q);
-                    f32x4 b4 = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (xf.b) b4 = quad(xf.b, q);
+                        for (int e = 0; e < 4; ++e) v[4 * q + e] = x4[e];
+                    } else if constexpr (XF == kInputAddRmsNorm) {
+                        const f32x4 a4 = quad(xf.a, q), w4 = quad(xf.w, q);
+                        f32x4 b4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if (xf.b) b4 = quad(xf.b, q);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        v[4 * q + e] = rms_value(xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e], scale, w4[e]);
-                } else {
-                    const f32x4 g4 = quad(xf.a, q), u4 = quad(xf.b, q);
+                        for (int e = 0; e < 4; ++e)
+                            v[4 * q + e] = rms_value(xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e], scale, w4[e]);
+                    } else {
+                        const f32x4 g4 = quad(xf.a, q), u4 = quad(xf.b, q);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[4 * q + e] = swiglu_value(g4[e], u4[e]);
+                        for (int e = 0; e < 4; ++e) v[4 * q + e] = swiglu_value(g4[e], u4[e]);
+                    }
+                }
+                const Q8KRow16 q = q8k_quantize_row16(v, lane);
+                *reinterpret_cast<u32x4*>(act.codes + kCodeStride * bl + 4 * j) =
+                    u32x4{q.packed[0], q.packed[1], q.packed[2], q.packed[3]};
+                act.sums[16 * bl + j] = static_cast<int16_t>(q.group_sum);
+                if (j == 0) act.scales[bl] = q.scale;
+            }
+        }
+        __syncthreads();  // activations of the chunk staged
+        auto process = [&](const Raw& cur, int p) {
+            const int bl = p % kb;  // block of the chunk (its staged activations)
+            float term = 0.0f;
+            if constexpr (FORMAT == kQ4_K) {
+                int dot, min_part;
+                q4k_dot(cur, act, bl, c, dot, min_part);
+                dot = group_sum_last_int<G>(dot);
+                min_part = group_sum_last_int<G>(min_part);
+                const float a = act.scales[bl];
+                if (a != 0.0f) {  // zero activation block: skipped (QuantizedKAvx2Kernel.cs:86)
+                    const float dA = __fmul_rn(half_bits_to_float(cur.head[0] & 0xFFFFu), a);
+                    const float dminA = __fmul_rn(half_bits_to_float(cur.head[0] >> 16), a);
+                    term = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot)),
+                                     __fmul_rn(dminA, static_cast<float>(min_part)));
+                }
+            } else {
+                int dot = q6k_dot(cur, act, bl, c);
+                dot = group_sum_last_int<G>(dot);
+                const float a = act.scales[bl];
+                if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, cur.d), static_cast<float>(dot));
+            }
+            if (c == G - 1) terms[p] = term;  // p = r * kb + bl
+        };
+        for (int base = 0; base < mine; base += kDepth) {
+#pragma unroll
+            for (int i = 0; i < kDepth; ++i) {
+                const int k = base + i;
+                if (k < mine) {
+                    process(buf[i], p0 + k * kPairsPerStep);
+                    if (k + kDepth < mine) load_pair(b0, kb, p0 + (k + kDepth) * kPairsPerStep, buf[i]);
                 }
             }
-            const Q8KRow16 q = q8k_quantize_row16(v, lane);
-            *reinterpret_cast<u32x4*>(act.codes + kCodeStride * b + 4 * j) =
-                u32x4{q.packed[0], q.packed[1], q.packed[2], q.packed[3]};
-            act.sums[16 * b + j] = static_cast<int16_t>(q.group_sum);
-            if (j == 0) act.scales[b] = q.scale;
         }
-    }
-    __syncthreads();  // activations staged
-    auto process = [&](const Raw& cur, int p) {
-        const int b = p % nb;
-        float term = 0.0f;
-        if constexpr (FORMAT == kQ4_K) {
-            int dot, min_part;
-            q4k_dot(cur, act, b, c, dot, min_part);
-            dot = group_sum_last_int<G>(dot);
-            min_part = group_sum_last_int<G>(min_part);
-            const float a = act.scales[b];
-            if (a != 0.0f) {  // zero activation block: skipped (QuantizedKAvx2Kernel.cs:86)
-                const float dA = __fmul_rn(half_bits_to_float(cur.head[0] & 0xFFFFu), a);
-                const float dminA = __fmul_rn(half_bits_to_float(cur.head[0] >> 16), a);
-                term = __fsub_rn(__fmul_rn(dA, static_cast<float>(dot)), __fmul_rn(dminA, static_cast<float>(min_part)));
-            }
-        } else {
-            int dot = q6k_dot(cur, act, b, c);
-            dot = group_sum_last_int<G>(dot);
-            const float a = act.scales[b];
-            if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, cur.d), static_cast<float>(dot));
+        __syncthreads();  // the chunk's terms are in LDS
+        if (threadIdx.x < rows) {
+            const float* t = terms + threadIdx.x * kb;
+            for (int b = 0; b < kb; ++b) acc = __fadd_rn(acc, t[b]);
         }
-        if (c == G - 1) terms[p] = term;  // p = r * nb + b
-    };
-    for (int base = 0; base < mine; base += kDepth) {
+        b0 += K;
+        if (b0 >= nb) break;
+        // Next chunk: its first pairs' payload is requested before the LDS is released.
+        kb = min(K, nb - b0);
+        mine = p0 < rows * kb ? (rows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
 #pragma unroll
-        for (int i = 0; i < kDepth; ++i) {
-            const int k = base + i;
-            if (k < mine) {
-                process(buf[i], p0 + k * kPairsPerStep);
-                if (k + kDepth < mine) load_pair(p0 + (k + kDepth) * kPairsPerStep, buf[i]);
-            }
-        }
+        for (int i = 0; i < kDepth; ++i)
+            if (i < mine) load_pair(b0, kb, p0 + i * kPairsPerStep, buf[i]);
+        __syncthreads();  // every thread is done with this chunk's activations and terms
     }
-    __syncthreads();
-    if (threadIdx.x < rows) {
-        // Block order from +0, as the reference accumulator (QuantizedKAvx2Kernel.cs:63, 90-94). A skipped
-        // block stored +0, and adding +0 to a sum that starts at +0 never changes it.
-        float acc = 0.0f;
-        const float* t = terms + threadIdx.x * nb;
-        for (int b = 0; b < nb; ++b) acc = __fadd_rn(acc, t[b]);
-        store_f32(m.y + static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x, acc);
-    }
+    if (threadIdx.x < rows) store_f32(m.y + static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x, acc);
 }
 
 }  // namespace
@@ -323,8 +343,10 @@ hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, Laun
     while (tile > 4 && groups_for(tile) < 1024 && (tile * s.blocks > 192 || groups_for(tile) < 192)) tile /= 2;
     while (tile > 4 && static_cast<int64_t>(tile) * s.row_bytes > 256 * 1024) tile /= 2;
     s.rows_per_wg = tile;
+    // Rows wider than the LDS holds are staged kint_max_blocks() blocks at a time.
+    s.chunk_blocks = s.blocks < kint_max_blocks() ? s.blocks : kint_max_blocks();
     dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
-    const size_t lds = kint_lds_bytes(s.blocks);
+    const size_t lds = kint_lds_bytes(s.chunk_blocks);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     if (s.format == kQ4_K)
         gemv_kint_kernel<kQ4_K, XF><<<grid, kThreads, lds, stream>>>(one, group, s, xf);

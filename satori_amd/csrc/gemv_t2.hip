@@ -55,20 +55,21 @@ struct T2Args {
 };
 
 // Builds the 64 pair tables of local tile u into buffer BUF: thread k writes entry k & 15 of pairs
-// k / 16 + 16 i. v(c0) x0 + v(c1) x1 is formed as fma(v1, x1, v0 * x0): both products are exact, so the
-// entry is the correctly rounded pair sum (a zero entry may be -0, which adds like +0 to sums that start
-// at +0).
+// k / 16 + 16 i. v(c0) x0 + v(c1) x1 is formed as sel(c0, x0) + sel(c1, x1) with sel(1, x) = x,
+// sel(2, x) = -x and sel(0, x) = sel(3, x) = +0, so the entry is the correctly rounded pair sum, and a
+// code-0 weight contributes nothing even when its activation is infinite or NaN, as the reference skips it
+// (Ternary2MatVec.cs:64-70). A zero entry may be -0, which adds like +0 to sums that start at +0.
 template <int BUF, int THREADS>
 __device__ __forceinline__ void build_tables(float (*tables)[kTableFloats], const float* xs, int u) {
     const int e = threadIdx.x & 15;
     const int c0 = e & 3, c1 = e >> 2;
-    const float v0 = c0 == 1 ? 1.0f : (c0 == 2 ? -1.0f : 0.0f);
-    const float v1 = c1 == 1 ? 1.0f : (c1 == 2 ? -1.0f : 0.0f);
 #pragma unroll
     for (int k = 0; k < kTableFloats / THREADS; ++k) {
         const int pair = (threadIdx.x >> 4) + k * (THREADS / 16);
         const float2 xp = *reinterpret_cast<const float2*>(xs + kTile * u + 2 * pair);
-        tables[BUF][pair * 16 + e] = __builtin_fmaf(v1, xp.y, v0 * xp.x);
+        const float a = c0 == 1 ? xp.x : (c0 == 2 ? -xp.x : 0.0f);
+        const float b = c1 == 1 ? xp.y : (c1 == 2 ? -xp.y : 0.0f);
+        tables[BUF][pair * 16 + e] = a + b;
     }
 }
 

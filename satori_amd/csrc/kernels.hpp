@@ -33,6 +33,7 @@ struct LaunchShape {
     int positions;      // activation vectors per call
     int rows_max;       // largest member row count (grid extent)
     int rows_per_wg;    // rows one workgroup owns (launcher-chosen)
+    int chunk_blocks;   // integer K product: blocks of the activation row staged in LDS at a time (launcher-chosen)
 };
 
 // FP32-activation MatVec for the GGUF formats (Q8_0, Q4_0, Q4_K, Q6_K) on the packed row-major payload.
@@ -197,14 +198,16 @@ hipError_t launch_add_rms_norm(float* residual, const float* addend, const float
 hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k, const float* k_bias, float* k_out,
                                    const float* v, const float* v_bias, float* v_out, int heads, int kv_heads,
                                    int head_dim, int position, double base, int rotary, hipStream_t stream);
-int attention_max_tokens();
-// Grouped attention over `tokens` cached positions. Long prefixes are split over up to 16 workgroups per head
-// (attention_splits) whose FP64 partials go to `scratch` (attention_scratch_bytes, which covers every token
-// count for these heads); a single split needs no scratch.
+// Grouped attention over `tokens` cached positions. Up to 32 tokens one workgroup per head; longer prefixes
+// are split over several workgroups per head (attention_splits) whose FP64 partials go to `scratch`
+// (attention_scratch_bytes: the bytes for `tokens`, which also cover every shorter prefix of these heads).
+// attention_supported is false only where one split's exponentials and staged query would not fit the LDS
+// (more than 134 million tokens).
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
                             int head_dim, int tokens, float* out, double* scratch, hipStream_t stream);
-int attention_splits(int tokens, int head_dim);
-size_t attention_scratch_bytes(int query_heads, int head_dim);
+int attention_splits(int tokens);
+size_t attention_scratch_bytes(int query_heads, int head_dim, int tokens);
+bool attention_supported(int tokens, int head_dim);
 hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns, int row, float* out,
                              hipStream_t stream);
 
@@ -213,8 +216,8 @@ hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns
 hipError_t launch_scale_check(const uint8_t* payload, int64_t blocks, int format, uint32_t* flag, hipStream_t stream);
 int kmfma_min_positions();
 
-// Widest row, in Q8_K blocks, the integer product accepts (its LDS holds the staged activation row and the
-// block terms of the workgroup's rows).
+// Blocks of the activation row the integer product stages in LDS at once (with the block terms of the
+// workgroup's rows); wider rows are processed in chunks of this many blocks, in block order.
 int kint_max_blocks();
 
 }  // namespace satori

@@ -86,8 +86,10 @@ struct satori_hip_context {
     bool live = true;
     int matrices = 0;
     satori::DeviceBuffer x, y, q8k;
-    satori::DeviceBuffer attention;  // split-attention partials (grouped attention over long prefixes)
-    int attention_steps = 0;         // live captured steps whose graph uses `attention`
+    // Split-attention partials (grouped attention over long prefixes), one buffer per stream the attention
+    // runs on, so attentions on different streams never share one; attentions on one stream run in order.
+    std::vector<std::pair<hipStream_t, satori::DeviceBuffer>> attention;
+    int attention_steps = 0;         // live captured steps whose graph uses the context stream's buffer
     bool captured_attention = false; // the capture in progress enqueued a split attention
     satori::PinnedBuffer host_x, host_y;
     // Stream capture (satori_hip_capture_begin / _end): the matrices and groups launched on the context
@@ -209,8 +211,6 @@ LaunchShape launch_shape(const Shape& s, int positions, int rows_max) {
 
 bool is_k(const Shape& s) { return s.format == SATORI_HIP_Q4_K || s.format == SATORI_HIP_Q6_K; }
 
-size_t kint_lds_limit_blocks() { return static_cast<size_t>(kint_max_blocks()); }
-
 // Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers.
 void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
     MatDesc d{m->payload, x, y, m->shape.rows, 0};
@@ -243,12 +243,6 @@ void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y,
     }
     MatDesc d{m->payload, x, y, s.rows, 0};
     check_hip(launch_gemv_kint(d, nullptr, 1, launch_shape(s, positions, s.rows), stream), "integer gemv launch");
-}
-
-void check_kint_width(const Shape& s) {
-    if (static_cast<size_t>(s.blocks) > kint_lds_limit_blocks())
-        fail(SATORI_HIP_E_NOT_SUPPORTED, "Integer K-format product supports at most " +
-                                             std::to_string(kint_lds_limit_blocks() * 256) + " columns.");
 }
 
 bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
@@ -425,8 +419,12 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     const size_t in_bytes = input_length * sizeof(float), out_bytes = output_length * sizeof(float);
     if (overlaps(input, in_bytes, output, out_bytes))
         fail(SATORI_HIP_E_ARGUMENT, "Output must not overlap input.");
-    for (size_t i = 0; i < input_length; ++i)
-        if (!std::isfinite(input[i])) fail(SATORI_HIP_E_ARGUMENT, "Expected finite FP32 input.");
+    // Only the plugin seam rejects non-finite activations: IQuantizedMatrix.Execute of a GPU backend
+    // (src/Satori.Backends.Vulkan/VulkanQ8Matrix.cs:82-83). Ternary2MatVec.Execute (Ternary2MatVec.cs:30-36)
+    // and QuantizedMatVec.ExecuteBatch (QuantizedMatVec.cs:104-116) take them and propagate them.
+    if (!batch && s.format != SATORI_HIP_TERNARY2)
+        for (size_t i = 0; i < input_length; ++i)
+            if (!std::isfinite(input[i])) fail(SATORI_HIP_E_ARGUMENT, "Expected finite FP32 input.");
 
     set_device(c);
     c->x.reserve(in_bytes);
@@ -434,7 +432,6 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     c->host_x.reserve(in_bytes);
     c->host_y.reserve(out_bytes);
     const bool integer = batch && is_k(s);
-    if (integer) check_kint_width(s);
     std::memcpy(c->host_x.ptr, input, in_bytes);
     check_hip(hipMemcpyAsync(c->x.ptr, c->host_x.ptr, in_bytes, hipMemcpyHostToDevice, c->stream), "input copy");
     if (integer)
@@ -657,7 +654,8 @@ int satori_hip_context_destroy(satori_hip_context* c) {
         c->x.release();
         c->y.release();
         c->q8k.release();
-        c->attention.release();
+        for (auto& entry : c->attention) entry.second.release();
+        c->attention.clear();
         c->host_x.release();
         c->host_y.release();
         (void)hipStreamDestroy(c->stream);
@@ -944,7 +942,6 @@ int satori_hip_matvec_batch_device(satori_hip_matrix* m, const float* input, int
         hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
         if (is_k(m->shape)) {
             if (positions > 256) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "At most 256 positions per call.");
-            check_kint_width(m->shape);
             enqueue_kint(m, input, positions, output, st);
         } else {
             enqueue_float(m, input, positions, output, st);
@@ -1045,7 +1042,6 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
                 set_device(c);
                 g->scratch = allocate_t2_scratch(g->plan);
             }
-            if (g->quantized) check_kint_width(first);
             set_device(c);
             check_hip(hipMalloc(reinterpret_cast<void**>(&g->descriptors), sizeof(MatDesc) * count), "hipMalloc");
             check_hip(hipMemcpy(g->descriptors, host.data(), sizeof(MatDesc) * count, hipMemcpyHostToDevice),
@@ -1114,8 +1110,10 @@ int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, co
             case SATORI_HIP_INPUT_ADD_RMS_NORM:
                 require(a, "a");
                 require(weights, "weights");
-                if (!std::isfinite(epsilon) || epsilon < 0.0f)
-                    fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "epsilon must be finite and non-negative.");
+                // The operator's own rule (TransformerOps.cs:17): epsilon finite and positive.
+                if (!std::isfinite(epsilon) || epsilon <= 0.0f)
+                    fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE,
+                         "Specified argument was out of the range of valid values. (Parameter 'epsilon')");
                 break;
             case SATORI_HIP_INPUT_SWIGLU:
                 require(a, "a");
@@ -1669,24 +1667,32 @@ int satori_hip_grouped_attention(satori_hip_context* c, const float* query, cons
         if (any_overlap(query, width, output, width) || any_overlap(keys, kv, output, width) ||
             any_overlap(values, kv, output, width))
             fail(SATORI_HIP_E_ARGUMENT, "Attention output overlaps input.");
-        if (tokens > attention_max_tokens())
-            fail(SATORI_HIP_E_NOT_SUPPORTED, "At most " + std::to_string(attention_max_tokens()) + " tokens per call.");
+        if (!attention_supported(tokens, head_dim))
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "The prefix is too long for one split of the attention's local memory.");
+        const hipStream_t st = op_stream(c, stream);
         double* scratch = nullptr;
-        if (attention_splits(tokens, head_dim) > 1) {
-            const size_t need = attention_scratch_bytes(query_heads, head_dim);
-            if (c->capturing && c->attention.bytes < need)
+        if (attention_splits(tokens) > 1) {
+            const size_t need = attention_scratch_bytes(query_heads, head_dim, tokens);
+            auto it = std::find_if(c->attention.begin(), c->attention.end(),
+                                   [&](const std::pair<hipStream_t, DeviceBuffer>& e) { return e.first == st; });
+            if (c->capturing && (it == c->attention.end() || it->second.bytes < need))
                 fail(SATORI_HIP_E_INVALID_OPERATION,
-                     "Run an attention of these heads once before capturing it (its workspace is allocated on first use).");
-            if (c->attention_steps > 0 && c->attention.bytes < need)  // captured steps hold the current buffer
+                     "Run an attention of these heads and tokens once before capturing it (its workspace is allocated "
+                     "on first use).");
+            if (it == c->attention.end()) {
+                c->attention.emplace_back(st, DeviceBuffer{});
+                it = c->attention.end() - 1;
+            }
+            DeviceBuffer& buffer = it->second;
+            if (st == c->stream && c->attention_steps > 0 && buffer.bytes < need)  // captured steps hold it
                 fail(SATORI_HIP_E_INVALID_OPERATION,
                      "The attention workspace cannot grow while captured steps use it: destroy them, or run the "
-                     "widest attention before capturing.");
-            c->attention.reserve(need);
-            if (c->capturing && op_stream(c, stream) == c->stream) c->captured_attention = true;
-            scratch = static_cast<double*>(c->attention.ptr);
+                     "longest attention before capturing.");
+            buffer.reserve(need);
+            if (c->capturing && st == c->stream) c->captured_attention = true;
+            scratch = static_cast<double*>(buffer.ptr);
         }
-        check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output, scratch,
-                                   op_stream(c, stream)),
+        check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output, scratch, st),
                   "attention launch");
     });
 }

@@ -283,10 +283,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // maximum m, the exponentials e_t = exp(score_t - m), their total l and the unnormalised sums
 // o_j = sum_t e_t * v_tj, all FP64; the combine kernel rescales each split by exp(m_split - M) with M the
 // head's maximum and divides by the rescaled total. Against the reference's softmax-then-sum this
-// reassociates FP64 operations only (far below the FP32 output's last place).
+// reassociates FP64 operations only (far below the FP32 output's last place). Any prefix length and head
+// width: up to 32 splits of at least 32 tokens, and more splits once a split would exceed 2,048 tokens (its
+// exponentials stay in LDS).
 constexpr int kSplitThreads = 256;
-constexpr int kMaxSplits = 32;
-constexpr int kCombineChunk = 16;  // splits whose values one combine thread loads at a time
+constexpr int kMinSplits = 32;         // splits of a long prefix before the per-split token bound applies
+constexpr int kMaxSplitTokens = 2048;  // tokens of one split (its FP64 exponentials in LDS: 16 KB)
+constexpr int kMaxSplitsPerLaunch = 65535;
+constexpr int kStagedQuery = 8192;     // query lanes staged in LDS; wider heads read the query from global memory
+constexpr int kCombineChunk = 16;      // splits whose values one combine thread loads at a time
+constexpr int kCombineWeights = 1024;  // split weights the combine kernel holds in LDS at a time
 
 __device__ __forceinline__ double split_reduce(double v, double* red, bool take_max) {
     red[threadIdx.x] = v;
@@ -301,20 +307,39 @@ __device__ __forceinline__ double split_reduce(double v, double* red, bool take_
     return r;
 }
 
+// Workgroup reduction of 256 doubles through wave shuffles and four partials in LDS (every thread gets it).
+__device__ __forceinline__ double wave_reduce_256(double v, double* red4, bool take_max) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const double other = __shfl_xor(v, o, 64);
+        v = take_max ? fmax(v, other) : v + other;
+    }
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double r = red4[0];
+#pragma unroll
+    for (int i = 1; i < kSplitThreads / 64; ++i) r = take_max ? fmax(r, red4[i]) : r + red4[i];
+    __syncthreads();
+    return r;
+}
+
 __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const float* __restrict__ q,
                                                                         const float* __restrict__ k,
                                                                         const float* __restrict__ v, int query_heads,
-                                                                        int kv_heads, int head_dim, int tokens,
+                                                                        int kv_heads, int head_dim, int tokens, int per,
                                                                         double* __restrict__ partial) {
-    extern __shared__ double es[];  // this split's exponentials
+    extern __shared__ double es[];  // this split's exponentials (per), then the staged query lanes
     __shared__ double red[kSplitThreads];
-    __shared__ float qs[512];
     const int head = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
-    const int per = (tokens + splits - 1) / splits;
-    const int t0 = split * per, t1 = min(tokens, t0 + per);
+    const int t0 = static_cast<int>(min(static_cast<int64_t>(split) * per, static_cast<int64_t>(tokens)));
+    const int t1 = min(tokens, t0 + per);
     const int kv_head = head / (query_heads / kv_heads);
     const int kv_width = kv_heads * head_dim;
     const double scale = 1.0 / __dsqrt_rn(static_cast<double>(head_dim));
+    const float* qh = q + static_cast<int64_t>(head) * head_dim;
+    float* qs = reinterpret_cast<float*>(es + per);
+    const bool staged = head_dim <= kStagedQuery;
+    const float* qsrc = staged ? qs : qh;
     // The first 16 values of this thread's output lane and token half are loaded before anything else, so
     // they arrive while the scores are computed.
     const int count = t1 - t0, half = (count + 1) / 2;
@@ -326,34 +351,43 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
 #pragma unroll
         for (int i = 0; i < 16; ++i) vpre[i] = va + i < vb ? vj[static_cast<int64_t>(va + i) * kv_width] : 0.0f;
     }
-    for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) qs[j] = q[static_cast<int64_t>(head) * head_dim + j];
+    if (staged)
+        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) qs[j] = qh[j];
     __syncthreads();
-    // Scores: eight threads per token, thread p summing lanes [p * head_dim / 8, (p + 1) * head_dim / 8) of
-    // the key row in order (16-byte loads, all in flight), the eight partial sums then added in order.
+    // Scores: eight threads per token, thread p summing lanes [p * piece, (p + 1) * piece) of the key row in
+    // order (16-byte loads, all in flight, when the eighths are whole quads), the eight partial sums then
+    // added in order.
     double local_max = -INFINITY;
-    const int piece = head_dim / 8, p8 = threadIdx.x & 7;
+    const bool quads = (head_dim & 31) == 0;
+    const int piece = (head_dim + 7) / 8, p8 = threadIdx.x & 7;
+    const int j_lo = min(head_dim, p8 * piece), j_hi = min(head_dim, j_lo + piece);
     for (int base = t0; base < t1; base += kSplitThreads / 8) {
         const int t = base + (threadIdx.x >> 3);
         double dot = 0;
         if (t < t1) {
-            const float* kt = k + static_cast<int64_t>(t) * kv_width + kv_head * head_dim + p8 * piece;
-            const float* qp = qs + p8 * piece;
-            for (int j0 = 0; j0 < piece; j0 += 16) {
-                f32x4 kv[4];
+            const float* kt = k + static_cast<int64_t>(t) * kv_width + kv_head * head_dim;
+            if (quads) {
+                const float* kp = kt + j_lo;
+                const float* qp = qsrc + j_lo;
+                for (int j0 = 0; j0 < piece; j0 += 16) {
+                    f32x4 kv[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (j0 + 4 * i < piece) {
-                        const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(kt + j0 + 4 * i));
-                        kv[i] = f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
-                                      __uint_as_float(raw[3])};
+                    for (int i = 0; i < 4; ++i)
+                        if (j0 + 4 * i < piece) {
+                            const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(kp + j0 + 4 * i));
+                            kv[i] = f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                          __uint_as_float(raw[3])};
+                        }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (j0 + 4 * i >= piece) break;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            dot = dot + static_cast<double>(qp[j0 + 4 * i + e]) * static_cast<double>(kv[i][e]);
                     }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (j0 + 4 * i >= piece) break;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        dot = dot + static_cast<double>(qp[j0 + 4 * i + e]) * static_cast<double>(kv[i][e]);
                 }
+            } else {
+                for (int j = j_lo; j < j_hi; ++j) dot = dot + static_cast<double>(qsrc[j]) * static_cast<double>(kt[j]);
             }
         }
         red[threadIdx.x] = dot;
@@ -410,42 +444,68 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
     }
 }
 
-// One workgroup per head: the splits' weights exp(m_s - M) once (FP64), then lane j's rescaled sum over the
-// splits in order, divided by the rescaled total.
+// One workgroup per head. The head's maximum M over the splits' maxima and the rescaled total
+// sum_s exp(m_s - M) l_s are workgroup reductions (each thread takes a strided share of the splits, then wave
+// shuffles); the splits' weights exp(m_s - M) are formed once per split into LDS. Output lane j is summed over
+// the splits in split order by `lanes_per` threads, each over a contiguous share of the splits with 16 loads
+// in flight, their partial sums then added in share order, and divided by the total.
 __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(const double* __restrict__ partial,
                                                                           int splits, int head_dim,
                                                                           float* __restrict__ out) {
-    __shared__ double weight[kMaxSplits];
-    __shared__ double total;
+    __shared__ double weight[kCombineWeights];
+    __shared__ double lane_part[kSplitThreads];
+    __shared__ double red4[kSplitThreads / 64];
     const int head = blockIdx.x;
-    const int stride = 2 + head_dim;
+    const int64_t stride = 2 + head_dim;
     const double* p = partial + static_cast<int64_t>(head) * splits * stride;
-    if (threadIdx.x < 64) {
-        double big = -INFINITY;
-        for (int s = 0; s < splits; ++s) big = fmax(big, p[s * stride]);
-        if (threadIdx.x < splits) {
-            const double* ps = p + threadIdx.x * stride;
-            weight[threadIdx.x] = ps[1] > 0 ? exp(ps[0] - big) : 0.0;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double t = 0;
-        for (int s = 0; s < splits; ++s) t = t + weight[s] * p[s * stride + 1];
-        total = t;
-    }
-    __syncthreads();
-    for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) {
+    double big = -INFINITY;
+    for (int s = threadIdx.x; s < splits; s += kSplitThreads) big = fmax(big, p[s * stride]);
+    big = wave_reduce_256(big, red4, true);
+    // Threads per output lane: up to 8 while the head's lanes fit the workgroup that many times.
+    int lanes_per = 1;
+    while (lanes_per < 8 && 2 * lanes_per * head_dim <= kSplitThreads) lanes_per *= 2;
+    const int width = kSplitThreads / lanes_per;
+    const int share = threadIdx.x / width;
+    const int chunks = (splits + kCombineWeights - 1) / kCombineWeights;
+    double total_part = 0;
+    double total = 0;
+    for (int j0 = 0; j0 < head_dim; j0 += width) {
+        const int j = j0 + threadIdx.x % width;
         double sum = 0;
-        for (int s0 = 0; s0 < splits; s0 += kCombineChunk) {  // in split order, a chunk of loads in flight
-            double o[kCombineChunk];
+        for (int chunk = 0; chunk < chunks; ++chunk) {
+            const int c0 = chunk * kCombineWeights, n = min(kCombineWeights, splits - c0);
+            if (chunks > 1 || j0 == 0) {  // this chunk's weights (once when they all fit)
+                __syncthreads();           // the previous chunk's weights are no longer read
+                for (int s = threadIdx.x; s < n; s += kSplitThreads) {
+                    const double* ps = p + (c0 + s) * stride;
+                    const double w = ps[1] > 0 ? exp(ps[0] - big) : 0.0;
+                    weight[s] = w;
+                    if (j0 == 0) total_part = total_part + w * ps[1];
+                }
+                __syncthreads();
+            }
+            if (j < head_dim) {
+                const int each = (n + lanes_per - 1) / lanes_per;
+                const int s_lo = min(n, share * each), s_hi = min(n, s_lo + each);
+                for (int s0 = s_lo; s0 < s_hi; s0 += kCombineChunk) {
+                    double o[kCombineChunk];
 #pragma unroll
-            for (int s = 0; s < kCombineChunk; ++s) o[s] = s0 + s < splits ? p[(s0 + s) * stride + 2 + j] : 0.0;
+                    for (int i = 0; i < kCombineChunk; ++i) o[i] = s0 + i < s_hi ? p[(c0 + s0 + i) * stride + 2 + j] : 0.0;
 #pragma unroll
-            for (int s = 0; s < kCombineChunk; ++s)
-                if (s0 + s < splits) sum = sum + weight[s0 + s] * o[s];
+                    for (int i = 0; i < kCombineChunk; ++i)
+                        if (s0 + i < s_hi) sum = sum + weight[s0 + i] * o[i];
+                }
+            }
         }
-        out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(sum / total);
+        if (j0 == 0) total = wave_reduce_256(total_part, red4, false);
+        lane_part[threadIdx.x] = sum;
+        __syncthreads();
+        if (share == 0 && j < head_dim) {
+            double lane_sum = lane_part[threadIdx.x];
+            for (int i = 1; i < lanes_per; ++i) lane_sum = lane_sum + lane_part[threadIdx.x + i * width];
+            out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(lane_sum / total);
+        }
+        __syncthreads();
     }
 }
 
@@ -541,24 +601,41 @@ hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k
     return hipGetLastError();
 }
 
-int attention_max_tokens() { return 6912; }  // FP64 scores in LDS: 54 KB, with the 8 KB reduction buffer and the 2 KB query 64 KB
-
-int attention_splits(int tokens, int head_dim) {
-    // At least 32 tokens per split, at most 32 splits (a 4096-token context: 128 tokens per split, 384
-    // workgroups for 12 heads; 16 and 64 splits measured slower there); heads wider than the staged query,
-    // or whose eighths are not whole 16-byte quads, stay whole.
-    if (head_dim > 512 || (head_dim & 31) != 0) return 1;
-    return std::max(1, std::min(kMaxSplits, (tokens + 31) / 32));
+int attention_splits(int tokens) {
+    // One workgroup per head up to 32 tokens; then at least 32 tokens per split and at most 32 splits (a
+    // 4096-token context: 128 tokens per split, 384 workgroups for 12 heads; 16 and 64 splits measured
+    // slower there), and beyond 65,536 tokens as many splits as keep each at most 2,048 tokens.
+    if (tokens <= 32) return 1;
+    int splits = std::min(kMinSplits, (tokens + 31) / 32);
+    splits = std::max(splits, (tokens + kMaxSplitTokens - 1) / kMaxSplitTokens);
+    return std::min(splits, kMaxSplitsPerLaunch);
 }
 
-size_t attention_scratch_bytes(int query_heads, int head_dim) {
-    return static_cast<size_t>(query_heads) * kMaxSplits * (2 + head_dim) * sizeof(double);
+size_t attention_scratch_bytes(int query_heads, int head_dim, int tokens) {
+    const int splits = std::max(kMinSplits, attention_splits(tokens));
+    return static_cast<size_t>(query_heads) * splits * (2 + head_dim) * sizeof(double);
+}
+
+namespace {
+
+size_t split_lds_bytes(int per, int head_dim) {
+    return static_cast<size_t>(per) * sizeof(double) +
+           (head_dim <= kStagedQuery ? static_cast<size_t>(head_dim) * sizeof(float) : 0);
+}
+
+}  // namespace
+
+bool attention_supported(int tokens, int head_dim) {
+    const int splits = attention_splits(tokens);
+    if (splits == 1) return true;
+    const int per = (tokens + splits - 1) / splits;
+    return split_lds_bytes(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
                             int head_dim, int tokens, float* out, double* scratch, hipStream_t stream) {
-    if (tokens > attention_max_tokens()) return hipErrorInvalidValue;
-    const int splits = attention_splits(tokens, head_dim);
+    if (!attention_supported(tokens, head_dim)) return hipErrorInvalidValue;
+    const int splits = attention_splits(tokens);
     if (splits == 1) {
         attention_kernel<<<query_heads, kAttnThreads, static_cast<size_t>(tokens) * sizeof(double), stream>>>(
             q, k, v, query_heads, kv_heads, head_dim, tokens, out);
@@ -566,8 +643,8 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
     }
     if (!scratch) return hipErrorInvalidValue;
     const int per = (tokens + splits - 1) / splits;
-    attention_split_kernel<<<dim3(query_heads, splits), kSplitThreads, static_cast<size_t>(per) * sizeof(double),
-                             stream>>>(q, k, v, query_heads, kv_heads, head_dim, tokens, scratch);
+    attention_split_kernel<<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes(per, head_dim), stream>>>(
+        q, k, v, query_heads, kv_heads, head_dim, tokens, per, scratch);
     attention_combine_kernel<<<query_heads, kSplitThreads, 0, stream>>>(scratch, splits, head_dim, out);
     return hipGetLastError();
 }

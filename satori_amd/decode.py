@@ -53,11 +53,20 @@ class DeviceDecoder:
         self.q_width = c.heads * c.head_dim
         self.kv_width = c.kv_heads * c.head_dim
         self._buffers = []
+        self.groups = []
+        self.final = None
+        self._folded = None  # groups with input transforms, made on first use
+        try:
+            self._build(context, config, layers, output)
+        except BaseException:
+            self.dispose()  # nothing half-built stays allocated or holds the caller's matrices
+            raise
 
+    def _build(self, context: HipContext, c: DecoderConfig, layers: list[dict], output: HipQuantizedMatrix) -> None:
         def buf(n):
             p = context.alloc(4 * n)
-            context.upload(p, np.zeros(n, np.float32))
             self._buffers.append(p)
+            context.upload(p, np.zeros(n, np.float32))
             return p
 
         self.residual, self.normed = buf(c.hidden), buf(c.hidden)
@@ -69,18 +78,18 @@ class DeviceDecoder:
         self.zero_kv = buf(self.kv_width)
         self.keys = [buf(c.max_tokens * self.kv_width) for _ in layers]
         self.values = [buf(c.max_tokens * self.kv_width) for _ in layers]
-        self.groups = []
         for m in layers:
-            self.groups.append({
-                "qkv": HipGroup(context, [m["q"], m["k"], m["v"]], [self.normed] * 3, [self.q, self.k, self.v], True),
-                "o": HipGroup(context, [m["o"]], [self.context_vec], [self.projected], True),
-                "gateup": HipGroup(context, [m["gate"], m["up"]], [self.normed] * 2, [self.gate, self.up], True),
-                "down": HipGroup(context, [m["down"]], [self.activated], [self.projected], True),
-            })
+            group = {}
+            self.groups.append(group)
+            group["qkv"] = HipGroup(context, [m["q"], m["k"], m["v"]], [self.normed] * 3, [self.q, self.k, self.v],
+                                    True)
+            group["o"] = HipGroup(context, [m["o"]], [self.context_vec], [self.projected], True)
+            group["gateup"] = HipGroup(context, [m["gate"], m["up"]], [self.normed] * 2, [self.gate, self.up], True)
+            group["down"] = HipGroup(context, [m["down"]], [self.activated], [self.projected], True)
         self.final = HipGroup(context, [output], [self.normed], [self.logits], True)
-        self._folded = None  # groups with input transforms, made on first use
-        # The split attention's workspace is allocated by its first call (for every token count of these
-        # heads): make that call now, so that a token can be captured before any has run.
+        # The split attention's workspace is allocated by its first call and covers every shorter prefix of
+        # these heads: make that call now at the cache capacity, so that a token can be captured before any
+        # has run.
         self.ops.grouped_attention(self.q, self.keys[0], self.values[0], c.heads, c.kv_heads, c.head_dim,
                                    c.max_tokens, self.context_vec)
 
@@ -174,10 +183,8 @@ class DeviceDecoder:
 
     def launches_per_token(self, fused: bool = True, folded: bool = False, position: int | None = None) -> int:
         """Kernel launches of one token. At a `position` whose prefix exceeds 32 tokens the attention is split
-        over several workgroups per head and combined by a second kernel (for head widths that are multiples
-        of 32 up to 512), one more launch per layer."""
-        c = self.cfg
-        split = position is not None and position + 1 > 32 and c.head_dim % 32 == 0 and c.head_dim <= 512
+        over several workgroups per head and combined by a second kernel, one more launch per layer."""
+        split = position is not None and position + 1 > 32
         extra = len(self.layers) if split else 0
         if folded:
             return 1 + 7 * len(self.layers) + 1 + extra
@@ -207,7 +214,10 @@ class DeviceDecoder:
         for g in self.groups:
             for gr in g.values():
                 gr.dispose()
-        self.final.dispose()
+        self.groups = []
+        if self.final is not None:
+            self.final.dispose()
+            self.final = None
         if self._folded is not None:
             for g in self._folded[0]:
                 for gr in g.values():

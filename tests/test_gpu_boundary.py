@@ -1,0 +1,353 @@
+"""GPU tests of the drop-in boundary's edges against the oracle, through the C ABI: non-finite activations
+where the reference takes them, integer K products of any width, grouped attention over long prefixes and
+odd head widths, split-attention workspaces per stream, and the operators' argument rules inside group
+input transforms.
+
+Bars: FP32 products |y_gpu - y_ref| <= 1e-5 * sum_i |w_i x_i| per finite row, and NaN / +Inf / -Inf exactly
+where the oracle has them; integer K products identical to the oracle (NaN where the oracle has NaN, every
+other output the same 32 bits); attention within one unit in the last place of the oracle.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import satori_amd as S
+from helpers import relative_bound, rng
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BQ = S.BlockQuantization
+
+
+def assert_same_specials_within(actual, expected, bound, what=""):
+    """NaN, +Inf and -Inf exactly where the oracle has them; finite outputs within the bound."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    assert np.array_equal(np.isnan(a), np.isnan(e)), f"{what}: NaN positions differ"
+    assert np.array_equal(np.isposinf(a), np.isposinf(e)), f"{what}: +Inf positions differ"
+    assert np.array_equal(np.isneginf(a), np.isneginf(e)), f"{what}: -Inf positions differ"
+    finite = np.isfinite(e)
+    err = np.abs(a[finite] - e[finite])
+    assert np.all(err <= np.asarray(bound)[finite]), f"{what}: max err {err.max() if err.size else 0}"
+
+
+def assert_bits_or_nan(actual, expected, what=""):
+    """Integer K products: NaN where the oracle has NaN, otherwise the same 32-bit pattern."""
+    a, e = np.asarray(actual, np.float32), np.asarray(expected, np.float32)
+    assert np.array_equal(np.isnan(a), np.isnan(e)), f"{what}: NaN positions differ"
+    keep = ~np.isnan(e)
+    bad = np.nonzero(a[keep].view(np.uint32) != e[keep].view(np.uint32))[0]
+    assert bad.size == 0, f"{what}: {bad.size} outputs differ, first {bad[:5]}"
+
+
+def _t2_payload(g, rows, columns, block):
+    blocks = -(-columns // block)
+    codes = g.integers(0, 3, size=(rows, blocks * block), dtype=np.uint8)
+    codes[:, columns:] = 0
+    return codes, blocks
+
+
+def _t2_pack(codes, scales, rows, blocks, block):
+    packed = codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6)
+    out = np.concatenate([scales.view(np.uint8).reshape(rows, blocks, 4), packed.reshape(rows, blocks, block // 4)],
+                         axis=2)
+    return np.ascontiguousarray(out.reshape(-1))
+
+
+# ---------------------------------------------------------------------------------------------
+# Non-finite activations
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_nonfinite_inputs_propagate_like_the_reference(context, block):
+    # Ternary2MatVec.Execute takes any activations (Ternary2MatVec.cs:30-36) and skips code-0 weights
+    # (:64-70), so a row is finite when its codes at the non-finite columns are all zero, +-Inf when it
+    # adds one infinity, NaN when it adds both or a NaN. Rows are built for each case.
+    g = rng(9090 + block)
+    rows, columns = 257, 1000
+    codes, blocks = _t2_payload(g, rows, columns, block)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    pos_inf, neg_inf, nan = 3, 517, 900
+    x[pos_inf], x[neg_inf], x[nan] = np.inf, -np.inf, np.nan
+    special = [pos_inf, neg_inf, nan]
+    for r in range(rows):
+        kind = r % 5
+        codes[r, special] = 0
+        if kind == 1:
+            codes[r, pos_inf] = 1       # +Inf
+        elif kind == 2:
+            codes[r, pos_inf] = 2       # -Inf
+        elif kind == 3:
+            codes[r, [pos_inf, neg_inf]] = 1  # +Inf + -Inf: NaN
+        elif kind == 4:
+            codes[r, nan] = 1 + r % 2   # NaN
+    scales = g.uniform(0.01, 2.0, size=(rows, blocks)).astype(np.float32)
+    payload = _t2_pack(codes, scales, rows, blocks, block)
+    m = context.create_ternary2(rows, columns, block, payload)
+    y = np.zeros(rows, np.float32)
+    m.execute(x, y)  # accepted: no ArgumentException for the Ternary2 surface
+    m.dispose()
+    expected = O.t2_matvec_scalar(payload, rows, columns, block, x)
+    wq = O.t2_dequantize(payload, rows, columns, block)
+    xf = np.where(np.isfinite(x), x, 0).astype(np.float32)
+    assert_same_specials_within(y, expected, relative_bound(wq, xf), f"Ternary2 B{block}")
+    assert np.isfinite(y[0::5]).all() and np.isposinf(y[1::5]).all() and np.isnan(y[3::5]).all()
+
+
+def test_gguf_plugin_seam_still_rejects_nonfinite_inputs(context):
+    # IQuantizedMatrix.Execute of a GPU backend rejects them (VulkanQ8Matrix.cs:82-83); the batched surface
+    # (QuantizedMatVec.ExecuteBatch) takes them.
+    g = rng(31)
+    data = S.quantize_weights((g.standard_normal((8, 64)) * 0.1).astype(np.float32), 8, 64, BQ.Q8_0)
+    m = context.create(data, S.QuantizedMatrixShape(8, 64, BQ.Q8_0))
+    x = np.ones(64, np.float32)
+    x[5] = np.nan
+    sentinel = np.full(8, 7.0, np.float32)
+    with pytest.raises(S.ArgumentException):
+        m.execute(x, sentinel)
+    assert np.all(sentinel == 7.0)
+    m.execute_batch(x, 1, sentinel)
+    assert np.isnan(sentinel).any()
+    m.dispose()
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+def test_legacy_batch_nonfinite_inputs_propagate(context, fmt):
+    # QuantizedMatVec.ExecuteBatch float path with non-finite activations: a zero weight times an infinity
+    # is NaN in the reference's products too (QuantizedMatVec.cs:221-281), so the specials land where the
+    # oracle's do; finite rows within the bound.
+    g = rng(404 + int(fmt))
+    rows, columns, positions = 96, 512, 3
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    w[:, 40:48] = 0  # rows whose codes are zero at the non-finite columns
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    x[0, 44] = np.inf       # only zero weights: NaN in every row (0 * Inf)
+    x[1, 100] = -np.inf
+    x[2, 300] = np.nan
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.zeros(positions * rows, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    m.dispose()
+    wq = O.decode_matrix(data, rows, columns, int(fmt))
+    for p in range(positions):
+        expected = O.q_matvec_scalar(data, rows, columns, int(fmt), x[p])
+        xf = np.where(np.isfinite(x[p]), x[p], 0).astype(np.float32)
+        assert_same_specials_within(y[p * rows:(p + 1) * rows], expected, relative_bound(wq, xf), f"{fmt.name} p{p}")
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("positions", [1, 3, 20])
+def test_k_batch_nonfinite_inputs_match_the_reference_bits(context, fmt, positions):
+    # Q8KCodec.QuantizeBlock with infinities and NaNs (Q8KCodec.cs:44-76): NaN never wins the maximum, an
+    # all-NaN-or-zero block quantizes to zero and is skipped, an infinite maximum gives inverse -0, codes 0
+    # and scale -Inf, whose block term is NaN. The integer kernel (1-15 positions) and the matrix-core
+    # kernel (16+) both follow it.
+    g = rng(77 + 10 * int(fmt) + positions)
+    rows, columns = 200, 2048
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    for p in range(positions):
+        kind = p % 4
+        if kind == 0:
+            x[p, 256 + 7] = np.nan                       # NaN inside a finite block
+        elif kind == 1:
+            x[p, 512:768] = 0
+            x[p, 512 + 3] = np.nan                       # NaN in an otherwise zero block: a zero block
+        elif kind == 2:
+            x[p, 1024 + 9] = np.inf                      # infinite block maximum
+        else:
+            x[p, 1536 + 1], x[p, 1536 + 2] = -np.inf, np.inf
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.zeros(positions * rows, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    m.dispose()
+    for p in range(positions):
+        expected = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x[p]))
+        assert_bits_or_nan(y[p * rows:(p + 1) * rows], expected, f"{fmt.name} position {p}")
+    for p in range(min(positions, 4)):
+        q = S.Q8KCodec.quantize_row(x[p], context)
+        assert np.array_equal(q, O.q8k_quantize_row(x[p])), f"Q8_K bytes, position {p}"
+
+
+# ---------------------------------------------------------------------------------------------
+# Integer K products of any width (QuantizedKAvx2Kernel.ExecuteQuantizedTiled has no width limit)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("rows,columns,positions", [(300, 29696, 1), (300, 29696, 3), (130, 29696, 16),
+                                                    (70, 65536, 1), (33, 57344, 2)])
+def test_k_batch_wide_rows_are_bit_exact(context, fmt, rows, columns, positions):
+    # Rows wider than one staging of the Q8_K row (112 blocks = 28,672 columns) are summed chunk by chunk in
+    # block order; 29,696 (116 blocks), 57,344 (two whole chunks) and 65,536 (256 blocks, a ragged last chunk).
+    g = rng(5150 + columns + rows + int(fmt))
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    x[0, 256 * 113:256 * 114] = 0  # a zero block in the second chunk is skipped
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.zeros(positions * rows, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    m.dispose()
+    for p in range(positions):
+        expected = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x[p]))
+        got = y[p * rows:(p + 1) * rows]
+        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), f"position {p}"
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+def test_wide_group_with_input_transform_equals_operator_then_group(context, fmt):
+    # A decode-step group at 29,696 columns computing RmsNorm(a + b) inside its launch equals the operator
+    # followed by the plain group (and the oracle's projection of the operator's output) bit for bit.
+    g = rng(8181 + int(fmt))
+    columns, rows = 29696, [64, 40]
+    datas = [S.quantize_weights((g.standard_normal((r, columns)) * 0.02).astype(np.float32), r, columns, fmt)
+             for r in rows]
+    mats = [context.create(d, S.QuantizedMatrixShape(r, columns, fmt)) for d, r in zip(datas, rows)]
+    a, b = (g.standard_normal(columns).astype(np.float32) for _ in range(2))
+    w = g.uniform(0.5, 1.5, columns).astype(np.float32)
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    da, db, dw = dev(a), dev(b), dev(w)
+    dsum, dx = dev(a.copy()), dev(np.zeros(columns, np.float32))
+    plain_out = [dev(np.zeros(r, np.float32)) for r in rows]
+    fused_out = [dev(np.zeros(r, np.float32)) for r in rows]
+    plain = S.HipGroup(context, mats, [dx, dx], plain_out, True)
+    fused = S.HipGroup(context, mats, [dx, dx], fused_out, True)
+    try:
+        ops = S.DeviceOps(context)
+        ops.add_rms_norm(dsum, db, dw, 1e-6, columns, dx)
+        plain.execute()
+        fused.set_input_add_rms_norm(da, db, dw, 1e-6)
+        fused.execute()
+        normed = context.download(np.zeros(columns, np.float32), dx)
+        for k, r in enumerate(rows):
+            want = context.download(np.zeros(r, np.float32), plain_out[k])
+            got = context.download(np.zeros(r, np.float32), fused_out[k])
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"member {k}"
+            expected = O.qk_matvec_quantized_avx2(datas[k], r, columns, int(fmt), O.q8k_quantize_row(normed))
+            assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), f"member {k} vs oracle"
+    finally:
+        plain.dispose()
+        fused.dispose()
+        for p in buffers:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
+def test_group_input_transform_rejects_nonpositive_epsilon(context):
+    # RmsNorm's rule (TransformerOps.cs:17) holds inside a group's input transform: epsilon must be positive.
+    data = S.quantize_weights(np.zeros((4, 256), np.float32), 4, 256, BQ.Q4_K)
+    m = context.create(data, S.QuantizedMatrixShape(4, 256, BQ.Q4_K))
+    bufs = [context.alloc(4 * 256) for _ in range(4)]
+    group = S.HipGroup(context, [m], [bufs[0]], [bufs[1]], True)
+    try:
+        for eps in (0.0, -1e-6, float("nan"), float("inf")):
+            with pytest.raises(S.ArgumentOutOfRangeException):
+                group.set_input_add_rms_norm(bufs[2], bufs[3], bufs[3], eps)
+        group.set_input_add_rms_norm(bufs[2], bufs[3], bufs[3], 1e-6)
+    finally:
+        group.dispose()
+        for p in bufs:
+            context.free(p)
+        m.dispose()
+
+
+# ---------------------------------------------------------------------------------------------
+# Grouped attention: any prefix length and head width (TransformerOps.cs:135-179 has no cap)
+# ---------------------------------------------------------------------------------------------
+
+def _within_ulp(actual, expected, name, ulps=1):
+    a, e = np.asarray(actual, np.float32), np.asarray(expected, np.float32)
+    spacing = np.spacing(np.maximum(np.abs(a), np.abs(e)).astype(np.float32)).astype(np.float64)
+    err = np.abs(a.astype(np.float64) - e.astype(np.float64))
+    assert np.all(err <= ulps * spacing), f"{name}: max err {err.max()} at {np.argmax(err - ulps * spacing)}"
+
+
+@pytest.mark.parametrize("tokens", [6913, 8192, 16384, 32768, 70001])
+def test_attention_long_prefixes_match_oracle(context, tokens):
+    # Qwen-1.5B heads (12 query, 2 key/value, 128 lanes): 32 splits up to 65,536 tokens, then splits of at
+    # most 2,048 tokens (70,001 tokens: 35 splits).
+    g = rng(tokens)
+    q = g.standard_normal(12 * 128).astype(np.float32)
+    keys = (g.standard_normal(tokens * 256) * 0.3).astype(np.float32)
+    values = g.standard_normal(tokens * 256).astype(np.float32)
+    out = np.zeros(12 * 128, np.float32)
+    S.TransformerOps.grouped_attention(q, keys, values, 12, 2, 128, tokens, out, context)
+    _within_ulp(out, O.grouped_attention(q, keys, values, 12, 2, 128, tokens), f"attention {tokens}")
+
+
+@pytest.mark.parametrize("head_dim,tokens,query_heads,kv_heads", [(80, 300, 14, 2), (80, 7000, 4, 1),
+                                                                  (24, 100, 3, 3), (1024, 100, 4, 2),
+                                                                  (8320, 40, 2, 1), (130, 33, 6, 3)])
+def test_attention_odd_head_widths_match_oracle(context, head_dim, tokens, query_heads, kv_heads):
+    # Head widths whose eighths are not whole 16-byte quads (80, 24, 130), wider than one workgroup's lanes
+    # (1024) and wider than the staged query (8,320 lanes: read from global memory).
+    g = rng(head_dim * 7 + tokens)
+    q = g.standard_normal(query_heads * head_dim).astype(np.float32)
+    keys = (g.standard_normal(tokens * kv_heads * head_dim) * 0.2).astype(np.float32)
+    values = g.standard_normal(tokens * kv_heads * head_dim).astype(np.float32)
+    out = np.zeros(query_heads * head_dim, np.float32)
+    S.TransformerOps.grouped_attention(q, keys, values, query_heads, kv_heads, head_dim, tokens, out, context)
+    _within_ulp(out, O.grouped_attention(q, keys, values, query_heads, kv_heads, head_dim, tokens),
+                f"attention {head_dim} x {tokens}")
+
+
+def _hip():
+    rt = ctypes.CDLL("libamdhip64.so.7")
+    rt.hipStreamCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+    rt.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    rt.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    return rt
+
+
+def test_split_attentions_on_two_streams_do_not_share_a_workspace(context):
+    # Two split attentions enqueued back to back on two streams (default priority) run concurrently; each
+    # stream has its own partials, so both results equal the oracle's.
+    S._ffi.lib()
+    rt = _hip()
+    streams = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for s in streams:
+        assert rt.hipStreamCreateWithFlags(ctypes.byref(s), 1) == 0  # non-blocking, default priority
+    g = rng(2468)
+    tokens = [3000, 5000]
+    cases, buffers = [], []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    try:
+        for t in tokens:
+            q = g.standard_normal(12 * 128).astype(np.float32)
+            k = (g.standard_normal(t * 256) * 0.3).astype(np.float32)
+            v = g.standard_normal(t * 256).astype(np.float32)
+            cases.append((q, k, v, t, dev(q), dev(k), dev(v), dev(np.zeros(12 * 128, np.float32))))
+        ops = S.DeviceOps(context)
+        for repeat in range(3):
+            for (q, k, v, t, dq, dk, dv, do), s in zip(cases, streams):
+                ops.grouped_attention(dq, dk, dv, 12, 2, 128, t, do, stream=s.value)
+            for s in streams:
+                assert rt.hipStreamSynchronize(s) == 0
+            for q, k, v, t, dq, dk, dv, do in cases:
+                out = context.download(np.zeros(12 * 128, np.float32), do)
+                _within_ulp(out, O.grouped_attention(q, k, v, 12, 2, 128, t), f"stream attention {t} #{repeat}")
+    finally:
+        for s in streams:
+            rt.hipStreamDestroy(s)
+        for p in buffers:
+            context.free(p)

@@ -1206,8 +1206,8 @@ def test_operators_match_oracle_at_decode_sizes(context):
         out = np.zeros(12 * 128, np.float32)
         T.grouped_attention(q, keys, values, 12, 2, 128, tokens, out, context)
         _within_ulp(out, O.grouped_attention(q, keys, values, 12, 2, 128, tokens), f"attention {tokens}")
-    # Split prefixes at other head widths: 96 (eighths of 12 lanes), 256, and 80 (not split: rows are not
-    # whole eighths of 16-byte quads), with 7 query heads per key/value head.
+    # Split prefixes at other head widths: 96 (eighths of 12 lanes), 256, and 80 (eighths that are not whole
+    # 16-byte quads: lane-by-lane key loads), with 7 query heads per key/value head.
     for head_dim, tokens in ((96, 100), (256, 65), (80, 300)):
         qq = g.standard_normal(14 * head_dim).astype(np.float32)
         keys = g.standard_normal(tokens * 2 * head_dim).astype(np.float32)
@@ -1239,9 +1239,12 @@ def test_operator_extremes_and_argument_errors(context):
     with pytest.raises(S.ArgumentException):
         T.grouped_attention(np.zeros(32, np.float32), np.zeros(48, np.float32), np.zeros(48, np.float32), 4, 3, 8, 3,
                             np.zeros(32, np.float32), context)
-    with pytest.raises(S.NotSupportedException):
-        T.attention(np.zeros(2, np.float32), np.zeros(2 * 6913, np.float32), np.zeros(2 * 6913, np.float32), 2, 6913,
-                    np.zeros(2, np.float32), context)
+    # No prefix cap (TransformerOps.cs:140-179): 6,913 tokens of one two-lane head run split, like any length.
+    keys = np.linspace(-1, 1, 2 * 6913).astype(np.float32)
+    out = np.zeros(2, np.float32)
+    T.attention(np.array([0.5, -0.25], np.float32), keys, keys[::-1].copy(), 2, 6913, out, context)
+    _within_ulp(out, O.grouped_attention(np.array([0.5, -0.25], np.float32), keys, keys[::-1].copy(), 1, 1, 2, 6913),
+                "attention 6913")
     # Partial overlap of device ranges is rejected before anything runs (TransformerOps.cs:7-11).
     import ctypes
     from satori_amd import _ffi
