@@ -22,6 +22,10 @@ The same line carries, labelled:
   prefill:   the same model's projections over 512 positions (ExecuteBatch in 256-position chunks);
              tokens/s and int8 TOP/s;
   loading:   upload rates of a GGUF tensor (device scale check), an STQ2 file and an STB1 bitplane file;
+  host_call: the drop-in host-buffer call on one matrix (copies, scan, launch, synchronisation), per format;
+  parity:    before anything of a workload is timed, the launches it times are checked against the oracle
+             (every copy of a grouped case, every launch of the decode step, sampled prefill positions); a
+             mismatch stops the benchmark with a non-zero exit before timing;
   roofline:  for the headline kernel, from HIP events on the launch stream;
   cpu_baseline: the restated reference AVX2 kernel (Ternary2Avx2Kernel) on one host core; each format's
              entry also carries its own restated reference AVX2 path timed on one core (cpu_gbs).
@@ -65,10 +69,18 @@ class HipEvents:
         self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
 
+        self.created = []
+
     def event(self):
         e = ctypes.c_void_p()
         assert self.rt.hipEventCreate(ctypes.byref(e)) == 0
+        self.created.append(e)
         return e
+
+    def close(self):
+        for e in self.created:
+            self.rt.hipEventDestroy(e)
+        self.created = []
 
     def record(self, event, stream):
         assert self.rt.hipEventRecord(event, ctypes.c_void_p(stream)) == 0
@@ -107,6 +119,7 @@ class Case:
         self.copies = copies or max(1, math.ceil(ROTATION_BYTES / payload_bytes))
         first = create()
         self.mats = [first] + [first.clone() for _ in range(self.copies - 1)]
+        self.x = x
         self.dx = ctx.alloc(x.nbytes)
         ctx.upload(self.dx, x)
         self.dy = [ctx.alloc(4 * rows) for _ in range(self.copies)]
@@ -165,6 +178,53 @@ def progress(message: str) -> None:
     print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
+class ParityError(RuntimeError):
+    """A timed launch's outputs disagree with the oracle: the benchmark stops before timing."""
+
+
+def fp32_bound(data, rows, columns, fmt, x, block=None) -> np.ndarray:
+    """1e-5 * sum_i |w_i x_i| per row (FP64) on the decoded weights (the oracle decodes them)."""
+    from oracle import oracle as O
+
+    ax = np.abs(x.astype(np.float64))
+    if fmt is None:
+        return 1e-5 * (np.abs(O.t2_dequantize(data, rows, columns, block).astype(np.float64)) @ ax)
+    row_bytes = data.size // rows
+    return 1e-5 * np.array([np.abs(O.q_decode_row(data[r * row_bytes:(r + 1) * row_bytes], columns, int(fmt))) @ ax
+                            for r in range(rows)])
+
+
+def check_case(ctx, case: Case, data, rows, columns, fmt, x, quantized) -> dict:
+    """Parity of the launch that is timed, before it is timed (the reference benchmark validates before it
+    measures, benchmarks/Satori.Benchmarks/Program.cs:38-61): one grouped launch, then every copy's output
+    against the oracle (checker only): Ternary2, Q8_0 and Q4_0 within 1e-5 * sum|w x| per row of the scalar
+    restatement, K formats on the Q8_K path identical to the ExecuteQuantizedTiled composition."""
+    from oracle import oracle as O
+
+    if fmt is None:
+        expected, bound = O.t2_matvec_scalar(data, rows, columns, quantized, x), fp32_bound(data, rows, columns,
+                                                                                            None, x, quantized)
+    elif quantized:
+        expected, bound = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x)), None
+    else:
+        expected, bound = O.q_matvec_scalar(data, rows, columns, int(fmt), x), fp32_bound(data, rows, columns, fmt, x)
+    case.run_group()
+    ctx.synchronize()
+    worst = 0.0
+    for i, dy in enumerate(case.dy):
+        y = ctx.download(np.zeros(rows, np.float32), dy)
+        if bound is None:
+            if not np.array_equal(y.view(np.uint32), expected.view(np.uint32)):
+                raise ParityError(f"{case.name}: copy {i} differs from the oracle")
+        else:
+            ratio = np.abs(y.astype(np.float64) - expected) / np.maximum(bound, 1e-300)
+            if not np.all(np.isfinite(y)) or not np.all(ratio <= 1.0):
+                raise ParityError(f"{case.name}: copy {i} outside 1e-5 * sum|w x| (worst ratio {ratio.max()})")
+            worst = max(worst, float(ratio.max()))
+    return {"parity_checked": True, "parity_copies": case.copies,
+            "parity": "bit-exact" if bound is None else f"max |err| / (1e-5 sum|w x|) = {worst:.3g}"}
+
+
 def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     progress(f"{case.name}: {case.copies} copies x {case.payload_bytes} B")
     warm_up(ctx, case.run_group, 0.25)
@@ -188,6 +248,31 @@ def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     return out
 
 
+def host_call_latency(case: Case, calls: int = 200) -> dict:
+    """The drop-in host call on one resident matrix, host buffers in and out (satori_hip_matvec: input copy,
+    finiteness scan where the surface has one, launch, output copy, stream synchronisation): median and
+    minimum wall time per call. K formats also through ExecuteBatch at one position (the Q8_K integer product,
+    the decode path)."""
+    m, x = case.mats[0], case.x
+    y = np.zeros(case.rows, np.float32)
+
+    def timed(fn):
+        fn()
+        samples = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            fn()
+            samples.append(time.perf_counter() - t0)
+        samples.sort()
+        return samples[len(samples) // 2] * 1e6, samples[0] * 1e6
+
+    out = {}
+    out["host_call_us_median"], out["host_call_us_min"] = timed(lambda: m.execute(x, y))
+    if case.quantized:
+        out["host_call_batch1_us_median"], out["host_call_batch1_us_min"] = timed(lambda: m.execute_batch(x, 1, y))
+    return out
+
+
 class DecodeModel:
     """A Qwen-1.5B-shaped model's projections: 28 layers of q 1536x1536, k and v 256x1536, o 1536x1536, gate and
     up 8960x1536 in Q4_K, down 1536x8960 in Q6_K, then the output projection 151936x1536 in Q6_K (197
@@ -200,9 +285,12 @@ class DecodeModel:
         d, kv, ffn, vocab = self.D, self.KV, self.FFN, self.VOCAB
         self.roles = {"q": (d, d, BQ.Q4_K), "k": (kv, d, BQ.Q4_K), "v": (kv, d, BQ.Q4_K), "o": (d, d, BQ.Q4_K),
                       "gate": (ffn, d, BQ.Q4_K), "up": (ffn, d, BQ.Q4_K), "down": (d, ffn, BQ.Q6_K)}
+        self.shapes = dict(self.roles, output=(vocab, d, BQ.Q6_K))
         first = {}
+        self.host = {}  # the payloads, for the parity check
         for name, (r, c, fmt) in self.roles.items():
             data, _ = make_gguf(fmt, r, c)
+            self.host[name] = data
             first[name] = ctx.create(data, S.QuantizedMatrixShape(r, c, fmt))
         # Output projection: rows of a 4096-row random Q6_K matrix repeated to 151,936 rows (rows are
         # independent byte ranges, so the payload is a valid matrix of that shape).
@@ -210,6 +298,7 @@ class DecodeModel:
         row_bytes = base.size // 4096
         tiled = np.tile(base.reshape(4096, row_bytes), (-(-vocab // 4096), 1))[:vocab].reshape(-1)
         self.output = ctx.create(tiled, S.QuantizedMatrixShape(vocab, d, BQ.Q6_K))
+        self.host["output"] = tiled
         self.layers = [{name: (first[name] if layer == 0 else first[name].clone()) for name in self.roles}
                        for layer in range(self.LAYERS)]
         payload = sum(r * (c // 256) * (144 if fmt == BQ.Q4_K else 210) for r, c, fmt in self.roles.values())
@@ -238,17 +327,36 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
     the path: their outputs are fixed random vectors. Also timed: the same groups launched eagerly."""
     d, ffn, vocab = model.D, model.FFN, model.VOCAB
     g = rng(2026)
-    h, attn, h2 = (model.device(g.standard_normal(d).astype(np.float32)) for _ in range(3))
-    act = model.device(g.standard_normal(ffn).astype(np.float32))
+    host_in = {"h": g.standard_normal(d).astype(np.float32), "attn": g.standard_normal(d).astype(np.float32),
+               "h2": g.standard_normal(d).astype(np.float32), "act": g.standard_normal(ffn).astype(np.float32)}
+    h, attn, h2, act = (model.device(host_in[k]) for k in ("h", "attn", "h2", "act"))
     out = {name: model.device(np.zeros(r, np.float32)) for name, (r, _, _) in model.roles.items()}
     logits = model.device(np.zeros(vocab, np.float32))
-    groups = []
+    out["output"] = logits
+    groups, members = [], []
     for m in model.layers:
         groups.append(S.HipGroup(ctx, [m["q"], m["k"], m["v"]], [h] * 3, [out["q"], out["k"], out["v"]], True))
         groups.append(S.HipGroup(ctx, [m["o"]], [attn], [out["o"]], True))
         groups.append(S.HipGroup(ctx, [m["gate"], m["up"]], [h2] * 2, [out["gate"], out["up"]], True))
         groups.append(S.HipGroup(ctx, [m["down"]], [act], [out["down"]], True))
+        members += [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
     groups.append(S.HipGroup(ctx, [model.output], [h], [logits], True))
+    members.append(("output",))
+    # Parity before timing: every launch of the step, one at a time, against the oracle (checker only).
+    from oracle import oracle as O
+    feeds = {"q": "h", "k": "h", "v": "h", "o": "attn", "gate": "h2", "up": "h2", "down": "act", "output": "h"}
+    expected = {}
+    for name, (r, c, fmt) in model.shapes.items():
+        expected[name] = O.qk_matvec_quantized_avx2(model.host[name], r, c, int(fmt),
+                                                    O.q8k_quantize_row(host_in[feeds[name]]))
+    for grp, names in zip(groups, members):
+        for name in names:
+            ctx.upload(out[name], np.full(model.shapes[name][0], np.nan, np.float32))
+        grp.execute()
+        for name in names:
+            y = ctx.download(np.zeros(model.shapes[name][0], np.float32), out[name])
+            if not np.array_equal(y.view(np.uint32), expected[name].view(np.uint32)):
+                raise ParityError(f"decode step: {name} differs from the oracle")
 
     def eager():
         for grp in groups:
@@ -267,6 +375,8 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
         grp.dispose()
     return {
         "model": "Qwen-1.5B-shaped decode step, random-init Q4_K/Q6_K weights, batch 1",
+        "parity_checked": True,
+        "parity": f"each of the {len(groups)} launches of one step bit-exact against the oracle before timing",
         "projections_per_token": 28 * 7 + 1,
         "kernel_launches_per_token": len(groups),
         "bytes_per_token": model.token_bytes,
@@ -352,6 +462,35 @@ def decode_token(ctx, events, model: DecodeModel, steps: int, warmup: int, posit
     }
 
 
+def token_eager(ctx, events, model: DecodeModel, steps: int, warmup: int, positions=(511, 4095)) -> dict:
+    """The whole decode token (folded operator sequence, as decode_token captures it) launched eagerly at the
+    given positions, for kernel statistics under a profiler (no graph)."""
+    from satori_amd.decode import DecoderConfig, DeviceDecoder
+    g = rng(2029)
+    out = {}
+    vectors = [{"attn_norm": model.device(g.uniform(0.5, 1.5, model.D).astype(np.float32)),
+                "ffn_norm": model.device(g.uniform(0.5, 1.5, model.D).astype(np.float32)),
+                "q_bias": model.device((g.standard_normal(model.D) * 0.1).astype(np.float32)),
+                "k_bias": model.device((g.standard_normal(model.KV) * 0.1).astype(np.float32)),
+                "v_bias": model.device((g.standard_normal(model.KV) * 0.1).astype(np.float32))}
+               for _ in model.layers]
+    out_norm = model.device(g.uniform(0.5, 1.5, model.D).astype(np.float32))
+    for position in positions:
+        cfg = DecoderConfig(hidden=model.D, heads=12, kv_heads=2, head_dim=128, ffn=model.FFN, epsilon=1e-6,
+                            rope_base=1e6, max_tokens=position + 1)
+        dec = DeviceDecoder(ctx, cfg, model.layers, vectors, out_norm, model.output, model.output)
+        for layer in range(len(model.layers)):
+            prefix = (g.standard_normal((cfg.max_tokens, model.KV)) * 0.5).astype(np.float32)
+            ctx.upload(dec.keys[layer], prefix)
+            ctx.upload(dec.values[layer], prefix[::-1].copy())
+        ms = time_launches(ctx, events, lambda: dec.enqueue(151, position, folded=True), steps, warmup)
+        out[f"position_{position}"] = {"eager_us_per_token": ms * 1e3,
+                                       "kernel_launches_per_token": dec.launches_per_token(folded=True,
+                                                                                           position=position)}
+        dec.dispose()
+    return out
+
+
 def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions: int = 512) -> dict:
     """The projections of a 512-token prefill: every layer projection over all positions in chunks of 256
     positions (the reference's chunk, and the ABI's limit for K formats), q/k/v and gate/up each as one
@@ -360,8 +499,11 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     counts 2 int8 operations per weight per position."""
     d, ffn = model.D, model.FFN
     g = rng(2027)
-    h, attn, h2 = (model.device(g.standard_normal(positions * d).astype(np.float32)) for _ in range(3))
-    act = model.device(g.standard_normal(positions * ffn).astype(np.float32))
+    host_in = {"h": g.standard_normal(positions * d).astype(np.float32),
+               "attn": g.standard_normal(positions * d).astype(np.float32),
+               "h2": g.standard_normal(positions * d).astype(np.float32),
+               "act": g.standard_normal(positions * ffn).astype(np.float32)}
+    h, attn, h2, act = (model.device(host_in[k]) for k in ("h", "attn", "h2", "act"))
     out = {name: model.device(np.zeros(positions * r, np.float32)) for name, (r, _, _) in model.roles.items()}
     logits = model.device(np.zeros(model.VOCAB, np.float32))
     inputs = {"q": h, "k": h, "v": h, "o": attn, "gate": h2, "up": h2, "down": act}
@@ -392,6 +534,23 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
         model.output.execute_batch_device(h + 4 * (positions - 1) * d, 1, logits)
 
     run()
+    # Parity before timing (checker only): the last layer's outputs at sampled positions of both chunks
+    # (tile edges 0/31/32, chunk edges 255/256, the last position) and the output projection, bit-exact.
+    from oracle import oracle as O
+    feeds = {"q": "h", "k": "h", "v": "h", "o": "attn", "gate": "h2", "up": "h2", "down": "act"}
+    sampled = [p for p in (0, 1, 31, 32, 100, 255, 256, 257, 300, 400, 511) if p < positions]
+    ctx.synchronize()
+    for name, (r, c, fmt) in model.roles.items():
+        y = ctx.download(np.zeros(positions * r, np.float32), out[name]).reshape(positions, r)
+        for p in sampled:
+            x = host_in[feeds[name]][p * c:(p + 1) * c]
+            want = O.qk_matvec_quantized_avx2(model.host[name], r, c, int(fmt), O.q8k_quantize_row(x))
+            if not np.array_equal(y[p].view(np.uint32), want.view(np.uint32)):
+                raise ParityError(f"prefill: {name} at position {p} differs from the oracle")
+    want = O.qk_matvec_quantized_avx2(model.host["output"], model.VOCAB, d, int(BQ.Q6_K),
+                                      O.q8k_quantize_row(host_in["h"][(positions - 1) * d:positions * d]))
+    if not np.array_equal(ctx.download(np.zeros(model.VOCAB, np.float32), logits).view(np.uint32), want.view(np.uint32)):
+        raise ParityError("prefill: output projection differs from the oracle")
     ms = time_launches(ctx, events, run, steps, warmup)
     for qkv, gateup, *_ in plan:
         qkv.dispose()
@@ -400,6 +559,8 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     ops = 2.0 * weights * positions + 2.0 * model.VOCAB * d
     return {
         "positions": positions,
+        "parity_checked": True,
+        "parity": f"last layer at positions {sampled} and the output projection bit-exact against the oracle",
         "ms": ms,
         "tokens_per_s": positions / (ms * 1e-3),
         "int8_tops": ops / (ms * 1e-3) / 1e12,
@@ -536,6 +697,7 @@ def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
     """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample."""
     from oracle import oracle as O
 
+    host = host_cpu()  # before pinning: the CPUs available to the process
     core = pin_one_core()
     y = np.zeros(rows, np.float32)
     O.t2_matvec_avx2(payload, rows, columns, block, x, y)  # warm
@@ -547,22 +709,35 @@ def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
         samples.append(time.perf_counter() - t0)
         iterations += 1
     elapsed = time.perf_counter() - start
+    return {
+        "value": payload.size * iterations / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "host_model": host["model"],
+        "host_logical_cpus": host["logical_cpus"],
+        "host_cpus_available": host["available"],
+        "sample": (f"restated reference AVX2 Ternary2Avx2Kernel (oracle/satori_oracle_avx2.c, -O3 -mavx2 -mfma) "
+                   f"on the same 4096x4096 B128 payload and x, {iterations} MatVecs over {elapsed:.1f} s, "
+                   f"1 thread pinned to core {core}; min {min(samples) * 1e3:.3f} ms, "
+                   f"median {sorted(samples)[len(samples) // 2] * 1e3:.3f} ms; host: {host['model']}, "
+                   f"{host['logical_cpus']} logical CPUs ({host['available']} available to this process)"),
+    }
+
+
+def host_cpu() -> dict:
+    """The host CPU's model name (as lscpu prints it) and logical CPU counts."""
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
     except OSError:
         pass
-    return {
-        "value": payload.size * iterations / elapsed / 1e9,
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": (f"restated reference AVX2 Ternary2Avx2Kernel (oracle/satori_oracle_avx2.c, -O3 -mavx2 -mfma) "
-                   f"on the same 4096x4096 B128 payload and x, {iterations} MatVecs over {elapsed:.1f} s, "
-                   f"1 thread pinned to core {core}; min {min(samples) * 1e3:.3f} ms, "
-                   f"median {sorted(samples)[len(samples) // 2] * 1e3:.3f} ms; host: {model}"),
-    }
+    try:
+        available = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        available = None
+    return {"model": model, "logical_cpus": os.cpu_count(), "available": available}
 
 
 def other_formats(ctx):
@@ -612,6 +787,9 @@ def main() -> int:
                     help="only the 512-position prefill (steps and warmup as given), for rocprofv3")
     ap.add_argument("--profile-decode", action="store_true",
                     help="only the decode step, launched eagerly (steps and warmup as given), for rocprofv3")
+    ap.add_argument("--profile-token", action="store_true",
+                    help="only the whole decode token at positions 511 and 4095, launched eagerly (steps and "
+                         "warmup as given), for rocprofv3")
     ap.add_argument("--profile-formats", action="store_true",
                     help="only the grouped launches of every format (steps and warmup as given), for rocprofv3")
     args = ap.parse_args()
@@ -620,13 +798,28 @@ def main() -> int:
               "(multi-GPU row sharding is design-only); run with --gpus 1", file=sys.stderr)
         return 2
 
+    # The context and the events are released before the process exits: the stream and the device work are
+    # torn down by the library, not by the runtime's exit path (a profiler attached to the process flushes
+    # its buffers at exit).
     ctx = S.HipContext(0)
     events = HipEvents()
+    try:
+        return run(args, ctx, events)
+    finally:
+        events.close()
+        try:
+            ctx.dispose()
+        except S.SatoriError as e:
+            print(f"bench.py: context not released: {e}", file=sys.stderr)
 
-    if args.profile_prefill or args.profile_decode:
+
+def run(args, ctx, events) -> int:
+    if args.profile_prefill or args.profile_decode or args.profile_token:
         model = DecodeModel(ctx)
         if args.profile_prefill:
             result = {"profile": "prefill", **prefill(ctx, events, model, args.steps, args.warmup)}
+        elif args.profile_token:
+            result = {"profile": "whole token (eager)", **token_eager(ctx, events, model, args.steps, args.warmup)}
         else:
             result = {"profile": "decode step (eager)",
                       **decode_step(ctx, events, model, args.steps, args.warmup, eager_only=True)}
@@ -658,6 +851,11 @@ def main() -> int:
     payload, x = make_ternary2(rows, columns, block)
     head = Case(ctx, "ternary2-4096-b128", lambda: ctx.create_ternary2(rows, columns, block, payload),
                 payload.size, rows, columns, x, False)
+    try:
+        head_parity = check_case(ctx, head, payload, rows, columns, None, x, block)
+    except ParityError as e:
+        print(f"bench.py: parity check failed, nothing timed: {e}", file=sys.stderr)
+        return 1
     warm_up(ctx, head.run_group, args.warmup_seconds)
     if args.profile:
         ms = time_launches(ctx, events, head.run_group, args.steps, args.warmup)
@@ -675,31 +873,40 @@ def main() -> int:
         head.close()
         return 0
     headline = measure(ctx, events, head, args.steps, args.warmup)
+    headline.update(head_parity)
     # Timed region of the headline itself, for the contract fields.
     ms_per_step = headline["launch_us"] * 1e-3
+    headline.update(host_call_latency(head))
     head.close()
 
     formats = {"ternary2-4096-b128": headline}
     cpu_cases = {"ternary2-4096-b128": (payload, rows, columns, None, x, block)}
-    if not args.quick:
-        for label, make in other_formats(ctx):
-            c, cpu_case = make()
-            formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
-            cpu_cases[label] = cpu_case
-            c.close()
-
     decode = pre = token = load = None
-    if not args.quick:
-        progress("decode step (197 projections per token)")
-        model = DecodeModel(ctx)
-        decode = decode_step(ctx, events, model, 50, 5)
-        progress("whole decode token (operators + projections, position 511)")
-        token = decode_token(ctx, events, model, 30, 3)
-        progress("prefill (512 positions)")
-        pre = prefill(ctx, events, model, 3, 1)
-        model.close()
-        progress("loading (GGUF, STQ2, STB1 uploads)")
-        load = loading(ctx)
+    try:
+        if not args.quick:
+            for label, make in other_formats(ctx):
+                c, cpu_case = make()
+                parity = check_case(ctx, c, *cpu_case)
+                formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
+                formats[label].update(parity)
+                formats[label].update(host_call_latency(c))
+                cpu_cases[label] = cpu_case
+                c.close()
+
+        if not args.quick:
+            progress("decode step (197 projections per token)")
+            model = DecodeModel(ctx)
+            decode = decode_step(ctx, events, model, 50, 5)
+            progress("whole decode token (operators + projections, position 511)")
+            token = decode_token(ctx, events, model, 30, 3)
+            progress("prefill (512 positions)")
+            pre = prefill(ctx, events, model, 3, 1)
+            model.close()
+            progress("loading (GGUF, STQ2, STB1 uploads)")
+            load = loading(ctx)
+    except ParityError as e:
+        print(f"bench.py: parity check failed: {e}", file=sys.stderr)
+        return 1
 
     progress("cpu baseline")
     cpu = cpu_baseline(payload, rows, columns, block, x, args.cpu_seconds)
@@ -721,6 +928,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(value / PUBLISHED_AVX2_T2_4096_B128, 1),
+        "vs_baseline_reference": (f"published AVX2 Ternary2 4096x4096 B128, one thread of a Core Ultra 7 155H: "
+                                  f"{PUBLISHED_AVX2_T2_4096_B128} GB/s (docs/benchmarks/avx2-2026-10-12)"),
+        "vs_same_run_cpu": round(value / cpu["value"], 1),
         "dtype": "f32",
         "data": "synthetic",
         "config": {
