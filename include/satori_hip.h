@@ -312,6 +312,17 @@ int satori_hip_attention_inputs(satori_hip_context* context, float* query, const
 int satori_hip_grouped_attention(satori_hip_context* context, const float* query, const float* keys,
                                  const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
                                  float* output, void* stream);
+/* satori_hip_grouped_attention without any allocation. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, hosts that forbid
+ * allocation after start-up). Same arguments, checks and results (the same kernels); the split partials go
+ * to a static device workspace of 4 MiB per device (resolved when the context is created, held until the
+ * process ends) instead of a context workspace: a call whose partials, query_heads * splits * (head_dim + 2)
+ * * 8 bytes, exceed it fails with SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE (12 heads of 128 lanes: prefixes up to
+ * 688,128 tokens). Every call on a device shares that workspace and leaves its partials there: calls that
+ * overlap in time on one device (other streams, other contexts) race and must be serialised by the caller. */
+int satori_hip_grouped_attention_static(satori_hip_context* context, const float* query, const float* keys,
+                                        const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
+                                        float* output, void* stream);
 /* GgufQuantizedMatrix.ReadRow (src/Satori.Formats.Gguf/GgufQuantizedMatrix.cs:54-61): row `row` of a resident
  * Q8_0 / Q4_K / Q6_K matrix decoded to FP32 `columns` floats (QuantizedRow.DecodeRow), bit-identical to the
  * reference's decode. Q4_0 and Ternary2 fail with SATORI_HIP_E_NOT_SUPPORTED. */

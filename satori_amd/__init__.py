@@ -1007,6 +1007,14 @@ class DeviceOps:
                                                       self._p(k_out), self._p(v), self._p(v_bias), self._p(v_out), heads,
                                                       kv_heads, head_dim, position, float(base), rotary, None))
 
+    def grouped_attention_static(self, q: int, k: int, v: int, query_heads: int, kv_heads: int, head_dim: int,
+                                 tokens: int, out: int, stream: int = 0) -> None:
+        """grouped_attention with no allocation (satori_hip_grouped_attention_static): the split partials go to
+        the device's static 4 MiB workspace, shared by every such call on the device."""
+        _check(_ffi.lib().satori_hip_grouped_attention_static(self._h, self._p(q), self._p(k), self._p(v),
+                                                              query_heads, kv_heads, head_dim, tokens, self._p(out),
+                                                              self._p(stream) if stream else None))
+
     def grouped_attention(self, q: int, k: int, v: int, query_heads: int, kv_heads: int, head_dim: int, tokens: int,
                           out: int, stream: int = 0) -> None:
         """`stream`: a HIP stream handle (0: the context stream)."""

@@ -69,6 +69,7 @@ SIGNATURES = {
     "satori_hip_swiglu": (I, [P, P, P, I, P, P]),
     "satori_hip_add": (I, [P, P, P, I, P, P]),
     "satori_hip_grouped_attention": (I, [P, P, P, P, I, I, I, I, P, P]),
+    "satori_hip_grouped_attention_static": (I, [P, P, P, P, I, I, I, I, P, P]),
     "satori_hip_add_rms_norm": (I, [P, P, P, P, ctypes.c_float, I, P, P]),
     "satori_hip_attention_inputs": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, ctypes.c_double, I, P]),
     "satori_hip_matrix_decode_row": (I, [P, I, P, P]),

@@ -208,6 +208,12 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
 int attention_splits(int tokens);
 size_t attention_scratch_bytes(int query_heads, int head_dim, int tokens);
 bool attention_supported(int tokens, int head_dim);
+// Partials one call of `tokens` tokens writes (0 when one workgroup per head needs none).
+size_t attention_partials_bytes(int query_heads, int head_dim, int tokens);
+// The no-allocation attention's partials: a file-scope device array of kStaticAttentionBytes per device. Its
+// device address on the current device (call with that device current; the address differs per device).
+constexpr size_t kStaticAttentionBytes = size_t(4) << 20;
+hipError_t static_attention_partials(double** partials);
 hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns, int row, float* out,
                              hipStream_t stream);
 

@@ -91,6 +91,9 @@ struct satori_hip_context {
     std::vector<std::pair<hipStream_t, satori::DeviceBuffer>> attention;
     int attention_steps = 0;         // live captured steps whose graph uses the context stream's buffer
     bool captured_attention = false; // the capture in progress enqueued a split attention
+    // The device address of the no-allocation attention's partials on this context's device (the file-scope
+    // array of transformer_ops.hip), resolved once when the context is created.
+    double* static_attention = nullptr;
     satori::PinnedBuffer host_x, host_y;
     // Stream capture (satori_hip_capture_begin / _end): the matrices and groups launched on the context
     // stream while capturing, referenced by the step the capture becomes.
@@ -630,8 +633,11 @@ int satori_hip_context_create(int device, satori_hip_context** context) {
         if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
             fail(SATORI_HIP_E_PLATFORM_NOT_SUPPORTED, std::string("Device is ") + prop.gcnArchName + ", not gfx950.");
         check_hip(hipSetDevice(device), "hipSetDevice");
+        double* partials = nullptr;
+        check_hip(static_attention_partials(&partials), "hipGetSymbolAddress");  // with `device` current
         auto* c = new satori_hip_context();
         c->device = device;
+        c->static_attention = partials;
         const hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
             delete c;
@@ -1652,23 +1658,37 @@ int satori_hip_attention_inputs(satori_hip_context* c, float* query, const float
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// GroupedAttention's argument rules (TransformerOps.cs:135-145), shared by both attention entry points.
+void check_attention(const float* query, const float* keys, const float* values, int query_heads, int kv_heads,
+                     int head_dim, int tokens, float* output) {
+    require(query, "query");
+    require(keys, "keys");
+    require(values, "values");
+    require(output, "output");
+    if (head_dim <= 0 || query_heads <= 0 || kv_heads <= 0 || query_heads % kv_heads != 0 || tokens <= 0)
+        fail(SATORI_HIP_E_ARGUMENT, "Invalid grouped-attention dimensions.");
+    const int64_t width = static_cast<int64_t>(query_heads) * head_dim;
+    const int64_t kv = static_cast<int64_t>(tokens) * kv_heads * head_dim;
+    if (width > INT32_MAX || kv > INT32_MAX) fail(SATORI_HIP_E_OVERFLOW, "Arithmetic operation resulted in an overflow.");
+    if (any_overlap(query, width, output, width) || any_overlap(keys, kv, output, width) ||
+        any_overlap(values, kv, output, width))
+        fail(SATORI_HIP_E_ARGUMENT, "Attention output overlaps input.");
+    if (!attention_supported(tokens, head_dim))
+        fail(SATORI_HIP_E_NOT_SUPPORTED, "The prefix is too long for one split of the attention's local memory.");
+}
+
+}  // namespace
+
+extern "C" {
+
 int satori_hip_grouped_attention(satori_hip_context* c, const float* query, const float* keys, const float* values,
                                  int query_heads, int kv_heads, int head_dim, int tokens, float* output, void* stream) {
     return op_call(c, [&] {
-        require(query, "query");
-        require(keys, "keys");
-        require(values, "values");
-        require(output, "output");
-        if (head_dim <= 0 || query_heads <= 0 || kv_heads <= 0 || query_heads % kv_heads != 0 || tokens <= 0)
-            fail(SATORI_HIP_E_ARGUMENT, "Invalid grouped-attention dimensions.");
-        const int64_t width = static_cast<int64_t>(query_heads) * head_dim;
-        const int64_t kv = static_cast<int64_t>(tokens) * kv_heads * head_dim;
-        if (width > INT32_MAX || kv > INT32_MAX) fail(SATORI_HIP_E_OVERFLOW, "Arithmetic operation resulted in an overflow.");
-        if (any_overlap(query, width, output, width) || any_overlap(keys, kv, output, width) ||
-            any_overlap(values, kv, output, width))
-            fail(SATORI_HIP_E_ARGUMENT, "Attention output overlaps input.");
-        if (!attention_supported(tokens, head_dim))
-            fail(SATORI_HIP_E_NOT_SUPPORTED, "The prefix is too long for one split of the attention's local memory.");
+        check_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output);
         const hipStream_t st = op_stream(c, stream);
         double* scratch = nullptr;
         if (attention_splits(tokens) > 1) {
@@ -1693,6 +1713,24 @@ int satori_hip_grouped_attention(satori_hip_context* c, const float* query, cons
             scratch = static_cast<double*>(buffer.ptr);
         }
         check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output, scratch, st),
+                  "attention launch");
+    });
+}
+
+int satori_hip_grouped_attention_static(satori_hip_context* c, const float* query, const float* keys,
+                                        const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
+                                        float* output, void* stream) {
+    return op_call(c, [&] {
+        check_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output);
+        const size_t need = attention_partials_bytes(query_heads, head_dim, tokens);
+        if (need > kStaticAttentionBytes)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE,
+                 "The attention needs " + std::to_string(need) + " bytes of partials (query_heads * splits * "
+                 "(head_dim + 2) * 8); the static workspace holds " + std::to_string(kStaticAttentionBytes) + ".");
+        // No workspace to allocate or grow: the partials (written in full before the combine reads them, so
+        // nothing needs clearing) go to the device's static array.
+        check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output,
+                                   c->static_attention, op_stream(c, stream)),
                   "attention launch");
     });
 }

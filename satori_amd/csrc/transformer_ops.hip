@@ -15,6 +15,11 @@
 #include "kernels.hpp"
 #include "ops_device.hpp"
 
+// Split-attention partials of the no-allocation entry point: one copy per device, alive until the process
+// ends, shared by every such call on that device (calls that overlap in time race on it). Host code never
+// names it in a launch: the device address comes from hipGetSymbolAddress (static_attention_partials).
+static __device__ __align__(256) unsigned char scratch[satori::kStaticAttentionBytes];
+
 namespace satori {
 namespace {
 
@@ -633,7 +638,7 @@ bool attention_supported(int tokens, int head_dim) {
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
-                            int head_dim, int tokens, float* out, double* scratch, hipStream_t stream) {
+                            int head_dim, int tokens, float* out, double* partials, hipStream_t stream) {
     if (!attention_supported(tokens, head_dim)) return hipErrorInvalidValue;
     const int splits = attention_splits(tokens);
     if (splits == 1) {
@@ -641,18 +646,31 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
             q, k, v, query_heads, kv_heads, head_dim, tokens, out);
         return hipGetLastError();
     }
-    if (!scratch) return hipErrorInvalidValue;
+    if (!partials) return hipErrorInvalidValue;
     const int per = (tokens + splits - 1) / splits;
     attention_split_kernel<<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes(per, head_dim), stream>>>(
-        q, k, v, query_heads, kv_heads, head_dim, tokens, per, scratch);
-    attention_combine_kernel<<<query_heads, kSplitThreads, 0, stream>>>(scratch, splits, head_dim, out);
+        q, k, v, query_heads, kv_heads, head_dim, tokens, per, partials);
+    attention_combine_kernel<<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out);
     return hipGetLastError();
+}
+
+size_t attention_partials_bytes(int query_heads, int head_dim, int tokens) {
+    const int splits = attention_splits(tokens);
+    return splits == 1 ? 0 : static_cast<size_t>(query_heads) * splits * (2 + head_dim) * sizeof(double);
 }
 
 hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns, int row, float* out,
                              hipStream_t stream) {
     decode_row_kernel<<<grid_for(columns), kThreads, 0, stream>>>(w, format, rows, columns, row, out);
     return hipGetLastError();
+}
+
+hipError_t static_attention_partials(double** partials) {
+    void* address = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    *partials = static_cast<double*>(address);
+    return hipSuccess;
 }
 
 }  // namespace satori
