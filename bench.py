@@ -321,10 +321,12 @@ class DecodeModel:
 
 
 def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_only: bool = False) -> dict:
-    """The projection sequence of one decode token (197 projections, batch 1) on the Q8_K integer path.
-    Projections that share an input form one group (q/k/v, gate/up); the 113 groups of a token are
-    captured once as a graph (satori_hip_step) and replayed. Attention, norms and SwiGLU are not part of
-    the path: their outputs are fixed random vectors. Also timed: the same groups launched eagerly."""
+    """The projection sequence of one decode token (197 projections, batch 1) on the Q8_K integer path, launched
+    as the whole token launches them. Projections that share an input form one group (q/k/v, gate/up); the
+    113 groups of a token are captured once as a graph (satori_hip_step) and replayed. Attention, norms and
+    SwiGLU are not part of the path: their outputs are fixed random vectors. q/k/v, o and gate/up quantize
+    their FP32 input inside their launch; down reads the Q8_K bytes its producer (SwiGLU) writes in the whole
+    token, here quantized once before timing. Also timed: the same groups launched eagerly."""
     d, ffn, vocab = model.D, model.FFN, model.VOCAB
     g = rng(2026)
     host_in = {"h": g.standard_normal(d).astype(np.float32), "attn": g.standard_normal(d).astype(np.float32),
@@ -342,6 +344,11 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
         members += [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
     groups.append(S.HipGroup(ctx, [model.output], [h], [logits], True))
     members.append(("output",))
+    act_q8k = model.device(np.zeros(ffn // 256 * 73, np.float32))  # 292 bytes per Q8_K block
+    S.DeviceOps(ctx).quantize_q8k(act, ffn, 1, act_q8k)
+    for grp, names in zip(groups, members):
+        if names == ("down",):
+            grp.set_input_q8k(act_q8k)
     # Parity before timing: every launch of the step, one at a time, against the oracle (checker only).
     from oracle import oracle as O
     feeds = {"q": "h", "k": "h", "v": "h", "o": "attn", "gate": "h2", "up": "h2", "down": "act", "output": "h"}

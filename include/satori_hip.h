@@ -209,6 +209,10 @@ int satori_hip_group_execute_batch(satori_hip_group* group, int positions, void*
  *    as satori_hip_add_rms_norm / satori_hip_rms_norm compute it; when residual_out is not NULL the launch
  *    also writes a + b there (it must not overlap a, b, the weights or the members' outputs);
  *  SATORI_HIP_INPUT_SWIGLU: input = SwiGlu(a, b), as satori_hip_swiglu;
+ *  SATORI_HIP_INPUT_Q8K: `a` points at the input already quantized to Q8_K (Q8KCodec.QuantizeRow bytes,
+ *    columns / 256 * 292, as satori_hip_swiglu_q8k or satori_hip_quantize_q8k_device write them): the launch
+ *    reads those bytes instead of quantizing (b, weights, epsilon and residual_out are ignored); the outputs
+ *    are those of the plain launch over the FP32 input the bytes were quantized from, bit for bit;
  *  SATORI_HIP_INPUT_PLAIN: back to reading inputs[i].
  * Vectors have the members' column count. One-position launches only (satori_hip_group_execute_batch
  * fails with SATORI_HIP_E_NOT_SUPPORTED). Not while steps replay the group (SATORI_HIP_E_ARGUMENT) or while
@@ -218,6 +222,7 @@ int satori_hip_group_execute_batch(satori_hip_group* group, int positions, void*
 #define SATORI_HIP_INPUT_PLAIN 0
 #define SATORI_HIP_INPUT_ADD_RMS_NORM 1
 #define SATORI_HIP_INPUT_SWIGLU 2
+#define SATORI_HIP_INPUT_Q8K 3
 int satori_hip_group_set_input(satori_hip_group* group, int kind, const float* a, const float* b,
                                const float* weights, float epsilon, float* residual_out);
 /* Fails with SATORI_HIP_E_ARGUMENT while a step replays the group. A matrix cannot be destroyed while a
@@ -292,6 +297,17 @@ int satori_hip_swiglu(satori_hip_context* context, const float* gate, const floa
                       void* stream);
 int satori_hip_add(satori_hip_context* context, const float* left, const float* right, int length, float* output,
                    void* stream);
+/* SwiGlu (TransformerOps.cs:40-50) and Q8KCodec.QuantizeRow of its output (src/Satori.Core/Q8KCodec.cs:85-93)
+ * in one launch: the activation of the down projection of DenseForward.Step (DenseForward.cs:156-160), which
+ * the reference quantizes inside ExecuteBatch (QuantizedMatVec.cs:136-219), quantized once by its producer for
+ * a group reading it with SATORI_HIP_INPUT_Q8K. length a positive multiple of 256; q8k receives
+ * length / 256 * 292 bytes, identical to the reference's; output (FP32, as satori_hip_swiglu) may be NULL. */
+int satori_hip_swiglu_q8k(satori_hip_context* context, const float* gate, const float* up, int length, float* output,
+                          void* q8k, void* stream);
+/* satori_hip_quantize_q8k over device buffers, enqueued like the operators: `positions` rows of `columns`
+ * floats (a positive multiple of 256) to [positions][columns / 256 * 292] Q8_K bytes. */
+int satori_hip_quantize_q8k_device(satori_hip_context* context, const float* input, int columns, int positions,
+                                   void* output, void* stream);
 /* Fused steps of DenseForward.Step, bit-identical to the separate calls: Add then RmsNorm
  * (DenseForward.cs:156-158: residual += addend, normed = RmsNorm(residual)), and the attention inputs of one
  * position (DenseForward.cs:128-151: the q/k/v bias adds when biases are given (NULL: none), RopeHalf of the
@@ -312,6 +328,17 @@ int satori_hip_attention_inputs(satori_hip_context* context, float* query, const
 int satori_hip_grouped_attention(satori_hip_context* context, const float* query, const float* keys,
                                  const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
                                  float* output, void* stream);
+/* The attention of one decode position with its inputs (DenseForward.cs:128-152):
+ * satori_hip_attention_inputs(query, query_bias, key, key_bias, keys + position * kv_width, value, value_bias,
+ * values + position * kv_width, ...) then satori_hip_grouped_attention(query, keys, values, ..., position + 1,
+ * output), with the same results bit for bit (the query rotated in place, the key and value written to row
+ * `position` of the caches); past 32 tokens the transform runs inside the split attention's launches, one
+ * launch fewer. Biases may be NULL. keys/values are the caches [position + 1][kv_heads * head_dim]; key and
+ * value must not overlap them. The workspace rules are those of satori_hip_grouped_attention. */
+int satori_hip_attention_decode(satori_hip_context* context, float* query, const float* query_bias, const float* key,
+                                const float* key_bias, const float* value, const float* value_bias, float* keys,
+                                float* values, int query_heads, int kv_heads, int head_dim, int position,
+                                double frequency_base, int rotary_dimensions, float* output, void* stream);
 /* satori_hip_grouped_attention without any allocation. No counterpart in the reference: for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, hosts that forbid
  * allocation after start-up). Same arguments, checks and results (the same kernels); the split partials go

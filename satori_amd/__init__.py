@@ -389,6 +389,11 @@ class HipGroup:
         _check(_ffi.lib().satori_hip_group_set_input(self._handle, 2, ctypes.c_void_p(gate), ctypes.c_void_p(up),
                                                      None, 0.0, None))
 
+    def set_input_q8k(self, q8k: int) -> None:
+        """The group reads its input already quantized to Q8_K at `q8k` (device bytes written by its producer,
+        DeviceOps.swiglu_q8k / quantize_q8k) instead of quantizing it."""
+        _check(_ffi.lib().satori_hip_group_set_input(self._handle, 3, ctypes.c_void_p(q8k), None, None, 0.0, None))
+
     def set_input_plain(self) -> None:
         """The group reads its creation inputs again."""
         _check(_ffi.lib().satori_hip_group_set_input(self._handle, 0, None, None, None, 0.0, None))
@@ -996,6 +1001,15 @@ class DeviceOps:
     def add(self, left: int, right: int, length: int, out: int) -> None:
         _check(_ffi.lib().satori_hip_add(self._h, self._p(left), self._p(right), length, self._p(out), None))
 
+    def swiglu_q8k(self, gate: int, up: int, length: int, out: int, q8k: int) -> None:
+        """SwiGlu with the Q8_K bytes of its output (out may be 0: no FP32 output)."""
+        _check(_ffi.lib().satori_hip_swiglu_q8k(self._h, self._p(gate), self._p(up), length,
+                                                self._p(out) if out else None, self._p(q8k), None))
+
+    def quantize_q8k(self, x: int, columns: int, positions: int, out: int) -> None:
+        """Q8KCodec.QuantizeRow of `positions` device rows into device Q8_K bytes."""
+        _check(_ffi.lib().satori_hip_quantize_q8k_device(self._h, self._p(x), columns, positions, self._p(out), None))
+
     def add_rms_norm(self, residual: int, addend: int, weights: int, epsilon: float, length: int, normed: int) -> None:
         _check(_ffi.lib().satori_hip_add_rms_norm(self._h, self._p(residual), self._p(addend), self._p(weights),
                                                   float(epsilon), length, self._p(normed), None))
@@ -1006,6 +1020,16 @@ class DeviceOps:
         _check(_ffi.lib().satori_hip_attention_inputs(self._h, self._p(q), self._p(q_bias), self._p(k), self._p(k_bias),
                                                       self._p(k_out), self._p(v), self._p(v_bias), self._p(v_out), heads,
                                                       kv_heads, head_dim, position, float(base), rotary, None))
+
+    def attention_decode(self, q: int, q_bias: int, k: int, k_bias: int, v: int, v_bias: int, keys: int, values: int,
+                         heads: int, kv_heads: int, head_dim: int, position: int, base: float, rotary: int,
+                         out: int) -> None:
+        """attention_inputs (cache slots of row `position`) then grouped_attention over position + 1 rows, in one
+        or two launches fewer; biases may be 0."""
+        _check(_ffi.lib().satori_hip_attention_decode(self._h, self._p(q), self._p(q_bias), self._p(k), self._p(k_bias),
+                                                      self._p(v), self._p(v_bias), self._p(keys), self._p(values), heads,
+                                                      kv_heads, head_dim, position, float(base), rotary, self._p(out),
+                                                      None))
 
     def grouped_attention_static(self, q: int, k: int, v: int, query_heads: int, kv_heads: int, head_dim: int,
                                  tokens: int, out: int, stream: int = 0) -> None:

@@ -64,7 +64,8 @@ __device__ __forceinline__ void load_unaligned(const uint8_t* p, uint32_t (&out)
 struct Q6KQuarter {
     u32x4 qla, qlb, qh;
     uint32_t sc;
-    float d;
+    uint32_t dpair;   // the aligned dword holding d (kept raw: converting it at load time would wait for it)
+    uint32_t dshift;  // 0 or 16: d's half of dpair
 };
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16);
@@ -77,9 +78,12 @@ __device__ __forceinline__ void q6k_load_quarter(const uint8_t* w, int64_t block
     r.qh = *(const SATORI_GLOBAL u32x4*)(record + 32);
     r.sc = load4_a4(w + blocks * 192 + index * 16 + 4 * c);
     // d array: 2 bytes per block from offset blocks * 208 (a multiple of 16); read the aligned dword.
-    const uint32_t pair = load4_a4(w + blocks * 208 + (index & ~int64_t(1)) * 2);
-    r.d = half_bits_to_float(pair >> (16 * static_cast<int>(index & 1)));
+    r.dpair = load4_a4(w + blocks * 208 + (index & ~int64_t(1)) * 2);
+    r.dshift = 16 * static_cast<uint32_t>(index & 1);
 }
+
+// The quarter's block scale d (FP16 -> FP32, exact), read where it is used.
+__device__ __forceinline__ float q6k_d(const Q6KQuarter& r) { return half_bits_to_float(r.dpair >> r.dshift); }
 
 // Q4KCodec.GetScaleMin (src/Satori.Core/Q4KCodec.cs:24-36) for sub-block j (0..7), from the dwords holding
 // scales[12] (head[1..3]). Both forms are computed from fixed dwords with a per-lane shift and one is

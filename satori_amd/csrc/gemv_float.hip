@@ -216,10 +216,11 @@ struct Q6_KChunk {
     }
     __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
         float ds[4], bias[4];
+        const float d = q6k_d(r);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int8_t s = static_cast<int8_t>(r.sc >> (8 * k));  // scale 8h + 2k + t
-            ds[k] = r.d * static_cast<float>(s);
+            ds[k] = d * static_cast<float>(s);
             bias[k] = -32.0f * ds[k];
         }
         float acc0 = 0.0f, acc1 = 0.0f;

@@ -59,6 +59,10 @@ constexpr int kTileRows = 64;
 // groups of LDS banks instead of the same four.
 constexpr int kCodeStride = 68;
 constexpr int kActDwords = kCodeStride + 1 + 8;  // codes, scale, group sums per block
+// Activation loads a thread issues before the weight loads: passes of 16 Q8_K blocks (48 blocks preloaded)
+// and elements of the RmsNorm sum of squares (2,048 columns).
+constexpr int kQ8KPasses = 3;  // 48 blocks
+constexpr int kNormPreload = 8;
 
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
@@ -144,14 +148,23 @@ __host__ __device__ inline int kint_red_offset(int blocks, int tile_rows) {
 
 static_assert(kThreads == kOpsThreads, "the RmsNorm reduction is the operators' 256-thread tree");
 
-template <int FORMAT, int XF>
-__global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const MatDesc* __restrict__ group,
-                                                              LaunchShape s, InputTransform xf) {
+// The members of a launch of up to kKintInlineMembers matrices travel in the kernel arguments, so the first
+// weight loads depend on no global-memory read; larger groups read a device array of descriptors.
+struct KintMembers {
+    MatDesc m[kKintInlineMembers];
+};
+
+template <int FORMAT, int XF, bool INLINE>
+__global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_members,
+                                                              const MatDesc* __restrict__ group, LaunchShape s,
+                                                              InputTransform xf) {
     constexpr int G = 4;  // lanes per (row, block) pair
     constexpr int kBlockBytes = FORMAT == kQ4_K ? 144 : 210;
     constexpr int kPairsPerStep = kThreads / G;
     using Raw = typename std::conditional<FORMAT == kQ4_K, Q4KRaw, Q6KRaw>::type;
-    const MatDesc m = group ? group[blockIdx.y] : one;
+    // Inline members come from the kernel arguments through the scalar cache; a larger group's descriptor is
+    // one global load.
+    const MatDesc m = INLINE ? inline_members.m[blockIdx.y] : group[blockIdx.y];
     const int tile_rows = s.rows_per_wg;
     const int row_begin = blockIdx.x * tile_rows;
     if (row_begin >= m.rows) return;
@@ -186,77 +199,152 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
                              static_cast<int64_t>(row_begin + row) * nb + b, c, r);
         }
     };
-    // This slot's pairs are p0, p0 + kPairsPerStep, ...; up to kDepth of them are loaded before the
-    // activations are quantized, and each processed pair's registers are refilled with the pair kDepth
-    // further on, so kDepth loads stay in flight.
+    // This slot's pairs are p0, p0 + kPairsPerStep, ...; kDepth of them are loaded before the activations
+    // are staged, and each processed pair's registers are refilled with the pair kDepth further on, so kDepth
+    // loads stay in flight.
     constexpr int kDepth = 3;
     const int p0 = threadIdx.x / G;
     int kb = min(K, nb);
     int mine = p0 < rows * kb ? (rows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
+    const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
+    auto quad = [](const float* p, int i) {
+        const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(p + i));
+        return f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                     __uint_as_float(raw[3])};
+    };
+
+    // The activation side is loaded first, then the weights: the waits for the activations then do not
+    // cover the weight loads issued after them. Every thread issues the same loads (addresses past the end
+    // are clamped and their values unused), so the load counts the waits are computed from are static.
+    const int tid = threadIdx.x;
+    const int j16 = tid & 15, bl0 = tid >> 4;
+    f32x4 xpre[4];                 // plain input: this thread's 16 values of the first pass
+    // Q8_K input: lane j16 of a 16-lane row copies block bl's code dwords [4 j16, 4 j16 + 4), and lane 0 its
+    // scale, lanes 1 and 2 its group sums; the first kQ8KPasses passes are loaded here.
+    u32x4 qcodes[kQ8KPasses], qaux[kQ8KPasses];
+    auto q8k_load = [&](const uint8_t* row, int bl, u32x4& codes, u32x4& aux) {
+        const uint8_t* block = row + static_cast<int64_t>(bl) * kQ8KBlockBytes;
+        codes = load16_a4(block + 4 + 16 * j16);
+        aux = load16_a4(block + (j16 == 0 ? 0 : 260 + 16 * (min(j16, 2) - 1)));
+    };
+    float npre_a[kNormPreload], npre_b[kNormPreload];  // RmsNorm input: the first terms of the sum of squares
+    if constexpr (XF == kInputPlain) {
+        const int i0 = 256 * min(bl0, kb - 1) + 16 * j16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xpre[q] = quad(xrow, i0 + 4 * q);
+    } else if constexpr (XF == kInputQ8K) {
+#pragma unroll
+        for (int k = 0; k < kQ8KPasses; ++k)
+            q8k_load(reinterpret_cast<const uint8_t*>(xf.a), min(bl0 + 16 * k, kb - 1), qcodes[k], qaux[k]);
+    } else if constexpr (XF == kInputAddRmsNorm) {
+#pragma unroll
+        for (int k = 0; k < kNormPreload; ++k) {
+            const int i = min(tid + kThreads * k, s.columns - 1);
+            npre_a[k] = xf.a[i];
+            npre_b[k] = xf.b ? xf.b[i] : 0.0f;
+        }
+    }
     Raw buf[kDepth];
 #pragma unroll
-    for (int i = 0; i < kDepth; ++i)
-        if (i < mine) load_pair(0, kb, p0 + i * kPairsPerStep, buf[i]);
+    for (int i = 0; i < kDepth; ++i) load_pair(0, kb, min(p0 + i * kPairsPerStep, rows * kb - 1), buf[i]);
 
     // Q8_K of the position's activations: one 16-lane row per block, sixteen blocks per pass. With an input
     // transform the activations are computed here from the operator's operands, in the operator's own
     // arithmetic (the RmsNorm sum of squares over the same 256-thread partition and tree, over the whole row).
-    const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
     double scale = 0.0;
     if constexpr (XF == kInputAddRmsNorm) {
         double* red = reinterpret_cast<double*>(smem + kint_red_offset(K, tile_rows));
         const bool writer = xf.residual_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
         double part = 0;
-        for (int i = threadIdx.x; i < s.columns; i += kThreads) {
-            const float r = xf.b ? __fadd_rn(xf.a[i], xf.b[i]) : xf.a[i];
+        auto term = [&](int i, float a, float b) {
+            const float r = xf.b ? __fadd_rn(a, b) : a;
             if (writer) xf.residual_out[i] = r;
             const double v = r;
             part = part + v * v;
-        }
+        };
+#pragma unroll
+        for (int k = 0; k < kNormPreload; ++k)
+            if (tid + kThreads * k < s.columns) term(tid + kThreads * k, npre_a[k], npre_b[k]);
+        for (int i = tid + kThreads * kNormPreload; i < s.columns; i += kThreads)
+            term(i, xf.a[i], xf.b ? xf.b[i] : 0.0f);
         scale = rms_scale(block_sum_256(part, red), s.columns, xf.epsilon);
     }
     // Block order from +0, as the reference accumulator (QuantizedKAvx2Kernel.cs:63, 90-94). A skipped
     // block stores +0, and adding +0 to a sum that starts at +0 never changes it.
     float acc = 0.0f;
     for (int b0 = 0;;) {
-        {
-            const int j = threadIdx.x & 15;
-            for (int bl = threadIdx.x >> 4; bl < kb; bl += kThreads / 16) {
+        if constexpr (XF == kInputQ8K) {
+            // The producer's Q8_K row (Q8KCodec layout, 292 bytes per block: scale, 256 codes, 16 int16 group
+            // sums) copied into the LDS arrays, one 16-lane row per block.
+            const uint8_t* row = reinterpret_cast<const uint8_t*>(xf.a) + static_cast<int64_t>(b0) * kQ8KBlockBytes;
+            auto put = [&](int bl, const u32x4& codes, const u32x4& aux) {
+                *reinterpret_cast<u32x4*>(act.codes + kCodeStride * bl + 4 * j16) = codes;
+                if (j16 == 0) {
+                    act.scales[bl] = __uint_as_float(aux[0]);
+                } else if (j16 <= 2) {
+                    uint32_t* sums = reinterpret_cast<uint32_t*>(act.sums) + 8 * bl + 4 * (j16 - 1);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sums[e] = aux[e];
+                }
+            };
+            int bl = bl0;
+            if (b0 == 0) {
+#pragma unroll
+                for (int k = 0; k < kQ8KPasses; ++k)
+                    if (bl0 + 16 * k < kb) put(bl0 + 16 * k, qcodes[k], qaux[k]);
+                bl += 16 * kQ8KPasses;
+            }
+            for (; bl < kb; bl += kThreads / 16) {
+                u32x4 codes, aux;
+                q8k_load(row, bl, codes, aux);
+                put(bl, codes, aux);
+            }
+        } else {
+            auto stage = [&](int bl, const f32x4 (&x4)[4]) {
                 float v[16];
-                const int i0 = 256 * (b0 + bl) + 16 * j;
-                auto quad = [&](const float* p, int q) {
-                    const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(p + i0 + 4 * q));
-                    return f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
-                                 __uint_as_float(raw[3])};
-                };
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[4 * q + e] = x4[q][e];
+                const Q8KRow16 qr = q8k_quantize_row16(v, lane);
+                *reinterpret_cast<u32x4*>(act.codes + kCodeStride * bl + 4 * j16) =
+                    u32x4{qr.packed[0], qr.packed[1], qr.packed[2], qr.packed[3]};
+                act.sums[16 * bl + j16] = static_cast<int16_t>(qr.group_sum);
+                if (j16 == 0) act.scales[bl] = qr.scale;
+            };
+            int bl = bl0;
+            if constexpr (XF == kInputPlain) {
+                if (b0 == 0) {
+                    if (bl < kb) stage(bl, xpre);
+                    bl += kThreads / 16;
+                }
+            }
+            for (; bl < kb; bl += kThreads / 16) {
+                const int i0 = 256 * (b0 + bl) + 16 * j16;
+                f32x4 x4[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     if constexpr (XF == kInputPlain) {
-                        const f32x4 x4 = quad(xrow, q);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) v[4 * q + e] = x4[e];
+                        x4[q] = quad(xrow, i0 + 4 * q);
                     } else if constexpr (XF == kInputAddRmsNorm) {
-                        const f32x4 a4 = quad(xf.a, q), w4 = quad(xf.w, q);
+                        const f32x4 a4 = quad(xf.a, i0 + 4 * q), w4 = quad(xf.w, i0 + 4 * q);
                         f32x4 b4 = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (xf.b) b4 = quad(xf.b, q);
+                        if (xf.b) b4 = quad(xf.b, i0 + 4 * q);
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            v[4 * q + e] = rms_value(xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e], scale, w4[e]);
+                            x4[q][e] = rms_value(xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e], scale, w4[e]);
                     } else {
-                        const f32x4 g4 = quad(xf.a, q), u4 = quad(xf.b, q);
+                        const f32x4 g4 = quad(xf.a, i0 + 4 * q), u4 = quad(xf.b, i0 + 4 * q);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[4 * q + e] = swiglu_value(g4[e], u4[e]);
+                        for (int e = 0; e < 4; ++e) x4[q][e] = swiglu_value(g4[e], u4[e]);
                     }
                 }
-                const Q8KRow16 q = q8k_quantize_row16(v, lane);
-                *reinterpret_cast<u32x4*>(act.codes + kCodeStride * bl + 4 * j) =
-                    u32x4{q.packed[0], q.packed[1], q.packed[2], q.packed[3]};
-                act.sums[16 * bl + j] = static_cast<int16_t>(q.group_sum);
-                if (j == 0) act.scales[bl] = q.scale;
+                stage(bl, x4);
             }
         }
         __syncthreads();  // activations of the chunk staged
-        auto process = [&](const Raw& cur, int p) {
+        // The FP32 term of pair p (valid on the pair's last lane).
+        auto term_of = [&](const Raw& cur, int p) {
             const int bl = p % kb;  // block of the chunk (its staged activations)
             float term = 0.0f;
             if constexpr (FORMAT == kQ4_K) {
@@ -275,16 +363,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
                 int dot = q6k_dot(cur, act, bl, c);
                 dot = group_sum_last_int<G>(dot);
                 const float a = act.scales[bl];
-                if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, cur.d), static_cast<float>(dot));
+                if (a != 0.0f) term = __fmul_rn(__fmul_rn(a, q6k_d(cur)), static_cast<float>(dot));
             }
-            if (c == G - 1) terms[p] = term;  // p = r * kb + bl
+            return term;
         };
+        // The slot's pairs in order; each processed pair's registers are refilled with the pair kDepth further
+        // on. (Computing a round's kDepth pairs unconditionally, to interleave their chains, measured slower on
+        // the decode step's small launches: the slots there hold fewer than kDepth pairs.)
         for (int base = 0; base < mine; base += kDepth) {
 #pragma unroll
             for (int i = 0; i < kDepth; ++i) {
                 const int k = base + i;
                 if (k < mine) {
-                    process(buf[i], p0 + k * kPairsPerStep);
+                    const float t = term_of(buf[i], p0 + k * kPairsPerStep);
+                    if (c == G - 1) terms[p0 + k * kPairsPerStep] = t;
                     if (k + kDepth < mine) load_pair(b0, kb, p0 + (k + kDepth) * kPairsPerStep, buf[i]);
                 }
             }
@@ -300,8 +392,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(MatDesc one, const 
         kb = min(K, nb - b0);
         mine = p0 < rows * kb ? (rows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
 #pragma unroll
-        for (int i = 0; i < kDepth; ++i)
-            if (i < mine) load_pair(b0, kb, p0 + i * kPairsPerStep, buf[i]);
+        for (int i = 0; i < kDepth; ++i) load_pair(b0, kb, min(p0 + i * kPairsPerStep, rows * kb - 1), buf[i]);
         __syncthreads();  // every thread is done with this chunk's activations and terms
     }
     if (threadIdx.x < rows) store_f32(m.y + static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x, acc);
@@ -327,9 +418,10 @@ int kint_max_blocks() {
 namespace {
 
 template <int XF>
-hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, const InputTransform& xf,
-                       hipStream_t stream) {
+hipError_t launch_kint(const MatDesc* members, const MatDesc* device_members, int count, LaunchShape s,
+                       const InputTransform& xf, hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
+    if (count > kKintInlineMembers && !device_members) return hipErrorInvalidValue;
     // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and either a
     // thread slot would hold more than three (row, block) pairs (the pairs it prefetches before quantizing)
     // or the grid has fewer than 192 workgroups. Measured on the decode step's groups: q/k/v and o take 8-16
@@ -337,8 +429,8 @@ hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, Laun
     // would stream more than 256 KB of payload, so long rows leave no long tail of workgroups at the end of
     // a launch (1536 x 8960 grouped: Q6_K 5.43 -> 5.76 TB/s, Q4_K 5.70 -> 5.86 TB/s at 32 rows; 16 rows
     // measured slower).
-    const int64_t members = static_cast<int64_t>(count) * s.positions;
-    auto groups_for = [&](int t) { return members * ((s.rows_max + t - 1) / t); };
+    const int64_t launched = static_cast<int64_t>(count) * s.positions;
+    auto groups_for = [&](int t) { return launched * ((s.rows_max + t - 1) / t); };
     int tile = kTileRows;
     while (tile > 4 && groups_for(tile) < 1024 && (tile * s.blocks > 192 || groups_for(tile) < 192)) tile /= 2;
     while (tile > 4 && static_cast<int64_t>(tile) * s.row_bytes > 256 * 1024) tile /= 2;
@@ -348,10 +440,20 @@ hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, Laun
     dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
     const size_t lds = kint_lds_bytes(s.chunk_blocks);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    if (s.format == kQ4_K)
-        gemv_kint_kernel<kQ4_K, XF><<<grid, kThreads, lds, stream>>>(one, group, s, xf);
+    KintMembers inline_members{};
+    const MatDesc* group = nullptr;
+    if (count <= kKintInlineMembers)
+        for (int i = 0; i < count; ++i) inline_members.m[i] = members[i];
+    else
+        group = device_members;
+    if (s.format == kQ4_K && group)
+        gemv_kint_kernel<kQ4_K, XF, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
+    else if (s.format == kQ4_K)
+        gemv_kint_kernel<kQ4_K, XF, true><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
+    else if (s.format == kQ6_K && group)
+        gemv_kint_kernel<kQ6_K, XF, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
     else if (s.format == kQ6_K)
-        gemv_kint_kernel<kQ6_K, XF><<<grid, kThreads, lds, stream>>>(one, group, s, xf);
+        gemv_kint_kernel<kQ6_K, XF, true><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -359,22 +461,23 @@ hipError_t launch_kint(const MatDesc& one, const MatDesc* group, int count, Laun
 
 }  // namespace
 
-hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape s,
+hipError_t launch_gemv_kint(const MatDesc* members, const MatDesc* device_members, int count, LaunchShape s,
                             hipStream_t stream) {
-    return launch_kint<kInputPlain>(one, group, count, s, InputTransform{}, stream);
+    return launch_kint<kInputPlain>(members, device_members, count, s, InputTransform{}, stream);
 }
 
-hipError_t launch_gemv_kint_transformed(const MatDesc* group, int count, LaunchShape s, const InputTransform& xf,
-                                        hipStream_t stream) {
+hipError_t launch_gemv_kint_transformed(const MatDesc* members, const MatDesc* device_members, int count,
+                                        LaunchShape s, const InputTransform& xf, hipStream_t stream) {
     if (s.positions != 1 || !xf.a) return hipErrorInvalidValue;
     switch (xf.kind) {
-        case kInputPlain: return launch_kint<kInputPlain>(MatDesc{}, group, count, s, xf, stream);
+        case kInputPlain: return launch_kint<kInputPlain>(members, device_members, count, s, xf, stream);
         case kInputAddRmsNorm:
             if (!xf.w) return hipErrorInvalidValue;
-            return launch_kint<kInputAddRmsNorm>(MatDesc{}, group, count, s, xf, stream);
+            return launch_kint<kInputAddRmsNorm>(members, device_members, count, s, xf, stream);
         case kInputSwiGlu:
             if (!xf.b) return hipErrorInvalidValue;
-            return launch_kint<kInputSwiGlu>(MatDesc{}, group, count, s, xf, stream);
+            return launch_kint<kInputSwiGlu>(members, device_members, count, s, xf, stream);
+        case kInputQ8K: return launch_kint<kInputQ8K>(members, device_members, count, s, xf, stream);
         default: return hipErrorInvalidValue;
     }
 }

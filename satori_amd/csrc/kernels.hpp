@@ -126,16 +126,21 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
 
 // Integer K-format product (Q4_K or Q6_K) against the Q8_K quantization of the FP32 activations, which each
 // workgroup computes itself (bit-exact with Q8KCodec.QuantizeRow); outputs bit-exact with the reference's
-// ExecuteQuantizedTiled composition.
-hipError_t launch_gemv_kint(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape,
+// ExecuteQuantizedTiled composition. `members` is a host array of the `count` descriptors; launches of up to
+// kKintInlineMembers pass them in the kernel arguments, larger ones read `device_members` (the same
+// descriptors in device memory).
+constexpr int kKintInlineMembers = 4;
+hipError_t launch_gemv_kint(const MatDesc* members, const MatDesc* device_members, int count, LaunchShape shape,
                             hipStream_t stream);
 
 // The shared input of a one-position K-format launch computed inside it from the decode step's operands
 // instead of read from `x` (every workgroup computes it; the operator's launch disappears):
 //  kInputAddRmsNorm: input = RmsNorm(a + b, w, epsilon) as add_rms_norm_kernel computes it (b may be null:
 //    RmsNorm(a)); a + b is written to residual_out (if not null) by one workgroup;
-//  kInputSwiGlu: input = SwiGlu(a, b) as swiglu_kernel computes it.
-constexpr int kInputPlain = 0, kInputAddRmsNorm = 1, kInputSwiGlu = 2;
+//  kInputSwiGlu: input = SwiGlu(a, b) as swiglu_kernel computes it;
+//  kInputQ8K: `a` points at the input already quantized (Q8KCodec.QuantizeRow bytes, 292 per block), as the
+//    producer of the activation wrote it; the launch copies it instead of quantizing.
+constexpr int kInputPlain = 0, kInputAddRmsNorm = 1, kInputSwiGlu = 2, kInputQ8K = 3;
 struct InputTransform {
     int kind;
     float epsilon;
@@ -144,8 +149,8 @@ struct InputTransform {
     const float* w;
     float* residual_out;
 };
-hipError_t launch_gemv_kint_transformed(const MatDesc* group, int count, LaunchShape shape,
-                                        const InputTransform& input, hipStream_t stream);
+hipError_t launch_gemv_kint_transformed(const MatDesc* members, const MatDesc* device_members, int count,
+                                        LaunchShape shape, const InputTransform& input, hipStream_t stream);
 
 // Integer K-format product (Q4_K or Q6_K) over `positions` positions on the matrix cores: quantizes the FP32
 // activations x ([positions][blocks * 256]) to Q8_K into `workspace` (kmfma_workspace_bytes), then the
@@ -192,6 +197,10 @@ hipError_t launch_rms_norm_heads(float* v, const float* w, float epsilon, int he
 hipError_t launch_rope(float* v, int heads, int head_dim, int position, double base, int rotary, bool half_split,
                        hipStream_t stream);
 hipError_t launch_swiglu(const float* gate, const float* up, int length, float* out, hipStream_t stream);
+// SwiGlu and the Q8_K quantization of its output (Q8KCodec.QuantizeRow bytes) in one launch; `out` may be
+// null (no FP32 output). length a multiple of 256.
+hipError_t launch_swiglu_q8k(const float* gate, const float* up, int length, float* out, uint8_t* q8k,
+                             hipStream_t stream);
 hipError_t launch_add(const float* left, const float* right, int length, float* out, hipStream_t stream);
 hipError_t launch_add_rms_norm(float* residual, const float* addend, const float* w, float epsilon, int length,
                                float* normed, hipStream_t stream);
@@ -208,6 +217,13 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
 int attention_splits(int tokens);
 size_t attention_scratch_bytes(int query_heads, int head_dim, int tokens);
 bool attention_supported(int tokens, int head_dim);
+// The attention-input transform of the decoded position (launch_attention_inputs with the cache slots of row
+// `position`) followed by the attention over the position + 1 cached rows, with the same results bit for bit;
+// on the split path the transform runs inside the split and combine launches (one launch fewer).
+hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k_new, const float* k_bias,
+                                   const float* v_new, const float* v_bias, float* k_cache, float* v_cache,
+                                   int query_heads, int kv_heads, int head_dim, int position, double base, int rotary,
+                                   float* out, double* partials, hipStream_t stream);
 // Partials one call of `tokens` tokens writes (0 when one workgroup per head needs none).
 size_t attention_partials_bytes(int query_heads, int head_dim, int tokens);
 // The no-allocation attention's partials: a file-scope device array of kStaticAttentionBytes per device. Its

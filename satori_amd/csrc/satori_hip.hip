@@ -245,7 +245,7 @@ void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y,
         return;
     }
     MatDesc d{m->payload, x, y, s.rows, 0};
-    check_hip(launch_gemv_kint(d, nullptr, 1, launch_shape(s, positions, s.rows), stream), "integer gemv launch");
+    check_hip(launch_gemv_kint(&d, nullptr, 1, launch_shape(s, positions, s.rows), stream), "integer gemv launch");
 }
 
 bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
@@ -451,9 +451,10 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
     const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
     const MatDesc none{};
     if (g->quantized && g->input.kind != kInputPlain) {
-        check_hip(launch_gemv_kint_transformed(g->descriptors, g->count, l, g->input, st), "integer gemv launch");
+        check_hip(launch_gemv_kint_transformed(g->host.data(), g->descriptors, g->count, l, g->input, st),
+                  "integer gemv launch");
     } else if (g->quantized) {
-        check_hip(launch_gemv_kint(none, g->descriptors, g->count, l, st), "integer gemv launch");
+        check_hip(launch_gemv_kint(g->host.data(), g->descriptors, g->count, l, st), "integer gemv launch");
     } else if (g->shape.format == SATORI_HIP_TERNARY2) {
         check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
     } else {
@@ -469,7 +470,7 @@ void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
     if (g->input.kind != kInputPlain)
         fail(SATORI_HIP_E_NOT_SUPPORTED, "An input transform applies to one-position group launches only.");
     if (positions < kmfma_min_positions()) {
-        check_hip(launch_gemv_kint(MatDesc{}, g->descriptors, g->count, launch_shape(s, positions, g->rows_max), st),
+        check_hip(launch_gemv_kint(g->host.data(), g->descriptors, g->count, launch_shape(s, positions, g->rows_max), st),
                   "integer gemv launch");
         return;
     }
@@ -1125,11 +1126,14 @@ int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, co
                 require(a, "a");
                 require(b, "b");
                 break;
+            case SATORI_HIP_INPUT_Q8K:
+                require(a, "a");
+                break;
             default: fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Unknown input transform.");
         }
         if (kind != SATORI_HIP_INPUT_PLAIN) {
             t.a = a;
-            t.b = b;
+            t.b = kind == SATORI_HIP_INPUT_Q8K ? nullptr : b;
             t.w = kind == SATORI_HIP_INPUT_ADD_RMS_NORM ? weights : nullptr;
             t.epsilon = epsilon;
             t.residual_out = kind == SATORI_HIP_INPUT_ADD_RMS_NORM ? residual_out : nullptr;
@@ -1599,6 +1603,38 @@ int satori_hip_swiglu(satori_hip_context* c, const float* gate, const float* up,
     });
 }
 
+int satori_hip_swiglu_q8k(satori_hip_context* c, const float* gate, const float* up, int length, float* output,
+                          void* q8k, void* stream) {
+    return op_call(c, [&] {
+        require(gate, "gate");
+        require(up, "up");
+        require(q8k, "q8k");
+        if (length <= 0 || length % 256 != 0) fail(SATORI_HIP_E_ARGUMENT, "Invalid Q8_K row dimensions.");
+        if (output && (partial_overlap(gate, length, output, length) || partial_overlap(up, length, output, length)))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        const int64_t q_floats = static_cast<int64_t>(length / 256) * kQ8KBlockBytes / 4;
+        if (any_overlap(q8k, q_floats, gate, length) || any_overlap(q8k, q_floats, up, length) ||
+            (output && any_overlap(q8k, q_floats, output, length)))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_swiglu_q8k(gate, up, length, output, static_cast<uint8_t*>(q8k), op_stream(c, stream)),
+                  "swiglu launch");
+    });
+}
+
+int satori_hip_quantize_q8k_device(satori_hip_context* c, const float* input, int columns, int positions, void* output,
+                                   void* stream) {
+    return op_call(c, [&] {
+        require(input, "input");
+        require(output, "output");
+        if (columns <= 0 || columns % 256 != 0) fail(SATORI_HIP_E_ARGUMENT, "Invalid Q8_K row dimensions.");
+        if (positions <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "positions must be positive.");
+        const int64_t n = static_cast<int64_t>(columns) * positions;
+        if (any_overlap(output, n / 256 * kQ8KBlockBytes / 4, input, n)) fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_q8k_quantize(input, columns, positions, static_cast<uint8_t*>(output), op_stream(c, stream)),
+                  "Q8_K launch");
+    });
+}
+
 int satori_hip_add(satori_hip_context* c, const float* left, const float* right, int length, float* output,
                    void* stream) {
     return op_call(c, [&] {
@@ -1681,6 +1717,32 @@ void check_attention(const float* query, const float* keys, const float* values,
         fail(SATORI_HIP_E_NOT_SUPPORTED, "The prefix is too long for one split of the attention's local memory.");
 }
 
+// The split attention's partials for a call on stream `st`: the context's buffer for that stream, allocated by
+// its first split attention and grown as prefixes grow (not while capturing, nor while captured steps hold the
+// context stream's buffer); null when the call needs none.
+double* attention_workspace(satori_hip_context* c, hipStream_t st, int query_heads, int head_dim, int tokens) {
+    if (attention_splits(tokens) <= 1) return nullptr;
+    const size_t need = attention_scratch_bytes(query_heads, head_dim, tokens);
+    auto it = std::find_if(c->attention.begin(), c->attention.end(),
+                           [&](const std::pair<hipStream_t, DeviceBuffer>& e) { return e.first == st; });
+    if (c->capturing && (it == c->attention.end() || it->second.bytes < need))
+        fail(SATORI_HIP_E_INVALID_OPERATION,
+             "Run an attention of these heads and tokens once before capturing it (its workspace is allocated "
+             "on first use).");
+    if (it == c->attention.end()) {
+        c->attention.emplace_back(st, DeviceBuffer{});
+        it = c->attention.end() - 1;
+    }
+    DeviceBuffer& buffer = it->second;
+    if (st == c->stream && c->attention_steps > 0 && buffer.bytes < need)  // captured steps hold it
+        fail(SATORI_HIP_E_INVALID_OPERATION,
+             "The attention workspace cannot grow while captured steps use it: destroy them, or run the "
+             "longest attention before capturing.");
+    buffer.reserve(need);
+    if (c->capturing && st == c->stream) c->captured_attention = true;
+    return static_cast<double*>(buffer.ptr);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1690,29 +1752,42 @@ int satori_hip_grouped_attention(satori_hip_context* c, const float* query, cons
     return op_call(c, [&] {
         check_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output);
         const hipStream_t st = op_stream(c, stream);
-        double* scratch = nullptr;
-        if (attention_splits(tokens) > 1) {
-            const size_t need = attention_scratch_bytes(query_heads, head_dim, tokens);
-            auto it = std::find_if(c->attention.begin(), c->attention.end(),
-                                   [&](const std::pair<hipStream_t, DeviceBuffer>& e) { return e.first == st; });
-            if (c->capturing && (it == c->attention.end() || it->second.bytes < need))
-                fail(SATORI_HIP_E_INVALID_OPERATION,
-                     "Run an attention of these heads and tokens once before capturing it (its workspace is allocated "
-                     "on first use).");
-            if (it == c->attention.end()) {
-                c->attention.emplace_back(st, DeviceBuffer{});
-                it = c->attention.end() - 1;
-            }
-            DeviceBuffer& buffer = it->second;
-            if (st == c->stream && c->attention_steps > 0 && buffer.bytes < need)  // captured steps hold it
-                fail(SATORI_HIP_E_INVALID_OPERATION,
-                     "The attention workspace cannot grow while captured steps use it: destroy them, or run the "
-                     "longest attention before capturing.");
-            buffer.reserve(need);
-            if (c->capturing && st == c->stream) c->captured_attention = true;
-            scratch = static_cast<double*>(buffer.ptr);
-        }
+        double* scratch = attention_workspace(c, st, query_heads, head_dim, tokens);
         check_hip(launch_attention(query, keys, values, query_heads, kv_heads, head_dim, tokens, output, scratch, st),
+                  "attention launch");
+    });
+}
+
+int satori_hip_attention_decode(satori_hip_context* c, float* query, const float* query_bias, const float* key,
+                                const float* key_bias, const float* value, const float* value_bias, float* keys,
+                                float* values, int query_heads, int kv_heads, int head_dim, int position,
+                                double frequency_base, int rotary_dimensions, float* output, void* stream) {
+    return op_call(c, [&] {
+        require(key, "key");
+        require(value, "value");
+        if (head_dim <= 0 || query_heads <= 0 || kv_heads <= 0 || position < 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'headDimension')");
+        if (!std::isfinite(frequency_base) || frequency_base <= 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'frequencyBase')");
+        if (rotary_dimensions <= 0 || rotary_dimensions > head_dim || rotary_dimensions % 2 != 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'rotaryDimensions')");
+        if (position == INT32_MAX) fail(SATORI_HIP_E_OVERFLOW, "Arithmetic operation resulted in an overflow.");
+        check_attention(query, keys, values, query_heads, kv_heads, head_dim, position + 1, output);
+        const int64_t qw = static_cast<int64_t>(query_heads) * head_dim, kw = static_cast<int64_t>(kv_heads) * head_dim;
+        const int64_t cache = (static_cast<int64_t>(position) + 1) * kw;
+        // The inputs and the cache must not overlap one another or the query and output (the launch reads the
+        // new key and value while it writes row `position` of the cache).
+        if (any_overlap(key, kw, keys, cache) || any_overlap(key, kw, values, cache) ||
+            any_overlap(value, kw, keys, cache) || any_overlap(value, kw, values, cache) ||
+            any_overlap(query, qw, keys, cache) || any_overlap(query, qw, values, cache) ||
+            any_overlap(keys, cache, values, cache) || any_overlap(key, kw, output, qw) ||
+            any_overlap(value, kw, output, qw))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        const hipStream_t st = op_stream(c, stream);
+        double* scratch = attention_workspace(c, st, query_heads, head_dim, position + 1);
+        check_hip(launch_attention_decode(query, query_bias, key, key_bias, value, value_bias, keys, values, query_heads,
+                                          kv_heads, head_dim, position, frequency_base, rotary_dimensions, output,
+                                          scratch, st),
                   "attention launch");
     });
 }

@@ -14,6 +14,7 @@
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "ops_device.hpp"
+#include "q8k_device.hpp"
 
 // Split-attention partials of the no-allocation entry point: one copy per device, alive until the process
 // ends, shared by every such call on that device (calls that overlap in time race on it). Host code never
@@ -80,6 +81,27 @@ __device__ __forceinline__ float biased(const float* x, const float* bias, int i
     return bias ? __fadd_rn(x[i], bias[i]) : x[i];
 }
 
+// RopeHalf of lane pair (kk, kk + rotary / 2) of one head (TransformerOps.cs:94-114): the angle
+// position / base^(2 kk / rotary) and both rotated lanes in FP64, each rounded once.
+__device__ __forceinline__ void rope_pair(double x, double y, int kk, int position, double base, int rotary, float& a,
+                                          float& b) {
+    const double angle = position / pow(base, 2.0 * kk / rotary);
+    const double sn = sin(angle), cs = cos(angle);
+    a = static_cast<float>(x * cs - y * sn);
+    b = static_cast<float>(x * sn + y * cs);
+}
+
+// Lane j of one head of `v` after the attention-input transform: biased, then rotated when j < rotary.
+__device__ __forceinline__ float input_lane(const float* v, const float* bias, int head_base, int j, int position,
+                                            double base, int rotary) {
+    if (j >= rotary) return biased(v, bias, head_base + j);
+    const int pairs = rotary / 2, kk = j < pairs ? j : j - pairs;
+    float a, b;
+    rope_pair(biased(v, bias, head_base + kk), biased(v, bias, head_base + kk + pairs), kk, position, base, rotary, a,
+              b);
+    return j < pairs ? a : b;
+}
+
 __global__ __launch_bounds__(kThreads) void attention_inputs_kernel(float* q, const float* q_bias, const float* k,
                                                                     const float* k_bias, float* k_out, const float* v,
                                                                     const float* v_bias, float* v_out, int heads,
@@ -95,13 +117,10 @@ __global__ __launch_bounds__(kThreads) void attention_inputs_kernel(float* q, co
         const int64_t index = is_q ? i : i - qp;
         const int head = static_cast<int>(index / pairs), kk = static_cast<int>(index % pairs);
         const int a = head * head_dim + kk, b = a + pairs;
-        const double angle = position / pow(base, 2.0 * kk / rotary);
-        const double sn = sin(angle), cs = cos(angle);
-        const double x = is_q ? biased(q, q_bias, a) : biased(k, k_bias, a);
-        const double y = is_q ? biased(q, q_bias, b) : biased(k, k_bias, b);
+        const float x = is_q ? biased(q, q_bias, a) : biased(k, k_bias, a);
+        const float y = is_q ? biased(q, q_bias, b) : biased(k, k_bias, b);
         float* dst = is_q ? q : k_out;
-        dst[a] = static_cast<float>(x * cs - y * sn);
-        dst[b] = static_cast<float>(x * sn + y * cs);
+        rope_pair(x, y, kk, position, base, rotary, dst[a], dst[b]);
         return;
     }
     i -= qp + kp;
@@ -168,6 +187,31 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const float* gate, con
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= length) return;
     out[i] = swiglu_value(gate[i], up[i]);
+}
+
+// SwiGlu of one 256-element block per wave (four consecutive elements per lane), then the block's Q8_K bytes
+// (Q8KCodec.QuantizeBlock, the quantizer the integer products use): the down projection's activation
+// quantized once by its producer. The FP32 outputs equal swiglu_kernel's.
+__global__ __launch_bounds__(64) void swiglu_q8k_kernel(const float* gate, const float* up, float* out,
+                                                        uint8_t* __restrict__ q8k) {
+    const int block = blockIdx.x, lane = threadIdx.x;
+    const int i0 = 256 * block + 4 * lane;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = swiglu_value(gate[i0 + i], up[i0 + i]);
+    if (out)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i0 + i] = v[i];
+    const Q8KLane q = q8k_quantize_values(v, lane);
+    uint8_t* dst = q8k + static_cast<int64_t>(block) * kQ8KBlockBytes;
+    if (q.zero) {
+        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+        for (int i = lane; i < kQ8KBlockBytes / 4; i += 64) d32[i] = 0u;
+        return;
+    }
+    reinterpret_cast<uint32_t*>(dst + 4)[lane] = q.packed;
+    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(dst + 260)[lane >> 2] = static_cast<int16_t>(q.group_sum);
+    if (lane == 0) reinterpret_cast<float*>(dst)[0] = q.scale;
 }
 
 __global__ __launch_bounds__(kThreads) void add_kernel(const float* left, const float* right, int length, float* out) {
@@ -328,36 +372,73 @@ __device__ __forceinline__ double wave_reduce_256(double v, double* red4, bool t
     return r;
 }
 
+// The attention inputs of the decoded position, applied inside the split attention (DecodeInputs): the query
+// biased and rotated while it is staged, the new key and value (row `position`, the prefix's last) formed by
+// the workgroups whose split holds that row and written to their cache slots by one of them.
+struct DecodeInputs {
+    const float* q_bias;
+    const float* k_new;
+    const float* k_bias;
+    const float* v_new;
+    const float* v_bias;
+    int position;
+    int rotary;
+    double base;
+};
+
+template <bool INPUTS>
 __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const float* __restrict__ q,
                                                                         const float* __restrict__ k,
                                                                         const float* __restrict__ v, int query_heads,
                                                                         int kv_heads, int head_dim, int tokens, int per,
-                                                                        double* __restrict__ partial) {
+                                                                        double* __restrict__ partial, DecodeInputs in,
+                                                                        float* k_cache, float* v_cache) {
     extern __shared__ double es[];  // this split's exponentials (per), then the staged query lanes
     __shared__ double red[kSplitThreads];
     const int head = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
     const int t0 = static_cast<int>(min(static_cast<int64_t>(split) * per, static_cast<int64_t>(tokens)));
     const int t1 = min(tokens, t0 + per);
-    const int kv_head = head / (query_heads / kv_heads);
+    const int group = query_heads / kv_heads;
+    const int kv_head = head / group;
     const int kv_width = kv_heads * head_dim;
     const double scale = 1.0 / __dsqrt_rn(static_cast<double>(head_dim));
     const float* qh = q + static_cast<int64_t>(head) * head_dim;
     float* qs = reinterpret_cast<float*>(es + per);
     const bool staged = head_dim <= kStagedQuery;
     const float* qsrc = staged ? qs : qh;
+    // With the inputs fused, the new row (the last token) is held in LDS, not read from the cache.
+    const bool has_new = INPUTS && t0 <= in.position && in.position < t1;
+    float* ks_new = qs + head_dim;
+    float* vs_new = ks_new + head_dim;
     // The first 16 values of this thread's output lane and token half are loaded before anything else, so
     // they arrive while the scores are computed.
     const int count = t1 - t0, half = (count + 1) / 2;
     const int vj0 = threadIdx.x & 127, vgroup = threadIdx.x >> 7;
     const int va = t0 + vgroup * half, vb = min(t1, va + half);
+    const bool v_new_here = has_new && vb == t1 && va < vb;  // this token half ends with the new row
+    const int vbc = v_new_here ? vb - 1 : vb;                // the half's rows read from the cache
     float vpre[16];
     if (vj0 < head_dim) {
         const float* vj = v + kv_head * head_dim + vj0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) vpre[i] = va + i < vb ? vj[static_cast<int64_t>(va + i) * kv_width] : 0.0f;
+        for (int i = 0; i < 16; ++i) vpre[i] = va + i < vbc ? vj[static_cast<int64_t>(va + i) * kv_width] : 0.0f;
     }
     if (staged)
-        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) qs[j] = qh[j];
+        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads)
+            qs[j] = INPUTS ? input_lane(q, in.q_bias, head * head_dim, j, in.position, in.base, in.rotary) : qh[j];
+    if (INPUTS && has_new) {
+        const bool writer = head % group == 0;
+        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) {
+            const float kj = input_lane(in.k_new, in.k_bias, kv_head * head_dim, j, in.position, in.base, in.rotary);
+            const float vj = biased(in.v_new, in.v_bias, kv_head * head_dim + j);
+            ks_new[j] = kj;
+            vs_new[j] = vj;
+            if (writer) {
+                k_cache[static_cast<int64_t>(in.position) * kv_width + kv_head * head_dim + j] = kj;
+                v_cache[static_cast<int64_t>(in.position) * kv_width + kv_head * head_dim + j] = vj;
+            }
+        }
+    }
     __syncthreads();
     // Scores: eight threads per token, thread p summing lanes [p * piece, (p + 1) * piece) of the key row in
     // order (16-byte loads, all in flight, when the eighths are whole quads), the eight partial sums then
@@ -366,10 +447,11 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
     const bool quads = (head_dim & 31) == 0;
     const int piece = (head_dim + 7) / 8, p8 = threadIdx.x & 7;
     const int j_lo = min(head_dim, p8 * piece), j_hi = min(head_dim, j_lo + piece);
-    for (int base = t0; base < t1; base += kSplitThreads / 8) {
+    const int ts = has_new ? t1 - 1 : t1;  // scores of cached rows
+    for (int base = t0; base < ts; base += kSplitThreads / 8) {
         const int t = base + (threadIdx.x >> 3);
         double dot = 0;
-        if (t < t1) {
+        if (t < ts) {
             const float* kt = k + static_cast<int64_t>(t) * kv_width + kv_head * head_dim;
             if (quads) {
                 const float* kp = kt + j_lo;
@@ -397,12 +479,29 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
         }
         red[threadIdx.x] = dot;
         __syncthreads();
-        if (p8 == 0 && t < t1) {
+        if (p8 == 0 && t < ts) {
             double total = red[threadIdx.x];
 #pragma unroll
             for (int i = 1; i < 8; ++i) total = total + red[threadIdx.x + i];
             const double sc = total * scale;
             es[t - t0] = sc;
+            local_max = fmax(local_max, sc);
+        }
+        __syncthreads();
+    }
+    if (INPUTS && has_new) {
+        // The new row's score, by eight threads over the same lane ranges, in the same order, as a cached row.
+        double dot = 0;
+        if (threadIdx.x < 8)
+            for (int j = j_lo; j < j_hi; ++j) dot = dot + static_cast<double>(qsrc[j]) * static_cast<double>(ks_new[j]);
+        red[threadIdx.x] = dot;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double total = red[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) total = total + red[i];
+            const double sc = total * scale;
+            es[t1 - 1 - t0] = sc;
             local_max = fmax(local_max, sc);
         }
         __syncthreads();
@@ -430,17 +529,18 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
             if (j0 == 0) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    if (va + i < vb) sum = sum + es[va + i - t0] * static_cast<double>(vpre[i]);
-                t = min(vb, va + 16);
+                    if (va + i < vbc) sum = sum + es[va + i - t0] * static_cast<double>(vpre[i]);
+                t = min(vbc, va + 16);
             }
-            for (; t + 16 <= vb; t += 16) {
+            for (; t + 16 <= vbc; t += 16) {
                 float vt[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) vt[i] = vj[static_cast<int64_t>(t + i) * kv_width];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) sum = sum + es[t + i - t0] * static_cast<double>(vt[i]);
             }
-            for (; t < vb; ++t) sum = sum + es[t - t0] * static_cast<double>(vj[static_cast<int64_t>(t) * kv_width]);
+            for (; t < vbc; ++t) sum = sum + es[t - t0] * static_cast<double>(vj[static_cast<int64_t>(t) * kv_width]);
+            if (v_new_here) sum = sum + es[t1 - 1 - t0] * static_cast<double>(vs_new[j]);  // the last row, last
         }
         red[threadIdx.x] = sum;
         __syncthreads();
@@ -454,9 +554,21 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
 // shuffles); the splits' weights exp(m_s - M) are formed once per split into LDS. Output lane j is summed over
 // the splits in split order by `lanes_per` threads, each over a contiguous share of the splits with 16 loads
 // in flight, their partial sums then added in share order, and divided by the total.
+template <bool INPUTS>
 __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(const double* __restrict__ partial,
                                                                           int splits, int head_dim,
-                                                                          float* __restrict__ out) {
+                                                                          float* __restrict__ out, float* q,
+                                                                          DecodeInputs in) {
+    if (INPUTS) {
+        // The query rotated in place, as the separate attention-inputs launch leaves it (the split workgroups
+        // have all read the original by now).
+        const int pairs = in.rotary / 2, base = blockIdx.x * head_dim;
+        for (int kk = threadIdx.x; kk < pairs; kk += kSplitThreads) {
+            const float x = biased(q, in.q_bias, base + kk), y = biased(q, in.q_bias, base + kk + pairs);
+            rope_pair(x, y, kk, in.position, in.base, in.rotary, q[base + kk], q[base + kk + pairs]);
+        }
+        for (int j = in.rotary + threadIdx.x; j < head_dim; j += kSplitThreads) q[base + j] = biased(q, in.q_bias, base + j);
+    }
     __shared__ double weight[kCombineWeights];
     __shared__ double lane_part[kSplitThreads];
     __shared__ double red4[kSplitThreads / 64];
@@ -584,6 +696,13 @@ hipError_t launch_swiglu(const float* gate, const float* up, int length, float* 
     return hipGetLastError();
 }
 
+hipError_t launch_swiglu_q8k(const float* gate, const float* up, int length, float* out, uint8_t* q8k,
+                             hipStream_t stream) {
+    if (length <= 0 || length % 256 != 0) return hipErrorInvalidValue;
+    swiglu_q8k_kernel<<<length / 256, 64, 0, stream>>>(gate, up, out, q8k);
+    return hipGetLastError();
+}
+
 hipError_t launch_add(const float* left, const float* right, int length, float* out, hipStream_t stream) {
     add_kernel<<<grid_for(length), kThreads, 0, stream>>>(left, right, length, out);
     return hipGetLastError();
@@ -637,6 +756,46 @@ bool attention_supported(int tokens, int head_dim) {
     return split_lds_bytes(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
 }
 
+namespace {
+
+size_t split_lds_bytes_inputs(int per, int head_dim) {
+    return static_cast<size_t>(per) * sizeof(double) + static_cast<size_t>(3) * head_dim * sizeof(float);
+}
+
+// The fused form needs the split path with the query staged and room for the new row's key and value.
+bool decode_fusable(int tokens, int head_dim) {
+    const int splits = attention_splits(tokens);
+    if (splits == 1 || head_dim > kStagedQuery) return false;
+    const int per = (tokens + splits - 1) / splits;
+    return split_lds_bytes_inputs(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
+}
+
+}  // namespace
+
+hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k_new, const float* k_bias,
+                                   const float* v_new, const float* v_bias, float* k_cache, float* v_cache,
+                                   int query_heads, int kv_heads, int head_dim, int position, double base, int rotary,
+                                   float* out, double* partials, hipStream_t stream) {
+    const int tokens = position + 1;
+    const int64_t kv_width = static_cast<int64_t>(kv_heads) * head_dim;
+    if (!decode_fusable(tokens, head_dim)) {  // the two launches it stands for
+        hipError_t e = launch_attention_inputs(q, q_bias, k_new, k_bias, k_cache + position * kv_width, v_new, v_bias,
+                                               v_cache + position * kv_width, query_heads, kv_heads, head_dim,
+                                               position, base, rotary, stream);
+        if (e != hipSuccess) return e;
+        return launch_attention(q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, out, partials, stream);
+    }
+    if (!partials) return hipErrorInvalidValue;
+    const int splits = attention_splits(tokens);
+    const int per = (tokens + splits - 1) / splits;
+    const DecodeInputs in{q_bias, k_new, k_bias, v_new, v_bias, position, rotary, base};
+    attention_split_kernel<true><<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes_inputs(per, head_dim),
+                                   stream>>>(q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, per, partials,
+                                             in, k_cache, v_cache);
+    attention_combine_kernel<true><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out, q, in);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention(const float* q, const float* k, const float* v, int query_heads, int kv_heads,
                             int head_dim, int tokens, float* out, double* partials, hipStream_t stream) {
     if (!attention_supported(tokens, head_dim)) return hipErrorInvalidValue;
@@ -648,9 +807,10 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
     }
     if (!partials) return hipErrorInvalidValue;
     const int per = (tokens + splits - 1) / splits;
-    attention_split_kernel<<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes(per, head_dim), stream>>>(
-        q, k, v, query_heads, kv_heads, head_dim, tokens, per, partials);
-    attention_combine_kernel<<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out);
+    attention_split_kernel<false><<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes(per, head_dim), stream>>>(
+        q, k, v, query_heads, kv_heads, head_dim, tokens, per, partials, DecodeInputs{}, nullptr, nullptr);
+    attention_combine_kernel<false><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out,
+                                                                              nullptr, DecodeInputs{});
     return hipGetLastError();
 }
 

@@ -12,9 +12,11 @@ cache writes) are one launch and each residual add shares a launch with the RmsN
 layer instead of 14, with bit-identical results. Folded (`folded=True`), each residual add + RmsNorm is
 computed inside the projection launch that consumes it (group input transforms; the residual alternates
 between two buffers, since the launch that writes it is also read by its other workgroups): 7 launches per
-layer, again with bit-identical results. SwiGlu stays its own launch: folded into the down projection, every
+layer, again with bit-identical results. SwiGlu stays its own launch (folded into the down projection, every
 workgroup would evaluate the FP64 exponentials of the whole 8960-wide vector, which costs more than the
-launch (measured: 2.12 ms per token with it folded, 1.73 ms without, 1.91 ms fused).
+launch: measured 2.12 ms per token with it folded, 1.73 ms without, 1.91 ms fused); in the folded sequence it
+also writes the Q8_K bytes of its output, which the down projection reads instead of quantizing in every
+workgroup.
 """
 from __future__ import annotations
 
@@ -75,6 +77,7 @@ class DeviceDecoder:
         self.context_vec, self.projected = buf(self.q_width), buf(c.hidden)
         self.gate, self.up, self.activated = buf(c.ffn), buf(c.ffn), buf(c.ffn)
         self.logits = buf(output.rows)
+        self.activated_q8k = buf(c.ffn // 256 * 73)  # Q8_K bytes of the down projection's input (292 per block)
         self.zero_kv = buf(self.kv_width)
         self.keys = [buf(c.max_tokens * self.kv_width) for _ in layers]
         self.values = [buf(c.max_tokens * self.kv_width) for _ in layers]
@@ -108,7 +111,9 @@ class DeviceDecoder:
                 gateup = HipGroup(ctx, [m["gate"], m["up"]], [self.normed] * 2, [self.gate, self.up], True)
                 gateup.set_input_add_rms_norm(self.residual_b, self.projected, vec["ffn_norm"], c.epsilon,
                                               self.residual)
-                folded.append({"qkv": qkv, "gateup": gateup})
+                down = HipGroup(ctx, [m["down"]], [self.activated], [self.projected], True)
+                down.set_input_q8k(self.activated_q8k)
+                folded.append({"qkv": qkv, "gateup": gateup, "down": down})
             final = HipGroup(ctx, [self.output], [self.normed], [self.logits], True)
             final.set_input_add_rms_norm(self.residual, self.projected, self.output_norm, c.epsilon, self.residual_b)
             self._folded = (folded, final)
@@ -118,8 +123,9 @@ class DeviceDecoder:
         """Enqueues one token at `position` (keys/values of positions < position are in the cache). Fused:
         the bias adds, RoPE and cache writes of a layer's attention inputs are one launch, and every residual
         add shares its launch with the RmsNorm that follows (bit-identical to the unfused sequence). Folded:
-        as fused, with the residual adds and RmsNorms computed inside the projections that consume them
-        (bit-identical as well; the residual after the token is left in the second buffer)."""
+        as fused, with the residual adds and RmsNorms computed inside the projections that consume them and the
+        attention inputs inside the split attention (bit-identical as well; the residual after the token is left
+        in the second buffer)."""
         c, ops = self.cfg, self.ops
         if not 0 <= position < c.max_tokens:
             raise ValueError("position outside the key/value cache")
@@ -127,18 +133,14 @@ class DeviceDecoder:
         if folded:
             groups, final = self._folded_groups()
             for layer, (g, fg, vec) in enumerate(zip(self.groups, groups, self.vectors)):
-                k_slot = self.keys[layer] + 4 * position * self.kv_width
-                v_slot = self.values[layer] + 4 * position * self.kv_width
                 fg["qkv"].execute()
-                ops.attention_inputs(self.q, vec.get("q_bias", 0), self.k, vec.get("k_bias", 0), k_slot, self.v,
-                                     vec.get("v_bias", 0), v_slot, c.heads, c.kv_heads, c.head_dim, position,
-                                     c.rope_base, c.head_dim)
-                ops.grouped_attention(self.q, self.keys[layer], self.values[layer], c.heads, c.kv_heads,
-                                      c.head_dim, position + 1, self.context_vec)
+                ops.attention_decode(self.q, vec.get("q_bias", 0), self.k, vec.get("k_bias", 0), self.v,
+                                     vec.get("v_bias", 0), self.keys[layer], self.values[layer], c.heads, c.kv_heads,
+                                     c.head_dim, position, c.rope_base, c.head_dim, self.context_vec)
                 g["o"].execute()
                 fg["gateup"].execute()
-                ops.swiglu(self.gate, self.up, c.ffn, self.activated)
-                g["down"].execute()
+                ops.swiglu_q8k(self.gate, self.up, c.ffn, 0, self.activated_q8k)
+                fg["down"].execute()
             final.execute()
             return
         if fused:
@@ -186,8 +188,8 @@ class DeviceDecoder:
         over several workgroups per head and combined by a second kernel, one more launch per layer."""
         split = position is not None and position + 1 > 32
         extra = len(self.layers) if split else 0
-        if folded:
-            return 1 + 7 * len(self.layers) + 1 + extra
+        if folded:  # attention inputs inside the split attention, or beside the one-workgroup attention
+            return 1 + 7 * len(self.layers) + 1
         if fused:
             return 2 + 9 * len(self.layers) + 1 + extra
         per_layer = 14 if all("q_bias" in v for v in self.vectors) else 13

@@ -351,3 +351,55 @@ def test_split_attentions_on_two_streams_do_not_share_a_workspace(context):
             rt.hipStreamDestroy(s)
         for p in buffers:
             context.free(p)
+
+
+@pytest.mark.parametrize("position,heads,kv_heads,head_dim,rotary,biases", [
+    (0, 12, 2, 128, 128, True), (31, 12, 2, 128, 128, True), (32, 12, 2, 128, 128, True),
+    (511, 12, 2, 128, 128, True), (4095, 12, 2, 128, 128, False), (70000, 4, 2, 128, 64, True),
+    (300, 14, 2, 80, 80, True), (100, 3, 3, 24, 16, False), (65, 4, 1, 1024, 512, True)])
+def test_attention_decode_equals_inputs_then_attention(context, position, heads, kv_heads, head_dim, rotary, biases):
+    # satori_hip_attention_decode (the attention inputs applied inside the split attention) against
+    # satori_hip_attention_inputs + satori_hip_grouped_attention: the output, the rotated query and the cache
+    # rows written at `position` are the same bits; the rest of the cache is untouched.
+    g = rng(position * 31 + head_dim)
+    qw, kw = heads * head_dim, kv_heads * head_dim
+    tokens = position + 1
+    q = g.standard_normal(qw).astype(np.float32)
+    k = g.standard_normal(kw).astype(np.float32)
+    v = g.standard_normal(kw).astype(np.float32)
+    qb, kb, vb = ((g.standard_normal(n) * 0.1).astype(np.float32) for n in (qw, kw, kw))
+    cache_k = (g.standard_normal(tokens * kw) * 0.3).astype(np.float32)
+    cache_v = g.standard_normal(tokens * kw).astype(np.float32)
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    ops = S.DeviceOps(context)
+    try:
+        results = []
+        for fused in (False, True):
+            dq, dk, dv = dev(q), dev(k), dev(v)
+            dqb, dkb, dvb = (dev(a) if biases else 0 for a in (qb, kb, vb))
+            dck, dcv = dev(cache_k), dev(cache_v)
+            out = dev(np.zeros(qw, np.float32))
+            if fused:
+                ops.attention_decode(dq, dqb, dk, dkb, dv, dvb, dck, dcv, heads, kv_heads, head_dim, position, 1e6,
+                                     rotary, out)
+            else:
+                ops.attention_inputs(dq, dqb, dk, dkb, dck + 4 * position * kw, dv, dvb, dcv + 4 * position * kw,
+                                     heads, kv_heads, head_dim, position, 1e6, rotary)
+                ops.grouped_attention(dq, dck, dcv, heads, kv_heads, head_dim, tokens, out)
+            results.append([context.download(np.zeros(n, np.float32), p) for p, n in
+                            ((out, qw), (dq, qw), (dck, tokens * kw), (dcv, tokens * kw))])
+        for name, a, b in zip(("output", "query", "keys", "values"), *results):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+        assert np.array_equal(results[1][2][:position * kw], cache_k[:position * kw])
+        expected = O.grouped_attention(results[0][1], results[0][2], results[0][3], heads, kv_heads, head_dim, tokens)
+        _within_ulp(results[1][0], expected, "fused attention vs oracle")
+    finally:
+        for p in buffers:
+            context.free(p)

@@ -1362,6 +1362,87 @@ def test_group_input_transforms_equal_separate_operators(context, fmt):
             m.dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("columns", [1536, 8960, 29696])
+def test_q8k_input_from_the_producer_equals_quantizing_in_the_launch(context, fmt, columns):
+    # SwiGlu writing the Q8_K bytes of its output (satori_hip_swiglu_q8k), the device quantizer
+    # (satori_hip_quantize_q8k_device) and a group reading those bytes (SATORI_HIP_INPUT_Q8K): the bytes are
+    # the oracle's Q8KCodec.QuantizeRow of the FP32 values, and the group's outputs equal the plain group's
+    # over the FP32 input bit for bit.
+    g = rng(6262 + columns + int(fmt))
+    rows = [200, 96]
+    mats = [context.create(S.quantize_weights((g.standard_normal((r, columns)) * 0.02).astype(np.float32), r,
+                                              columns, fmt), S.QuantizedMatrixShape(r, columns, fmt)) for r in rows]
+    gate = (g.standard_normal(columns) * 4).astype(np.float32)
+    up = g.standard_normal(columns).astype(np.float32)
+    gate[256:512] = -200.0  # a block whose SwiGlu outputs are all (negative) zeros
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    q8k_bytes = columns // 256 * 292
+    dgate, dup = dev(gate), dev(up)
+    dact, dact2 = dev(np.zeros(columns, np.float32)), dev(np.zeros(columns, np.float32))
+    dq, dq2 = dev(np.zeros(q8k_bytes // 4, np.float32)), dev(np.zeros(q8k_bytes // 4, np.float32))
+    plain_out = [dev(np.zeros(r, np.float32)) for r in rows]
+    q8k_out = [dev(np.zeros(r, np.float32)) for r in rows]
+    plain = S.HipGroup(context, mats, [dact, dact], plain_out, True)
+    fed = S.HipGroup(context, mats, [dact, dact], q8k_out, True)
+    ops = S.DeviceOps(context)
+    try:
+        ops.swiglu(dgate, dup, columns, dact)
+        ops.swiglu_q8k(dgate, dup, columns, dact2, dq)
+        act = context.download(np.zeros(columns, np.float32), dact)
+        assert np.array_equal(context.download(np.zeros(columns, np.float32), dact2).view(np.uint32), act.view(np.uint32))
+        q = context.download(np.zeros(q8k_bytes, np.uint8), dq)
+        assert np.array_equal(q, O.q8k_quantize_row(act)), "SwiGlu Q8_K bytes"
+        ops.quantize_q8k(dact, columns, 1, dq2)
+        assert np.array_equal(context.download(np.zeros(q8k_bytes, np.uint8), dq2), q), "device quantizer"
+        ops.swiglu_q8k(dgate, dup, columns, 0, dq2)  # no FP32 output
+        assert np.array_equal(context.download(np.zeros(q8k_bytes, np.uint8), dq2), q)
+        plain.execute()
+        fed.set_input_q8k(dq)
+        fed.execute()
+        for k, r in enumerate(rows):
+            want = context.download(np.zeros(r, np.float32), plain_out[k])
+            got = context.download(np.zeros(r, np.float32), q8k_out[k])
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"member {k}"
+        with pytest.raises(S.NotSupportedException):
+            fed.execute_batch(16)
+        with pytest.raises(S.ArgumentException):  # not a multiple of 256
+            ops.swiglu_q8k(dgate, dup, 300, 0, dq)
+    finally:
+        plain.dispose()
+        fed.dispose()
+        for p in buffers:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
+def test_device_q8k_quantizer_positions_match_oracle(context):
+    g = rng(808)
+    columns, positions = 2048, 5
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    x[1] = 0
+    x[2, :256] = 1e-30
+    dx = context.alloc(x.nbytes)
+    dq = context.alloc(positions * columns // 256 * 292)
+    try:
+        context.upload(dx, x)
+        S.DeviceOps(context).quantize_q8k(dx, columns, positions, dq)
+        got = context.download(np.zeros(positions * columns // 256 * 292, np.uint8), dq).reshape(positions, -1)
+        for p in range(positions):
+            assert np.array_equal(got[p], O.q8k_quantize_row(x[p])), p
+    finally:
+        context.free(dx)
+        context.free(dq)
+
+
 def _check_status(code):
     S._check(code)
 
@@ -1461,7 +1542,7 @@ def test_device_decode_token_matches_host_composition(context):
         dec.enqueue(7, 41, folded=True)  # eager work between replays
         folded.execute()
         assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), ("folded", replay)
-    assert dec.launches_per_token(folded=True, position=position) == 2 + 8 * n_layers  # split attention
+    assert dec.launches_per_token(folded=True, position=position) == 2 + 7 * n_layers  # inputs inside the attention
     with pytest.raises(S.ArgumentException):
         dev_layers[0]["q"].dispose()  # held by the decoder's group
     with pytest.raises(S.InvalidOperationException):
