@@ -328,17 +328,26 @@ int satori_hip_attention_inputs(satori_hip_context* context, float* query, const
 int satori_hip_grouped_attention(satori_hip_context* context, const float* query, const float* keys,
                                  const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
                                  float* output, void* stream);
+/* The sines and cosines of the RoPE angles (RopeHalf, TransformerOps.cs:94-114) of positions 0 .. positions - 1
+ * for (rotary_dimensions, frequency_base), as the rotation kernels compute them: row p holds the
+ * rotary_dimensions / 2 sines then the cosines, as doubles (positions * rotary_dimensions of them). A table for
+ * satori_hip_attention_decode, computed once per session instead of once per token. */
+int satori_hip_rope_table(satori_hip_context* context, int positions, int rotary_dimensions, double frequency_base,
+                          double* table, void* stream);
 /* The attention of one decode position with its inputs (DenseForward.cs:128-152):
  * satori_hip_attention_inputs(query, query_bias, key, key_bias, keys + position * kv_width, value, value_bias,
  * values + position * kv_width, ...) then satori_hip_grouped_attention(query, keys, values, ..., position + 1,
  * output), with the same results bit for bit (the query rotated in place, the key and value written to row
  * `position` of the caches); past 32 tokens the transform runs inside the split attention's launches, one
  * launch fewer. Biases may be NULL. keys/values are the caches [position + 1][kv_heads * head_dim]; key and
- * value must not overlap them. The workspace rules are those of satori_hip_grouped_attention. */
+ * value must not overlap them. rope_table is a satori_hip_rope_table table of at least position + 1 rows for
+ * (rotary_dimensions, frequency_base), or NULL (the angles are then computed in the launch). The workspace rules
+ * are those of satori_hip_grouped_attention. */
 int satori_hip_attention_decode(satori_hip_context* context, float* query, const float* query_bias, const float* key,
                                 const float* key_bias, const float* value, const float* value_bias, float* keys,
                                 float* values, int query_heads, int kv_heads, int head_dim, int position,
-                                double frequency_base, int rotary_dimensions, float* output, void* stream);
+                                double frequency_base, int rotary_dimensions, const double* rope_table, float* output,
+                                void* stream);
 /* satori_hip_grouped_attention without any allocation. No counterpart in the reference: for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, hosts that forbid
  * allocation after start-up). Same arguments, checks and results (the same kernels); the split partials go

@@ -1023,13 +1023,17 @@ class DeviceOps:
 
     def attention_decode(self, q: int, q_bias: int, k: int, k_bias: int, v: int, v_bias: int, keys: int, values: int,
                          heads: int, kv_heads: int, head_dim: int, position: int, base: float, rotary: int,
-                         out: int) -> None:
-        """attention_inputs (cache slots of row `position`) then grouped_attention over position + 1 rows, in one
-        or two launches fewer; biases may be 0."""
+                         out: int, rope_table: int = 0) -> None:
+        """attention_inputs (cache slots of row `position`) then grouped_attention over position + 1 rows, one
+        launch fewer; biases and rope_table (a rope_table() table) may be 0."""
         _check(_ffi.lib().satori_hip_attention_decode(self._h, self._p(q), self._p(q_bias), self._p(k), self._p(k_bias),
                                                       self._p(v), self._p(v_bias), self._p(keys), self._p(values), heads,
-                                                      kv_heads, head_dim, position, float(base), rotary, self._p(out),
-                                                      None))
+                                                      kv_heads, head_dim, position, float(base), rotary,
+                                                      self._p(rope_table) if rope_table else None, self._p(out), None))
+
+    def rope_table(self, positions: int, rotary: int, base: float, table: int) -> None:
+        """RoPE sines and cosines of positions 0 .. positions - 1 into `table` (positions * rotary doubles)."""
+        _check(_ffi.lib().satori_hip_rope_table(self._h, positions, rotary, float(base), self._p(table), None))
 
     def grouped_attention_static(self, q: int, k: int, v: int, query_heads: int, kv_heads: int, head_dim: int,
                                  tokens: int, out: int, stream: int = 0) -> None:

@@ -72,7 +72,8 @@ SIGNATURES = {
     "satori_hip_quantize_q8k_device": (I, [P, P, I, I, P, P]),
     "satori_hip_grouped_attention": (I, [P, P, P, P, I, I, I, I, P, P]),
     "satori_hip_grouped_attention_static": (I, [P, P, P, P, I, I, I, I, P, P]),
-    "satori_hip_attention_decode": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, ctypes.c_double, I, P, P]),
+    "satori_hip_attention_decode": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, ctypes.c_double, I, P, P, P]),
+    "satori_hip_rope_table": (I, [P, I, I, ctypes.c_double, P, P]),
     "satori_hip_add_rms_norm": (I, [P, P, P, P, ctypes.c_float, I, P, P]),
     "satori_hip_attention_inputs": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, ctypes.c_double, I, P]),
     "satori_hip_matrix_decode_row": (I, [P, I, P, P]),

@@ -220,10 +220,13 @@ bool attention_supported(int tokens, int head_dim);
 // The attention-input transform of the decoded position (launch_attention_inputs with the cache slots of row
 // `position`) followed by the attention over the position + 1 cached rows, with the same results bit for bit;
 // on the split path the transform runs inside the split and combine launches (one launch fewer).
+// `rope` is row `position` of a launch_rope_table table for (rotary, base), or null (computed in the launch).
 hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k_new, const float* k_bias,
                                    const float* v_new, const float* v_bias, float* k_cache, float* v_cache,
                                    int query_heads, int kv_heads, int head_dim, int position, double base, int rotary,
-                                   float* out, double* partials, hipStream_t stream);
+                                   const double* rope, float* out, double* partials, hipStream_t stream);
+// RoPE sines and cosines of positions 0 .. positions - 1: row p = rotary / 2 sines, then the cosines (doubles).
+hipError_t launch_rope_table(int positions, int rotary, double base, double* table, hipStream_t stream);
 // Partials one call of `tokens` tokens writes (0 when one workgroup per head needs none).
 size_t attention_partials_bytes(int query_heads, int head_dim, int tokens);
 // The no-allocation attention's partials: a file-scope device array of kStaticAttentionBytes per device. Its

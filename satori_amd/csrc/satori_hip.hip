@@ -1761,7 +1761,8 @@ int satori_hip_grouped_attention(satori_hip_context* c, const float* query, cons
 int satori_hip_attention_decode(satori_hip_context* c, float* query, const float* query_bias, const float* key,
                                 const float* key_bias, const float* value, const float* value_bias, float* keys,
                                 float* values, int query_heads, int kv_heads, int head_dim, int position,
-                                double frequency_base, int rotary_dimensions, float* output, void* stream) {
+                                double frequency_base, int rotary_dimensions, const double* rope_table, float* output,
+                                void* stream) {
     return op_call(c, [&] {
         require(key, "key");
         require(value, "value");
@@ -1785,10 +1786,25 @@ int satori_hip_attention_decode(satori_hip_context* c, float* query, const float
             fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
         const hipStream_t st = op_stream(c, stream);
         double* scratch = attention_workspace(c, st, query_heads, head_dim, position + 1);
+        const double* rope = rope_table ? rope_table + static_cast<int64_t>(position) * rotary_dimensions : nullptr;
         check_hip(launch_attention_decode(query, query_bias, key, key_bias, value, value_bias, keys, values, query_heads,
-                                          kv_heads, head_dim, position, frequency_base, rotary_dimensions, output,
+                                          kv_heads, head_dim, position, frequency_base, rotary_dimensions, rope, output,
                                           scratch, st),
                   "attention launch");
+    });
+}
+
+int satori_hip_rope_table(satori_hip_context* c, int positions, int rotary_dimensions, double frequency_base,
+                          double* table, void* stream) {
+    return op_call(c, [&] {
+        require(table, "table");
+        if (positions <= 0) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "positions must be positive.");
+        if (!std::isfinite(frequency_base) || frequency_base <= 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'frequencyBase')");
+        if (rotary_dimensions <= 0 || rotary_dimensions % 2 != 0)
+            fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Specified argument was out of the range of valid values. (Parameter 'rotaryDimensions')");
+        check_hip(launch_rope_table(positions, rotary_dimensions, frequency_base, table, op_stream(c, stream)),
+                  "rope table launch");
     });
 }
 

@@ -82,24 +82,23 @@ __device__ __forceinline__ float biased(const float* x, const float* bias, int i
 }
 
 // RopeHalf of lane pair (kk, kk + rotary / 2) of one head (TransformerOps.cs:94-114): the angle
-// position / base^(2 kk / rotary) and both rotated lanes in FP64, each rounded once.
-__device__ __forceinline__ void rope_pair(double x, double y, int kk, int position, double base, int rotary, float& a,
-                                          float& b) {
+// position / base^(2 kk / rotary) in FP64, then both rotated lanes in FP64, each rounded once.
+__device__ __forceinline__ void rope_angle(int kk, int position, double base, int rotary, double& sn, double& cs) {
     const double angle = position / pow(base, 2.0 * kk / rotary);
-    const double sn = sin(angle), cs = cos(angle);
+    sn = sin(angle);
+    cs = cos(angle);
+}
+
+__device__ __forceinline__ void rope_apply(double x, double y, double sn, double cs, float& a, float& b) {
     a = static_cast<float>(x * cs - y * sn);
     b = static_cast<float>(x * sn + y * cs);
 }
 
-// Lane j of one head of `v` after the attention-input transform: biased, then rotated when j < rotary.
-__device__ __forceinline__ float input_lane(const float* v, const float* bias, int head_base, int j, int position,
-                                            double base, int rotary) {
-    if (j >= rotary) return biased(v, bias, head_base + j);
-    const int pairs = rotary / 2, kk = j < pairs ? j : j - pairs;
-    float a, b;
-    rope_pair(biased(v, bias, head_base + kk), biased(v, bias, head_base + kk + pairs), kk, position, base, rotary, a,
-              b);
-    return j < pairs ? a : b;
+__device__ __forceinline__ void rope_pair(double x, double y, int kk, int position, double base, int rotary, float& a,
+                                          float& b) {
+    double sn, cs;
+    rope_angle(kk, position, base, rotary, sn, cs);
+    rope_apply(x, y, sn, cs, a, b);
 }
 
 __global__ __launch_bounds__(kThreads) void attention_inputs_kernel(float* q, const float* q_bias, const float* k,
@@ -187,6 +186,17 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const float* gate, con
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= length) return;
     out[i] = swiglu_value(gate[i], up[i]);
+}
+
+// The RoPE angles' sines and cosines of `positions` positions (rope_angle, the same FP64 values the rotation
+// kernels compute): row p holds the rotary / 2 sines, then the cosines.
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(int positions, int rotary, double base, double* table) {
+    const int pairs = rotary / 2;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= static_cast<int64_t>(positions) * pairs) return;
+    const int p = static_cast<int>(i / pairs), kk = static_cast<int>(i % pairs);
+    double* row = table + static_cast<int64_t>(p) * rotary;
+    rope_angle(kk, p, base, rotary, row[kk], row[pairs + kk]);
 }
 
 // SwiGlu of one 256-element block per wave (four consecutive elements per lane), then the block's Q8_K bytes
@@ -381,6 +391,7 @@ struct DecodeInputs {
     const float* k_bias;
     const float* v_new;
     const float* v_bias;
+    const double* rope;  // the position's sines then cosines (launch_rope_table), or null: computed here
     int position;
     int rotary;
     double base;
@@ -410,6 +421,29 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
     const bool has_new = INPUTS && t0 <= in.position && in.position < t1;
     float* ks_new = qs + head_dim;
     float* vs_new = ks_new + head_dim;
+    // With the inputs fused (heads of at most 256 lanes), thread j owns lane j of the head: it loads what the
+    // transformed query lane needs (and, where the new row lives, the key and value lanes) before anything
+    // else, then rotates them after the cache loads below are issued.
+    // Every thread issues the same loads (lane indices clamped, absent operands replaced by present ones whose
+    // values are then unused), so the waits below are counted statically and do not cover the cache loads.
+    const int pairs = in.rotary / 2, jl = min(static_cast<int>(threadIdx.x), head_dim - 1);
+    const bool rot = jl < in.rotary;
+    const int kk = jl < pairs ? jl : (rot ? jl - pairs : 0);
+    const int ia = rot ? kk : jl, ib = rot ? kk + pairs : jl;  // the lane pair read (one lane past the rotation)
+    float qx = 0.0f, qy = 0.0f, qxb = 0.0f, qyb = 0.0f, kx = 0.0f, ky = 0.0f, kxb = 0.0f, kyb = 0.0f;
+    float vl = 0.0f, vlb = 0.0f;
+    double sn = 0.0, cs = 0.0;
+    if (INPUTS) {
+        const int qb = head * head_dim;
+        const float* qbias = in.q_bias ? in.q_bias : q;
+        const double* rope = in.rope ? in.rope : partial;
+        qx = q[qb + ia];
+        qy = q[qb + ib];
+        qxb = qbias[qb + ia];
+        qyb = qbias[qb + ib];
+        sn = rope[kk];
+        cs = rope[pairs + kk];
+    }
     // The first 16 values of this thread's output lane and token half are loaded before anything else, so
     // they arrive while the scores are computed.
     const int count = t1 - t0, half = (count + 1) / 2;
@@ -423,31 +457,72 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
 #pragma unroll
         for (int i = 0; i < 16; ++i) vpre[i] = va + i < vbc ? vj[static_cast<int64_t>(va + i) * kv_width] : 0.0f;
     }
-    if (staged)
-        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads)
-            qs[j] = INPUTS ? input_lane(q, in.q_bias, head * head_dim, j, in.position, in.base, in.rotary) : qh[j];
-    if (INPUTS && has_new) {
-        const bool writer = head % group == 0;
-        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) {
-            const float kj = input_lane(in.k_new, in.k_bias, kv_head * head_dim, j, in.position, in.base, in.rotary);
-            const float vj = biased(in.v_new, in.v_bias, kv_head * head_dim + j);
-            ks_new[j] = kj;
-            vs_new[j] = vj;
-            if (writer) {
-                k_cache[static_cast<int64_t>(in.position) * kv_width + kv_head * head_dim + j] = kj;
-                v_cache[static_cast<int64_t>(in.position) * kv_width + kv_head * head_dim + j] = vj;
+    // Key quads of this thread's first score (heads of up to 128 lanes: its whole eighth), also loaded before
+    // the query is staged.
+    const bool quads = (head_dim & 31) == 0;
+    const int piece = (head_dim + 7) / 8, p8 = threadIdx.x & 7;
+    const int j_lo = min(head_dim, p8 * piece), j_hi = min(head_dim, j_lo + piece);
+    const int ts = has_new ? t1 - 1 : t1;  // scores of cached rows
+    const bool kfirst = quads && piece <= 16 && t0 + (threadIdx.x >> 3) < ts;
+    f32x4 kpre[4];
+    if (kfirst) {
+        const float* kp = k + static_cast<int64_t>(t0 + (threadIdx.x >> 3)) * kv_width + kv_head * head_dim + j_lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * i < piece) {
+                const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(kp + 4 * i));
+                kpre[i] = f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                __uint_as_float(raw[3])};
+            }
+    }
+    if (INPUTS && has_new) {  // the new row's key and value lanes, in the workgroups whose split holds it
+        const int kb = kv_head * head_dim;
+        kx = in.k_new[kb + ia];
+        ky = in.k_new[kb + ib];
+        if (in.k_bias) {
+            kxb = in.k_bias[kb + ia];
+            kyb = in.k_bias[kb + ib];
+        }
+        vl = in.v_new[kb + jl];
+        if (in.v_bias) vlb = in.v_bias[kb + jl];
+    }
+    if (INPUTS) {
+        if (static_cast<int>(threadIdx.x) < head_dim) {
+            // The attention-input transform of lane j (as attention_inputs_kernel: biased, then rotated).
+            if (rot && !in.rope) rope_angle(kk, in.position, in.base, in.rotary, sn, cs);
+            auto lane = [&](float x, float y, float xb, float yb, bool bias) {
+                const float xv = bias ? __fadd_rn(x, xb) : x, yv = bias ? __fadd_rn(y, yb) : y;
+                if (!rot) return xv;
+                float a, b;
+                rope_apply(xv, yv, sn, cs, a, b);
+                return jl < pairs ? a : b;
+            };
+            const float qj = lane(qx, qy, qxb, qyb, in.q_bias != nullptr);
+            qs[jl] = qj;
+            if (split == 0) {  // the rotated query, for the combine launch to store in place
+                float* q_rot =
+                    reinterpret_cast<float*>(partial + static_cast<int64_t>(query_heads) * splits * (2 + head_dim));
+                q_rot[head * head_dim + jl] = qj;
+            }
+            if (has_new) {
+                const float kj = lane(kx, ky, kxb, kyb, in.k_bias != nullptr);
+                const float vj = in.v_bias ? __fadd_rn(vl, vlb) : vl;
+                ks_new[jl] = kj;
+                vs_new[jl] = vj;
+                if (head % group == 0) {  // one workgroup of the key/value head writes the cache row
+                    k_cache[static_cast<int64_t>(in.position) * kv_width + kv_head * head_dim + jl] = kj;
+                    v_cache[static_cast<int64_t>(in.position) * kv_width + kv_head * head_dim + jl] = vj;
+                }
             }
         }
+    } else if (staged) {
+        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) qs[j] = qh[j];
     }
     __syncthreads();
     // Scores: eight threads per token, thread p summing lanes [p * piece, (p + 1) * piece) of the key row in
     // order (16-byte loads, all in flight, when the eighths are whole quads), the eight partial sums then
     // added in order.
     double local_max = -INFINITY;
-    const bool quads = (head_dim & 31) == 0;
-    const int piece = (head_dim + 7) / 8, p8 = threadIdx.x & 7;
-    const int j_lo = min(head_dim, p8 * piece), j_hi = min(head_dim, j_lo + piece);
-    const int ts = has_new ? t1 - 1 : t1;  // scores of cached rows
     for (int base = t0; base < ts; base += kSplitThreads / 8) {
         const int t = base + (threadIdx.x >> 3);
         double dot = 0;
@@ -460,7 +535,9 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
                     f32x4 kv[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        if (j0 + 4 * i < piece) {
+                        if (base == t0 && kfirst)
+                            kv[i] = kpre[i];
+                        else if (j0 + 4 * i < piece) {
                             const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(kp + j0 + 4 * i));
                             kv[i] = f32x4{__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
                                           __uint_as_float(raw[3])};
@@ -561,13 +638,11 @@ __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(const 
                                                                           DecodeInputs in) {
     if (INPUTS) {
         // The query rotated in place, as the separate attention-inputs launch leaves it (the split workgroups
-        // have all read the original by now).
-        const int pairs = in.rotary / 2, base = blockIdx.x * head_dim;
-        for (int kk = threadIdx.x; kk < pairs; kk += kSplitThreads) {
-            const float x = biased(q, in.q_bias, base + kk), y = biased(q, in.q_bias, base + kk + pairs);
-            rope_pair(x, y, kk, in.position, in.base, in.rotary, q[base + kk], q[base + kk + pairs]);
-        }
-        for (int j = in.rotary + threadIdx.x; j < head_dim; j += kSplitThreads) q[base + j] = biased(q, in.q_bias, base + j);
+        // have all read the original by now): split 0 of each head left it after the partials.
+        const float* q_rot =
+            reinterpret_cast<const float*>(partial + static_cast<int64_t>(gridDim.x) * splits * (2 + head_dim));
+        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads)
+            q[blockIdx.x * head_dim + j] = q_rot[blockIdx.x * head_dim + j];
     }
     __shared__ double weight[kCombineWeights];
     __shared__ double lane_part[kSplitThreads];
@@ -737,7 +812,9 @@ int attention_splits(int tokens) {
 
 size_t attention_scratch_bytes(int query_heads, int head_dim, int tokens) {
     const int splits = std::max(kMinSplits, attention_splits(tokens));
-    return static_cast<size_t>(query_heads) * splits * (2 + head_dim) * sizeof(double);
+    // The partials, then the rotated query of the fused decode form.
+    return static_cast<size_t>(query_heads) * splits * (2 + head_dim) * sizeof(double) +
+           static_cast<size_t>(query_heads) * head_dim * sizeof(float);
 }
 
 namespace {
@@ -762,20 +839,31 @@ size_t split_lds_bytes_inputs(int per, int head_dim) {
     return static_cast<size_t>(per) * sizeof(double) + static_cast<size_t>(3) * head_dim * sizeof(float);
 }
 
-// The fused form needs the split path with the query staged and room for the new row's key and value.
+// The fused form needs the split path, one thread per lane of the head (at most 256 lanes) and room for the new
+// row's key and value. It is taken while splits hold at most 64 tokens: measured per layer of a Qwen-1.5B
+// token (12 / 2 heads of 128 lanes, 28 layers' caches), fused against the separate input launch, 12.5 vs
+// 13.6 us at 512 tokens (16 splits of 32) but 22.6 vs 20.7 us at 4,096 (32 splits of 128), where the fused
+// split launch's longer score and value loops cost more than the launch it saves.
 bool decode_fusable(int tokens, int head_dim) {
     const int splits = attention_splits(tokens);
-    if (splits == 1 || head_dim > kStagedQuery) return false;
+    if (splits == 1 || head_dim > kSplitThreads || (tokens + splits - 1) / splits > 64) return false;
     const int per = (tokens + splits - 1) / splits;
     return split_lds_bytes_inputs(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
 }
 
 }  // namespace
 
+hipError_t launch_rope_table(int positions, int rotary, double base, double* table, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(positions) * (rotary / 2);
+    if (n <= 0) return hipSuccess;
+    rope_table_kernel<<<grid_for(n), kThreads, 0, stream>>>(positions, rotary, base, table);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k_new, const float* k_bias,
                                    const float* v_new, const float* v_bias, float* k_cache, float* v_cache,
                                    int query_heads, int kv_heads, int head_dim, int position, double base, int rotary,
-                                   float* out, double* partials, hipStream_t stream) {
+                                   const double* rope, float* out, double* partials, hipStream_t stream) {
     const int tokens = position + 1;
     const int64_t kv_width = static_cast<int64_t>(kv_heads) * head_dim;
     if (!decode_fusable(tokens, head_dim)) {  // the two launches it stands for
@@ -788,9 +876,9 @@ hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k
     if (!partials) return hipErrorInvalidValue;
     const int splits = attention_splits(tokens);
     const int per = (tokens + splits - 1) / splits;
-    const DecodeInputs in{q_bias, k_new, k_bias, v_new, v_bias, position, rotary, base};
-    attention_split_kernel<true><<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes_inputs(per, head_dim),
-                                   stream>>>(q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, per, partials,
+    const DecodeInputs in{q_bias, k_new, k_bias, v_new, v_bias, rope, position, rotary, base};
+    attention_split_kernel<true><<<dim3(query_heads, splits), kSplitThreads,
+                                   split_lds_bytes_inputs(per, head_dim), stream>>>(q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, per, partials,
                                              in, k_cache, v_cache);
     attention_combine_kernel<true><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out, q, in);
     return hipGetLastError();

@@ -81,6 +81,9 @@ class DeviceDecoder:
         self.zero_kv = buf(self.kv_width)
         self.keys = [buf(c.max_tokens * self.kv_width) for _ in layers]
         self.values = [buf(c.max_tokens * self.kv_width) for _ in layers]
+        # RoPE sines and cosines of every cache position (doubles), computed once for the session.
+        self.rope = buf(2 * c.max_tokens * c.head_dim)
+        self.ops.rope_table(c.max_tokens, c.head_dim, c.rope_base, self.rope)
         for m in layers:
             group = {}
             self.groups.append(group)
@@ -136,7 +139,7 @@ class DeviceDecoder:
                 fg["qkv"].execute()
                 ops.attention_decode(self.q, vec.get("q_bias", 0), self.k, vec.get("k_bias", 0), self.v,
                                      vec.get("v_bias", 0), self.keys[layer], self.values[layer], c.heads, c.kv_heads,
-                                     c.head_dim, position, c.rope_base, c.head_dim, self.context_vec)
+                                     c.head_dim, position, c.rope_base, c.head_dim, self.context_vec, self.rope)
                 g["o"].execute()
                 fg["gateup"].execute()
                 ops.swiglu_q8k(self.gate, self.up, c.ffn, 0, self.activated_q8k)

@@ -355,7 +355,8 @@ def test_split_attentions_on_two_streams_do_not_share_a_workspace(context):
 
 @pytest.mark.parametrize("position,heads,kv_heads,head_dim,rotary,biases", [
     (0, 12, 2, 128, 128, True), (31, 12, 2, 128, 128, True), (32, 12, 2, 128, 128, True),
-    (511, 12, 2, 128, 128, True), (4095, 12, 2, 128, 128, False), (70000, 4, 2, 128, 64, True),
+    (511, 12, 2, 128, 128, True), (2047, 12, 2, 128, 128, True), (2048, 12, 2, 128, 128, True),
+    (4095, 12, 2, 128, 128, False), (70000, 4, 2, 128, 64, True),
     (300, 14, 2, 80, 80, True), (100, 3, 3, 24, 16, False), (65, 4, 1, 1024, 512, True)])
 def test_attention_decode_equals_inputs_then_attention(context, position, heads, kv_heads, head_dim, rotary, biases):
     # satori_hip_attention_decode (the attention inputs applied inside the split attention) against
@@ -387,8 +388,11 @@ def test_attention_decode_equals_inputs_then_attention(context, position, heads,
             dck, dcv = dev(cache_k), dev(cache_v)
             out = dev(np.zeros(qw, np.float32))
             if fused:
+                table = context.alloc(8 * (position + 1) * rotary)
+                buffers.append(table)
+                ops.rope_table(position + 1, rotary, 1e6, table)
                 ops.attention_decode(dq, dqb, dk, dkb, dv, dvb, dck, dcv, heads, kv_heads, head_dim, position, 1e6,
-                                     rotary, out)
+                                     rotary, out, table if position % 2 else 0)
             else:
                 ops.attention_inputs(dq, dqb, dk, dkb, dck + 4 * position * kw, dv, dvb, dcv + 4 * position * kw,
                                      heads, kv_heads, head_dim, position, 1e6, rotary)
