@@ -63,6 +63,9 @@ constexpr int kActDwords = kCodeStride + 1 + 8;  // codes, scale, group sums per
 // and elements of the RmsNorm sum of squares (2,048 columns).
 constexpr int kQ8KPasses = 3;  // 48 blocks
 constexpr int kNormPreload = 8;
+// An RmsNorm input row of at most this many columns keeps its summed values (residual + addend) in LDS
+// between the sum of squares and the quantization, instead of reading both operands again.
+constexpr int kNormStageColumns = 8192;
 
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
@@ -228,6 +231,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
         aux = load16_a4(block + (j16 == 0 ? 0 : 260 + 16 * (min(j16, 2) - 1)));
     };
     float npre_a[kNormPreload], npre_b[kNormPreload];  // RmsNorm input: the first terms of the sum of squares
+    f32x4 wpre[4];                                      // RmsNorm input: the norm weights of the first pass
     if constexpr (XF == kInputPlain) {
         const int i0 = 256 * min(bl0, kb - 1) + 16 * j16;
 #pragma unroll
@@ -243,6 +247,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
             npre_a[k] = xf.a[i];
             npre_b[k] = xf.b ? xf.b[i] : 0.0f;
         }
+        const int i0 = 256 * min(bl0, kb - 1) + 16 * j16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wpre[q] = quad(xf.w, i0 + 4 * q);
     }
     Raw buf[kDepth];
 #pragma unroll
@@ -252,6 +259,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
     // transform the activations are computed here from the operator's operands, in the operator's own
     // arithmetic (the RmsNorm sum of squares over the same 256-thread partition and tree, over the whole row).
     double scale = 0.0;
+    // Summed RmsNorm input (residual + addend) kept in LDS after the reduction's 256 doubles.
+    float* rstage = reinterpret_cast<float*>(smem + kint_red_offset(K, tile_rows) + 2 * kThreads);
+    const bool rstaged = XF == kInputAddRmsNorm && s.columns <= kNormStageColumns;
     if constexpr (XF == kInputAddRmsNorm) {
         double* red = reinterpret_cast<double*>(smem + kint_red_offset(K, tile_rows));
         const bool writer = xf.residual_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
@@ -259,6 +269,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
         auto term = [&](int i, float a, float b) {
             const float r = xf.b ? __fadd_rn(a, b) : a;
             if (writer) xf.residual_out[i] = r;
+            if (rstaged) rstage[i] = r;  // visible to every thread after the reduction's barriers
             const double v = r;
             part = part + v * v;
         };
@@ -327,12 +338,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
                     if constexpr (XF == kInputPlain) {
                         x4[q] = quad(xrow, i0 + 4 * q);
                     } else if constexpr (XF == kInputAddRmsNorm) {
-                        const f32x4 a4 = quad(xf.a, i0 + 4 * q), w4 = quad(xf.w, i0 + 4 * q);
-                        f32x4 b4 = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (xf.b) b4 = quad(xf.b, i0 + 4 * q);
+                        const bool first = b0 == 0 && bl == bl0;  // the pass whose weights were preloaded
+                        const f32x4 w4 = first ? wpre[q] : quad(xf.w, i0 + 4 * q);
+                        f32x4 r4;
+                        if (rstaged) {
+                            r4 = *reinterpret_cast<const f32x4*>(rstage + i0 + 4 * q);
+                        } else {
+                            const f32x4 a4 = quad(xf.a, i0 + 4 * q);
+                            f32x4 b4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                            if (xf.b) b4 = quad(xf.b, i0 + 4 * q);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            x4[q][e] = rms_value(xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e], scale, w4[e]);
+                            for (int e = 0; e < 4; ++e) r4[e] = xf.b ? __fadd_rn(a4[e], b4[e]) : a4[e];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) x4[q][e] = rms_value(r4[e], scale, w4[e]);
                     } else {
                         const f32x4 g4 = quad(xf.a, i0 + 4 * q), u4 = quad(xf.b, i0 + 4 * q);
 #pragma unroll
@@ -407,8 +426,10 @@ hipError_t launch_q8k_quantize(const float* x, int columns, int positions, uint8
     return hipGetLastError();
 }
 
-size_t kint_lds_bytes(int blocks) {
-    return static_cast<size_t>(kint_red_offset(blocks, kTileRows)) * sizeof(uint32_t) + kThreads * sizeof(double);
+size_t kint_lds_bytes(int blocks, int rms_columns) {
+    const size_t staged = rms_columns <= kNormStageColumns ? static_cast<size_t>(rms_columns) * sizeof(float) : 0;
+    return static_cast<size_t>(kint_red_offset(blocks, kTileRows)) * sizeof(uint32_t) + kThreads * sizeof(double) +
+           staged;
 }
 
 int kint_max_blocks() {
@@ -438,7 +459,7 @@ hipError_t launch_kint(const MatDesc* members, const MatDesc* device_members, in
     // Rows wider than the LDS holds are staged kint_max_blocks() blocks at a time.
     s.chunk_blocks = s.blocks < kint_max_blocks() ? s.blocks : kint_max_blocks();
     dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
-    const size_t lds = kint_lds_bytes(s.chunk_blocks);
+    const size_t lds = kint_lds_bytes(s.chunk_blocks, XF == kInputAddRmsNorm ? s.columns : 0);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     KintMembers inline_members{};
     const MatDesc* group = nullptr;

@@ -12,19 +12,30 @@ namespace satori {
 
 constexpr int kOpsThreads = 256;
 
-// Sum of one double per thread over a 256-thread workgroup (tree in LDS, fixed order: deterministic).
-// `red` holds 256 doubles; every thread of the workgroup must call it.
-__device__ __forceinline__ double block_sum_256(double v, double* red) {
-    red[threadIdx.x] = v;
+// Reduction (sum or maximum) of one double per thread over a 256-thread workgroup in a fixed pairwise tree
+// (deterministic): at stride s = 128, 64, ..., 1, value t < s becomes op(value t, value t + s). The first
+// wave forms the strides 128 and 64 from the LDS copy, then the strides 32 to 1 in registers with lane
+// shuffles (lane t < s combines lane t + s: the same operations in the same order as the tree in LDS), so
+// the tree costs three barriers instead of ten. `red` holds 256 doubles; every thread of the workgroup must
+// call it, and every thread gets the result.
+__device__ __forceinline__ double block_tree_256(double v, double* red, bool take_max) {
+    const int t = threadIdx.x;
+    auto op = [take_max](double a, double b) { return take_max ? fmax(a, b) : a + b; };
+    red[t] = v;
     __syncthreads();
-    for (int s = kOpsThreads / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
-        __syncthreads();
+    if (t < 64) {
+        double x = op(op(red[t], red[t + 128]), op(red[t + 64], red[t + 192]));
+#pragma unroll
+        for (int s = 32; s > 0; s >>= 1) x = op(x, __shfl_down(x, s, 64));
+        if (t == 0) red[0] = x;
     }
+    __syncthreads();
     const double r = red[0];
     __syncthreads();
     return r;
 }
+
+__device__ __forceinline__ double block_sum_256(double v, double* red) { return block_tree_256(v, red, false); }
 
 // 1 / sqrt(mean of squares + epsilon) from the sum of squares of `length` values.
 __device__ __forceinline__ double rms_scale(double sum, int length, float epsilon) {

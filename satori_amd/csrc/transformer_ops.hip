@@ -28,17 +28,7 @@ constexpr int kThreads = kOpsThreads;
 
 __device__ __forceinline__ double block_sum(double v, double* red) { return block_sum_256(v, red); }
 
-__device__ __forceinline__ double block_max(double v, double* red) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int s = kThreads / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] = fmax(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    const double r = red[0];
-    __syncthreads();
-    return r;
-}
+__device__ __forceinline__ double block_max(double v, double* red) { return block_tree_256(v, red, true); }
 
 // RmsNorm (TransformerOps.cs:13-21), one workgroup per vector of `length`; output may equal input.
 __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float* x, const float* __restrict__ w, float epsilon,
@@ -354,16 +344,7 @@ constexpr int kCombineChunk = 16;      // splits whose values one combine thread
 constexpr int kCombineWeights = 1024;  // split weights the combine kernel holds in LDS at a time
 
 __device__ __forceinline__ double split_reduce(double v, double* red, bool take_max) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int s = kSplitThreads / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s)
-            red[threadIdx.x] = take_max ? fmax(red[threadIdx.x], red[threadIdx.x + s]) : red[threadIdx.x] + red[threadIdx.x + s];
-        __syncthreads();
-    }
-    const double r = red[0];
-    __syncthreads();
-    return r;
+    return block_tree_256(v, red, take_max);
 }
 
 // Workgroup reduction of 256 doubles through wave shuffles and four partials in LDS (every thread gets it).
