@@ -631,14 +631,51 @@ __global__ __launch_bounds__(kSplitThreads) void attention_combine_kernel(const 
     const int head = blockIdx.x;
     const int64_t stride = 2 + head_dim;
     const double* p = partial + static_cast<int64_t>(head) * splits * stride;
-    double big = -INFINITY;
-    for (int s = threadIdx.x; s < splits; s += kSplitThreads) big = fmax(big, p[s * stride]);
-    big = wave_reduce_256(big, red4, true);
     // Threads per output lane: up to 8 while the head's lanes fit the workgroup that many times.
     int lanes_per = 1;
     while (lanes_per < 8 && 2 * lanes_per * head_dim <= kSplitThreads) lanes_per *= 2;
     const int width = kSplitThreads / lanes_per;
     const int share = threadIdx.x / width;
+    const int split_share = (splits + lanes_per - 1) / lanes_per;  // splits per thread of an output lane
+    if (splits <= kSplitThreads && head_dim <= width && split_share <= kCombineChunk) {
+        // A decode-sized head (one split per thread, one pass over the lanes): every global read is issued
+        // before the first reduction, so the kernel waits on memory once. The same operations in the same
+        // order as the general path below.
+        const int j = threadIdx.x % width;
+        const int s_lo = min(splits, share * split_share), s_hi = min(splits, s_lo + split_share);
+        double m_s = -INFINITY, l_s = 0.0;
+        if (threadIdx.x < splits) {
+            m_s = p[threadIdx.x * stride];
+            l_s = p[threadIdx.x * stride + 1];
+        }
+        double o[kCombineChunk];
+#pragma unroll
+        for (int i = 0; i < kCombineChunk; ++i)
+            o[i] = j < head_dim && s_lo + i < s_hi ? p[(s_lo + i) * stride + 2 + j] : 0.0;
+        const double m = wave_reduce_256(m_s, red4, true);
+        double total_part = 0;
+        if (threadIdx.x < splits) {
+            const double w = l_s > 0 ? exp(m_s - m) : 0.0;
+            weight[threadIdx.x] = w;
+            total_part = total_part + w * l_s;
+        }
+        const double total = wave_reduce_256(total_part, red4, false);  // its barrier publishes the weights
+        double sum = 0;
+#pragma unroll
+        for (int i = 0; i < kCombineChunk; ++i)
+            if (s_lo + i < s_hi) sum = sum + weight[s_lo + i] * o[i];
+        lane_part[threadIdx.x] = sum;
+        __syncthreads();
+        if (share == 0 && j < head_dim) {
+            double lane_sum = lane_part[threadIdx.x];
+            for (int i = 1; i < lanes_per; ++i) lane_sum = lane_sum + lane_part[threadIdx.x + i * width];
+            out[static_cast<int64_t>(head) * head_dim + j] = static_cast<float>(lane_sum / total);
+        }
+        return;
+    }
+    double big = -INFINITY;
+    for (int s = threadIdx.x; s < splits; s += kSplitThreads) big = fmax(big, p[s * stride]);
+    big = wave_reduce_256(big, red4, true);
     const int chunks = (splits + kCombineWeights - 1) / kCombineWeights;
     double total_part = 0;
     double total = 0;
