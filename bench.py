@@ -242,9 +242,19 @@ def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     cache_ms = time_launches(ctx, events, case.run_cache, max(2, steps // 2), 1)
     out["cache_resident_gbs"] = step_bytes / (cache_ms * 1e-3) / 1e9
     if single:
+        # One launch per matrix, issued back to back from Python (the ctypes call and the library's host
+        # work included), then the same launches captured once and replayed (the device time per launch).
         single_ms = time_launches(ctx, events, case.run_single, max(2, steps // 4), 1)
         out["single_launch_us"] = single_ms * 1e3 / case.copies
         out["single_launch_gbs"] = step_bytes / (single_ms * 1e-3) / 1e9
+        ctx.capture_begin()
+        case.run_single()
+        replay = ctx.capture_end()
+        try:
+            graph_ms = time_launches(ctx, events, replay.execute, max(2, steps // 4), 1)
+        finally:
+            replay.dispose()
+        out["single_launch_graph_us"] = graph_ms * 1e3 / case.copies
     return out
 
 
@@ -894,7 +904,7 @@ def run(args, ctx, events) -> int:
             for label, make in other_formats(ctx):
                 c, cpu_case = make()
                 parity = check_case(ctx, c, *cpu_case)
-                formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10, single=False)
+                formats[label] = measure(ctx, events, c, max(50, args.steps // 2), 10)
                 formats[label].update(parity)
                 formats[label].update(host_call_latency(c))
                 cpu_cases[label] = cpu_case
