@@ -26,6 +26,8 @@ __device__ __forceinline__ uint32_t load4_a4(const uint8_t* p) {
 
 __device__ __forceinline__ uint64_t load8_a8(const uint8_t* p) { return *(const SATORI_GLOBAL uint64_t*)(p); }
 
+__device__ __forceinline__ uint32_t load2_a2(const uint8_t* p) { return *(const SATORI_GLOBAL uint16_t*)(p); }
+
 __device__ __forceinline__ float load_f32(const float* p) { return *(const SATORI_GLOBAL float*)(p); }
 
 // Non-temporal loads for data that one instruction reads exactly once per launch (the Ternary2 panel

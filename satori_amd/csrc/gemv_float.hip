@@ -45,17 +45,24 @@ struct Q8_0Chunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    // Regrouped device layout: 32-byte code records, then the FP16 scales.
-    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
-        const int64_t count = static_cast<int64_t>(m.rows) * s.blocks;
-        const int64_t index = static_cast<int64_t>(row) * s.blocks + chunk;
-        const u32x4 a = load16_a4(m.w + index * 32), b = load16_a4(m.w + index * 32 + 16);
+    // Regrouped device layout: 32-byte code records, then the FP16 scales. A row's records and scales start
+    // at fixed addresses, computed once per row.
+    struct Row {
+        const uint8_t* codes;
+        const uint8_t* scales;
+    };
+    __device__ static Row row_ref(const MatDesc& m, const LaunchShape& s, int row) {
+        const int64_t first = static_cast<int64_t>(row) * s.blocks;
+        return Row{m.w + first * 32, m.w + static_cast<int64_t>(m.rows) * s.blocks * 32 + first * 2};
+    }
+    __device__ static void load(const Row& w, int chunk, Regs& r) {
+        const u32x4 a = load16_a4(w.codes + chunk * 32), b = load16_a4(w.codes + chunk * 32 + 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             r.q[i] = a[i];
             r.q[4 + i] = b[i];
         }
-        r.scale = half_bits_to_float(load4_a4(m.w + count * 32 + (index & ~int64_t(1)) * 2) >> (16 * (index & 1)));
+        r.scale = half_bits_to_float(load2_a2(w.scales + chunk * 2));
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -77,9 +84,10 @@ struct Q8_0Chunk {
 
 // ------------------------------------------------------------------------------------------------
 // Q4_0: f16 d + 16 bytes, w[j] = d * ((b[j] & 15) - 8), w[j + 16] = d * ((b[j] >> 4) - 8)
-// (docs/gguf-subset-v1.md:93; QuantizedMatVec.cs:71-72). Each nibble is turned into the signed byte
-// 16 * (q - 8) by one XOR and one mask per four weights, so the conversion is one SDWA op per weight;
-// the factor 16 is removed exactly with the power-of-two scale 1/16.
+// (docs/gguf-subset-v1.md:93; QuantizedMatVec.cs:71-72). The device copy holds every code byte XOR 0x88
+// (applied at upload), so each nibble is q ^ 8, whose signed 4-bit value is q - 8; a mask (and a shift for
+// the low nibbles) per four weights turns the nibbles into the signed bytes 16 * (q - 8), and the conversion
+// is one SDWA op per weight; the factor 16 is removed exactly with the power-of-two scale 1/16.
 // ------------------------------------------------------------------------------------------------
 struct Q4_0Chunk {
     static constexpr int kRowUnroll = 2;
@@ -94,14 +102,20 @@ struct Q4_0Chunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    // Regrouped device layout: 16-byte code records, then the FP16 scales.
-    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
-        const int64_t count = static_cast<int64_t>(m.rows) * s.blocks;
-        const int64_t index = static_cast<int64_t>(row) * s.blocks + chunk;
-        const u32x4 a = load16_a4(m.w + index * 16);
+    // Regrouped device layout: 16-byte code records (bytes XOR 0x88), then the FP16 scales.
+    struct Row {
+        const uint8_t* codes;
+        const uint8_t* scales;
+    };
+    __device__ static Row row_ref(const MatDesc& m, const LaunchShape& s, int row) {
+        const int64_t first = static_cast<int64_t>(row) * s.blocks;
+        return Row{m.w + first * 16, m.w + static_cast<int64_t>(m.rows) * s.blocks * 16 + first * 2};
+    }
+    __device__ static void load(const Row& w, int chunk, Regs& r) {
+        const u32x4 a = load16_a4(w.codes + chunk * 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.q[i] = a[i];
-        r.scale = half_bits_to_float(load4_a4(m.w + count * 16 + (index & ~int64_t(1)) * 2) >> (16 * (index & 1)));
+        r.scale = half_bits_to_float(load2_a2(w.scales + chunk * 2));
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -112,7 +126,7 @@ struct Q4_0Chunk {
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            const uint32_t v = r.q[d] ^ 0x88888888u;        // nibble q -> q ^ 8, whose signed 4-bit value is q - 8
+            const uint32_t v = r.q[d];                       // nibbles q ^ 8 (signed 4-bit value q - 8)
             const uint32_t lo = (v << 4) & 0xF0F0F0F0u;      // bytes 16 * (q_low - 8): weights 4d + i
             const uint32_t hi = v & 0xF0F0F0F0u;             // bytes 16 * (q_high - 8): weights 16 + 4d + i
 #pragma unroll
@@ -147,8 +161,12 @@ struct Q4_KChunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks * 8; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
-        const uint8_t* block = m.w + row * s.row_bytes + (chunk >> 3) * 144;
+    using Row = const uint8_t*;  // the row's first block
+    __device__ static Row row_ref(const MatDesc& m, const LaunchShape& s, int row) {
+        return m.w + static_cast<int64_t>(row) * s.row_bytes;
+    }
+    __device__ static void load(Row w, int chunk, Regs& r) {
+        const uint8_t* block = w + (chunk >> 3) * 144;
         r.head = load16_a4(block);
         r.qs = load16_a4(block + 16 + 16 * (chunk & 7));
         r.g = (chunk & 7) >> 1;
@@ -202,9 +220,15 @@ struct Q6_KChunk {
     __device__ static Consts consts() { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks * 4; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
-    __device__ static void load(const MatDesc& m, const LaunchShape& s, int row, int chunk, Regs& r) {
-        q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * s.blocks,
-                         static_cast<int64_t>(row) * s.blocks + (chunk >> 2), chunk & 3, r);
+    struct Row {
+        const uint8_t* w;
+        int64_t count, first;  // blocks of the matrix; the row's first block
+    };
+    __device__ static Row row_ref(const MatDesc& m, const LaunchShape& s, int row) {
+        return Row{m.w, static_cast<int64_t>(m.rows) * s.blocks, static_cast<int64_t>(row) * s.blocks};
+    }
+    __device__ static void load(const Row& w, int chunk, Regs& r) {
+        q6k_load_quarter(w.w, w.count, w.first + (chunk >> 2), chunk & 3, r);
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -327,13 +351,13 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
 #pragma unroll
         for (int u = 0; u < kRowUnroll; ++u) {
             const int row = first + u * kStride + sub;
-            if (active && row < row_end) F::load(m, s, row, lr, cur[u]);
+            if (active && row < row_end) F::load(F::row_ref(m, s, row), lr, cur[u]);
         }
         for (int base = first; base < row_end; base += kStep) {
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) {
                 const int row = base + kStep + u * kStride + sub;
-                if (active && row < row_end) F::load(m, s, row, lr, nxt[u]);
+                if (active && row < row_end) F::load(F::row_ref(m, s, row), lr, nxt[u]);
             }
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) {
@@ -348,8 +372,12 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
     } else {
         for (int base = first; base < row_end; base += kStep) {
             float acc[kRowUnroll];
+            typename F::Row rows[kRowUnroll];  // (rows past the end are never loaded)
 #pragma unroll
-            for (int u = 0; u < kRowUnroll; ++u) acc[u] = 0.0f;
+            for (int u = 0; u < kRowUnroll; ++u) {
+                acc[u] = 0.0f;
+                rows[u] = F::row_ref(m, s, base + u * kStride + sub);
+            }
             int c = lr;
             for (; c + L < nchunks; c += 2 * L) {  // two chunks per step: both rows' loads of both in flight
                 typename F::Regs ra[kRowUnroll], rb[kRowUnroll];
@@ -357,8 +385,8 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
                 for (int u = 0; u < kRowUnroll; ++u) {
                     const int row = base + u * kStride + sub;
                     if (row < row_end) {
-                        F::load(m, s, row, c, ra[u]);
-                        F::load(m, s, row, c + L, rb[u]);
+                        F::load(rows[u], c, ra[u]);
+                        F::load(rows[u], c + L, rb[u]);
                     }
                 }
                 F::load_x(xf, c, xr);
@@ -380,7 +408,7 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
 #pragma unroll
                 for (int u = 0; u < kRowUnroll; ++u) {
                     const int row = base + u * kStride + sub;
-                    if (row < row_end) F::load(m, s, row, c, regs[u]);
+                    if (row < row_end) F::load(rows[u], c, regs[u]);
                 }
 #pragma unroll
                 for (int u = 0; u < kRowUnroll; ++u) {
@@ -428,10 +456,23 @@ hipError_t launch_lanes(const MatDesc& one, const MatDesc* group, const LaunchSh
 template <class F>
 hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, int chunks,
                          int padded, hipStream_t stream) {
-    // Lanes per row: enough for one chunk per lane when the row is short, capped at the wave.
+    // Lanes per row: enough for one chunk per lane when the row is short, capped at the wave. A longer row
+    // takes the lane count (64, 32, 16 or 8) that leaves the fewest lanes idle in its last pass, the larger
+    // on a tie (4096 x 11008 Q4_0: 344 chunks are 43 passes of 8 lanes, against 6 passes of 64 with 40
+    // lanes idle in the last).
     int lanes = 8;
     while (lanes < 64 && lanes < chunks) lanes <<= 1;
     const bool one_chunk = chunks <= lanes;
+    if (!one_chunk) {
+        int64_t best = -1;
+        for (int l = 64; l >= 8; l >>= 1) {
+            const int64_t slots = static_cast<int64_t>((chunks + l - 1) / l) * l;
+            if (best < 0 || slots < best) {
+                best = slots;
+                lanes = l;
+            }
+        }
+    }
     const size_t lds = staged_lds_bytes<F>(padded);
     const bool wide = !one_chunk && lds > kWideLdsBytes && lds <= kMaxLdsBytes;
     const int waves = (wide ? kWideThreads : kThreads) / 64;

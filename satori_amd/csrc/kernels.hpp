@@ -82,7 +82,8 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
 
 // ---- Q8_0 / Q4_0 device layout ----
 // The same bytes regrouped so that code loads are aligned: for the n = rows * blocks blocks in row-major
-// order, n code records (Q8_0: the 32 signed bytes; Q4_0: the 16 nibble bytes), then the n FP16 scales.
+// order, n code records (Q8_0: the 32 signed bytes; Q4_0: the 16 nibble bytes XOR 0x88, so each nibble holds
+// q - 8 in two's complement), then the n FP16 scales.
 constexpr int legacy_record_bytes(int format) { return format == kQ8_0 ? 32 : 16; }
 
 // How a Ternary2 launch is cut: workgroups of `waves` waves (one 64-row panel each) take equal ranges of

@@ -321,17 +321,22 @@ std::vector<uint8_t> q6k_regroup(const Shape& s, const uint8_t* packed) {
 }
 
 // Regroups a validated Q8_0 / Q4_0 payload into the device layout of kernels.hpp: aligned code records, then
-// the FP16 scales.
+// the FP16 scales. Q4_0 code bytes are stored XOR 0x88 (each nibble q as q ^ 8, the two's-complement nibble
+// of q - 8).
 std::vector<uint8_t> legacy_regroup(const Shape& s, const uint8_t* packed) {
     const int64_t n = static_cast<int64_t>(s.rows) * s.blocks;
     const int record = legacy_record_bytes(s.format);
     std::vector<uint8_t> out(static_cast<size_t>(n) * s.block_bytes);
     uint8_t* codes = out.data();
     uint8_t* scales = codes + n * record;
+    const bool q4 = s.format == SATORI_HIP_Q4_0;
     for (int64_t i = 0; i < n; ++i) {
         const uint8_t* block = packed + i * s.block_bytes;
         std::memcpy(scales + i * 2, block, 2);
-        std::memcpy(codes + i * record, block + 2, static_cast<size_t>(record));
+        uint8_t* dst = codes + i * record;
+        std::memcpy(dst, block + 2, static_cast<size_t>(record));
+        if (q4)
+            for (int k = 0; k < record; ++k) dst[k] ^= 0x88;
     }
     return out;
 }
