@@ -219,6 +219,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
     // The activation side is loaded first, then the weights: the waits for the activations then do not
     // cover the weight loads issued after them. Every thread issues the same loads (addresses past the end
     // are clamped and their values unused), so the load counts the waits are computed from are static.
+    // Launches of up to kKintInlineMembers members (the decode step's latency-bound groups) do this; larger
+    // groups stream from HBM and keep the registers for occupancy (the preloads take the plain-input Q4_K
+    // kernel from 127 to 138 VGPRs, three waves per SIMD instead of four: 8960 x 1536 grouped measured
+    // 5.53 against 5.86 TB/s).
+    constexpr bool kPreload = INLINE;
     const int tid = threadIdx.x;
     const int j16 = tid & 15, bl0 = tid >> 4;
     f32x4 xpre[4];                 // plain input: this thread's 16 values of the first pass
@@ -232,11 +237,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
     };
     float npre_a[kNormPreload], npre_b[kNormPreload];  // RmsNorm input: the first terms of the sum of squares
     f32x4 wpre[4];                                      // RmsNorm input: the norm weights of the first pass
-    if constexpr (XF == kInputPlain) {
+    if constexpr (XF == kInputPlain && kPreload) {
         const int i0 = 256 * min(bl0, kb - 1) + 16 * j16;
 #pragma unroll
         for (int q = 0; q < 4; ++q) xpre[q] = quad(xrow, i0 + 4 * q);
-    } else if constexpr (XF == kInputQ8K) {
+    } else if constexpr (XF == kInputQ8K && kPreload) {
 #pragma unroll
         for (int k = 0; k < kQ8KPasses; ++k)
             q8k_load(reinterpret_cast<const uint8_t*>(xf.a), min(bl0 + 16 * k, kb - 1), qcodes[k], qaux[k]);
@@ -299,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
                 }
             };
             int bl = bl0;
-            if (b0 == 0) {
+            if (kPreload && b0 == 0) {
 #pragma unroll
                 for (int k = 0; k < kQ8KPasses; ++k)
                     if (bl0 + 16 * k < kb) put(bl0 + 16 * k, qcodes[k], qaux[k]);
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
                 if (j16 == 0) act.scales[bl] = qr.scale;
             };
             int bl = bl0;
-            if constexpr (XF == kInputPlain) {
+            if constexpr (XF == kInputPlain && kPreload) {
                 if (b0 == 0) {
                     if (bl < kb) stage(bl, xpre);
                     bl += kThreads / 16;
