@@ -354,7 +354,7 @@ int satori_hip_attention_decode(satori_hip_context* context, float* query, const
  * to a static device workspace of 4 MiB per device (resolved when the context is created, held until the
  * process ends) instead of a context workspace: a call whose partials, query_heads * splits * (head_dim + 2)
  * * 8 bytes, exceed it fails with SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE (12 heads of 128 lanes: prefixes up to
- * 688,128 tokens). Every call on a device shares that workspace and leaves its partials there: calls that
+ * 686,080 tokens). Every call on a device shares that workspace and leaves its partials there: calls that
  * overlap in time on one device (other streams, other contexts) race and must be serialised by the caller. */
 int satori_hip_grouped_attention_static(satori_hip_context* context, const float* query, const float* keys,
                                         const float* values, int query_heads, int kv_heads, int head_dim, int tokens,
