@@ -315,6 +315,14 @@ int satori_hip_quantize_q8k_device(satori_hip_context* context, const float* inp
  * cache slots). */
 int satori_hip_add_rms_norm(satori_hip_context* context, float* residual, const float* addend, const float* weights,
                             float epsilon, int length, float* normed, void* stream);
+/* satori_hip_add_rms_norm, and Q8KCodec.QuantizeRow of `normed` (src/Satori.Core/Q8KCodec.cs:85-93) into q8k
+ * in the same launch: the input of the projections after the residual add of DenseForward.Step
+ * (DenseForward.cs:149, :156-158), which the reference quantizes inside ExecuteBatch, quantized once by its
+ * producer for a group reading it with SATORI_HIP_INPUT_Q8K. length a positive multiple of 256; q8k receives
+ * length / 256 * 292 bytes, identical to the reference's; normed and residual as satori_hip_add_rms_norm. */
+int satori_hip_add_rms_norm_q8k(satori_hip_context* context, float* residual, const float* addend,
+                                const float* weights, float epsilon, int length, float* normed, void* q8k,
+                                void* stream);
 int satori_hip_attention_inputs(satori_hip_context* context, float* query, const float* query_bias, const float* key,
                                 const float* key_bias, float* key_out, const float* value, const float* value_bias,
                                 float* value_out, int query_heads, int kv_heads, int head_dim, int position,

@@ -1014,6 +1014,12 @@ class DeviceOps:
         _check(_ffi.lib().satori_hip_add_rms_norm(self._h, self._p(residual), self._p(addend), self._p(weights),
                                                   float(epsilon), length, self._p(normed), None))
 
+    def add_rms_norm_q8k(self, residual: int, addend: int, weights: int, epsilon: float, length: int, normed: int,
+                         q8k: int) -> None:
+        """add_rms_norm with the Q8_K bytes of `normed` written to q8k as well (for a group reading Q8_K)."""
+        _check(_ffi.lib().satori_hip_add_rms_norm_q8k(self._h, self._p(residual), self._p(addend), self._p(weights),
+                                                      float(epsilon), length, self._p(normed), self._p(q8k), None))
+
     def attention_inputs(self, q: int, q_bias: int, k: int, k_bias: int, k_out: int, v: int, v_bias: int, v_out: int,
                          heads: int, kv_heads: int, head_dim: int, position: int, base: float, rotary: int) -> None:
         """Biases may be 0 (none)."""

@@ -69,6 +69,7 @@ SIGNATURES = {
     "satori_hip_swiglu": (I, [P, P, P, I, P, P]),
     "satori_hip_add": (I, [P, P, P, I, P, P]),
     "satori_hip_swiglu_q8k": (I, [P, P, P, I, P, P, P]),
+    "satori_hip_add_rms_norm_q8k": (I, [P, P, P, P, ctypes.c_float, I, P, P, P]),
     "satori_hip_quantize_q8k_device": (I, [P, P, I, I, P, P]),
     "satori_hip_grouped_attention": (I, [P, P, P, P, I, I, I, I, P, P]),
     "satori_hip_grouped_attention_static": (I, [P, P, P, P, I, I, I, I, P, P]),

@@ -205,6 +205,9 @@ hipError_t launch_swiglu_q8k(const float* gate, const float* up, int length, flo
 hipError_t launch_add(const float* left, const float* right, int length, float* out, hipStream_t stream);
 hipError_t launch_add_rms_norm(float* residual, const float* addend, const float* w, float epsilon, int length,
                                float* normed, hipStream_t stream);
+// launch_add_rms_norm, and the Q8_K bytes of `normed` (Q8KCodec.QuantizeRow) into q8k; length a multiple of 256.
+hipError_t launch_add_rms_norm_q8k(float* residual, const float* addend, const float* w, float epsilon, int length,
+                                   float* normed, uint8_t* q8k, hipStream_t stream);
 hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k, const float* k_bias, float* k_out,
                                    const float* v, const float* v_bias, float* v_out, int heads, int kv_heads,
                                    int head_dim, int position, double base, int rotary, hipStream_t stream);

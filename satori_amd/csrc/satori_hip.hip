@@ -1670,6 +1670,28 @@ int satori_hip_add_rms_norm(satori_hip_context* c, float* residual, const float*
     });
 }
 
+int satori_hip_add_rms_norm_q8k(satori_hip_context* c, float* residual, const float* addend, const float* weights,
+                                float epsilon, int length, float* normed, void* q8k, void* stream) {
+    return op_call(c, [&] {
+        require(residual, "residual");
+        require(addend, "addend");
+        require(weights, "weights");
+        require(normed, "normed");
+        require(q8k, "q8k");
+        if (length <= 0 || length % 256 != 0) fail(SATORI_HIP_E_ARGUMENT, "Invalid Q8_K row dimensions.");
+        check_epsilon(epsilon);
+        const int64_t q_floats = static_cast<int64_t>(length / 256) * kQ8KBlockBytes / 4;
+        if (partial_overlap(addend, length, residual, length) || any_overlap(normed, length, residual, length) ||
+            any_overlap(weights, length, normed, length) || any_overlap(addend, length, normed, length) ||
+            any_overlap(q8k, q_floats, residual, length) || any_overlap(q8k, q_floats, addend, length) ||
+            any_overlap(q8k, q_floats, weights, length) || any_overlap(q8k, q_floats, normed, length))
+            fail(SATORI_HIP_E_ARGUMENT, "Partial overlap.");
+        check_hip(launch_add_rms_norm_q8k(residual, addend, weights, epsilon, length, normed,
+                                          static_cast<uint8_t*>(q8k), op_stream(c, stream)),
+                  "add_rms_norm_q8k launch");
+    });
+}
+
 int satori_hip_attention_inputs(satori_hip_context* c, float* query, const float* query_bias, const float* key,
                                 const float* key_bias, float* key_out, const float* value, const float* value_bias,
                                 float* value_out, int query_heads, int kv_heads, int head_dim, int position,

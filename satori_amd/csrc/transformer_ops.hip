@@ -63,6 +63,48 @@ __global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(float* residual,
     for (int i = threadIdx.x; i < length; i += kThreads) normed[i] = rms_value(residual[i], scale, w[i]);
 }
 
+// Add then RmsNorm as add_rms_norm_kernel, the normalised row also written as Q8_K bytes
+// (Q8KCodec.QuantizeRow) for the projection that reads it: the same partition, tree and per-element
+// expressions, then one wave per 256-element block quantizes the normalised values from the summed row
+// kept in LDS, so `normed` equals add_rms_norm_kernel's and `q8k` the quantizer's bytes of it, bit for bit.
+constexpr int kNormQ8KStaged = 12288;  // longest row kept in LDS (48 KB); longer rows take two launches
+__global__ __launch_bounds__(kThreads) void add_rms_norm_q8k_kernel(float* residual, const float* addend,
+                                                                    const float* __restrict__ w, float epsilon,
+                                                                    int length, float* normed,
+                                                                    uint8_t* __restrict__ q8k) {
+    __shared__ double red[kThreads];
+    extern __shared__ float summed[];  // length floats
+    double part = 0;
+    for (int i = threadIdx.x; i < length; i += kThreads) {
+        const float r = __fadd_rn(residual[i], addend[i]);
+        residual[i] = r;
+        summed[i] = r;
+        const double v = r;
+        part = part + v * v;
+    }
+    const double scale = rms_scale(block_sum(part, red), length, epsilon);  // its barriers publish `summed`
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int b = wave; b < length / 256; b += kThreads / 64) {
+        const int i0 = 256 * b + 4 * lane;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = rms_value(summed[i0 + e], scale, w[i0 + e]);
+            normed[i0 + e] = v[e];
+        }
+        const Q8KLane q = q8k_quantize_values(v, lane);
+        uint8_t* dst = q8k + static_cast<int64_t>(b) * kQ8KBlockBytes;
+        if (q.zero) {
+            uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+            for (int i = lane; i < kQ8KBlockBytes / 4; i += 64) d32[i] = 0u;
+            continue;
+        }
+        reinterpret_cast<uint32_t*>(dst + 4)[lane] = q.packed;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(dst + 260)[lane >> 2] = static_cast<int16_t>(q.group_sum);
+        if (lane == 0) reinterpret_cast<float*>(dst)[0] = q.scale;
+    }
+}
+
 // The attention inputs of one decode position (DenseForward.cs:128-151): q += q_bias and k + k_bias,
 // v + v_bias (when the biases are given), then RopeHalf of q and of the key, the key and value written to
 // their cache slots. Same per-element operations as Add and RopeHalf, so the outputs equal the separate
@@ -804,6 +846,19 @@ hipError_t launch_add(const float* left, const float* right, int length, float* 
 hipError_t launch_add_rms_norm(float* residual, const float* addend, const float* w, float epsilon, int length,
                                float* normed, hipStream_t stream) {
     add_rms_norm_kernel<<<1, kThreads, 0, stream>>>(residual, addend, w, epsilon, length, normed);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rms_norm_q8k(float* residual, const float* addend, const float* w, float epsilon, int length,
+                                   float* normed, uint8_t* q8k, hipStream_t stream) {
+    if (length <= 0 || length % 256 != 0) return hipErrorInvalidValue;
+    if (length > kNormQ8KStaged) {
+        const hipError_t e = launch_add_rms_norm(residual, addend, w, epsilon, length, normed, stream);
+        if (e != hipSuccess) return e;
+        return launch_q8k_quantize(normed, length, 1, q8k, stream);
+    }
+    add_rms_norm_q8k_kernel<<<1, kThreads, static_cast<size_t>(length) * sizeof(float), stream>>>(
+        residual, addend, w, epsilon, length, normed, q8k);
     return hipGetLastError();
 }
 

@@ -9,14 +9,15 @@ cache slot) -> half-split RoPE of q and the new key -> grouped attention over th
 add. Then the final RmsNorm and the output projection. The K-format projections quantize their input to Q8_K
 inside their own launch, so no separate quantization runs. By default the attention inputs (bias adds, RoPE,
 cache writes) are one launch and each residual add shares a launch with the RmsNorm after it: 9 launches per
-layer instead of 14, with bit-identical results. Folded (`folded=True`), each residual add + RmsNorm is
-computed inside the projection launch that consumes it (group input transforms; the residual alternates
-between two buffers, since the launch that writes it is also read by its other workgroups): 7 launches per
-layer, again with bit-identical results. SwiGlu stays its own launch (folded into the down projection, every
-workgroup would evaluate the FP64 exponentials of the whole 8960-wide vector, which costs more than the
-launch: measured 2.12 ms per token with it folded, 1.73 ms without, 1.91 ms fused); in the folded sequence it
-also writes the Q8_K bytes of its output, which the down projection reads instead of quantizing in every
-workgroup.
+layer instead of 14, with bit-identical results. Folded (`folded=True`), the residual add + RmsNorm before
+q/k/v and before gate/up is computed inside those projection launches (group input transforms; the residual
+alternates between two buffers, since the launch that writes it is also read by its other workgroups), the
+attention inputs run inside the split attention, and the add + RmsNorm before the output projection, whose
+launch has 2,374 workgroups, is one single-workgroup launch that also writes the Q8_K bytes the projection
+reads (computed in each of its workgroups it costs more than the launch; for gate/up, with 560 workgroups,
+the fold measured faster). SwiGlu likewise writes the Q8_K bytes of its output for the down projection
+(folded into down, every workgroup would evaluate the FP64 exponentials of the whole 8960-wide vector:
+measured 2.12 ms per token that way). Again bit-identical results.
 """
 from __future__ import annotations
 
@@ -78,6 +79,7 @@ class DeviceDecoder:
         self.gate, self.up, self.activated = buf(c.ffn), buf(c.ffn), buf(c.ffn)
         self.logits = buf(output.rows)
         self.activated_q8k = buf(c.ffn // 256 * 73)  # Q8_K bytes of the down projection's input (292 per block)
+        self.normed_q8k = buf(c.hidden // 256 * 73)  # Q8_K bytes of the output projection's input
         self.zero_kv = buf(self.kv_width)
         self.keys = [buf(c.max_tokens * self.kv_width) for _ in layers]
         self.values = [buf(c.max_tokens * self.kv_width) for _ in layers]
@@ -101,24 +103,23 @@ class DeviceDecoder:
 
     def _folded_groups(self):
         """Per layer the q/k/v group reading RmsNorm(residual + previous down output) (layer 0: RmsNorm of the
-        embedding row) and writing the sum to the second residual buffer, and the gate/up group reading
-        RmsNorm(second residual + o output) and writing the sum back; then the output group reading
-        RmsNorm(residual + last down output)."""
+        embedding row) and writing the sum to the second residual buffer, the gate/up group reading
+        RmsNorm(second residual + o output) and writing the sum back, and the down group reading the Q8_K bytes
+        of SwiGlu; then the output group reading the Q8_K bytes of RmsNorm(residual + last down output)."""
         if self._folded is None:
             c, ctx = self.cfg, self.ctx
             folded = []
             for layer, (m, vec) in enumerate(zip(self.layers, self.vectors)):
+                read, written = self.residual, self.residual_b
                 qkv = HipGroup(ctx, [m["q"], m["k"], m["v"]], [self.normed] * 3, [self.q, self.k, self.v], True)
-                qkv.set_input_add_rms_norm(self.residual, self.projected if layer else 0, vec["attn_norm"],
-                                           c.epsilon, self.residual_b)
+                qkv.set_input_add_rms_norm(read, self.projected if layer else 0, vec["attn_norm"], c.epsilon, written)
                 gateup = HipGroup(ctx, [m["gate"], m["up"]], [self.normed] * 2, [self.gate, self.up], True)
-                gateup.set_input_add_rms_norm(self.residual_b, self.projected, vec["ffn_norm"], c.epsilon,
-                                              self.residual)
+                gateup.set_input_add_rms_norm(written, self.projected, vec["ffn_norm"], c.epsilon, read)
                 down = HipGroup(ctx, [m["down"]], [self.activated], [self.projected], True)
                 down.set_input_q8k(self.activated_q8k)
                 folded.append({"qkv": qkv, "gateup": gateup, "down": down})
             final = HipGroup(ctx, [self.output], [self.normed], [self.logits], True)
-            final.set_input_add_rms_norm(self.residual, self.projected, self.output_norm, c.epsilon, self.residual_b)
+            final.set_input_q8k(self.normed_q8k)
             self._folded = (folded, final)
         return self._folded
 
@@ -127,8 +128,7 @@ class DeviceDecoder:
         the bias adds, RoPE and cache writes of a layer's attention inputs are one launch, and every residual
         add shares its launch with the RmsNorm that follows (bit-identical to the unfused sequence). Folded:
         as fused, with the residual adds and RmsNorms computed inside the projections that consume them and the
-        attention inputs inside the split attention (bit-identical as well; the residual after the token is left
-        in the second buffer)."""
+        attention inputs inside the split attention (bit-identical as well)."""
         c, ops = self.cfg, self.ops
         if not 0 <= position < c.max_tokens:
             raise ValueError("position outside the key/value cache")
@@ -144,6 +144,8 @@ class DeviceDecoder:
                 fg["gateup"].execute()
                 ops.swiglu_q8k(self.gate, self.up, c.ffn, 0, self.activated_q8k)
                 fg["down"].execute()
+            ops.add_rms_norm_q8k(self.residual, self.projected, self.output_norm, c.epsilon, c.hidden, self.normed,
+                                 self.normed_q8k)
             final.execute()
             return
         if fused:
@@ -204,9 +206,9 @@ class DeviceDecoder:
         over several workgroups per head and combined by a second kernel, one more launch per layer."""
         split = position is not None and position + 1 > 32
         extra = len(self.layers) if split else 0
-        if folded:  # q/k/v, the decode attention, o, gate/up, SwiGlu to Q8_K, down per layer
+        if folded:  # q/k/v, the decode attention, o, gate/up, SwiGlu to Q8_K, down; add + RmsNorm to Q8_K, output
             attention = self._decode_attention_launches(position + 1 if position is not None else 1)
-            return 1 + (5 + attention) * len(self.layers) + 1
+            return 1 + (5 + attention) * len(self.layers) + 2
         if fused:
             return 2 + 9 * len(self.layers) + 1 + extra
         per_layer = 14 if all("q_bias" in v for v in self.vectors) else 13

@@ -1424,6 +1424,49 @@ def test_q8k_input_from_the_producer_equals_quantizing_in_the_launch(context, fm
             m.dispose()
 
 
+@pytest.mark.parametrize("columns", [1536, 8960, 12288, 16384])
+def test_add_rms_norm_q8k_equals_add_rms_norm_then_quantizer(context, columns):
+    # satori_hip_add_rms_norm_q8k: residual, normed and the Q8_K bytes equal satori_hip_add_rms_norm followed
+    # by the device quantizer bit for bit, and the bytes equal the oracle's Q8KCodec.QuantizeRow of `normed`
+    # (12,288 columns is the longest row the single launch keeps in LDS; 16,384 takes the two-launch form).
+    g = rng(4545 + columns)
+    residual = (g.standard_normal(columns) * 3).astype(np.float32)
+    addend = g.standard_normal(columns).astype(np.float32)
+    weights = g.uniform(0.5, 1.5, columns).astype(np.float32)
+    weights[512:768] = 0.0  # a block whose normalised values are all zeros
+    q8k_bytes = columns // 256 * 292
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    ops = S.DeviceOps(context)
+    try:
+        r1, r2, da, dw = dev(residual), dev(residual), dev(addend), dev(weights)
+        n1, n2 = dev(np.zeros(columns, np.float32)), dev(np.zeros(columns, np.float32))
+        q1, q2 = dev(np.zeros(q8k_bytes // 4, np.float32)), dev(np.full(q8k_bytes // 4, np.nan, np.float32))
+        ops.add_rms_norm(r1, da, dw, 1e-6, columns, n1)
+        ops.quantize_q8k(n1, columns, 1, q1)
+        ops.add_rms_norm_q8k(r2, da, dw, 1e-6, columns, n2, q2)
+        down = lambda p, n, t=np.float32: context.download(np.zeros(n, t), p)
+        assert np.array_equal(down(r2, columns).view(np.uint32), down(r1, columns).view(np.uint32)), "residual"
+        normed = down(n1, columns)
+        assert np.array_equal(down(n2, columns).view(np.uint32), normed.view(np.uint32)), "normed"
+        q = down(q2, q8k_bytes, np.uint8)
+        assert np.array_equal(q, down(q1, q8k_bytes, np.uint8)), "Q8_K bytes"
+        assert np.array_equal(q, O.q8k_quantize_row(normed)), "Q8_K bytes against the oracle"
+        with pytest.raises(S.ArgumentException):  # not a multiple of 256
+            ops.add_rms_norm_q8k(r2, da, dw, 1e-6, columns - 100, n2, q2)
+        with pytest.raises(S.ArgumentOutOfRangeException):  # the operator's epsilon rule
+            ops.add_rms_norm_q8k(r2, da, dw, 0.0, columns, n2, q2)
+    finally:
+        for p in buffers:
+            context.free(p)
+
+
 def test_device_q8k_quantizer_positions_match_oracle(context):
     g = rng(808)
     columns, positions = 2048, 5
@@ -1542,7 +1585,7 @@ def test_device_decode_token_matches_host_composition(context):
         dec.enqueue(7, 41, folded=True)  # eager work between replays
         folded.execute()
         assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), ("folded", replay)
-    assert dec.launches_per_token(folded=True, position=position) == 2 + 7 * n_layers  # inputs inside the attention
+    assert dec.launches_per_token(folded=True, position=position) == 3 + 7 * n_layers  # inputs inside the attention
     with pytest.raises(S.ArgumentException):
         dev_layers[0]["q"].dispose()  # held by the decoder's group
     with pytest.raises(S.InvalidOperationException):
