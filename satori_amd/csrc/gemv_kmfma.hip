@@ -318,8 +318,9 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
     const int row_c = row < rows ? row : rows - 1;  // rows past the last compute on a live row, store nothing
     const int rounds = (blocks + S - 1) / S;
 
-    // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [32i, 32i + 32) of each block's codes,
-    // bytes [4i, 4i + 4) of its group sums and, for i < 8 S, four scales.
+    // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [16i, 16i + 16) and [4096 + 16i, +16)
+    // of each block's codes (16-byte slices at a 16-byte stride: the LDS writes of a wave touch every bank once
+    // per pass), bytes [4i, 4i + 4) of its group sums and, for i < 8 S, four scales.
     u32x4 sc0[S], sc1[S];
     uint32_t ssum[S];
     u32x4 sscale = {0u, 0u, 0u, 0u};
@@ -328,9 +329,9 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
         for (int s = 0; s < S; ++s) {
             const int b = k * S + s;
             if (b < blocks) {
-                const uint8_t* src = codes + (static_cast<int64_t>(b) * tiles + t) * 8192 + 32 * threadIdx.x;
+                const uint8_t* src = codes + (static_cast<int64_t>(b) * tiles + t) * 8192 + 16 * threadIdx.x;
                 sc0[s] = load16_a4(src);
-                sc1[s] = load16_a4(src + 16);
+                sc1[s] = load16_a4(src + 4096);
                 ssum[s] = load4_a4(sums + (static_cast<int64_t>(b) * tiles + t) * 1024 + 4 * threadIdx.x);
             }
         }
@@ -345,8 +346,8 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             if (k * S + s < blocks) {
-                *reinterpret_cast<u32x4*>(stage[s].codes + 32 * threadIdx.x) = sc0[s];
-                *reinterpret_cast<u32x4*>(stage[s].codes + 32 * threadIdx.x + 16) = sc1[s];
+                *reinterpret_cast<u32x4*>(stage[s].codes + 16 * threadIdx.x) = sc0[s];
+                *reinterpret_cast<u32x4*>(stage[s].codes + 4096 + 16 * threadIdx.x) = sc1[s];
                 *reinterpret_cast<uint32_t*>(stage[s].sums + 4 * threadIdx.x) = ssum[s];
             }
         }
