@@ -28,6 +28,20 @@ import numpy as np
 from . import DeviceOps, HipContext, HipGroup, HipQuantizedMatrix, HipStep
 
 
+def decode_attention_launches(tokens: int, head_dim: int) -> int:
+    """Launches of satori_hip_attention_decode over `tokens` cached tokens, by the library's rule: up to 32
+    tokens, the attention inputs and the one-workgroup attention (2); beyond, the split attention over
+    max(min(32, ceil(tokens / 32)), ceil(tokens / 2048)) workgroups per head, with the inputs inside it
+    (split + combine: 2) while the head fits one workgroup's lanes (at most 256) and each split holds at most
+    64 tokens, else beside it (inputs + split + combine: 3)."""
+    if tokens <= 32:
+        return 2
+    splits = max(min(32, (tokens + 31) // 32), (tokens + 2047) // 2048)
+    per = -(-tokens // splits)
+    fits = per * 8 + 3 * head_dim * 4 + 256 * 8 <= 64 * 1024
+    return 2 if head_dim <= 256 and per <= 64 and fits else 3
+
+
 @dataclass
 class DecoderConfig:
     hidden: int          # embedding width
@@ -188,26 +202,13 @@ class DeviceDecoder:
             ops.rms_norm(self.residual, self.output_norm, c.epsilon, c.hidden, self.normed)
         self.final.execute()
 
-    def _decode_attention_launches(self, tokens: int) -> int:
-        """Launches of satori_hip_attention_decode over `tokens` cached tokens, by the library's rule: the
-        attention inputs run inside the split attention (split + combine) while the head fits one workgroup's
-        lanes (at most 256) and each split holds at most 64 tokens; otherwise they run beside it (inputs +
-        split + combine, or inputs + the one-workgroup attention up to 32 tokens)."""
-        if tokens <= 32:
-            return 2
-        splits = max(min(32, (tokens + 31) // 32), (tokens + 2047) // 2048)
-        per = -(-tokens // splits)
-        head_dim = self.cfg.head_dim
-        fits = per * 8 + 3 * head_dim * 4 + 256 * 8 <= 64 * 1024
-        return 2 if head_dim <= 256 and per <= 64 and fits else 3
-
     def launches_per_token(self, fused: bool = True, folded: bool = False, position: int | None = None) -> int:
         """Kernel launches of one token. At a `position` whose prefix exceeds 32 tokens the attention is split
         over several workgroups per head and combined by a second kernel, one more launch per layer."""
         split = position is not None and position + 1 > 32
         extra = len(self.layers) if split else 0
         if folded:  # q/k/v, the decode attention, o, gate/up, SwiGlu to Q8_K, down; add + RmsNorm to Q8_K, output
-            attention = self._decode_attention_launches(position + 1 if position is not None else 1)
+            attention = decode_attention_launches(position + 1 if position is not None else 1, self.cfg.head_dim)
             return 1 + (5 + attention) * len(self.layers) + 2
         if fused:
             return 2 + 9 * len(self.layers) + 1 + extra

@@ -170,3 +170,16 @@ def test_fixture_blocks_pass_product_validation():
     for fixture, fmt in (("q4k-v1.json", BQ.Q4_K), ("q6k-v1.json", BQ.Q6_K)):
         for case in load_json(fixture)["cases"]:
             S.QuantizedMatVec.validate_payload(hexbytes(case["block_hex"]), S.QuantizedMatrixShape(1, 256, fmt))
+
+
+@pytest.mark.parametrize("tokens,head_dim,launches", [
+    (1, 128, 2), (32, 128, 2),        # one workgroup per head: inputs + attention
+    (33, 128, 2), (512, 128, 2),      # split with the inputs inside it: split + combine
+    (2048, 128, 2),                   # 32 splits of 64 tokens, the last fused length
+    (2049, 128, 3), (4096, 128, 3),   # 32 splits of 65 / 128 tokens: inputs + split + combine
+    (65537, 128, 3),                  # more than 32 splits once a split would exceed 2,048 tokens
+    (512, 320, 3),                    # a head wider than the split workgroup's 256 lanes
+])
+def test_decode_attention_launch_count_follows_split_rule(tokens, head_dim, launches):
+    from satori_amd.decode import decode_attention_launches
+    assert decode_attention_launches(tokens, head_dim) == launches
