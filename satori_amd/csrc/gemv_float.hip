@@ -31,6 +31,7 @@ constexpr int kWideLdsBytes = 40 * 1024;
 // ------------------------------------------------------------------------------------------------
 struct Q8_0Chunk {
     static constexpr int kRowUnroll = 2;
+    static constexpr bool kPipelineShortLanes = false;
     // Payload cap per workgroup (0: none): more, smaller workgroups leave a shorter tail at the end of a large
     // launch (4096x4096 grouped: 5.79 -> 5.96 TB/s); Q4_0 measured slower with the cap (its longer rows make
     // the per-workgroup activation staging the larger cost).
@@ -39,7 +40,7 @@ struct Q8_0Chunk {
     static constexpr int kPadShift = 5;
     struct Regs {
         uint32_t q[8];
-        float scale;
+        uint32_t scale;  // FP16 bits, converted where the dot uses them (not at the load, which would wait)
     };
     struct Consts {};
     __device__ static Consts consts() { return Consts{}; }
@@ -62,7 +63,7 @@ struct Q8_0Chunk {
             r.q[i] = a[i];
             r.q[4 + i] = b[i];
         }
-        r.scale = half_bits_to_float(load2_a2(w.scales + chunk * 2));
+        r.scale = load2_a2(w.scales + chunk * 2);
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -78,7 +79,7 @@ struct Q8_0Chunk {
             acc0 = __builtin_fmaf(sbyte_to_float(r.q[d], 2), x[4 * d + 2], acc0);
             acc1 = __builtin_fmaf(sbyte_to_float(r.q[d], 3), x[4 * d + 3], acc1);
         }
-        return r.scale * (acc0 + acc1);
+        return half_bits_to_float(r.scale) * (acc0 + acc1);
     }
 };
 
@@ -91,12 +92,16 @@ struct Q8_0Chunk {
 // ------------------------------------------------------------------------------------------------
 struct Q4_0Chunk {
     static constexpr int kRowUnroll = 2;
+    // Long rows with fewer than 64 lanes each load the next two chunks while computing the current two
+    // (4096 x 11008 grouped: 5.23 -> 5.71 TB/s at 163 VGPRs, three waves per SIMD instead of four); the
+    // other formats' register sets are larger, and their loops keep one step in flight.
+    static constexpr bool kPipelineShortLanes = true;
     static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 5;
     struct Regs {
         uint32_t q[4];
-        float scale;
+        uint32_t scale;  // FP16 bits, converted where the dot uses them (not at the load, which would wait)
     };
     struct Consts {};
     __device__ static Consts consts() { return Consts{}; }
@@ -117,7 +122,7 @@ struct Q4_0Chunk {
         const u32x4 a = stream16(w.codes + chunk * 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.q[i] = a[i];
-        r.scale = half_bits_to_float(load2_a2(w.scales + chunk * 2));
+        r.scale = load2_a2(w.scales + chunk * 2);
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -137,7 +142,7 @@ struct Q4_0Chunk {
                 acc1 = __builtin_fmaf(sbyte_to_float(hi, i), x[16 + 4 * d + i], acc1);
             }
         }
-        return r.scale * ((acc0 + acc1) * 0.0625f);
+        return half_bits_to_float(r.scale) * ((acc0 + acc1) * 0.0625f);
     }
 };
 
@@ -151,6 +156,7 @@ struct Q4_0Chunk {
 
 struct Q4_KChunk {
     static constexpr int kRowUnroll = 2;
+    static constexpr bool kPipelineShortLanes = false;
     static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 6;
@@ -214,6 +220,7 @@ struct Q4_KChunk {
 // ------------------------------------------------------------------------------------------------
 struct Q6_KChunk {
     static constexpr int kRowUnroll = 1;
+    static constexpr bool kPipelineShortLanes = false;
     static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 64;
     static constexpr int kPadShift = 7;
@@ -330,6 +337,8 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
     constexpr int kStride = THREADS / 64 * kRowsPerPass;  // rows between a lane's consecutive rows
     constexpr int kRowUnroll = F::kRowUnroll;
     constexpr int kStep = kStride * kRowUnroll;      // rows per iteration of the whole workgroup
+    // Software-pipelined chunk loop (see the format): staged activations and fewer than 64 lanes per row.
+    constexpr bool kPipelined = F::kPipelineShortLanes && L < 64 && XLDS;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane / L;
@@ -381,27 +390,81 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
                 rows[u] = F::row_ref(m, s, base + u * kStride + sub);
             }
             int c = lr;
-            for (; c + L < nchunks; c += 2 * L) {  // two chunks per step: both rows' loads of both in flight
-                typename F::Regs ra[kRowUnroll], rb[kRowUnroll];
+            if constexpr (kPipelined) {
+                // Two chunks per step, the next step's loaded while this step's are computed: register sets A
+                // and B take turns. Rows past the end load and compute on the last live row (nothing is
+                // stored for them), so no load sits behind a branch.
+                typename F::Row live[kRowUnroll];
 #pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u) {
-                    const int row = base + u * kStride + sub;
-                    if (row < row_end) {
-                        F::load(rows[u], c, ra[u]);
-                        F::load(rows[u], c + L, rb[u]);
+                for (int u = 0; u < kRowUnroll; ++u)
+                    live[u] = F::row_ref(m, s, min(base + u * kStride + sub, row_end - 1));
+                auto load_pair = [&](int cc, typename F::Regs (&r0)[kRowUnroll],
+                                     typename F::Regs (&r1)[kRowUnroll]) {
+#pragma unroll
+                    for (int u = 0; u < kRowUnroll; ++u) {
+                        F::load(live[u], cc, r0[u]);
+                        F::load(live[u], cc + L, r1[u]);
+                    }
+                };
+                auto dot_pair = [&](int cc, const typename F::Regs (&r0)[kRowUnroll],
+                                    const typename F::Regs (&r1)[kRowUnroll]) {
+                    F::load_x(xf, cc, xr);
+#pragma unroll
+                    for (int u = 0; u < kRowUnroll; ++u) acc[u] += F::dot(r0[u], xr, k);
+                    F::load_x(xf, cc + L, xr);
+#pragma unroll
+                    for (int u = 0; u < kRowUnroll; ++u) acc[u] += F::dot(r1[u], xr, k);
+                };
+                // The steady-state loop issues its loads unconditionally, so the compiler's wait before each
+                // step counts exactly the loads issued after that step's own.
+                typename F::Regs a0[kRowUnroll], a1[kRowUnroll], b0[kRowUnroll], b1[kRowUnroll];
+                int pairs = lr < nchunks ? (nchunks - lr + L - 1) / L / 2 : 0;
+                if (pairs > 0) {
+                    load_pair(c, a0, a1);
+                    for (; pairs >= 3; pairs -= 2) {  // (scheduling barriers keep each step's loads in place)
+                        load_pair(c + 2 * L, b0, b1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        dot_pair(c, a0, a1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        load_pair(c + 4 * L, a0, a1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        dot_pair(c + 2 * L, b0, b1);
+                        __builtin_amdgcn_sched_barrier(0);
+                        c += 4 * L;
+                    }
+                    if (pairs == 2) {
+                        load_pair(c + 2 * L, b0, b1);
+                        dot_pair(c, a0, a1);
+                        dot_pair(c + 2 * L, b0, b1);
+                        c += 4 * L;
+                    } else {
+                        dot_pair(c, a0, a1);
+                        c += 2 * L;
                     }
                 }
-                F::load_x(xf, c, xr);
+            } else {
+                for (; c + L < nchunks; c += 2 * L) {  // two chunks per step: both rows' loads of both in flight
+                    typename F::Regs ra[kRowUnroll], rb[kRowUnroll];
 #pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u) {
-                    const int row = base + u * kStride + sub;
-                    if (row < row_end) acc[u] += F::dot(ra[u], xr, k);
-                }
-                F::load_x(xf, c + L, xr);
+                    for (int u = 0; u < kRowUnroll; ++u) {
+                        const int row = base + u * kStride + sub;
+                        if (row < row_end) {
+                            F::load(rows[u], c, ra[u]);
+                            F::load(rows[u], c + L, rb[u]);
+                        }
+                    }
+                    F::load_x(xf, c, xr);
 #pragma unroll
-                for (int u = 0; u < kRowUnroll; ++u) {
-                    const int row = base + u * kStride + sub;
-                    if (row < row_end) acc[u] += F::dot(rb[u], xr, k);
+                    for (int u = 0; u < kRowUnroll; ++u) {
+                        const int row = base + u * kStride + sub;
+                        if (row < row_end) acc[u] += F::dot(ra[u], xr, k);
+                    }
+                    F::load_x(xf, c + L, xr);
+#pragma unroll
+                    for (int u = 0; u < kRowUnroll; ++u) {
+                        const int row = base + u * kStride + sub;
+                        if (row < row_end) acc[u] += F::dot(rb[u], xr, k);
+                    }
                 }
             }
             for (; c < nchunks; c += L) {
