@@ -79,7 +79,10 @@ __device__ __forceinline__ int64_t pack_code_offset(int b, int t, int tiles, int
     return (static_cast<int64_t>(b) * tiles + t) * 8192 + j * (8192 / chunks) + (32 * h + r) * half + k % half;
 }
 
-// One wave per (position, block): four blocks of one position per workgroup.
+// One wave per block and four consecutive positions, one 16-lane row per position (the 16-lane quantizer:
+// lane j holds the block's group j, codes 16j .. 16j + 15, which land contiguous in the operand order and
+// whose group sum needs no cross-lane step); four blocks per workgroup. Positions past the last are zero
+// codes, sums and scale (computed on the last position's values, then cleared).
 __global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict__ x, int columns, int positions,
                                                          int tiles, int chunks, uint8_t* __restrict__ codes,
                                                          float* __restrict__ scales, _Float16* __restrict__ sums) {
@@ -87,21 +90,37 @@ __global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= blocks) return;
     const int lane = threadIdx.x & 63;
-    const int p = blockIdx.y;
+    const int j = lane & 15;
+    const int p = blockIdx.y * 4 + (lane >> 4);
     const int t = p >> 5, r = p & 31;
-    Q8KLane q{0u, 0, 0.0f, true};
-    if (p < positions) {
-        float v[4];
-        q8k_load_values(x + static_cast<int64_t>(p) * columns + 256 * b, lane, v);
-        q = q8k_quantize_values(v, lane);
+    const float* src = x + static_cast<int64_t>(min(p, positions - 1)) * columns + 256 * b + 16 * j;
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(src + 4 * q));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * q + e] = __uint_as_float(raw[e]);
     }
-    store_u32(reinterpret_cast<uint32_t*>(codes + pack_code_offset(b, t, tiles, chunks, 4 * lane, r)), q.packed);
-    if (lane == 0) store_f32(scales + (static_cast<int64_t>(b) * tiles + t) * 32 + r, q.scale);
-    if ((lane & 3) == 0) {  // lane 4g holds the sum of group g (codes 16g .. 16g + 15)
-        const int g = lane >> 2;
-        sums[(static_cast<int64_t>(b) * tiles + t) * 512 + (32 * (g >> 3) + r) * 8 + (g & 7)] =
-            static_cast<_Float16>(static_cast<float>(q.group_sum));
+    Q8KRow16 qr = q8k_quantize_row16(v, lane);
+    if (p >= positions) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) qr.packed[w] = 0u;
+        qr.group_sum = 0;
+        qr.scale = 0.0f;
     }
+    const int64_t bt = static_cast<int64_t>(b) * tiles + t;
+    // Codes 16j .. 16j + 15 in pieces of 128 / chunks bytes (one 16-byte piece for Q4_K, two 8-byte for Q6_K).
+    if (chunks == 8) {
+        *reinterpret_cast<u32x4*>(codes + pack_code_offset(b, t, tiles, chunks, 16 * j, r)) =
+            u32x4{qr.packed[0], qr.packed[1], qr.packed[2], qr.packed[3]};
+    } else {
+        *reinterpret_cast<uint2*>(codes + pack_code_offset(b, t, tiles, chunks, 16 * j, r)) =
+            uint2{qr.packed[0], qr.packed[1]};
+        *reinterpret_cast<uint2*>(codes + pack_code_offset(b, t, tiles, chunks, 16 * j + 8, r)) =
+            uint2{qr.packed[2], qr.packed[3]};
+    }
+    sums[bt * 512 + (32 * (j >> 3) + r) * 8 + (j & 7)] = static_cast<_Float16>(static_cast<float>(qr.group_sum));
+    if (j == 0) store_f32(scales + bt * 32 + r, qr.scale);
 }
 
 // The weights one lane needs for one block: its row's data for its k half of every chunk.
@@ -487,7 +506,7 @@ hipError_t launch_kmfma_pack(int format, const float* x, int blocks, int positio
     if (format != kQ4_K && format != kQ6_K) return hipErrorInvalidValue;
     const int tiles = (positions + kTile - 1) / kTile;
     const int chunks = format == kQ4_K ? 8 : 16;
-    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile), 256, 0, stream>>>(
+    kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile / 4), 256, 0, stream>>>(
         x, blocks * 256, positions, tiles, chunks, workspace,
         reinterpret_cast<float*>(workspace + kmfma_scales_offset(blocks, tiles)),
         reinterpret_cast<_Float16*>(workspace + kmfma_sums_offset(blocks, tiles)));
