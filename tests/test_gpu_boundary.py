@@ -305,6 +305,33 @@ def test_attention_odd_head_widths_match_oracle(context, head_dim, tokens, query
                 f"attention {head_dim} x {tokens}")
 
 
+@pytest.mark.parametrize("query_heads,kv_heads,head_dim,tokens", [(12, 2, 128, 4096), (12, 2, 128, 2049),
+                                                                  (28, 4, 128, 3000), (32, 4, 64, 8192),
+                                                                  (4, 1, 80, 7000), (18, 2, 128, 4096)])
+def test_grouped_query_split_equals_per_head_split(context, query_heads, kv_heads, head_dim, tokens):
+    # Query heads sharing a key/value head: the same attention with every key/value head repeated once per
+    # query head (one query head per key/value head) must give the same bits, whichever workgroup layout each
+    # takes (one workgroup per key/value head serving its query heads, or one per query head), and both must
+    # match the oracle. Group sizes 6, 7, 8 and 4 (80 lanes: eighths of 10 lanes), and 9 (past the grouped
+    # form's 8).
+    g = rng(query_heads * 1000 + tokens)
+    group = query_heads // kv_heads
+    q = g.standard_normal(query_heads * head_dim).astype(np.float32)
+    keys = (g.standard_normal((tokens, kv_heads, head_dim)) * 0.3).astype(np.float32)
+    values = g.standard_normal((tokens, kv_heads, head_dim)).astype(np.float32)
+    out = np.zeros(query_heads * head_dim, np.float32)
+    S.TransformerOps.grouped_attention(q, keys.reshape(-1), values.reshape(-1), query_heads, kv_heads, head_dim,
+                                       tokens, out, context)
+    wide_k = np.repeat(keys, group, axis=1).reshape(-1)
+    wide_v = np.repeat(values, group, axis=1).reshape(-1)
+    per_head = np.zeros(query_heads * head_dim, np.float32)
+    S.TransformerOps.grouped_attention(q, wide_k, wide_v, query_heads, query_heads, head_dim, tokens, per_head,
+                                       context)
+    assert np.array_equal(out.view(np.uint32), per_head.view(np.uint32))
+    _within_ulp(out, O.grouped_attention(q, keys.reshape(-1), values.reshape(-1), query_heads, kv_heads, head_dim,
+                                         tokens), f"attention {query_heads}/{kv_heads} x {tokens}")
+
+
 def _hip():
     rt = ctypes.CDLL("libamdhip64.so.7")
     rt.hipStreamCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
