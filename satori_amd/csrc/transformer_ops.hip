@@ -420,19 +420,42 @@ struct DecodeInputs {
     double base;
 };
 
+// Units (key/value head, split), dealt to the 8 XCDs round-robin; each XCD runs its units' query heads on
+// consecutive workgroups of its own: workgroup w is slot w / 8 of XCD w % 8, slot k serving query head k % group
+// of the XCD's unit k / group. The grid has 8 * ceil(units / 8) * group workgroups; those past the last unit
+// return false.
+__device__ __forceinline__ bool split_unit(int w, int group, int kv_heads, int splits, int& head, int& split) {
+    const int xcd = w & 7, k = w >> 3;
+    const int unit = (k / group) * 8 + xcd;
+    if (unit >= kv_heads * splits) return false;
+    const int kv_head = unit / splits;
+    split = unit - kv_head * splits;
+    head = kv_head * group + k % group;
+    return true;
+}
+
+int split_grid(int query_heads, int kv_heads, int splits) {
+    const int group = query_heads / kv_heads;
+    return 8 * ((kv_heads * splits + 7) / 8) * group;
+}
+
 template <bool INPUTS>
 __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const float* __restrict__ q,
                                                                         const float* __restrict__ k,
                                                                         const float* __restrict__ v, int query_heads,
                                                                         int kv_heads, int head_dim, int tokens, int per,
-                                                                        double* __restrict__ partial, DecodeInputs in,
-                                                                        float* k_cache, float* v_cache) {
+                                                                        int splits, double* __restrict__ partial,
+                                                                        DecodeInputs in, float* k_cache, float* v_cache) {
     extern __shared__ double es[];  // this split's exponentials (per), then the staged query lanes
     __shared__ double red[kSplitThreads];
-    const int head = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+    // Workgroup -> (query head, split): the query heads that share a key/value head and a split run on one
+    // XCD (workgroup ids are dealt to the 8 XCDs round-robin), so that XCD's L2 fetches their key and value
+    // rows once for all of them (split_unit).
+    const int group = query_heads / kv_heads;
+    int head, split;
+    if (!split_unit(blockIdx.x, group, kv_heads, splits, head, split)) return;  // whole workgroup
     const int t0 = static_cast<int>(min(static_cast<int64_t>(split) * per, static_cast<int64_t>(tokens)));
     const int t1 = min(tokens, t0 + per);
-    const int group = query_heads / kv_heads;
     const int kv_head = head / group;
     const int kv_width = kv_heads * head_dim;
     const double scale = 1.0 / __dsqrt_rn(static_cast<double>(head_dim));
@@ -950,9 +973,9 @@ hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k
     const int splits = attention_splits(tokens);
     const int per = (tokens + splits - 1) / splits;
     const DecodeInputs in{q_bias, k_new, k_bias, v_new, v_bias, rope, position, rotary, base};
-    attention_split_kernel<true><<<dim3(query_heads, splits), kSplitThreads,
-                                   split_lds_bytes_inputs(per, head_dim), stream>>>(q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, per, partials,
-                                             in, k_cache, v_cache);
+    attention_split_kernel<true><<<split_grid(query_heads, kv_heads, splits), kSplitThreads,
+                                   split_lds_bytes_inputs(per, head_dim), stream>>>(
+        q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, per, splits, partials, in, k_cache, v_cache);
     attention_combine_kernel<true><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out, q, in);
     return hipGetLastError();
 }
@@ -968,8 +991,9 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
     }
     if (!partials) return hipErrorInvalidValue;
     const int per = (tokens + splits - 1) / splits;
-    attention_split_kernel<false><<<dim3(query_heads, splits), kSplitThreads, split_lds_bytes(per, head_dim), stream>>>(
-        q, k, v, query_heads, kv_heads, head_dim, tokens, per, partials, DecodeInputs{}, nullptr, nullptr);
+    attention_split_kernel<false><<<split_grid(query_heads, kv_heads, splits), kSplitThreads,
+                                    split_lds_bytes(per, head_dim), stream>>>(
+        q, k, v, query_heads, kv_heads, head_dim, tokens, per, splits, partials, DecodeInputs{}, nullptr, nullptr);
     attention_combine_kernel<false><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out,
                                                                               nullptr, DecodeInputs{});
     return hipGetLastError();
