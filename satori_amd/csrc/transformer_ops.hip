@@ -375,10 +375,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // o_j = sum_t e_t * v_tj, all FP64; the combine kernel rescales each split by exp(m_split - M) with M the
 // head's maximum and divides by the rescaled total. Against the reference's softmax-then-sum this
 // reassociates FP64 operations only (far below the FP32 output's last place). Any prefix length and head
-// width: up to 32 splits of at least 32 tokens, and more splits once a split would exceed 2,048 tokens (its
-// exponentials stay in LDS).
+// width: up to 32 splits of at least 32 tokens, up to 64 of at least 128 beyond 4,096 tokens, and more
+// splits once a split would exceed 2,048 tokens (its exponentials stay in LDS).
 constexpr int kSplitThreads = 256;
-constexpr int kMinSplits = 32;         // splits of a long prefix before the per-split token bound applies
+constexpr int kMinSplits = 32;         // splits of a prefix of up to 4,096 tokens
+constexpr int kLongSplits = 64;        // splits of a longer prefix before the per-split token bound applies
 constexpr int kMaxSplitTokens = 2048;  // tokens of one split (its FP64 exponentials in LDS: 16 KB)
 constexpr int kMaxSplitsPerLaunch = 65535;
 constexpr int kStagedQuery = 8192;     // query lanes staged in LDS; wider heads read the query from global memory
@@ -898,10 +899,13 @@ hipError_t launch_attention_inputs(float* q, const float* q_bias, const float* k
 
 int attention_splits(int tokens) {
     // One workgroup per head up to 32 tokens; then at least 32 tokens per split and at most 32 splits (a
-    // 4096-token context: 128 tokens per split, 384 workgroups for 12 heads; 16 and 64 splits measured
-    // slower there), and beyond 65,536 tokens as many splits as keep each at most 2,048 tokens.
+    // 4096-token context: 128 tokens per split, 384 workgroups for 12 heads; 16 splits measured slower, 64
+    // no faster alone and slower once the decode fuses its inputs at 64 tokens per split); beyond 4,096
+    // tokens 128 tokens per split up to 64 splits (8,192 tokens: 21.5 against 26.0 us per layer with 32
+    // splits); and beyond that as many splits as keep each at most 2,048 tokens.
     if (tokens <= 32) return 1;
     int splits = std::min(kMinSplits, (tokens + 31) / 32);
+    splits = std::max(splits, std::min(kLongSplits, (tokens + 127) / 128));
     splits = std::max(splits, (tokens + kMaxSplitTokens - 1) / kMaxSplitTokens);
     return std::min(splits, kMaxSplitsPerLaunch);
 }

@@ -276,10 +276,10 @@ def _within_ulp(actual, expected, name, ulps=1):
     assert np.all(err <= ulps * spacing), f"{name}: max err {err.max()} at {np.argmax(err - ulps * spacing)}"
 
 
-@pytest.mark.parametrize("tokens", [6913, 8192, 16384, 32768, 70001])
+@pytest.mark.parametrize("tokens", [4097, 6913, 8192, 16384, 32768, 70001, 131073])
 def test_attention_long_prefixes_match_oracle(context, tokens):
-    # Qwen-1.5B heads (12 query, 2 key/value, 128 lanes): 32 splits up to 65,536 tokens, then splits of at
-    # most 2,048 tokens (70,001 tokens: 35 splits).
+    # Qwen-1.5B heads (12 query, 2 key/value, 128 lanes): 32 splits up to 4,096 tokens, then splits of 128
+    # tokens up to 64 (6,913 tokens: 55 splits), then 64 splits of up to 2,048 tokens.
     g = rng(tokens)
     q = g.standard_normal(12 * 128).astype(np.float32)
     keys = (g.standard_normal(tokens * 256) * 0.3).astype(np.float32)

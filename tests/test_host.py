@@ -177,7 +177,9 @@ def test_fixture_blocks_pass_product_validation():
     (33, 128, 2), (512, 128, 2),      # split with the inputs inside it: split + combine
     (2048, 128, 2),                   # 32 splits of 64 tokens, the last fused length
     (2049, 128, 3), (4096, 128, 3),   # 32 splits of 65 / 128 tokens: inputs + split + combine
-    (65537, 128, 3),                  # more than 32 splits once a split would exceed 2,048 tokens
+    (4097, 128, 3), (8192, 128, 3),   # 33 / 64 splits of 125 / 128 tokens
+    (131072, 128, 3), (131073, 128, 3),  # 64 splits of 2,048 tokens, then as many as keep a split at 2,048
+    (65537, 128, 3),
     (512, 320, 3),                    # a head wider than the split workgroup's 256 lanes
 ])
 def test_decode_attention_launch_count_follows_split_rule(tokens, head_dim, launches):
