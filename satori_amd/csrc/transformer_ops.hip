@@ -940,13 +940,16 @@ size_t split_lds_bytes_inputs(int per, int head_dim) {
 }
 
 // The fused form needs the split path, one thread per lane of the head (at most 256 lanes) and room for the new
-// row's key and value. It is taken while splits hold at most 64 tokens: measured per layer of a Qwen-1.5B
-// token (12 / 2 heads of 128 lanes, 28 layers' caches), fused against the separate input launch, 12.5 vs
-// 13.6 us at 512 tokens (16 splits of 32) but 22.6 vs 20.7 us at 4,096 (32 splits of 128), where the fused
+// row's key and value. It is taken while splits hold at most 80 tokens: measured per layer of a Qwen-1.5B
+// token (12 / 2 heads of 128 lanes, 28 layers' caches, attention and combine), fused against the separate
+// input launch, 11.1 vs 12.2 us at 512 tokens (16 splits of 32), 15.1 vs 17.0 at 2,049 (65 per split), 17.5
+// vs 18.5 at 2,560 (80), but 19.1 vs 16.9 at 3,072 (96) and 20.7 vs 18.6 at 4,096 (128), where the fused
 // split launch's longer score and value loops cost more than the launch it saves.
+constexpr int kFusedSplitTokens = 80;
+
 bool decode_fusable(int tokens, int head_dim) {
     const int splits = attention_splits(tokens);
-    if (splits == 1 || head_dim > kSplitThreads || (tokens + splits - 1) / splits > 64) return false;
+    if (splits == 1 || head_dim > kSplitThreads || (tokens + splits - 1) / splits > kFusedSplitTokens) return false;
     const int per = (tokens + splits - 1) / splits;
     return split_lds_bytes_inputs(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
 }

@@ -33,13 +33,13 @@ def decode_attention_launches(tokens: int, head_dim: int) -> int:
     tokens, the attention inputs and the one-workgroup attention (2); beyond, the split attention over
     max(min(32, ceil(tokens / 32)), min(64, ceil(tokens / 128)), ceil(tokens / 2048)) workgroups per head,
     with the inputs inside it (split + combine: 2) while the head fits one workgroup's lanes (at most 256)
-    and each split holds at most 64 tokens, else beside it (inputs + split + combine: 3)."""
+    and each split holds at most 80 tokens, else beside it (inputs + split + combine: 3)."""
     if tokens <= 32:
         return 2
     splits = max(min(32, (tokens + 31) // 32), min(64, (tokens + 127) // 128), (tokens + 2047) // 2048)
     per = -(-tokens // splits)
     fits = per * 8 + 3 * head_dim * 4 + 256 * 8 <= 64 * 1024
-    return 2 if head_dim <= 256 and per <= 64 and fits else 3
+    return 2 if head_dim <= 256 and per <= 80 and fits else 3
 
 
 @dataclass

@@ -383,6 +383,7 @@ def test_split_attentions_on_two_streams_do_not_share_a_workspace(context):
 @pytest.mark.parametrize("position,heads,kv_heads,head_dim,rotary,biases", [
     (0, 12, 2, 128, 128, True), (31, 12, 2, 128, 128, True), (32, 12, 2, 128, 128, True),
     (511, 12, 2, 128, 128, True), (2047, 12, 2, 128, 128, True), (2048, 12, 2, 128, 128, True),
+    (2559, 12, 2, 128, 128, True), (2560, 12, 2, 128, 128, True),
     (4095, 12, 2, 128, 128, False), (70000, 4, 2, 128, 64, True),
     (300, 14, 2, 80, 80, True), (100, 3, 3, 24, 16, False), (65, 4, 1, 1024, 512, True)])
 def test_attention_decode_equals_inputs_then_attention(context, position, heads, kv_heads, head_dim, rotary, biases):

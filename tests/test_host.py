@@ -175,8 +175,9 @@ def test_fixture_blocks_pass_product_validation():
 @pytest.mark.parametrize("tokens,head_dim,launches", [
     (1, 128, 2), (32, 128, 2),        # one workgroup per head: inputs + attention
     (33, 128, 2), (512, 128, 2),      # split with the inputs inside it: split + combine
-    (2048, 128, 2),                   # 32 splits of 64 tokens, the last fused length
-    (2049, 128, 3), (4096, 128, 3),   # 32 splits of 65 / 128 tokens: inputs + split + combine
+    (2048, 128, 2), (2049, 128, 2),   # 32 splits of 64 / 65 tokens
+    (2560, 128, 2),                   # 32 splits of 80 tokens, the last fused length
+    (2561, 128, 3), (4096, 128, 3),   # 32 splits of 81 / 128 tokens: inputs + split + combine
     (4097, 128, 3), (8192, 128, 3),   # 33 / 64 splits of 125 / 128 tokens
     (131072, 128, 3), (131073, 128, 3),  # 64 splits of 2,048 tokens, then as many as keep a split at 2,048
     (65537, 128, 3),
