@@ -116,6 +116,7 @@ class Case:
     def __init__(self, ctx, name, create, payload_bytes, rows, columns, x, quantized, copies=None):
         self.ctx, self.name, self.payload_bytes, self.rows, self.columns = ctx, name, payload_bytes, rows, columns
         self.quantized = quantized
+        self.expected = self.bound = None  # set by check_case
         self.copies = copies or max(1, math.ceil(ROTATION_BYTES / payload_bytes))
         first = create()
         self.mats = [first] + [first.clone() for _ in range(self.copies - 1)]
@@ -208,21 +209,30 @@ def check_case(ctx, case: Case, data, rows, columns, fmt, x, quantized) -> dict:
         expected, bound = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x)), None
     else:
         expected, bound = O.q_matvec_scalar(data, rows, columns, int(fmt), x), fp32_bound(data, rows, columns, fmt, x)
+    case.expected, case.bound = expected, bound
     case.run_group()
+    worst = check_outputs(ctx, case, "grouped launch")
+    return {"parity_checked": True, "parity_copies": case.copies,
+            "parity": "bit-exact" if bound is None else f"max |err| / (1e-5 sum|w x|) = {worst:.3g}"}
+
+
+def check_outputs(ctx, case: Case, what: str) -> float:
+    """Every copy's output against the expected values check_case stored (raises ParityError); returns the
+    worst error as a fraction of the bound (0 for bit-exact comparisons)."""
     ctx.synchronize()
     worst = 0.0
     for i, dy in enumerate(case.dy):
-        y = ctx.download(np.zeros(rows, np.float32), dy)
-        if bound is None:
-            if not np.array_equal(y.view(np.uint32), expected.view(np.uint32)):
-                raise ParityError(f"{case.name}: copy {i} differs from the oracle")
+        y = ctx.download(np.zeros(case.rows, np.float32), dy)
+        ctx.upload(dy, np.full(case.rows, np.nan, np.float32))  # the next launch checked must write it again
+        if case.bound is None:
+            if not np.array_equal(y.view(np.uint32), case.expected.view(np.uint32)):
+                raise ParityError(f"{case.name} ({what}): copy {i} differs from the oracle")
         else:
-            ratio = np.abs(y.astype(np.float64) - expected) / np.maximum(bound, 1e-300)
+            ratio = np.abs(y.astype(np.float64) - case.expected) / np.maximum(case.bound, 1e-300)
             if not np.all(np.isfinite(y)) or not np.all(ratio <= 1.0):
-                raise ParityError(f"{case.name}: copy {i} outside 1e-5 * sum|w x| (worst ratio {ratio.max()})")
+                raise ParityError(f"{case.name} ({what}): copy {i} outside 1e-5 * sum|w x| (worst ratio {ratio.max()})")
             worst = max(worst, float(ratio.max()))
-    return {"parity_checked": True, "parity_copies": case.copies,
-            "parity": "bit-exact" if bound is None else f"max |err| / (1e-5 sum|w x|) = {worst:.3g}"}
+    return worst
 
 
 def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
@@ -244,6 +254,10 @@ def measure(ctx, events, case: Case, steps, warmup, single=True) -> dict:
     if single:
         # One launch per matrix, issued back to back from Python (the ctypes call and the library's host
         # work included), then the same launches captured once and replayed (the device time per launch).
+        if case.expected is not None:  # single matrices may take another plan than the group
+            case.run_single()
+            check_outputs(ctx, case, "single launches")
+            out["single_launch_parity_checked"] = True
         single_ms = time_launches(ctx, events, case.run_single, max(2, steps // 4), 1)
         out["single_launch_us"] = single_ms * 1e3 / case.copies
         out["single_launch_gbs"] = step_bytes / (single_ms * 1e-3) / 1e9

@@ -23,6 +23,8 @@
 // they sit at the start of the plan's scratch buffer.
 // (Letting the last workgroup of an item add them itself needs device-scope release/acquire fences per
 // workgroup, which on gfx950 write back and invalidate the L2 and cost more than the second launch.)
+// A single matrix at one position whose workgroups all fit on the chip at once runs instead one kernel,
+// t2_slice_kernel below, whose column slices meet through atomic exchanges (no fences, no second launch).
 #include <algorithm>
 #include <cstring>
 #include <type_traits>
@@ -247,6 +249,152 @@ __global__ __launch_bounds__(64 * W) void t2_fixup_kernel(MatDesc one, const Mat
     store_f32(m.y + static_cast<int64_t>(f.position) * m.rows + row, sum);
 }
 
+// ---- One matrix at one position: column slices joined in the kernel ----
+//
+// A single MatVec is latency-bound, and the stream-K plan's second launch is a large part of its time. Here
+// workgroup (panel, slice) owns one 64-row panel and a contiguous slice of its tiles; each wave takes one
+// tile at a time with its own pair tables, so no wave waits for tables another wave builds. The waves' row sums are added in LDS in wave order, and
+// the S slices of a panel are joined by a binary tree of 64-bit atomic exchanges per row: the two siblings
+// of a node each swap (1 << 32 | bits of their sum) into the node's slot; the one that finds the slot empty
+// is done, the other adds the two sums (left + right, whichever came first) and carries the result up, and
+// puts the slot back to empty. Each value travels inside the atomic that the reader sees, so no fence is
+// needed, and the order of every addition is fixed by the tree, so results do not depend on scheduling.
+// The slots start empty (zeroed with the plan's scratch) and every launch leaves them empty.
+struct T2SliceArgs {
+    int columns;
+    int tiles;
+    int chunks;
+    int slots;
+    int panels;
+    int slices;                     // S
+    int groups;                     // tiles per slice
+    int pad_;
+    unsigned long long* exchange;   // [tree node][panels * 64], zero
+};
+
+constexpr int kSliceMaxWaves = 16;  // 16 waves x 4 KB of tables fill the 64 KB of LDS the kernel uses
+constexpr int kSliceMaxSlices = 8;  // at most three levels of exchanges
+
+// Orders this wave's LDS accesses across the call: the LDS executes one wave's instructions in issue
+// order, so once the wave has waited for its own outstanding LDS operations, keeping the compiler from moving
+// loads and stores across the point is all that the other lanes' table entries need.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int B>
+__global__ __launch_bounds__(64 * kSliceMaxWaves) void t2_slice_kernel(MatDesc one, const MatDesc* __restrict__ group,
+                                                                      T2SliceArgs a) {
+    const MatDesc m = group ? group[0] : one;
+    extern __shared__ float lds[];  // [waves][kTableFloats] tables, then [waves][64] wave sums
+    const int waves = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* table = lds + wave * kTableFloats;
+    const int panel = blockIdx.x / a.slices, slice = blockIdx.x - panel * a.slices;
+    const int g_begin = slice * a.groups, g_end = min(a.tiles, g_begin + a.groups);
+    const uint8_t* codes = m.w + static_cast<int64_t>(panel) * a.chunks * 1024 + lane * 16;
+    const uint8_t* scales =
+        m.w + static_cast<int64_t>(a.panels) * a.chunks * 1024 + static_cast<int64_t>(panel) * a.slots * 256 + lane * 4;
+    // Table entry (c0 + 4 c1) of the lane's pair: entries 4 c1 .. 4 c1 + 3 are written as one 16-byte store.
+    const auto build = [&](float x0, float x1) {
+        const float4 lo = make_float4(0.0f, x0, -x0, 0.0f);
+#pragma unroll
+        for (int c1 = 0; c1 < 4; ++c1) {
+            const float h = c1 == 1 ? x1 : (c1 == 2 ? -x1 : 0.0f);
+            *reinterpret_cast<float4*>(table + lane * 16 + 4 * c1) =
+                make_float4(lo.x + h, lo.y + h, lo.z + h, lo.w + h);
+        }
+    };
+    // Wave w takes tiles g_begin + w, + waves, ... A B = 256 block spans two tiles, which may go to different
+    // waves or slices: each half's sum is multiplied by the block scale on its own.
+    float acc = 0.0f;
+    for (int u = g_begin + wave; u < g_end; u += waves) {
+        // The activations first: the table build then waits only for them, while the codes stream in.
+        const int col = u * kTile + 2 * lane;
+        const float x0 = col < a.columns ? load_f32(m.x + col) : 0.0f;
+        const float x1 = col + 1 < a.columns ? load_f32(m.x + col + 1) : 0.0f;
+        const u32x4 c0 = stream16(codes + (2 * u) * 1024);
+        const u32x4 c1 = stream16(codes + (2 * u + 1) * 1024);
+        float s0, s1 = 0.0f;
+        if constexpr (B == 64) {
+            s0 = __uint_as_float(stream4(scales + (2 * u) * 256));
+            s1 = __uint_as_float(stream4(scales + (2 * u + 1) * 256));
+        } else if constexpr (B == 128) {
+            s0 = __uint_as_float(stream4(scales + u * 256));
+        } else {
+            s0 = __uint_as_float(stream4(scales + (u >> 1) * 256));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the build waits for x
+        build(x0, x1);
+        wave_lds_order();  // every lane's pair table written
+        float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const u32x4& rec = half == 0 ? c0 : c1;
+            float s0p = 0.0f, s1p = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t l4 = rec[d] & 0x3C3C3C3Cu;
+                const uint32_t h4 = __builtin_amdgcn_alignbit(rec[(d + 1) & 3], rec[d], 4) & 0x3C3C3C3Cu;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int pair = 32 * half + 8 * d + 2 * k;
+                    const uint32_t ia = __builtin_amdgcn_perm(0u, l4, 0x0C0C0C00u | k);
+                    const uint32_t ib = __builtin_amdgcn_perm(0u, h4, 0x0C0C0C00u | k);
+                    const char* base = reinterpret_cast<const char*>(table + pair * 16);
+                    const float ta = *reinterpret_cast<const float*>(base + ia);
+                    const float tb = *reinterpret_cast<const float*>(base + 64 + ib);
+                    if (d == 0 && k == 0) {
+                        s0p = ta;
+                        s1p = tb;
+                    } else {
+                        s0p += ta;
+                        s1p += tb;
+                    }
+                }
+            }
+            (half == 0 ? lo : hi) = s0p + s1p;
+        }
+        wave_lds_order();  // the tables read before the next tile's build overwrites them
+        if constexpr (B == 64) {
+            acc += lo * s0;
+            acc += hi * s1;
+        } else {
+            acc += (lo + hi) * s0;
+        }
+    }
+    __syncthreads();  // every wave is done with its tables
+    float* sums = lds;
+    sums[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    float piece = 0.0f;
+    for (int w = 0; w < waves; ++w) piece += sums[w * 64 + lane];
+
+    const int row = panel * kT2PanelRows + lane;
+    const int64_t stride = static_cast<int64_t>(a.panels) * kT2PanelRows;
+    unsigned long long* level = a.exchange;
+    int i = slice;
+    for (int count = a.slices; count > 1; count = (count + 1) >> 1) {
+        if ((i ^ 1) < count) {  // the node has both children at this level
+            unsigned long long* slot = level + static_cast<int64_t>(i >> 1) * stride + row;
+            const unsigned long long mine = (1ull << 32) | __float_as_uint(piece);
+            const unsigned long long old =
+                __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == 0) return;  // first to arrive: the sibling carries the pair
+            const float other = __uint_as_float(static_cast<uint32_t>(old));
+            piece = (i & 1) ? other + piece : piece + other;
+            __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        level += static_cast<int64_t>(count >> 1) * stride;
+        i >>= 1;
+    }
+    if (row < m.rows) store_f32(m.y + row, piece);
+}
+
 template <int B, int W>
 hipError_t launch(const MatDesc& one, const MatDesc* group, const T2Plan& plan, const T2Args& a,
                   hipStream_t stream) {
@@ -284,6 +432,21 @@ int t2_resident_workgroups(int block_size, int waves, int staged_tiles) {
     return n;
 }
 
+// Workgroups of the sliced kernel with `waves` waves that fit on a CU at once (1 if unknown).
+static int t2_slice_resident_workgroups(int block_size, int waves) {
+    const void* f = nullptr;
+    switch (block_size) {
+        case 64: f = reinterpret_cast<const void*>(&t2_slice_kernel<64>); break;
+        case 128: f = reinterpret_cast<const void*>(&t2_slice_kernel<128>); break;
+        case 256: f = reinterpret_cast<const void*>(&t2_slice_kernel<256>); break;
+        default: return 1;
+    }
+    int n = 0;
+    const size_t lds = static_cast<size_t>(waves) * kTableFloats * sizeof(float);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 64 * waves, lds) != hipSuccess || n < 1) return 1;
+    return n;
+}
+
 namespace {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -305,6 +468,40 @@ T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positio
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
         cus = 256;
+
+    // One matrix at one position: the sliced kernel, one tile per wave, when all its workgroups fit on the
+    // chip at once and a panel needs at most kSliceMaxSlices slices: eight waves per workgroup if that fits
+    // (more, smaller workgroups), else sixteen; otherwise sixteen waves that take several tiles each.
+    if (count == 1 && positions == 1) {
+        const auto fits = [&](int waves, int slices) {
+            return static_cast<int64_t>(l.panels) * slices <=
+                   static_cast<int64_t>(t2_slice_resident_workgroups(block_size, waves)) * cus;
+        };
+        int waves = 0, per = 0;
+        for (const int w : {8, kSliceMaxWaves}) {
+            if (ceil_div(l.tiles, w) <= kSliceMaxSlices && fits(w, static_cast<int>(ceil_div(l.tiles, w)))) {
+                waves = per = w;
+                break;
+            }
+        }
+        if (waves == 0) {
+            per = static_cast<int>(ceil_div(l.tiles, kSliceMaxSlices));
+            if (fits(kSliceMaxWaves, static_cast<int>(ceil_div(l.tiles, per)))) waves = kSliceMaxWaves;
+        }
+        if (waves > 0) {
+            const int slices = static_cast<int>(ceil_div(l.tiles, per));
+            int64_t nodes = 0;  // exchange slots per row: the internal nodes of the slices' tree
+            for (int c = slices; c > 1; c = (c + 1) >> 1) nodes += c >> 1;
+            p.slices = slices;
+            p.slice_groups = per;
+            p.waves = std::min({waves, per, l.tiles});  // no wave without a tile
+            p.workgroups = l.panels * slices;
+            p.scratch_bytes = std::max<size_t>(256, static_cast<size_t>(nodes) * l.panels * kT2PanelRows * 8);
+            p.tables.assign(p.scratch_bytes, 0);
+            return p;
+        }
+    }
+
     // Eight waves (eight panels) per workgroup share each tile's tables when that still leaves at least
     // eight tiles per workgroup on a full chip; otherwise four.
     const int64_t members = static_cast<int64_t>(count) * positions;
@@ -367,6 +564,21 @@ hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, Launch
         plan.staged_tiles > kMaxStagedTiles)
         return hipErrorInvalidValue;
     const T2Layout l = t2_layout(s.rows_max, s.columns, s.block_size);
+    if (plan.slices > 0) {
+        if (count != 1 || s.positions != 1 || plan.waves < 1 || plan.waves > kSliceMaxWaves ||
+            plan.workgroups != l.panels * plan.slices)
+            return hipErrorInvalidValue;
+        const T2SliceArgs a{s.columns, l.tiles,       l.chunks,          l.slots, l.panels, plan.slices,
+                            plan.slice_groups, 0, static_cast<unsigned long long*>(scratch)};
+        const size_t lds = static_cast<size_t>(plan.waves) * kTableFloats * sizeof(float);
+        switch (s.block_size) {
+            case 64: t2_slice_kernel<64><<<plan.workgroups, 64 * plan.waves, lds, stream>>>(one, group, a); break;
+            case 128: t2_slice_kernel<128><<<plan.workgroups, 64 * plan.waves, lds, stream>>>(one, group, a); break;
+            case 256: t2_slice_kernel<256><<<plan.workgroups, 64 * plan.waves, lds, stream>>>(one, group, a); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     const int W = plan.waves;
     char* base = static_cast<char*>(scratch);
     const T2Args a{s.columns,

@@ -90,8 +90,11 @@ constexpr int legacy_record_bytes(int format) { return format == kQ8_0 ? 32 : 16
 // the launch's (panel group, tile) units; items cut between two ranges are finished by a second kernel.
 // The launch needs a device scratch buffer of `scratch_bytes` whose start holds the plan's tables (range
 // starts, cut items): copy `tables` there once before the first launch; the rest holds per-workgroup
-// partial sums. Launches that share a scratch buffer must not overlap in time. A plan is valid for the
-// launch shape, member count and positions it was made for, on the device that was current.
+// partial sums. A single matrix at one position small enough for the chip to hold all its workgroups at
+// once is instead sliced: one kernel, workgroup (panel, column slice), slices joined through atomic
+// exchange slots in the scratch (`tables` is their zeroed image, and every launch leaves them zero).
+// Launches that share a scratch buffer must not overlap in time. A plan is valid for the launch shape,
+// member count and positions it was made for, on the device that was current.
 struct T2Fixup {
     int member, position, panel0;  // the cut item
     int first, last;               // ranges holding its pieces
@@ -101,12 +104,16 @@ struct T2Fixup {
 
 struct T2Plan {
     int rows_max, columns, block_size, count, positions;  // what the plan was made for
-    int waves;                                            // waves per workgroup: 4 or 8
+    int waves;                                            // waves per workgroup: 4 or 8 (sliced: 1-16)
     int workgroups;                                       // ranges (one workgroup each)
     int staged_tiles;                                     // longest segment: activation tiles staged in LDS
     int fixups;                                           // items cut between ranges
+    int slices;               // > 0: one matrix at one position, sliced (the column slices of a panel are
+                              // joined in the kernel); 0: stream-K ranges plus the fix-up kernel
+    int slice_groups;         // sliced: tiles per column slice
     size_t fixup_offset, partial_offset, scratch_bytes;  // scratch layout
-    std::vector<uint8_t> tables;                         // host image of [starts][fixups]
+    std::vector<uint8_t> tables;                         // host image of [starts][fixups] (sliced: zeroed
+                                                         // exchange slots)
 };
 
 // Throws nothing; returns a plan with workgroups == 0 when the launch is too large to plan (more than

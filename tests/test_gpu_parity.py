@@ -175,6 +175,36 @@ def test_ternary2_grouped_pair_tables(context, block, columns, members):
         m.dispose()
 
 
+# A single matrix at one position takes the sliced plan when the chip holds all of its workgroups at once:
+# eight waves per workgroup when at most eight slices of eight tiles cover a row and the workgroups fit,
+# else sixteen; rows too wide for eight slices of sixteen tiles get sixteen waves taking several tiles each.
+# The slices of a panel are joined by a tree of atomic exchanges (1 to 8 slices; an odd count promotes the
+# slice without a sibling). The shapes reach each branch (3, 5, 6, 7 and 8 slices among them). Each matrix
+# is run three times, with another matrix's launch in between, and must give the same bits every time (the
+# exchange slots return to empty after each launch).
+@pytest.mark.parametrize("rows,columns", [(1, 1), (64, 128), (65, 1000), (200, 3072), (4000, 4100), (130, 7168),
+                                          (4096, 4096), (11008, 4096), (4096, 11008), (300, 129 * 128),
+                                          (100, 65536)])
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_single_matrix_sliced_plans(context, block, rows, columns):
+    g = rng(9001 + block + rows + columns)
+    payload = _t2_random_payload(g, rows, columns, block)
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    m = context.create_ternary2(rows, columns, block, payload)
+    other = context.create_ternary2(64, 256, block, _t2_random_payload(g, 64, 256, block))
+    first = run(m, x)
+    run(other, g.uniform(-1, 1, 256).astype(np.float32))
+    for _ in range(2):
+        again = run(m, x)
+        assert np.array_equal(again.view(np.uint32), first.view(np.uint32)), "repeated launches differ"
+    m.dispose()
+    other.dispose()
+    wq = O.t2_dequantize(payload, rows, columns, block)
+    bound = relative_bound(wq, x)
+    assert_within(first, O.t2_matvec_scalar(payload, rows, columns, block, x), bound, f"{rows}x{columns} B{block} vs scalar")
+    assert_within(first, fp64_matvec(wq, x), bound, f"{rows}x{columns} B{block} vs FP64")
+
+
 def test_ternary2_zero_rows_are_exactly_zero(context):
     # Ternary2Tests.cs:57-58: an all-zero row next to non-zero rows.
     w, x = O.corpus_random_matrix(7, 2 * 128 + 3)
