@@ -17,12 +17,11 @@
 // 32-position tile and walks its blocks in order, loading block b+1 while it computes block b.
 //
 // Q4_K: Dot = sum_j s_j * D_j with D_j = sum over sub-block j (32 weights) of q * c: one 32x32x32 MFMA per
-// sub-block and an int24 multiply-add by s_j; Min = sum_j m_j * (bsum_2j + bsum_2j+1) is one 32x32x16 FP16
-// product of the 16 group sums with m_(g/2). Q6_K: Dot = sum_k sc_k * D_k - 32 * sum_k sc_k * bsum_k over
-// the 16 groups of 16 weights: one 32x32x16 MFMA per group and a multiply-add by sc_k, and one FP16 product
-// of the group sums with sc_k. All magnitudes stay below 2^23 before the int24 multiply
-// (|D_j| <= 32 * 15 * 127, |D_k| <= 16 * 63 * 127) and below 2^31 after; the FP16 products are exact
-// (operands of at most 11 significant bits, sums below 2^24).
+// sub-block and an int24 multiply-add by s_j (|D_j| <= 32 * 15 * 127 fits 24 bits, the sum 31); Min =
+// sum_j m_j * (bsum_2j + bsum_2j+1) is one 32x32x16 FP16 product of the 16 group sums with m_(g/2), exact
+// (operands of at most 11 significant bits, sums below 2^24). Q6_K reads its weights as two int8 planes of
+// the pre-scaled, centred weight sc * (q - 32) (built once per matrix, below), so Dot is two 32x32x32 MFMA
+// chains over the block's K steps and one combination, 128 hi + lo.
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -123,50 +122,6 @@ __global__ __launch_bounds__(256) void kmfma_pack_kernel(const float* __restrict
     if (j == 0) store_f32(scales + bt * 32 + r, qr.scale);
 }
 
-// The weights one lane needs for one block: its row's data for its k half of every chunk.
-struct Q4KRegs {
-    u32x4 head;   // d, dmin, packed 6-bit scales and mins
-    u32x4 qs[4];  // qs[32g + 16h, +16) for g = 0..3
-};
-
-struct Q6KRegs {
-    uint32_t qla[4][2], qlb[4][2], qh[4][2];  // this lane's 8 bytes of each quarter's arrays
-    u32x4 sc;                                 // quarter c's scale of form kk at byte 4c + kk (group 32c' + ...)
-    uint32_t dpair;                           // the FP16 d of this block (and its neighbour)
-};
-
-__device__ __forceinline__ void load_weights(const uint8_t* wrow, int b, int h, Q4KRegs& r) {
-    const uint8_t* block = wrow + static_cast<int64_t>(b) * 144;
-    r.head = load16_a4(block);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) r.qs[g] = load16_a4(block + 16 + 32 * g + 16 * h);
-}
-
-__device__ __forceinline__ void load_weights(const uint8_t* w, int64_t count, int64_t index, int h, Q6KRegs& r) {
-    const uint8_t* record = w + index * 192;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint8_t* q = record + 48 * c + 8 * h;
-        r.qla[c][0] = load4_a4(q);
-        r.qla[c][1] = load4_a4(q + 4);
-        r.qlb[c][0] = load4_a4(q + 16);
-        r.qlb[c][1] = load4_a4(q + 20);
-        r.qh[c][0] = load4_a4(q + 32);
-        r.qh[c][1] = load4_a4(q + 36);
-    }
-    r.sc = load16_a4(w + count * 192 + index * 16);
-    r.dpair = load4_a4(w + count * 208 + (index & ~int64_t(1)) * 2);
-}
-
-__device__ __forceinline__ uint32_t q6k_form(uint32_t a, uint32_t b, uint32_t hb, int kk) {
-    switch (kk) {
-        case 0: return (a & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u);
-        case 1: return (b & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u);
-        case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u);
-        default: return ((b >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u);
-    }
-}
-
 // A block's packed codes, group sums and scales staged in LDS: the 8 KB of codes in operand order, the 1 KB of
 // FP16 group sums in operand order, then the tile's 32 position scales.
 struct StagedBlock {
@@ -183,6 +138,24 @@ __device__ __forceinline__ f32x4 staged_scales(const StagedBlock& sb, int q, int
     return *reinterpret_cast<const f32x4*>(sb.scales + 8 * q + 4 * h);
 }
 
+__device__ __forceinline__ i32x4 staged_codes16(const StagedBlock& sb, int j, int lane) {
+    return *reinterpret_cast<const i32x4*>(sb.codes + 1024 * j + 16 * lane);
+}
+
+// ---- Q4_K: the resident payload ----
+// The weights one lane needs for one block: its row's data for its k half of every chunk.
+struct Q4KRegs {
+    u32x4 head;   // d, dmin, packed 6-bit scales and mins
+    u32x4 qs[4];  // qs[32g + 16h, +16) for g = 0..3
+};
+
+__device__ __forceinline__ void load_weights(const uint8_t* wrow, int b, int h, Q4KRegs& r) {
+    const uint8_t* block = wrow + static_cast<int64_t>(b) * 144;
+    r.head = load16_a4(block);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r.qs[g] = load16_a4(block + 16 + 32 * g + 16 * h);
+}
+
 // The block's FP32 terms of the lane's 16 (row, position) outputs, from the staged codes. A zero activation
 // block contributes +0 or -0 (the reference skips it, QuantizedKAvx2Kernel.cs:86): its scale is 0 and every
 // resident block scale is finite (checked at upload), and adding a zero to a sum that starts at +0 never
@@ -194,10 +167,6 @@ __device__ __forceinline__ i32x4 q4k_weights(const Q4KRegs& r, int j) {
     const int shift = 4 * (j & 1);
     return i32x4{static_cast<int>((raw[0] >> shift) & 0x0F0F0F0Fu), static_cast<int>((raw[1] >> shift) & 0x0F0F0F0Fu),
                  static_cast<int>((raw[2] >> shift) & 0x0F0F0F0Fu), static_cast<int>((raw[3] >> shift) & 0x0F0F0F0Fu)};
-}
-
-__device__ __forceinline__ i32x4 staged_codes16(const StagedBlock& sb, int j, int lane) {
-    return *reinterpret_cast<const i32x4*>(sb.codes + 1024 * j + 16 * lane);
 }
 
 __device__ __forceinline__ void block_terms(const Q4KRegs& r, const StagedBlock& sb, int lane, float (&term)[16]) {
@@ -238,55 +207,122 @@ __device__ __forceinline__ void block_terms(const Q4KRegs& r, const StagedBlock&
     }
 }
 
-__device__ __forceinline__ long q6k_weights(const Q6KRegs& r, int k, int& sc) {
-    const int c = 2 * (k >> 3) + (k & 1), kk = (k & 7) >> 1;
-    sc = static_cast<int8_t>(r.sc[c] >> (8 * kk));
-    return static_cast<long>(q6k_form(r.qla[c][0], r.qlb[c][0], r.qh[c][0], kk)) |
-           (static_cast<long>(q6k_form(r.qla[c][1], r.qlb[c][1], r.qh[c][1], kk)) << 32);
+// ---- Q6_K: weight planes ----
+// The Q6_K product reads each matrix's weights pre-scaled and centred (kmfma_planes_bytes): w = sc * (q - 32),
+// sc the int8 scale of the weight's group of 16 and q its 6-bit code (-4064..4096), split exactly as
+// w = 128 hi + lo with lo = w & 127 (0..127) and hi = (w - lo) / 128 (-32..32): two int8 planes. The block's
+// integer product of the reference, Dot = sum_k sc_k (q_k - 32) c_k (Q6KCodec.DotProduct), is then
+// 128 sum hi c + sum lo c, which the MFMA accumulates exactly over the block's eight K steps of 32
+// (|128 sum hi c| <= 128 * 256 * 32 * 127, and the total, stay below 2^31): no group scale, code assembly
+// or centring is left to the vector ALU (they took about 450 of its 574 instructions per 32 x 32 block tile
+// on the resident layout). Q4_K keeps its payload: its planes (0..945 = 128 hi + lo) cost four times its
+// bytes per weight in L2 traffic for little VALU saved, and measured slower (gate/up 30 -> 39 us).
+//
+// Record of row tile rt (32 rows; rows past the last are zero) and block b, at (rt * blocks + b) * 16,512:
+//   [0, 16384)      plane p (0: hi, 1: lo), K step j (weights 32j .. 32j + 31): 1 KB in second-operand order,
+//                   lane l = 32h + r holding the 16 bytes of row 32 rt + r, weights 32j + 16h .. + 15;
+//   [16384, 16512)  per row r of the tile, d as a float (exact from FP16).
+constexpr int kPlaneRecord = 16512;
+constexpr int kPlaneScales = 16384;
+
+// Q6_K weight k of block n of the regrouped device layout (count blocks in all) times its group scale, with
+// the code centred: sc_(k/16) * (q_k - 32) (Q6KCodec.DecodeBlock's q1..q4 of half k / 128).
+__device__ __forceinline__ int q6k_scaled_weight(const uint8_t* w, int64_t count, int64_t n, int k) {
+    const int h = k >> 7, x = k & 127, kk = x >> 5, t = (x >> 4) & 1, i = x & 15;
+    const uint8_t* quarter = w + n * 192 + 48 * (2 * h + t);
+    const uint32_t ql = quarter[(kk & 1) * 16 + i];            // ql[64h + 16t + i] or ql[64h + 32 + 16t + i]
+    const uint32_t low = kk >= 2 ? ql >> 4 : ql & 0xFu;
+    const uint32_t high = (static_cast<uint32_t>(quarter[32 + i]) >> (2 * kk)) & 3u;  // qh[32h + 16t + i]
+    const int q = static_cast<int>(low | (high << 4));
+    const int sc = static_cast<int8_t>(w[count * 192 + n * 16 + 4 * (2 * h + t) + kk]);  // sc[8h + 2kk + t]
+    return sc * (q - 32);
 }
 
-__device__ __forceinline__ long staged_codes8(const StagedBlock& sb, int k, int lane) {
-    return *reinterpret_cast<const long*>(sb.codes + 512 * k + 8 * lane);
+// One workgroup per (block, row tile) builds its record from the resident regrouped layout.
+__global__ __launch_bounds__(256) void kmfma_planes_kernel(const uint8_t* __restrict__ w, int rows, int blocks,
+                                                           uint8_t* __restrict__ planes) {
+    const int b = blockIdx.x, rt = blockIdx.y;
+    uint8_t* rec = planes + (static_cast<int64_t>(rt) * blocks + b) * kPlaneRecord;
+    const int64_t count = static_cast<int64_t>(rows) * blocks;
+    for (int item = threadIdx.x; item < 512; item += 256) {
+        const int j = item >> 6, l = item & 63, r = l & 31, h = l >> 5;
+        const int row = rt * kTile + r;
+        uint32_t hi[4] = {0u, 0u, 0u, 0u}, lo[4] = {0u, 0u, 0u, 0u};
+        if (row < rows) {
+            for (int i = 0; i < 16; ++i) {
+                const int v = q6k_scaled_weight(w, count, static_cast<int64_t>(row) * blocks + b, 32 * j + 16 * h + i);
+                const int vlo = v & 127, vhi = (v - vlo) / 128;  // v = 128 vhi + vlo exactly
+                lo[i >> 2] |= static_cast<uint32_t>(vlo) << (8 * (i & 3));
+                hi[i >> 2] |= (static_cast<uint32_t>(vhi) & 0xFFu) << (8 * (i & 3));
+            }
+        }
+        *reinterpret_cast<u32x4*>(rec + j * 1024 + 16 * l) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u32x4*>(rec + (8 + j) * 1024 + 16 * l) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    }
+    if (threadIdx.x < kTile) {
+        const int r = threadIdx.x, row = rt * kTile + r;
+        float d = 0.0f;
+        if (row < rows) {
+            const uint8_t* dp = w + count * 208 + (static_cast<int64_t>(row) * blocks + b) * 2;
+            d = half_bits_to_float(static_cast<uint32_t>(dp[0]) | (static_cast<uint32_t>(dp[1]) << 8));
+        }
+        *reinterpret_cast<float*>(rec + kPlaneScales + 4 * r) = d;
+    }
 }
 
-__device__ __forceinline__ void block_terms(const Q6KRegs& r, const StagedBlock& stage, int lane, int64_t index,
+// The planes one lane holds for one block, and its row's d.
+struct PlaneRegs {
+    i32x4 w[2][8];  // [plane][K step]
+    float d;
+};
+
+__device__ __forceinline__ i32x4 load_plane(const uint8_t* rec, int p, int j, int lane) {
+    return *(const SATORI_GLOBAL i32x4*)(rec + (8 * p + j) * 1024 + 16 * lane);
+}
+
+__device__ __forceinline__ float load_plane_d(const uint8_t* rec, int lane) {
+    return __uint_as_float(load4_a4(rec + kPlaneScales + 4 * (lane & 31)));
+}
+
+__device__ __forceinline__ void load_planes(const uint8_t* rec, int lane, PlaneRegs& r) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        r.w[0][j] = load_plane(rec, 0, j, lane);
+        r.w[1][j] = load_plane(rec, 1, j, lane);
+    }
+    r.d = load_plane_d(rec, lane);
+}
+
+// The block's FP32 terms (a d) Dot of the lane's 16 (row, position) outputs (QuantizedKAvx2Kernel.cs:94) from
+// the staged codes, refilling each K step's plane registers with the next block's (record `next`) as soon as
+// the step's two products have read them. A zero activation block contributes +0 or -0 (the reference skips
+// it, QuantizedKAvx2Kernel.cs:86): its scale is 0, every resident block scale is finite (checked at upload),
+// and adding a zero to a sum that starts at +0 never changes it.
+__device__ __forceinline__ void block_terms(PlaneRegs& r, const uint8_t* next, const StagedBlock& sb, int lane,
                                             float (&term)[16]) {
     const int h = lane >> 5;
-    const float d = half_bits_to_float(r.dpair >> (16 * static_cast<int>(index & 1)));
-    int dot[16];
+    i32x16 hi = {}, lo = {};
+    i32x4 c_next = staged_codes16(sb, 0, lane);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) dot[i] = 0;
-    int sc;
-    i32x16 cur = mfma16(staged_codes8(stage, 0, lane), q6k_weights(r, 0, sc), i32x16{});
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {  // group k: weights 16k .. 16k + 15 of the block
-        i32x16 next;
-        int sn = 0;
-        if (k + 1 < 16) next = mfma16(staged_codes8(stage, k + 1, lane), q6k_weights(r, k + 1, sn), i32x16{});
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dot[i] = mad24(sc, cur[i], dot[i]);
-        __builtin_amdgcn_sched_barrier(0);
-        if (k + 1 < 16) {
-            cur = next;
-            sc = sn;
-        }
+    for (int j = 0; j < 8; ++j) {
+        const i32x4 c = c_next;
+        if (j + 1 < 8) c_next = staged_codes16(sb, j + 1, lane);  // read a step ahead
+        hi = mfma32(c, r.w[0][j], hi);
+        lo = mfma32(c, r.w[1][j], lo);
+        r.w[0][j] = load_plane(next, 0, j, lane);
+        r.w[1][j] = load_plane(next, 1, j, lane);
+        __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, a block ahead of its use
     }
-    // Centring sum = sum over the 16 groups k of sc_k * sum_k: one FP16 product (|sum_k| <= 2032,
-    // |sc_k| <= 128, |total| < 2^23). Group 8h + e's scale is byte e / 2 of dword 2h + e % 2.
-    const uint32_t s0 = h ? r.sc[2] : r.sc[0], s1 = h ? r.sc[3] : r.sc[1];
-    f16x8 sw;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        sw[e] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((e & 1 ? s1 : s0) >> (8 * (e >> 1)))));
-    const f32x16 cent = mfma_f16(staged_sums(stage, lane), sw);
+    const float d = r.d;
+    r.d = load_plane_d(next, lane);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const f32x4 a4 = staged_scales(stage, q, h);
+        const f32x4 a4 = staged_scales(sb, q, h);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
-            // sum sc * (q - 32) * code = dot - 32 * centring, exact in int32 (cent[i] is an exact integer).
-            term[i] = __fmul_rn(__fmul_rn(a4[e], d), static_cast<float>(dot[i] - 32 * static_cast<int>(cent[i])));
+            const float dot = static_cast<float>(hi[i] * 128 + lo[i]);  // the exact Dot, as the reference converts it
+            term[i] = __fmul_rn(__fmul_rn(a4[e], d), dot);
         }
     }
 }
@@ -321,9 +357,7 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
     while (mi + 1 < a.count && u >= a.units[mi]) u -= a.units[mi++];
     if (u >= a.units[mi]) return;  // whole workgroup
     const KmfmaMember& m = a.m[mi];
-    const uint8_t* __restrict__ w = m.w;
     const int rows = m.rows, blocks = a.blocks, tiles = a.tiles;
-    const int64_t row_bytes = m.row_bytes;
     const uint8_t* __restrict__ codes = m.workspace;
     const uint8_t* __restrict__ sums = m.workspace + kmfma_sums_offset(blocks, tiles);
     const float* __restrict__ scales = reinterpret_cast<const float*>(m.workspace + kmfma_scales_offset(blocks, tiles));
@@ -334,7 +368,6 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
     const int way = wave % S, rt = wave / S;
     const int h = lane >> 5;
     const int row = (group * SP::R + rt) * kTile + (lane & 31);
-    const int row_c = row < rows ? row : rows - 1;  // rows past the last compute on a live row, store nothing
     const int rounds = (blocks + S - 1) / S;
 
     // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [16i, 16i + 16) and [4096 + 16i, +16)
@@ -406,49 +439,67 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
         }
     };
 
-    using Regs = typename std::conditional<FORMAT == kQ4_K, Q4KRegs, Q6KRegs>::type;
-    const uint8_t* wrow = w + row_c * row_bytes;
-    const int64_t count = static_cast<int64_t>(rows) * blocks;
-    const int64_t base = static_cast<int64_t>(row_c) * blocks;
-    auto load_w = [&](int b, Regs& r) {
-        if (b < blocks) {
-            if constexpr (FORMAT == kQ4_K)
-                load_weights(wrow, b, h, r);
-            else
-                load_weights(w, count, base + b, h, r);
-        }
+    auto zero = [](float (&term)[16]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) term[i] = 0.0f;
     };
-    auto round = [&](int k, Regs& cur, Regs& nxt) {
-        __syncthreads();  // the previous round's staged blocks (and exchanged terms) are no longer read
-        stage_store(k);
-        if (k + 1 < rounds) {
-            stage_load(k + 1);
-            load_w((k + 1) * S + way, nxt);
-        }
-        __syncthreads();  // round k staged
-        const int b = k * S + way;
-        float term[16];
-        if (b < blocks) {
-            if constexpr (FORMAT == kQ4_K)
+    if constexpr (FORMAT == kQ4_K) {
+        // Round k: this way's block k S + way, from registers loaded one round ahead.
+        const uint8_t* wrow = m.w + static_cast<int64_t>(row < rows ? row : rows - 1) * m.row_bytes;  // rows past
+        auto load_w = [&](int b, Q4KRegs& r) {                                  // the last compute on a live row
+            if (b < blocks) load_weights(wrow, b, h, r);
+        };
+        auto round = [&](int k, Q4KRegs& cur, Q4KRegs& nxt) {
+            __syncthreads();  // the previous round's staged blocks (and exchanged terms) are no longer read
+            stage_store(k);
+            if (k + 1 < rounds) {
+                stage_load(k + 1);
+                load_w((k + 1) * S + way, nxt);
+            }
+            __syncthreads();  // round k staged
+            const int b = k * S + way;
+            float term[16];
+            if (b < blocks)
                 block_terms(cur, stage[way], lane, term);
             else
-                block_terms(cur, stage[way], lane, base + b, term);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) term[i] = 0.0f;
+                zero(term);
+            add_round(term);
+        };
+        Q4KRegs ra, rb;
+        stage_load(0);
+        load_w(way, ra);
+        int k = 0;
+        for (; k + 1 < rounds; k += 2) {
+            round(k, ra, rb);
+            round(k + 1, rb, ra);
         }
-        add_round(term);
-    };
-
-    Regs ra, rb;
-    stage_load(0);
-    load_w(way, ra);
-    int k = 0;
-    for (; k + 1 < rounds; k += 2) {
-        round(k, ra, rb);
-        round(k + 1, rb, ra);
+        if (k < rounds) round(k, ra, rb);
+    } else {
+        // The row tile's plane records (a tile past the last computes on the last one and stores nothing).
+        // Round k: this way's block k S + way; its block terms refill the plane registers with the way's next
+        // block (k + 1) S + way while they run.
+        const int row_tiles = (rows + kTile - 1) / kTile;
+        const uint8_t* tile_rec =
+            m.w + static_cast<int64_t>(min(group * SP::R + rt, row_tiles - 1)) * blocks * kPlaneRecord;
+        auto rec = [&](int b) { return tile_rec + static_cast<int64_t>(min(b, blocks - 1)) * kPlaneRecord; };
+        PlaneRegs r;
+        auto round = [&](int k) {
+            __syncthreads();
+            stage_store(k);
+            if (k + 1 < rounds) stage_load(k + 1);
+            __syncthreads();
+            const int b = k * S + way;
+            float term[16];
+            if (b < blocks)
+                block_terms(r, rec(b + S), stage[way], lane, term);
+            else
+                zero(term);
+            add_round(term);
+        };
+        stage_load(0);
+        load_planes(rec(way), lane, r);
+        for (int k = 0; k < rounds; ++k) round(k);
     }
-    if (k < rounds) round(k, ra, rb);
 
     if (row >= rows) return;
 #pragma unroll
@@ -505,7 +556,7 @@ hipError_t launch_kmfma_pack(int format, const float* x, int blocks, int positio
     if (positions <= 0 || blocks <= 0) return hipSuccess;
     if (format != kQ4_K && format != kQ6_K) return hipErrorInvalidValue;
     const int tiles = (positions + kTile - 1) / kTile;
-    const int chunks = format == kQ4_K ? 8 : 16;
+    const int chunks = 8;  // K steps of 32 for both formats (the weight planes are pre-scaled)
     kmfma_pack_kernel<<<dim3((blocks + 3) / 4, tiles * kTile / 4), 256, 0, stream>>>(
         x, blocks * 256, positions, tiles, chunks, workspace,
         reinterpret_cast<float*>(workspace + kmfma_scales_offset(blocks, tiles)),
@@ -540,6 +591,18 @@ hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8
     if (e != hipSuccess) return e;
     const KmfmaMember one{w, workspace, y, rows, 0, row_bytes};
     return launch_kmfma_product(format, &one, 1, blocks, positions, stream);
+}
+
+size_t kmfma_planes_bytes(int rows, int blocks) {
+    return static_cast<size_t>((rows + kTile - 1) / kTile) * static_cast<size_t>(blocks) * kPlaneRecord;
+}
+
+hipError_t launch_kmfma_planes(const uint8_t* w, int rows, int blocks, uint8_t* planes, hipStream_t stream) {
+    if (rows <= 0 || blocks <= 0) return hipSuccess;
+    const int row_tiles = (rows + kTile - 1) / kTile;
+    if (row_tiles > 65535) return hipErrorInvalidValue;  // grid y
+    kmfma_planes_kernel<<<dim3(blocks, row_tiles), 256, 0, stream>>>(w, rows, blocks, planes);
+    return hipGetLastError();
 }
 
 }  // namespace satori

@@ -162,22 +162,28 @@ hipError_t launch_gemv_kint_transformed(const MatDesc* members, const MatDesc* d
 
 // Integer K-format product (Q4_K or Q6_K) over `positions` positions on the matrix cores: quantizes the FP32
 // activations x ([positions][blocks * 256]) to Q8_K into `workspace` (kmfma_workspace_bytes), then the
-// product; outputs bit-exact with launch_gemv_kint's. Used from kmfma_min_positions() positions on.
+// product; outputs bit-exact with launch_gemv_kint's. Used from kmfma_min_positions() positions on. `w` is
+// the resident payload for Q4_K (row_bytes per row) and the matrix's weight planes for Q6_K.
 hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
                              int blocks, int64_t row_bytes, int positions, hipStream_t stream);
 size_t kmfma_workspace_bytes(int blocks, int positions);
+
+// The Q6_K matrix-core product reads the weights as pre-scaled int8 planes (2.02 bytes a weight, layout in
+// gemv_kmfma.hip), built once from the regrouped resident layout `w` into a buffer of kmfma_planes_bytes.
+size_t kmfma_planes_bytes(int rows, int blocks);
+hipError_t launch_kmfma_planes(const uint8_t* w, int rows, int blocks, uint8_t* planes, hipStream_t stream);
 
 // The same product in two steps, for several matrices of one format and width: launch_kmfma_pack quantizes
 // one activation array into a workspace, and launch_kmfma_product runs up to kKmfmaMaxMembers products in one
 // launch, member i reading the workspace packed from its input (members may share one).
 constexpr int kKmfmaMaxMembers = 4;
 struct KmfmaMember {
-    const uint8_t* w;          // resident payload (Q4_K) or its regrouped device layout (Q6_K)
+    const uint8_t* w;          // Q4_K: the resident payload; Q6_K: the weight planes (launch_kmfma_planes)
     const uint8_t* workspace;  // packed activations (launch_kmfma_pack, kmfma_workspace_bytes)
     float* y;                  // output [positions][rows]
     int rows;
     int pad_;
-    int64_t row_bytes;
+    int64_t row_bytes;         // Q4_K
 };
 struct KmfmaArgs {
     KmfmaMember m[kKmfmaMaxMembers];

@@ -110,6 +110,7 @@ struct satori_hip_matrix {
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
     satori::DeviceBuffer q8k;    // K formats: Q8_K activations of the last many-position product
+    satori::DeviceBuffer planes; // Q6_K: the matrix-core weight planes, built by the first many-position product
     int groups = 0;              // live groups and captured steps that launch this matrix
     int steps = 0;               // captured steps that launch this matrix directly (they hold its q8k buffer)
     bool live = true;
@@ -224,6 +225,27 @@ void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, fl
         check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");
 }
 
+// The weights a many-position (matrix-core) product reads: the resident payload for Q4_K; for Q6_K the weight
+// planes, built on the device by the matrix's first many-position product (2.02 bytes a weight, kept until
+// the matrix is destroyed). The build completes before this returns, so a later product on any stream reads
+// whole planes; it cannot be recorded in a capture.
+const uint8_t* ensure_planes(satori_hip_matrix* m, hipStream_t stream) {
+    if (m->shape.format != SATORI_HIP_Q6_K) return m->payload;
+    if (m->planes.ptr) return static_cast<const uint8_t*>(m->planes.ptr);
+    if (m->context->capturing)
+        fail(SATORI_HIP_E_INVALID_OPERATION,
+             "Run this many-position product once before capturing it (its workspace is allocated on first use).");
+    const Shape& s = m->shape;
+    m->planes.reserve(kmfma_planes_bytes(s.rows, s.blocks));
+    hipError_t e = launch_kmfma_planes(m->payload, s.rows, s.blocks, static_cast<uint8_t*>(m->planes.ptr), stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) {
+        m->planes.release();
+        check_hip(e, "weight planes");
+    }
+    return static_cast<const uint8_t*>(m->planes.ptr);
+}
+
 // Enqueue the Q8_K integer product. Few positions: one kernel that quantizes the activations itself; many:
 // quantize all positions into the matrix's Q8_K buffer, then the matrix-core product (same outputs). The
 // buffer belongs to the matrix, so many-position executions of one matrix that overlap in time race.
@@ -238,8 +260,9 @@ void enqueue_kint(satori_hip_matrix* m, const float* x, int positions, float* y,
             fail(SATORI_HIP_E_INVALID_OPERATION,
                  "The workspace of this matrix cannot grow while a captured step launches it: destroy the step, "
                  "or run the largest product before capturing.");
+        const uint8_t* planes = ensure_planes(m, stream);
         m->q8k.reserve(need);
-        check_hip(launch_gemv_kmfma(m->payload, s.format, x, static_cast<uint8_t*>(m->q8k.ptr), y, s.rows, s.blocks,
+        check_hip(launch_gemv_kmfma(planes, s.format, x, static_cast<uint8_t*>(m->q8k.ptr), y, s.rows, s.blocks,
                                     s.row_bytes, positions, stream),
                   "matrix-core gemv launch");
         return;
@@ -356,6 +379,7 @@ void allocate_matrix(satori_hip_matrix* m, int64_t device_bytes) {
 
 void free_matrix(satori_hip_matrix* m) {
     m->q8k.release();
+    m->planes.release();
     if (m->payload) (void)hipFree(m->payload);
     if (m->scratch) (void)hipFree(m->scratch);
     m->payload = nullptr;
@@ -494,6 +518,15 @@ void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
         fail(SATORI_HIP_E_INVALID_OPERATION,
              "The workspace of this group cannot grow while a captured step replays it: destroy the step, "
              "or run the largest product before capturing.");
+    // Each member's weight planes (the member matrix of descriptor i is the one whose payload it reads).
+    std::vector<const uint8_t*> planes(g->count);
+    for (int i = 0; i < g->count; ++i) {
+        satori_hip_matrix* owner = nullptr;
+        for (satori_hip_matrix* m : g->members)
+            if (m->payload == g->host[i].w) owner = m;
+        if (!owner) fail(SATORI_HIP_E_INVALID_OPERATION, "Group member not found.");
+        planes[i] = ensure_planes(owner, st);
+    }
     g->batch.reserve(per * inputs.size());
     uint8_t* ws = static_cast<uint8_t*>(g->batch.ptr);
     for (size_t k = 0; k < inputs.size(); ++k)
@@ -503,7 +536,7 @@ void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
         KmfmaMember members[kKmfmaMaxMembers];
         for (int j = 0; j < n; ++j) {
             const MatDesc& d = g->host[i0 + j];
-            members[j] = KmfmaMember{d.w, ws + slot[i0 + j] * per, d.y, d.rows, 0, s.row_bytes};
+            members[j] = KmfmaMember{planes[i0 + j], ws + slot[i0 + j] * per, d.y, d.rows, 0, s.row_bytes};
         }
         check_hip(launch_kmfma_product(s.format, members, n, s.blocks, positions, st), "matrix-core gemv launch");
     }
