@@ -829,6 +829,9 @@ def main() -> int:
     ap.add_argument("--profile-token", action="store_true",
                     help="only the whole decode token at positions 511 and 4095, launched eagerly (steps and "
                          "warmup as given), for rocprofv3")
+    ap.add_argument("--profile-single", action="store_true",
+                    help="only the headline matrix's single launches (one per resident copy, checked against the "
+                         "oracle first), steps and warmup as given, for rocprofv3")
     ap.add_argument("--profile-formats", action="store_true",
                     help="only the grouped launches of every format (steps and warmup as given), for rocprofv3")
     args = ap.parse_args()
@@ -896,6 +899,15 @@ def run(args, ctx, events) -> int:
         print(f"bench.py: parity check failed, nothing timed: {e}", file=sys.stderr)
         return 1
     warm_up(ctx, head.run_group, args.warmup_seconds)
+    if args.profile_single:
+        head.run_single()
+        check_outputs(ctx, head, "single launches")
+        ms = time_launches(ctx, events, head.run_single, args.steps, args.warmup)
+        print(json.dumps({"profile": "ternary2-4096-b128 single launches", "copies": head.copies,
+                          "launches": (args.steps + args.warmup + 1) * head.copies,
+                          "launch_us": round(ms * 1e3 / head.copies, 3)}))
+        head.close()
+        return 0
     if args.profile:
         ms = time_launches(ctx, events, head.run_group, args.steps, args.warmup)
         gbs = head.copies * payload.size / (ms * 1e-3) / 1e9
