@@ -607,6 +607,47 @@ def test_k_matrix_core_batch_equals_per_position(context, fmt, rows, columns, po
     m.dispose()
 
 
+def _q6k_extreme_blocks(g, rows: int, blocks: int) -> np.ndarray:
+    """Q6_K rows whose weight products reach the ends of their range: group scales -128 and 127 with codes 0
+    and 63 (sc * (q - 32) from -4064 to 4096, the planes' hi part from -32 to 32), mixed with random blocks;
+    finite FP16 d values including subnormal, negative and zero."""
+    out = g.integers(0, 256, size=(rows, blocks, 210), dtype=np.uint8)
+    kind = g.integers(0, 4, size=(rows, blocks))
+    for r in range(rows):
+        for b in range(blocks):
+            blk = out[r, b]
+            if kind[r, b] == 0:    # q = 0 everywhere (q - 32 = -32)
+                blk[:192] = 0
+            elif kind[r, b] == 1:  # q = 63 everywhere (q - 32 = 31)
+                blk[:192] = 0xFF
+            if kind[r, b] < 3:
+                blk[192:208] = np.where(g.integers(0, 2, 16) == 0, 0x80, 0x7F).astype(np.uint8)  # sc -128 / 127
+    d = g.choice(np.array([0x3C00, 0x0001, 0xBC00, 0x0000, 0x2E66, 0x7BFF], np.uint16), size=(rows, blocks))
+    out[:, :, 208:210] = d.view(np.uint8).reshape(rows, blocks, 2)
+    return np.ascontiguousarray(out.reshape(-1))
+
+
+@pytest.mark.parametrize("rows,columns,positions", [(70, 1536, 33), (33, 8960, 64)])
+def test_k_matrix_core_q6k_extreme_products(context, rows, columns, positions):
+    # The Q6_K matrix-core product reads pre-scaled weight planes: its extremes (the largest |sc * (q - 32)|
+    # against activation codes of +-127, |Dot| near 2^27) must give the reference's outputs bit for bit, as
+    # must the single-position kernel on the resident layout.
+    g = rng(31337 + rows + columns)
+    data = _q6k_extreme_blocks(g, rows, columns // 256)
+    x = g.standard_normal((positions, columns), dtype=np.float32)
+    x[0] = np.where(g.integers(0, 2, columns) == 0, -1.0, 1.0)  # every code +-127
+    x[1] = 0.0
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, BQ.Q6_K))
+    y = np.full(positions * rows, np.nan, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    expected = O.q_matvec_batch(data, rows, columns, int(BQ.Q6_K), x.reshape(-1), positions)
+    assert np.array_equal(y.view(np.uint32), expected.view(np.uint32))
+    single = np.zeros(rows, np.float32)
+    m.execute_batch(x[0], 1, single)
+    assert np.array_equal(single.view(np.uint32), expected[:rows].view(np.uint32))
+    m.dispose()
+
+
 @pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
 @pytest.mark.parametrize("positions", [1, 9, 16, 77, 256])
 def test_k_group_batch_equals_member_batches(context, fmt, positions):
