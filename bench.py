@@ -522,6 +522,44 @@ def token_eager(ctx, events, model: DecodeModel, steps: int, warmup: int, positi
     return out
 
 
+def batch_fp32(ctx, events, steps: int = 20, warmup: int = 3, positions: int = 256) -> dict:
+    """ExecuteBatch of the FP32-activation formats (QuantizedMatVec.ExecuteBatchFloat / ExecuteBatchRows) at
+    256 positions on the BASELINE Q8_0 and Q4_0 shapes, through the device entry point: the activations are
+    split into exact bf16 parts once per call and the matrix-core product reads each matrix once per
+    32-position tile. Parity first (sampled positions within 1e-5 * sum|w x| of the oracle's scalar
+    product), then timed. `per_position_gbs` is the payload bytes times positions over the time, the rate a
+    per-position MatVec would have to stream at to match."""
+    from oracle import oracle as O
+
+    out = {}
+    for label, fmt, rows, columns in (("q8_0-4096x4096", BQ.Q8_0, 4096, 4096),
+                                      ("q4_0-11008x4096", BQ.Q4_0, 11008, 4096),
+                                      ("q4_0-4096x11008", BQ.Q4_0, 4096, 11008)):
+        data, _ = make_gguf(fmt, rows, columns)
+        g = rng(99 + rows)
+        x = g.standard_normal((positions, columns), dtype=np.float32)
+        m = ctx.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+        dx, dy = ctx.alloc(x.nbytes), ctx.alloc(4 * rows * positions)
+        ctx.upload(dx, x)
+        m.execute_batch_device(dx, positions, dy)
+        ctx.synchronize()
+        y = ctx.download(np.zeros(positions * rows, np.float32), dy).reshape(positions, rows)
+        wq = np.abs(O.decode_matrix(data, rows, columns, int(fmt)).astype(np.float64))
+        for p in (0, 1, 31, 32, positions // 2, positions - 1):
+            want = O.q_matvec_scalar(data, rows, columns, int(fmt), x[p])
+            bound = 1e-5 * (wq @ np.abs(x[p].astype(np.float64)))
+            if not np.all(np.abs(y[p].astype(np.float64) - want) <= bound):
+                raise ParityError(f"batch {label}: position {p} outside 1e-5 * sum|w x| of the oracle")
+        ms = time_launches(ctx, events, lambda: m.execute_batch_device(dx, positions, dy), steps, warmup)
+        out[label] = {"positions": positions, "parity_checked": True, "us_per_call": ms * 1e3,
+                      "gflops": 2.0 * rows * columns * positions / (ms * 1e-3) / 1e9,
+                      "per_position_gbs": data.size * positions / (ms * 1e-3) / 1e9}
+        ctx.free(dx)
+        ctx.free(dy)
+        m.dispose()
+    return out
+
+
 def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions: int = 512) -> dict:
     """The projections of a 512-token prefill: every layer projection over all positions in chunks of 256
     positions (the reference's chunk, and the ABI's limit for K formats), q/k/v and gate/up each as one
@@ -932,7 +970,7 @@ def run(args, ctx, events) -> int:
 
     formats = {"ternary2-4096-b128": headline}
     cpu_cases = {"ternary2-4096-b128": (payload, rows, columns, None, x, block)}
-    decode = pre = token = load = None
+    decode = pre = token = load = fbatch = None
     try:
         if not args.quick:
             for label, make in other_formats(ctx):
@@ -953,6 +991,8 @@ def run(args, ctx, events) -> int:
             progress("prefill (512 positions)")
             pre = prefill(ctx, events, model, 3, 1)
             model.close()
+            progress("FP32-activation batches (256 positions)")
+            fbatch = batch_fp32(ctx, events)
             progress("loading (GGUF, STQ2, STB1 uploads)")
             load = loading(ctx)
     except ParityError as e:
@@ -1010,6 +1050,8 @@ def run(args, ctx, events) -> int:
         "decode_token": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in token.items()}
                          if token else None),
         "prefill": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in pre.items()} if pre else None),
+        "batch_fp32": ({label: {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+                        for label, r in fbatch.items()} if fbatch else None),
         "loading": ({k: round(v, 2) for k, v in load.items()} if load else None),
         "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in formats.items()},

@@ -21,7 +21,8 @@ OUT = os.path.join(HERE, "libsatori_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
-SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "gemv_kmfma.hip", "scale_check.hip",
+SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "gemv_kmfma.hip", "gemv_fbatch.hip",
+           "scale_check.hip",
            "transformer_ops.hip",
            "host_cpu.cpp", "gguf.cpp"]
 

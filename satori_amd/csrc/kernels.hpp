@@ -168,6 +168,15 @@ hipError_t launch_gemv_kmfma(const uint8_t* w, int format, const float* x, uint8
                              int blocks, int64_t row_bytes, int positions, hipStream_t stream);
 size_t kmfma_workspace_bytes(int blocks, int positions);
 
+// FP32-activation product (Q8_0 or Q4_0) over `positions` positions on the matrix cores (gemv_fbatch.hip):
+// splits x ([positions][columns]) into three exact bf16 parts in `workspace` (fbatch_workspace_bytes), then
+// the product on the resident device layout `w`; within 1e-5 * sum |w x| of the scalar reference like the
+// single-position kernel. Used from fbatch_min_positions() positions on.
+int fbatch_min_positions();
+size_t fbatch_workspace_bytes(int columns, int positions);
+hipError_t launch_gemv_fbatch(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
+                              int columns, int positions, hipStream_t stream);
+
 // The Q6_K matrix-core product reads the weights as pre-scaled int8 planes (2.02 bytes a weight, layout in
 // gemv_kmfma.hip), built once from the regrouped resident layout `w` into a buffer of kmfma_planes_bytes.
 size_t kmfma_planes_bytes(int rows, int blocks);

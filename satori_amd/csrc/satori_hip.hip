@@ -109,7 +109,8 @@ struct satori_hip_matrix {
     int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
-    satori::DeviceBuffer q8k;    // K formats: Q8_K activations of the last many-position product
+    satori::DeviceBuffer q8k;    // activations of the last many-position product (K formats: packed Q8_K;
+                                 // Q8_0 / Q4_0: split bf16 parts)
     satori::DeviceBuffer planes; // Q6_K: the matrix-core weight planes, built by the first many-position product
     int groups = 0;              // live groups and captured steps that launch this matrix
     int steps = 0;               // captured steps that launch this matrix directly (they hold its q8k buffer)
@@ -215,11 +216,35 @@ LaunchShape launch_shape(const Shape& s, int positions, int rows_max) {
 
 bool is_k(const Shape& s) { return s.format == SATORI_HIP_Q4_K || s.format == SATORI_HIP_Q6_K; }
 
-// Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers.
-void enqueue_float(const satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
-    MatDesc d{m->payload, x, y, m->shape.rows, 0};
-    const LaunchShape l = launch_shape(m->shape, positions, m->shape.rows);
-    if (m->shape.format == SATORI_HIP_TERNARY2)
+// Enqueue one FP32-activation product: x [positions][C] -> y [positions][R], all device pointers. Q8_0 and
+// Q4_0 over fbatch_min_positions() positions or more run on the matrix cores, 256 positions per launch pair,
+// with the split activations in the matrix's activation buffer (executions of one matrix that overlap in
+// time race on it).
+void enqueue_float(satori_hip_matrix* m, const float* x, int positions, float* y, hipStream_t stream) {
+    const Shape& s = m->shape;
+    if ((s.format == SATORI_HIP_Q8_0 || s.format == SATORI_HIP_Q4_0) && positions >= fbatch_min_positions()) {
+        constexpr int kChunk = 256;
+        const size_t need = fbatch_workspace_bytes(s.columns, std::min(positions, kChunk));
+        if (m->context->capturing && m->q8k.bytes < need)
+            fail(SATORI_HIP_E_INVALID_OPERATION,
+                 "Run this many-position product once before capturing it (its workspace is allocated on first use).");
+        if (m->steps > 0 && m->q8k.bytes < need)  // a captured step holds the current buffer
+            fail(SATORI_HIP_E_INVALID_OPERATION,
+                 "The workspace of this matrix cannot grow while a captured step launches it: destroy the step, "
+                 "or run the largest product before capturing.");
+        m->q8k.reserve(need);
+        for (int p0 = 0; p0 < positions; p0 += kChunk) {
+            const int n = std::min(kChunk, positions - p0);
+            check_hip(launch_gemv_fbatch(m->payload, s.format, x + static_cast<int64_t>(p0) * s.columns,
+                                         static_cast<uint8_t*>(m->q8k.ptr), y + static_cast<int64_t>(p0) * s.rows,
+                                         s.rows, s.columns, n, stream),
+                      "matrix-core gemv launch");
+        }
+        return;
+    }
+    MatDesc d{m->payload, x, y, s.rows, 0};
+    const LaunchShape l = launch_shape(s, positions, s.rows);
+    if (s.format == SATORI_HIP_TERNARY2)
         check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->scratch, stream), "Ternary2 launch");
     else
         check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");

@@ -837,6 +837,47 @@ def test_legacy_batch_matches_per_position(context, fmt):
     m.dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+@pytest.mark.parametrize("rows,columns,positions", [(37, 288, 32), (100, 1024, 33), (129, 2048, 64),
+                                                    (4096, 4096, 256), (11008, 4096, 40), (300, 11008, 100),
+                                                    (70, 512, 600)])
+def test_legacy_matrix_core_batch(context, fmt, rows, columns, positions):
+    # From 32 positions on, Q8_0 / Q4_0 batches run on the matrix cores (exact bf16 splits of x, FP32
+    # sums; 256 positions per launch, so 600 positions take three). Every position within 1e-5 * sum |w x|
+    # of the FP64 product, sampled positions also of the scalar reference (BatchedMatVecTests.cs:61-88);
+    # a zero position, one of large magnitude, and NaN / +Inf inputs, whose non-finite outputs must match the
+    # single-position kernel's (the reference's IEEE products).
+    g = rng(808 + rows + columns + positions)
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    x[1] = 0.0
+    x[2] *= np.float32(1e20)
+    x[3, 5] = np.nan
+    x[4, columns - 1] = np.inf
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.full(positions * rows, np.nan, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    y = y.reshape(positions, rows)
+    wq = O.decode_matrix(data, rows, columns, int(fmt)).astype(np.float64)
+    finite = [p for p in range(positions) if p not in (3, 4)]
+    xf = x[finite].astype(np.float64)
+    exact, bound = np.zeros((positions, rows)), np.zeros((positions, rows))
+    exact[finite] = xf @ wq.T
+    bound[finite] = np.abs(xf) @ np.abs(wq).T * 1e-5 + 1e-30
+    for p in finite:
+        assert_within(y[p], exact[p], bound[p], f"position {p} vs FP64")
+    for p in sorted({0, 1, 2, positions // 2, positions - 1} - {3, 4}):
+        assert_within(y[p], O.q_matvec_scalar(data, rows, columns, int(fmt), x[p]), bound[p], f"position {p} vs scalar")
+    single = np.zeros(rows, np.float32)
+    for p in (3, 4):
+        m.execute_batch(x[p], 1, single)  # one position: the single-position kernel
+        assert np.array_equal(np.isnan(y[p]), np.isnan(single)), f"position {p}: NaN pattern"
+        inf = np.isinf(single)
+        assert np.array_equal(np.isinf(y[p]), inf) and np.array_equal(y[p][inf], single[inf]), f"position {p}: Inf"
+    m.dispose()
+
+
 # ---------------------------------------------------------------------------------------------
 # Contract: errors, output commit, disposal, device and group entry points
 # ---------------------------------------------------------------------------------------------
