@@ -62,16 +62,19 @@ def _t2_pack(codes, scales, rows, blocks, block):
 # Non-finite activations
 # ---------------------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("columns", [1000, 5000])
 @pytest.mark.parametrize("block", [64, 128, 256])
-def test_ternary2_nonfinite_inputs_propagate_like_the_reference(context, block):
+def test_ternary2_nonfinite_inputs_propagate_like_the_reference(context, block, columns):
     # Ternary2MatVec.Execute takes any activations (Ternary2MatVec.cs:30-36) and skips code-0 weights
     # (:64-70), so a row is finite when its codes at the non-finite columns are all zero, +-Inf when it
-    # adds one infinity, NaN when it adds both or a NaN. Rows are built for each case.
-    g = rng(9090 + block)
-    rows, columns = 257, 1000
+    # adds one infinity, NaN when it adds both or a NaN. Rows are built for each case. At 5000 columns the
+    # single-matrix plan cuts each row into five column slices joined by atomic exchanges, and the
+    # non-finite columns lie in different slices, so the specials travel through the exchanges.
+    g = rng(9090 + block + columns)
+    rows = 257
     codes, blocks = _t2_payload(g, rows, columns, block)
     x = g.uniform(-1, 1, columns).astype(np.float32)
-    pos_inf, neg_inf, nan = 3, 517, 900
+    pos_inf, neg_inf, nan = 3, columns // 2 + 17, columns - 100
     x[pos_inf], x[neg_inf], x[nan] = np.inf, -np.inf, np.nan
     special = [pos_inf, neg_inf, nan]
     for r in range(rows):
