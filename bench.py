@@ -872,6 +872,9 @@ def main() -> int:
                          "oracle first), steps and warmup as given, for rocprofv3")
     ap.add_argument("--profile-formats", action="store_true",
                     help="only the grouped launches of every format (steps and warmup as given), for rocprofv3")
+    ap.add_argument("--profile-batch", action="store_true",
+                    help="only the FP32-activation batches at 256 positions (checked against the oracle first; "
+                         "steps and warmup as given), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the library runs the MatVec on a single MI355X "
@@ -905,6 +908,10 @@ def run(args, ctx, events) -> int:
                       **decode_step(ctx, events, model, args.steps, args.warmup, eager_only=True)}
         model.close()
         print(json.dumps(result))
+        return 0
+
+    if args.profile_batch:
+        print(json.dumps({"profile": "FP32-activation batches", **batch_fp32(ctx, events, args.steps, args.warmup)}))
         return 0
 
     if args.profile_formats:
