@@ -265,6 +265,10 @@ hipError_t launch_decode_row(const uint8_t* w, int format, int rows, int columns
 // Block-scale finiteness of an uploaded GGUF matrix (device layout; `blocks` = rows * blocks per row): a
 // non-zero *flag afterwards (the caller zeroes it first) means some block has a non-finite scale.
 hipError_t launch_scale_check(const uint8_t* payload, int64_t blocks, int format, uint32_t* flag, hipStream_t stream);
+// Copies `bytes` (a multiple of 4, at most kKernelCopyMaxBytes; both addresses 16-byte aligned) with a kernel
+// on `stream`; either side may be pinned host memory from hipHostMalloc.
+constexpr size_t kKernelCopyMaxBytes = size_t(1) << 20;
+hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t stream);
 int kmfma_min_positions();
 
 // Blocks of the activation row the integer product stages in LDS at once (with the block terms of the

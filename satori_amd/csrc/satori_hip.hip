@@ -490,12 +490,20 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     c->host_y.reserve(out_bytes);
     const bool integer = batch && is_k(s);
     std::memcpy(c->host_x.ptr, input, in_bytes);
-    check_hip(hipMemcpyAsync(c->x.ptr, c->host_x.ptr, in_bytes, hipMemcpyHostToDevice, c->stream), "input copy");
+    // Vectors of up to kKernelCopyMaxBytes move by a copy kernel over the host link, larger ones by the
+    // copy engine.
+    const auto move = [&](const void* src, void* dst, size_t bytes, hipMemcpyKind kind, const char* what) {
+        if (bytes <= kKernelCopyMaxBytes)
+            check_hip(launch_copy_words(src, dst, bytes, c->stream), what);
+        else
+            check_hip(hipMemcpyAsync(dst, src, bytes, kind, c->stream), what);
+    };
+    move(c->host_x.ptr, c->x.ptr, in_bytes, hipMemcpyHostToDevice, "input copy");
     if (integer)
         enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
     else
         enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
-    check_hip(hipMemcpyAsync(c->host_y.ptr, c->y.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "output copy");
+    move(c->y.ptr, c->host_y.ptr, out_bytes, hipMemcpyDeviceToHost, "output copy");
     check_hip(hipStreamSynchronize(c->stream), "stream");
     std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
 }
