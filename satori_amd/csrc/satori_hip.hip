@@ -444,6 +444,16 @@ satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* 
 }
 
 // Host-buffer MatVec shared by matvec and matvec_batch.
+// A host-buffer call's vector between its pinned staging buffer and the device, on the context stream: up to
+// kKernelCopyMaxBytes by a copy kernel over the host link, larger ones by the copy engine.
+void move_vector(satori_hip_context* c, const void* src, void* dst, size_t bytes, hipMemcpyKind kind,
+                 const char* what) {
+    if (bytes <= kKernelCopyMaxBytes)
+        check_hip(launch_copy_words(src, dst, bytes, c->stream), what);
+    else
+        check_hip(hipMemcpyAsync(dst, src, bytes, kind, c->stream), what);
+}
+
 void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, int positions, float* output,
                  size_t output_length, bool batch) {
     require(m, "matrix");
@@ -490,20 +500,12 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     c->host_y.reserve(out_bytes);
     const bool integer = batch && is_k(s);
     std::memcpy(c->host_x.ptr, input, in_bytes);
-    // Vectors of up to kKernelCopyMaxBytes move by a copy kernel over the host link, larger ones by the
-    // copy engine.
-    const auto move = [&](const void* src, void* dst, size_t bytes, hipMemcpyKind kind, const char* what) {
-        if (bytes <= kKernelCopyMaxBytes)
-            check_hip(launch_copy_words(src, dst, bytes, c->stream), what);
-        else
-            check_hip(hipMemcpyAsync(dst, src, bytes, kind, c->stream), what);
-    };
-    move(c->host_x.ptr, c->x.ptr, in_bytes, hipMemcpyHostToDevice, "input copy");
+    move_vector(c, c->host_x.ptr, c->x.ptr, in_bytes, hipMemcpyHostToDevice, "input copy");
     if (integer)
         enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
     else
         enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
-    move(c->y.ptr, c->host_y.ptr, out_bytes, hipMemcpyDeviceToHost, "output copy");
+    move_vector(c, c->y.ptr, c->host_y.ptr, out_bytes, hipMemcpyDeviceToHost, "output copy");
     check_hip(hipStreamSynchronize(c->stream), "stream");
     std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
 }
@@ -979,12 +981,11 @@ int satori_hip_quantize_q8k(satori_hip_context* c, const float* input, int colum
         c->host_x.reserve(in_bytes);
         c->host_y.reserve(out_bytes);
         std::memcpy(c->host_x.ptr, input, in_bytes);
-        check_hip(hipMemcpyAsync(c->x.ptr, c->host_x.ptr, in_bytes, hipMemcpyHostToDevice, c->stream), "input copy");
+        move_vector(c, c->host_x.ptr, c->x.ptr, in_bytes, hipMemcpyHostToDevice, "input copy");
         check_hip(launch_q8k_quantize(static_cast<const float*>(c->x.ptr), columns, 1,
                                       static_cast<uint8_t*>(c->q8k.ptr), c->stream),
                   "Q8_K launch");
-        check_hip(hipMemcpyAsync(c->host_y.ptr, c->q8k.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream),
-                  "output copy");
+        move_vector(c, c->q8k.ptr, c->host_y.ptr, out_bytes, hipMemcpyDeviceToHost, "output copy");
         check_hip(hipStreamSynchronize(c->stream), "stream");
         std::memcpy(output, c->host_y.ptr, out_bytes);
     });
