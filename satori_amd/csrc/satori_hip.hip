@@ -495,17 +495,18 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
 
     set_device(c);
     c->x.reserve(in_bytes);
-    c->y.reserve(out_bytes);
     c->host_x.reserve(in_bytes);
     c->host_y.reserve(out_bytes);
     const bool integer = batch && is_k(s);
     std::memcpy(c->host_x.ptr, input, in_bytes);
     move_vector(c, c->host_x.ptr, c->x.ptr, in_bytes, hipMemcpyHostToDevice, "input copy");
+    // The product kernels store each output element once (no read-back, no atomics on y), so they write
+    // straight into the pinned output staging buffer over the host link: no output copy follows.
+    float* y = static_cast<float*>(c->host_y.ptr);
     if (integer)
-        enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
+        enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, y, c->stream);
     else
-        enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, static_cast<float*>(c->y.ptr), c->stream);
-    move_vector(c, c->y.ptr, c->host_y.ptr, out_bytes, hipMemcpyDeviceToHost, "output copy");
+        enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, y, c->stream);
     check_hip(hipStreamSynchronize(c->stream), "stream");
     std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
 }
