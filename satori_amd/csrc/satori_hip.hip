@@ -500,13 +500,18 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
     const bool integer = batch && is_k(s);
     std::memcpy(c->host_x.ptr, input, in_bytes);
     move_vector(c, c->host_x.ptr, c->x.ptr, in_bytes, hipMemcpyHostToDevice, "input copy");
-    // The product kernels store each output element once (no read-back, no atomics on y), so they write
-    // straight into the pinned output staging buffer over the host link: no output copy follows.
-    float* y = static_cast<float*>(c->host_y.ptr);
+    // The product kernels store each output element once (no read-back, no atomics on y), so outputs of up
+    // to kKernelCopyMaxBytes are written straight into the pinned output staging buffer over the host link;
+    // larger ones (many-position batches) go to device memory and then through the copy engine.
+    const bool direct = out_bytes <= kKernelCopyMaxBytes;
+    if (!direct) c->y.reserve(out_bytes);
+    float* y = static_cast<float*>(direct ? c->host_y.ptr : c->y.ptr);
     if (integer)
         enqueue_kint(m, static_cast<const float*>(c->x.ptr), positions, y, c->stream);
     else
         enqueue_float(m, static_cast<const float*>(c->x.ptr), positions, y, c->stream);
+    if (!direct)
+        check_hip(hipMemcpyAsync(c->host_y.ptr, c->y.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "output copy");
     check_hip(hipStreamSynchronize(c->stream), "stream");
     std::memcpy(output, c->host_y.ptr, out_bytes);  // commit only after success
 }
