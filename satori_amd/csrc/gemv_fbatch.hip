@@ -5,17 +5,26 @@
 // total += Scale * sum), so the weights are read once per 32-position tile instead of once per position.
 //
 // Exact operands. A block's codes q are small integers (Q8_0: -128..127; Q4_0: -8..7), exact in bf16. Each
-// activation x is split into three bf16 parts x = hi + lo + lolo, each the next 8 significant bits of x cut
-// by truncation (x - hi and (x - hi) - lo are exact in FP32, and the last part has at most 8 significant
-// bits), so the split is exact for every normal x and never rounds up into an overflow; an infinite or NaN x
+// activation x is split into three bf16 parts x = hi + lo + lolo, each the next 8 significant bits cut by
+// truncation (x - hi and (x - hi) - lo are exact in FP32, and the last part has at most 8 significant bits).
+// bf16 has FP32's exponent range, but a part below 2^-126 would be a bf16 subnormal: its bits below 2^-133 do
+// not fit and the matrix cores may flush it. So each position is first lifted by an exact power of two 2^k
+// (k >= 0) that brings its largest |x| into [2^64, 2^65). Every nonzero bit of a lifted x then weighs at least
+// 2^(-149 + k); in a position whose largest |x| is below 2^42 (k >= 23) every nonzero part is a normal bf16,
+// so the split is exact for every finite element, subnormals included. In a position with a larger |x| a
+// part can be subnormal only for an element below 2^-174 of the largest. From 2^64 on k = 0, so a product
+// that overflows in the reference overflows here too. An infinite or NaN x keeps k = 0 for its position and
 // keeps itself as hi (a NaN as the canonical quiet NaN) with zero lo and lolo, so q * x gives the IEEE
-// result of the single product. Every q * part product is exact in FP32 (at most 16 significant bits), so
-// the block sum sum_k q_k x_k is three bf16 MFMA chains accumulating in FP32; only the FP32 additions are
-// rounded, in an order of their own, within 1e-5 * sum |w x| of the reference like every FP32 path here.
+// result of the single product. Every q * part product is exact in FP32 (at most 16 significant bits), the
+// sums of a lifted position stay below 2^120, and the block sum sum_k q_k x_k is three bf16 MFMA chains
+// accumulating in FP32. Only the FP32 additions round, in an order of their own, and the final scaling by
+// 2^-k rounds once where the result is subnormal: within 1e-5 * sum |w x| + n * 2^-149 of the reference,
+// like every FP32 path here.
 //
-// Two launches: fbatch_pack_kernel splits the activations into a workspace in MFMA first-operand order, and
-// fbatch_kernel runs the product: waves of 32-row x 32-position tiles, four row tiles per workgroup sharing
-// the split activations staged in LDS a round of W blocks at a time, one block of the round per way.
+// Three launches: fbatch_lift_kernel finds each position's lifting exponent, fbatch_pack_kernel splits the
+// lifted activations into a workspace in MFMA first-operand order, and fbatch_kernel runs the product: waves
+// of 32-row x 32-position tiles, four row tiles per workgroup sharing the split activations staged in LDS a
+// round of W blocks at a time, one block of the round per way.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -31,7 +40,62 @@ constexpr int kBlockTileBytes = 3 * 2 * kPartBytes;    // 3 parts x 2 K steps of
 
 // Workspace: for 32-column block b and 32-position tile t, 6 KB at (b * tiles + t) * 6144: part s (0: hi,
 // 1: lo, 2: lolo), K step st (columns 32b + 16st .. + 15) at (2s + st) * 1024, lane l = 32h + p holding the
-// 8 bf16 of position 32t + p, columns 32b + 16st + 8h .. + 7. Positions past the last are zero.
+// 8 bf16 of position 32t + p, columns 32b + 16st + 8h .. + 7. Positions past the last are zero. After the
+// blocks x tiles records: one int32 lifting exponent k per position (tiles x 32 of them, zero past the last).
+
+// The exponent k lifting the largest |x| of a position into [2^64, 2^65), from the largest magnitude's FP32
+// bits: 0 for a zero or non-finite position, and for magnitudes of 2^64 and more.
+__device__ __forceinline__ int lift_exponent(uint32_t max_bits) {
+    if (max_bits == 0u || max_bits >= 0x7F800000u) return 0;
+    const int e = max_bits >= 0x00800000u ? static_cast<int>(max_bits >> 23) - 127  // normal: floor(log2)
+                                          : (31 - __clz(static_cast<int>(max_bits))) - 149;  // subnormal
+    return e >= 64 ? 0 : 64 - e;
+}
+
+// One workgroup per position tile slot (32 per tile): the lifting exponent of position p (0 past the last).
+// Rows of 16-byte-aligned activations are read in 16-byte pieces, four per thread in flight.
+__global__ __launch_bounds__(256) void fbatch_lift_kernel(const float* __restrict__ x, int columns, int positions,
+                                                          int* __restrict__ lift) {
+    __shared__ uint32_t wave_max[4];
+    const int p = blockIdx.x;
+    uint32_t m = 0u;
+    if (p < positions) {
+        const float* row = x + static_cast<int64_t>(p) * columns;
+        uint32_t m1 = 0u, m2 = 0u, m3 = 0u;
+        const auto mag = [](uint32_t bits) { return bits & 0x7FFFFFFFu; };
+        if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) {  // rows are 128-byte multiples: all aligned
+            const int pieces = columns >> 2;
+            int i = threadIdx.x;
+            for (; i + 768 < pieces; i += 1024) {
+                const u32x4 a = *(const SATORI_GLOBAL u32x4*)(row + 4 * i);
+                const u32x4 b = *(const SATORI_GLOBAL u32x4*)(row + 4 * (i + 256));
+                const u32x4 c = *(const SATORI_GLOBAL u32x4*)(row + 4 * (i + 512));
+                const u32x4 d = *(const SATORI_GLOBAL u32x4*)(row + 4 * (i + 768));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    m = max(m, mag(a[e]));
+                    m1 = max(m1, mag(b[e]));
+                    m2 = max(m2, mag(c[e]));
+                    m3 = max(m3, mag(d[e]));
+                }
+            }
+            for (; i < pieces; i += 256) {
+                const u32x4 a = *(const SATORI_GLOBAL u32x4*)(row + 4 * i);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) m = max(m, mag(a[e]));
+            }
+        } else {
+            for (int c = threadIdx.x; c < columns; c += 256) m = max(m, mag(__float_as_uint(load_f32(row + c))));
+        }
+        m = max(max(m, m1), max(m2, m3));  // magnitudes order like their bits; NaN bits exceed every finite
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), off)));
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        lift[p] = lift_exponent(max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3])));
+}
 
 // The three bf16 parts of x (bit patterns in the low 16 bits).
 __device__ __forceinline__ void split3(float x, uint32_t& hi, uint32_t& lo, uint32_t& lolo) {
@@ -53,7 +117,8 @@ __device__ __forceinline__ void split3(float x, uint32_t& hi, uint32_t& lo, uint
 
 // One thread per (block, position tile, K step, lane): the 8 activations of its operand slot, split.
 __global__ __launch_bounds__(256) void fbatch_pack_kernel(const float* __restrict__ x, int columns, int positions,
-                                                          int tiles, uint8_t* __restrict__ workspace) {
+                                                          int tiles, uint8_t* __restrict__ workspace,
+                                                          const int* __restrict__ lift) {
     const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     const int blocks = columns / 32;
     if (item >= static_cast<int64_t>(blocks) * tiles * 128) return;
@@ -65,6 +130,7 @@ __global__ __launch_bounds__(256) void fbatch_pack_kernel(const float* __restric
     uint32_t part[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
     if (p < positions) {
         const float* src = x + static_cast<int64_t>(p) * columns + c0;
+        const int k = lift[p];
         float v[8];
         if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
             const u32x4 a = *(const SATORI_GLOBAL u32x4*)(src), c = *(const SATORI_GLOBAL u32x4*)(src + 4);
@@ -80,7 +146,7 @@ __global__ __launch_bounds__(256) void fbatch_pack_kernel(const float* __restric
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             uint32_t h, l, ll;
-            split3(v[e], h, l, ll);
+            split3(__builtin_amdgcn_ldexpf(v[e], k), h, l, ll);  // exact: the lifted value is at most 2^65
             const int shift = 16 * (e & 1);
             part[0][e >> 1] |= h << shift;
             part[1][e >> 1] |= l << shift;
@@ -135,6 +201,7 @@ __device__ __forceinline__ f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, co
 struct FbatchArgs {
     const uint8_t* w;          // device layout (code records, then FP16 scales)
     const uint8_t* workspace;  // split activations (fbatch_pack_kernel)
+    const int* lift;           // per position: the exponent its activations were lifted by
     float* y;                  // [positions][rows]
     int rows, blocks, positions, tiles;
 };
@@ -281,7 +348,9 @@ __global__ __launch_bounds__(256 * W) void fbatch_kernel(FbatchArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int p = t * kTile + 8 * (i >> 2) + 4 * h + (i & 3);
-        if (p < a.positions) store_f32(a.y + static_cast<int64_t>(p) * a.rows + row, acc[i]);
+        // Undo the position's lifting: exact unless the result is subnormal, where it rounds once.
+        if (p < a.positions)
+            store_f32(a.y + static_cast<int64_t>(p) * a.rows + row, __builtin_amdgcn_ldexpf(acc[i], -a.lift[p]));
     }
 }
 
@@ -294,7 +363,7 @@ int fbatch_min_positions() { return 32; }
 
 size_t fbatch_workspace_bytes(int columns, int positions) {
     const int tiles = (positions + kTile - 1) / kTile;
-    return static_cast<size_t>(columns / 32) * tiles * kBlockTileBytes;
+    return static_cast<size_t>(columns / 32) * tiles * kBlockTileBytes + static_cast<size_t>(tiles) * kTile * 4;
 }
 
 hipError_t launch_gemv_fbatch(const uint8_t* w, int format, const float* x, uint8_t* workspace, float* y, int rows,
@@ -305,14 +374,18 @@ hipError_t launch_gemv_fbatch(const uint8_t* w, int format, const float* x, uint
     const int tiles = (positions + kTile - 1) / kTile;
     const int64_t items = static_cast<int64_t>(blocks) * tiles * 128;
     if ((items + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
-    fbatch_pack_kernel<<<static_cast<unsigned>((items + 255) / 256), 256, 0, stream>>>(x, columns, positions, tiles,
-                                                                                      workspace);
+    int* lift = reinterpret_cast<int*>(workspace + static_cast<size_t>(blocks) * tiles * kBlockTileBytes);
+    fbatch_lift_kernel<<<static_cast<unsigned>(tiles * kTile), 256, 0, stream>>>(x, columns, positions, lift);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    fbatch_pack_kernel<<<static_cast<unsigned>((items + 255) / 256), 256, 0, stream>>>(x, columns, positions, tiles,
+                                                                                      workspace, lift);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t units = static_cast<int64_t>((rows + 4 * kTile - 1) / (4 * kTile)) * tiles;
     const int64_t grid = (units + 7) / 8 * 8;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
-    const FbatchArgs a{w, workspace, y, rows, blocks, positions, tiles};
+    const FbatchArgs a{w, workspace, lift, y, rows, blocks, positions, tiles};
     // Ways per row tile: as many (4, 2, 1) as keep every workgroup resident at once (two workgroups of 16
     // waves, four of 8 or eight of 4 per CU), so no second wave of workgroups trails the first.
     const int W = units <= 512 ? 4 : (units <= 1024 ? 2 : 1);

@@ -864,7 +864,8 @@ def test_legacy_matrix_core_batch(context, fmt, rows, columns, positions):
     xf = x[finite].astype(np.float64)
     exact, bound = np.zeros((positions, rows)), np.zeros((positions, rows))
     exact[finite] = xf @ wq.T
-    bound[finite] = np.abs(xf) @ np.abs(wq).T * 1e-5 + 1e-30
+    # Q8Validation.cs:46: the reference's subnormal floor n * float.Epsilon, n = C + C/32 + 2.
+    bound[finite] = np.abs(xf) @ np.abs(wq).T * 1e-5 + (columns + columns // 32 + 2) * TINY
     for p in finite:
         assert_within(y[p], exact[p], bound[p], f"position {p} vs FP64")
     for p in sorted({0, 1, 2, positions // 2, positions - 1} - {3, 4}):
@@ -875,6 +876,105 @@ def test_legacy_matrix_core_batch(context, fmt, rows, columns, positions):
         assert np.array_equal(np.isnan(y[p]), np.isnan(single)), f"position {p}: NaN pattern"
         inf = np.isinf(single)
         assert np.array_equal(np.isinf(y[p]), inf) and np.array_equal(y[p][inf], single[inf]), f"position {p}: Inf"
+    m.dispose()
+
+
+def _tiny_positions(g, positions, columns, mixed):
+    """Activation rows of tiny magnitude (NumericalCorpus.cs:24-27 carries 1e-30, subnormal and 1e-38 cases):
+    N(0,1) scaled to 1e-36 and 1e-38, FP32 subnormals, TINY alternating, normal elements mixed with 1e-38 and
+    subnormal ones, and magnitudes spread over 2^-150..2^0; with `mixed`, every other position is N(0,1)."""
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    kinds = []
+    for p in range(positions):
+        if mixed and p % 2 == 0:
+            kinds.append("normal")
+            continue
+        kind = ("1e-36", "1e-38", "subnormal", "tiny", "half-1e-38", "spread")[(p // (2 if mixed else 1)) % 6]
+        row = g.standard_normal(columns)
+        if kind == "1e-36":
+            v = row * 1e-36
+        elif kind == "1e-38":
+            v = row * 1e-38
+        elif kind == "subnormal":
+            v = g.integers(-(1 << 22), 1 << 22, columns).astype(np.float64) * TINY
+        elif kind == "tiny":
+            v = np.where(np.arange(columns) % 2 == 0, TINY, -TINY)
+        elif kind == "half-1e-38":
+            v = np.where(np.arange(columns) % 2 == 0, row, row * 1e-38)
+            v[::7] = g.integers(-1000, 1000, v[::7].size) * TINY
+        else:
+            v = row * np.exp2(g.uniform(-150.0, 0.0, columns))
+        x[p] = v.astype(np.float32)
+        kinds.append(kind)
+    return x, kinds
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_legacy_tiny_activations_within_reference_floor(context, fmt, mixed):
+    # Positions of 1e-36, 1e-38 and subnormal activations, alone and among normal positions, through the
+    # matrix-core batch (>= 32 positions) and the single-position kernels (ExecuteBatch at one position, and
+    # the IQuantizedMatrix form): every output within 1e-5 * sum|w x| + n * float.Epsilon (Q8Validation.cs:46,
+    # n = C + C/32 + 2) of the FP64 product and of the scalar reference (QuantizedMatVec.cs:45-78).
+    g = rng(4242 + int(fmt) + (7 if mixed else 0))
+    rows, columns, positions = 300, 1024, 40
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x, kinds = _tiny_positions(g, positions, columns, mixed)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    y = np.full(positions * rows, np.nan, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    y = y.reshape(positions, rows)
+    wq = O.decode_matrix(data, rows, columns, int(fmt)).astype(np.float64)
+    floor = (columns + columns // 32 + 2) * TINY
+    single = np.zeros(rows, np.float32)
+    for p in range(positions):
+        xp = x[p].astype(np.float64)
+        exact = wq @ xp
+        bound = 1e-5 * (np.abs(wq) @ np.abs(xp)) + floor
+        scalar = O.q_matvec_scalar(data, rows, columns, int(fmt), x[p])
+        what = f"position {p} ({kinds[p]})"
+        assert_within(y[p], exact, bound, what + " batch vs FP64")
+        assert_within(y[p], scalar, bound, what + " batch vs scalar")
+        if kinds[p] != "normal" or p < 2:
+            m.execute_batch(x[p], 1, single)
+            assert_within(single, exact, bound, what + " single position vs FP64")
+            assert_within(single, scalar, bound, what + " single position vs scalar")
+            m.execute(x[p], single)
+            assert_within(single, scalar, bound, what + " execute vs scalar")
+    m.dispose()
+
+
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+def test_k_tiny_activations_float_and_integer_paths(context, fmt):
+    # The K formats with the same tiny positions: the FP32-activation MatVec (IQuantizedMatrix.Execute,
+    # QuantizedMatVec.ExecuteScalar's DotBlock, QuantizedMatVec.cs:56-65) within 1e-5 * sum|w x| + n *
+    # float.Epsilon of the scalar reference, and the Q8_K integer path (ExecuteBatch) bit-identical to the
+    # reference's ExecuteQuantizedTiled composition, at one position and as a 40-position matrix-core batch.
+    g = rng(5151 + int(fmt))
+    rows, columns, positions = 256, 1536, 40
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    data = S.quantize_weights(w, rows, columns, fmt)
+    x, kinds = _tiny_positions(g, positions, columns, True)
+    m = context.create(data, S.QuantizedMatrixShape(rows, columns, fmt))
+    wq = O.decode_matrix(data, rows, columns, int(fmt)).astype(np.float64)
+    floor = (columns + columns // 256 + 2) * TINY
+    y = np.zeros(positions * rows, np.float32)
+    m.execute_batch(x.reshape(-1), positions, y)
+    single = np.zeros(rows, np.float32)
+    for p in range(positions):
+        what = f"position {p} ({kinds[p]})"
+        ref = O.qk_matvec_quantized_avx2(data, rows, columns, int(fmt), O.q8k_quantize_row(x[p]))
+        assert np.array_equal(y[p * rows:(p + 1) * rows].view(np.uint32), ref.view(np.uint32)), what + " batch"
+        if kinds[p] == "normal" and p >= 2:
+            continue
+        m.execute_batch(x[p], 1, single)
+        assert np.array_equal(single.view(np.uint32), ref.view(np.uint32)), what + " one position"
+        m.execute(x[p], single)
+        xp = x[p].astype(np.float64)
+        bound = 1e-5 * (np.abs(wq) @ np.abs(xp)) + floor
+        assert_within(single, O.q_matvec_scalar(data, rows, columns, int(fmt), x[p]), bound, what + " float")
+        assert_within(single, wq @ xp, bound, what + " float vs FP64")
     m.dispose()
 
 
