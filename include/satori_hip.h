@@ -167,7 +167,15 @@ int satori_hip_quantize_q8k(satori_hip_context* context, const float* input, int
 /* ---- MatVec, device buffers, asynchronous (resident pipelines and benchmarks) ----
  * Same arithmetic as the host-buffer calls. input/output are device pointers; the work is enqueued on
  * `stream` (NULL = the context stream) and the call returns without waiting. No input validation
- * beyond shapes; the caller keeps the buffers alive until the stream has passed the work. */
+ * beyond shapes; the caller keeps the buffers alive until the stream has passed the work.
+ * A matrix's launches share its device workspace (Ternary2: the exchange slots or partial sums of its
+ * launch plan; K formats: the packed Q8_K of many-position products; Q8_0 / Q4_0: the split activations of
+ * many-position products), so executions of one matrix on different streams must not overlap in time:
+ * the outputs of overlapping executions are undefined. Later executions are not affected (each Ternary2
+ * launch tags its exchanges with its own number, so nothing an overlapping launch leaves behind is added
+ * in), except the replays of a captured step or capture that overlapped: those reuse their recorded
+ * launch's number, so recreate such a step. For concurrent streams, give each stream its own copy
+ * (satori_hip_matrix_clone). The same holds for groups (satori_hip_group_execute). */
 int satori_hip_matvec_device(satori_hip_matrix* matrix, const float* input, float* output, void* stream);
 int satori_hip_matvec_batch_device(satori_hip_matrix* matrix, const float* input, int positions, float* output,
                                    void* stream);
@@ -362,7 +370,7 @@ int satori_hip_attention_decode(satori_hip_context* context, float* query, const
  * to a static device workspace of 4 MiB per device (resolved when the context is created, held until the
  * process ends) instead of a context workspace: a call whose partials, query_heads * splits * (head_dim + 2)
  * * 8 bytes, exceed it fails with SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE (12 heads of 128 lanes: prefixes up to
- * 686,080 tokens). Every call on a device shares that workspace and leaves its partials there: calls that
+ * 688,128 tokens). Every call on a device shares that workspace and leaves its partials there: calls that
  * overlap in time on one device (other streams, other contexts) race and must be serialised by the caller. */
 int satori_hip_grouped_attention_static(satori_hip_context* context, const float* query, const float* keys,
                                         const float* values, int query_heads, int kv_heads, int head_dim, int tokens,

@@ -255,11 +255,14 @@ __global__ __launch_bounds__(64 * W) void t2_fixup_kernel(MatDesc one, const Mat
 // workgroup (panel, slice) owns one 64-row panel and a contiguous slice of its tiles; each wave takes one
 // tile at a time with its own pair tables, so no wave waits for tables another wave builds. The waves' row sums are added in LDS in wave order, and
 // the S slices of a panel are joined by a binary tree of 64-bit atomic exchanges per row: the two siblings
-// of a node each swap (1 << 32 | bits of their sum) into the node's slot; the one that finds the slot empty
-// is done, the other adds the two sums (left + right, whichever came first) and carries the result up, and
-// puts the slot back to empty. Each value travels inside the atomic that the reader sees, so no fence is
-// needed, and the order of every addition is fixed by the tree, so results do not depend on scheduling.
-// The slots start empty (zeroed with the plan's scratch) and every launch leaves them empty.
+// of a node each swap (generation << 32 | bits of their sum) into the node's slot; the one that finds no
+// value of its own launch's generation there is done, the other adds the two sums (left + right, whichever
+// came first) and carries the result up, and puts the slot back to empty. Each value travels inside the
+// atomic that the reader sees, so no fence is needed, and the order of every addition is fixed by the tree,
+// so results do not depend on scheduling. The slots start empty (zeroed with the plan's scratch) and a
+// launch that overlaps no other launch of the same scratch leaves them empty. Launches that do overlap can
+// leave a value behind; it carries another launch's generation (the host numbers every launch, and never
+// uses 0), so a later launch takes it for an empty slot instead of adding it.
 struct T2SliceArgs {
     int columns;
     int tiles;
@@ -268,8 +271,8 @@ struct T2SliceArgs {
     int panels;
     int slices;                     // S
     int groups;                     // tiles per slice
-    int pad_;
-    unsigned long long* exchange;   // [tree node][panels * 64], zero
+    uint32_t generation;            // this launch's tag in the exchange slots (never 0)
+    unsigned long long* exchange;   // [tree node][panels * 64]
 };
 
 constexpr int kSliceMaxWaves = 16;  // 16 waves x 4 KB of tables fill the 64 KB of LDS the kernel uses
@@ -381,10 +384,11 @@ __global__ __launch_bounds__(64 * kSliceMaxWaves) void t2_slice_kernel(MatDesc o
     for (int count = a.slices; count > 1; count = (count + 1) >> 1) {
         if ((i ^ 1) < count) {  // the node has both children at this level
             unsigned long long* slot = level + static_cast<int64_t>(i >> 1) * stride + row;
-            const unsigned long long mine = (1ull << 32) | __float_as_uint(piece);
+            const unsigned long long mine = (static_cast<unsigned long long>(a.generation) << 32) | __float_as_uint(piece);
             const unsigned long long old =
                 __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (old == 0) return;  // first to arrive: the sibling carries the pair
+            // First to arrive (empty, or a value an overlapping launch left): the sibling carries the pair.
+            if (static_cast<uint32_t>(old >> 32) != a.generation) return;
             const float other = __uint_as_float(static_cast<uint32_t>(old));
             piece = (i & 1) ? other + piece : piece + other;
             __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -557,8 +561,9 @@ T2Plan t2_plan(int rows_max, int columns, int block_size, int count, int positio
 }
 
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape s, const T2Plan& plan,
-                     void* scratch, hipStream_t stream) {
+                     void* scratch, uint32_t generation, hipStream_t stream) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
+    if (generation == 0) return hipErrorInvalidValue;
     if (plan.workgroups < 1 || scratch == nullptr || plan.rows_max != s.rows_max || plan.columns != s.columns ||
         plan.block_size != s.block_size || plan.count != count || plan.positions != s.positions ||
         plan.staged_tiles > kMaxStagedTiles)
@@ -569,7 +574,7 @@ hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, Launch
             plan.workgroups != l.panels * plan.slices)
             return hipErrorInvalidValue;
         const T2SliceArgs a{s.columns, l.tiles,       l.chunks,          l.slots, l.panels, plan.slices,
-                            plan.slice_groups, 0, static_cast<unsigned long long*>(scratch)};
+                            plan.slice_groups, generation, static_cast<unsigned long long*>(scratch)};
         const size_t lds = static_cast<size_t>(plan.waves) * kTableFloats * sizeof(float);
         switch (s.block_size) {
             case 64: t2_slice_kernel<64><<<plan.workgroups, 64 * plan.waves, lds, stream>>>(one, group, a); break;

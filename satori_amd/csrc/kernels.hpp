@@ -92,9 +92,11 @@ constexpr int legacy_record_bytes(int format) { return format == kQ8_0 ? 32 : 16
 // starts, cut items): copy `tables` there once before the first launch; the rest holds per-workgroup
 // partial sums. A single matrix at one position small enough for the chip to hold all its workgroups at
 // once is instead sliced: one kernel, workgroup (panel, column slice), slices joined through atomic
-// exchange slots in the scratch (`tables` is their zeroed image, and every launch leaves them zero).
-// Launches that share a scratch buffer must not overlap in time. A plan is valid for the launch shape,
-// member count and positions it was made for, on the device that was current.
+// exchange slots in the scratch (`tables` is their zeroed image); each launch tags its exchanges with a
+// generation, a nonzero number that differs from the previous launches' (next_t2_generation).
+// Launches that share a scratch buffer must not overlap in time: overlapping ones give undefined outputs,
+// and the generation tags keep what they leave in the slots from reaching later launches. A plan is valid
+// for the launch shape, member count and positions it was made for, on the device that was current.
 struct T2Fixup {
     int member, position, panel0;  // the cut item
     int first, last;               // ranges holding its pieces
@@ -126,7 +128,13 @@ int t2_resident_workgroups(int block_size, int waves, int staged_tiles);
 // Ternary2 MatVec on the panel layout (MatDesc::w points at it), with the plan made for this launch and
 // its scratch buffer (tables already copied).
 hipError_t launch_t2(const MatDesc& one, const MatDesc* group, int count, LaunchShape shape, const T2Plan& plan,
-                     void* scratch, hipStream_t stream);
+                     void* scratch, uint32_t generation, hipStream_t stream);
+
+// The next launch's generation for a scratch buffer whose last launch used `last` (1, 2, ..., skipping 0).
+inline uint32_t next_t2_generation(uint32_t& last) {
+    if (++last == 0) last = 1;
+    return last;
+}
 
 // Q8_K quantization of `positions` rows of `columns` floats (columns a multiple of 256), bit-exact with
 // Q8KCodec.QuantizeRow. Output [positions][columns / 256 * 292].

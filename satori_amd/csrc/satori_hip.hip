@@ -109,6 +109,7 @@ struct satori_hip_matrix {
     int64_t device_bytes = 0;    // bytes at `payload` (slack excluded)
     satori::T2Plan plan{};       // Ternary2 launch plan of a single execution
     void* scratch = nullptr;     // Ternary2 range scratch (device), when the plan has several ranges
+    uint32_t t2_generation = 0;  // the last Ternary2 launch's tag in the scratch's exchange slots
     satori::DeviceBuffer q8k;    // activations of the last many-position product (K formats: packed Q8_K;
                                  // Q8_0 / Q4_0: split bf16 parts)
     satori::DeviceBuffer planes; // Q6_K: the matrix-core weight planes, built by the first many-position product
@@ -129,6 +130,7 @@ struct satori_hip_group {
     satori::InputTransform input{};            // K groups: input computed in the launch (kInputPlain: read x)
     satori::T2Plan plan{};                     // Ternary2 groups
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
+    uint32_t t2_generation = 0;                // the last Ternary2 launch's tag in the scratch's exchange slots
     std::vector<satori_hip_matrix*> members;   // distinct member matrices (each counts this group)
     int steps = 0;                             // live steps that replay this group
     bool live = true;
@@ -245,7 +247,8 @@ void enqueue_float(satori_hip_matrix* m, const float* x, int positions, float* y
     MatDesc d{m->payload, x, y, s.rows, 0};
     const LaunchShape l = launch_shape(s, positions, s.rows);
     if (s.format == SATORI_HIP_TERNARY2)
-        check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->scratch, stream), "Ternary2 launch");
+        check_hip(launch_t2(d, nullptr, 1, l, m->plan, m->scratch, next_t2_generation(m->t2_generation), stream),
+                  "Ternary2 launch");
     else
         check_hip(launch_gemv_float(d, nullptr, 1, l, stream), "gemv launch");
 }
@@ -526,7 +529,9 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
     } else if (g->quantized) {
         check_hip(launch_gemv_kint(g->host.data(), g->descriptors, g->count, l, st), "integer gemv launch");
     } else if (g->shape.format == SATORI_HIP_TERNARY2) {
-        check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, st), "Ternary2 launch");
+        check_hip(launch_t2(none, g->descriptors, g->count, l, g->plan, g->scratch, next_t2_generation(g->t2_generation),
+                            st),
+                  "Ternary2 launch");
     } else {
         check_hip(launch_gemv_float(none, g->descriptors, g->count, l, st), "gemv launch");
     }
