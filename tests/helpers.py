@@ -103,3 +103,16 @@ def special_scale_payload(fmt, rows, columns, scales):
                     lo, hi = (j + b) % 16, (15 - j + b) % 16
                     data[off + 2 + j] = lo | (hi << 4)
     return data
+
+
+def attention_boundary_case():
+    """The closed-form inputs of VulkanAttentionTests.cs:17-22 (6 heads of 48 lanes, 128 tokens) and the
+    FP64 expected outputs of fixtures/operators/attention-boundaries-v1.json, keyed by token count."""
+    width = 288
+    i = np.arange(width)
+    q = ((i % 17 - 8) * 0.125).astype(np.float32)
+    token = np.arange(128)[:, None]
+    keys = (((token * 13 + i * 7) % 31 - 15) * 0.0625).astype(np.float32)
+    values = (((token * 5 + i * 11) % 37 - 18) * 0.125).astype(np.float32)
+    cases = {c["count"]: np.array(c["expected"], np.float64) for c in load_json("attention-boundaries-v1.json")["cases"]}
+    return q, keys, values, cases

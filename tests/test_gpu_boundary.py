@@ -383,6 +383,60 @@ def test_split_attentions_on_two_streams_do_not_share_a_workspace(context):
             context.free(p)
 
 
+def test_attention_boundary_fixture(context):
+    # VulkanAttentionTests.cs:17-29 with fixtures/operators/attention-boundaries-v1.json: 6 heads of 48 lanes at
+    # 1, 2, 32, 64 and 128 tokens (across the one-workgroup form's 32-token limit), within 2e-6 + 2e-6 |e| of the
+    # reference's FP64 outputs, and the negated values within the same bound of the negated outputs. Three
+    # entry points: the grouped attention (host buffers), its no-allocation form, and the decode form (the
+    # attention inputs of position count - 1 applied in the launch). The decode form rotates the query and the
+    # new key by RopeHalf at that position; rotations keep dot products, so with the cached keys rotated by the
+    # same angle (the oracle's RopeHalf, rounded to FP32) it computes the fixture's attention up to those
+    # roundings (1.8% of the bound in the oracle).
+    from helpers import attention_boundary_case
+
+    q, keys, values, cases = attention_boundary_case()
+    ops = S.DeviceOps(context)
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(max(arr.nbytes, 4))
+        context.upload(p, np.ascontiguousarray(arr))
+        buffers.append(p)
+        return p
+
+    def check(actual, expected, name):
+        err = np.abs(np.asarray(actual, np.float64) - expected)
+        assert np.all(np.isfinite(actual)), name
+        assert np.all(err <= 2e-6 + 2e-6 * np.abs(expected)), f"{name}: max err {err.max()}"
+
+    try:
+        for count, expected in cases.items():
+            for sign in (1, -1):
+                v = (sign * values[:count]).astype(np.float32)
+                out = np.zeros(288, np.float32)
+                S.TransformerOps.grouped_attention(q, keys[:count].reshape(-1), v.reshape(-1), 6, 6, 48, count, out,
+                                                   context)
+                check(sign * out, expected, f"grouped attention {count} sign {sign}")
+                dout = dev(np.zeros(288, np.float32))
+                ops.grouped_attention_static(dev(q), dev(keys[:count]), dev(v), 6, 6, 48, count, dout)
+                check(sign * context.download(np.zeros(288, np.float32), dout), expected,
+                      f"static attention {count} sign {sign}")
+                position = count - 1
+                cache_k = np.stack([O.rope_half(keys[j], 48, position, 10000.0, 48) for j in range(count)])
+                cache_k[position] = 0.0  # written by the launch
+                cache_v = v.copy()
+                cache_v[position] = 0.0
+                dq, dck, dcv = dev(q), dev(cache_k), dev(cache_v)
+                dout = dev(np.zeros(288, np.float32))
+                ops.attention_decode(dq, 0, dev(keys[position]), 0, dev(v[position]), 0, dck, dcv, 6, 6, 48, position,
+                                     10000.0, 48, dout)
+                check(sign * context.download(np.zeros(288, np.float32), dout), expected,
+                      f"decode attention {count} sign {sign}")
+    finally:
+        for p in buffers:
+            context.free(p)
+
+
 @pytest.mark.parametrize("position,heads,kv_heads,head_dim,rotary,biases", [
     (0, 12, 2, 128, 128, True), (31, 12, 2, 128, 128, True), (32, 12, 2, 128, 128, True),
     (511, 12, 2, 128, 128, True), (2047, 12, 2, 128, 128, True), (2048, 12, 2, 128, 128, True),

@@ -78,3 +78,26 @@ def test_oracle_closed_forms():
     assert abs(O.swiglu(f32([-30.0]), f32([1.0]))[0] - (-30.0 / (1 + np.exp(30.0)))) < 1e-16
     assert O.rms_norm(f32([3.0, 4.0]), f32([2.0, 0.5]), np.float32(1e-30)).tolist() == \
         [np.float32(3 / np.sqrt(12.5) * 2), np.float32(4 / np.sqrt(12.5) * 0.5)]
+
+
+def test_oracle_matches_attention_boundary_fixture():
+    # VulkanAttentionTests.cs:17-29 against fixtures/operators/attention-boundaries-v1.json: 6 heads of 48
+    # lanes (query and key/value heads alike), 1, 2, 32, 64 and 128 tokens, |a - e| <= 2e-6 + 2e-6 |e|, and
+    # the negated values give the negated output. The fixture's reading (score = q.k / sqrt(48), max-subtracted
+    # softmax, weighted value sum, one key/value head per query head) is pinned by an FP64 brute force that
+    # reproduces it to 1e-12.
+    from helpers import attention_boundary_case
+
+    q, keys, values, cases = attention_boundary_case()
+    assert sorted(cases) == [1, 2, 32, 64, 128]
+    for count, expected in cases.items():
+        brute = np.zeros(288)
+        for h in range(6):
+            lanes = slice(48 * h, 48 * h + 48)
+            scores = keys[:count, lanes].astype(np.float64) @ q[lanes].astype(np.float64) / np.sqrt(48.0)
+            e = np.exp(scores - scores.max())
+            brute[lanes] = (e / e.sum()) @ values[:count, lanes].astype(np.float64)
+        assert np.all(np.abs(brute - expected) <= 1e-12 * (1 + np.abs(expected))), f"{count}: brute force"
+        k, v = keys[:count].reshape(-1), values[:count].reshape(-1)
+        within_fixture(O.grouped_attention(q, k, v, 6, 6, 48, count), expected, f"attention {count}")
+        within_fixture(-O.grouped_attention(q, k, -v, 6, 6, 48, count), expected, f"negated {count}")
