@@ -344,6 +344,27 @@ class DecodeModel:
             self.ctx.free(p)
 
 
+# The input each projection of a layer reads (q/k/v the normed residual, o the attention output, gate/up the
+# second normed residual, down the SwiGLU output), and the output projection's.
+FEEDS = {"q": "h", "k": "h", "v": "h", "o": "attn", "gate": "h2", "up": "h2", "down": "act", "output": "h"}
+
+
+def decode_inputs(model: "DecodeModel") -> dict:
+    """The decode step's fixed FP32 projection inputs (seeded)."""
+    g = rng(2026)
+    return {"h": g.standard_normal(model.D).astype(np.float32), "attn": g.standard_normal(model.D).astype(np.float32),
+            "h2": g.standard_normal(model.D).astype(np.float32), "act": g.standard_normal(model.FFN).astype(np.float32)}
+
+
+def prefill_inputs(model: "DecodeModel", positions: int) -> dict:
+    """The prefill's fixed FP32 projection inputs, [positions][columns] flattened (seeded)."""
+    g = rng(2027)
+    return {"h": g.standard_normal(positions * model.D).astype(np.float32),
+            "attn": g.standard_normal(positions * model.D).astype(np.float32),
+            "h2": g.standard_normal(positions * model.D).astype(np.float32),
+            "act": g.standard_normal(positions * model.FFN).astype(np.float32)}
+
+
 def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_only: bool = False) -> dict:
     """The projection sequence of one decode token (197 projections, batch 1) on the Q8_K integer path, launched
     as the whole token launches them. Projections that share an input form one group (q/k/v, gate/up); the
@@ -352,9 +373,7 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
     their FP32 input inside their launch; down reads the Q8_K bytes its producer (SwiGLU) writes in the whole
     token, here quantized once before timing. Also timed: the same groups launched eagerly."""
     d, ffn, vocab = model.D, model.FFN, model.VOCAB
-    g = rng(2026)
-    host_in = {"h": g.standard_normal(d).astype(np.float32), "attn": g.standard_normal(d).astype(np.float32),
-               "h2": g.standard_normal(d).astype(np.float32), "act": g.standard_normal(ffn).astype(np.float32)}
+    host_in = decode_inputs(model)
     h, attn, h2, act = (model.device(host_in[k]) for k in ("h", "attn", "h2", "act"))
     out = {name: model.device(np.zeros(r, np.float32)) for name, (r, _, _) in model.roles.items()}
     logits = model.device(np.zeros(vocab, np.float32))
@@ -375,11 +394,10 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
             grp.set_input_q8k(act_q8k)
     # Parity before timing: every launch of the step, one at a time, against the oracle (checker only).
     from oracle import oracle as O
-    feeds = {"q": "h", "k": "h", "v": "h", "o": "attn", "gate": "h2", "up": "h2", "down": "act", "output": "h"}
     expected = {}
     for name, (r, c, fmt) in model.shapes.items():
         expected[name] = O.qk_matvec_quantized_avx2(model.host[name], r, c, int(fmt),
-                                                    O.q8k_quantize_row(host_in[feeds[name]]))
+                                                    O.q8k_quantize_row(host_in[FEEDS[name]]))
     for grp, names in zip(groups, members):
         for name in names:
             ctx.upload(out[name], np.full(model.shapes[name][0], np.nan, np.float32))
@@ -567,11 +585,7 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     and the output projection for the last position only (DenseSession.cs:156-159). The FLOP-based rate
     counts 2 int8 operations per weight per position."""
     d, ffn = model.D, model.FFN
-    g = rng(2027)
-    host_in = {"h": g.standard_normal(positions * d).astype(np.float32),
-               "attn": g.standard_normal(positions * d).astype(np.float32),
-               "h2": g.standard_normal(positions * d).astype(np.float32),
-               "act": g.standard_normal(positions * ffn).astype(np.float32)}
+    host_in = prefill_inputs(model, positions)
     h, attn, h2, act = (model.device(host_in[k]) for k in ("h", "attn", "h2", "act"))
     out = {name: model.device(np.zeros(positions * r, np.float32)) for name, (r, _, _) in model.roles.items()}
     logits = model.device(np.zeros(model.VOCAB, np.float32))
@@ -611,13 +625,12 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     # Parity before timing (checker only): the last layer's outputs at sampled positions of both chunks
     # (tile edges 0/31/32, chunk edges 255/256, the last position) and the output projection, bit-exact.
     from oracle import oracle as O
-    feeds = {"q": "h", "k": "h", "v": "h", "o": "attn", "gate": "h2", "up": "h2", "down": "act"}
     sampled = [p for p in (0, 1, 31, 32, 100, 255, 256, 257, 300, 400, 511) if p < positions]
     ctx.synchronize()
     for name, (r, c, fmt) in model.roles.items():
         y = ctx.download(np.zeros(positions * r, np.float32), out[name]).reshape(positions, r)
         for p in sampled:
-            x = host_in[feeds[name]][p * c:(p + 1) * c]
+            x = host_in[FEEDS[name]][p * c:(p + 1) * c]
             want = O.qk_matvec_quantized_avx2(model.host[name], r, c, int(fmt), O.q8k_quantize_row(x))
             if not np.array_equal(y[p].view(np.uint32), want.view(np.uint32)):
                 raise ParityError(f"prefill: {name} at position {p} differs from the oracle")
@@ -770,6 +783,74 @@ def cpu_format(data, rows, columns, fmt, x, quantized, seconds) -> dict:
             "cpu_ms_median": sorted(samples)[len(samples) // 2] * 1e3, "cpu_runs": len(samples)}
 
 
+def cpu_decode_step(host, shapes, host_in, seconds) -> dict:
+    """The decode step's 197 projections on one host core through the restated reference path (oracle):
+    per projection Q8KCodec.QuantizeRow of its FP32 input, then QuantizedKAvx2Kernel.ExecuteQuantizedTiled at
+    one position -- what QuantizedMatVec.ExecuteBatch runs for each projection of DenseForward.Step
+    (DenseForward.cs:119; QuantizedMatVec.cs:136-219), quantization included. Each of the 28 layers has its
+    own copy of the payloads, as on the GPU (no layer finds another's weights in the caches)."""
+    from oracle import oracle as O
+
+    layers = [{name: host[name].copy() for name in shapes if name != "output"} for _ in range(28)]
+    ys = {name: np.zeros(r, np.float32) for name, (r, _, _) in shapes.items()}
+
+    def token():
+        for layer in layers:
+            for name, data in layer.items():
+                r, c, fmt = shapes[name]
+                O.qk_matvec_quantized_avx2(data, r, c, int(fmt), O.q8k_quantize_row(host_in[FEEDS[name]]), ys[name])
+        r, c, fmt = shapes["output"]
+        O.qk_matvec_quantized_avx2(host["output"], r, c, int(fmt), O.q8k_quantize_row(host_in["h"]), ys["output"])
+
+    token()  # warm
+    samples, start = [], time.perf_counter()
+    while time.perf_counter() - start < seconds or len(samples) < 3:
+        t0 = time.perf_counter()
+        token()
+        samples.append(time.perf_counter() - t0)
+    best, median = min(samples), sorted(samples)[len(samples) // 2]
+    return {"cpu_ms_per_token": best * 1e3, "cpu_ms_per_token_median": median * 1e3, "cpu_tokens": len(samples),
+            "cpu_sample": ("restated reference Q8KCodec.QuantizeRow + ExecuteQuantizedTiled at one position "
+                           "(oracle/satori_oracle_avx2.c), per projection, 197 projections of 28 distinct layer "
+                           f"copies; {len(samples)} tokens, 1 thread pinned; min reported")}
+
+
+def cpu_prefill_chunk(host, shapes, host_in, positions: int, repeats: int) -> dict:
+    """One 256-position layer-chunk of the prefill on one host core through the restated reference path: per
+    projection Q8KCodec.QuantizeRow of its 256 input rows, then ExecuteQuantizedTiled over the 256 positions
+    (QuantizedKAvx2Kernel.cs:47-99, the reference's tile), as DenseForward.LayerBatch calls ExecuteBatch per
+    projection. The whole prefill is that times 28 layers times the chunks, plus the output projection of the
+    last position (extrapolated, labelled)."""
+    from oracle import oracle as O
+
+    def chunk():
+        for name, data in host.items():
+            if name == "output":
+                continue
+            r, c, fmt = shapes[name]
+            x = host_in[FEEDS[name]][:positions * c]
+            acts = np.concatenate([O.q8k_quantize_row(x[p * c:(p + 1) * c]) for p in range(positions)])
+            O.qk_matvec_quantized_tiled_avx2(data, r, c, int(fmt), acts, positions, ys[name])
+
+    ys = {name: np.zeros(positions * r, np.float32) for name, (r, _, _) in shapes.items() if name != "output"}
+    samples = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        chunk()
+        samples.append(time.perf_counter() - t0)
+    r, c, fmt = shapes["output"]
+    t0 = time.perf_counter()
+    O.qk_matvec_quantized_avx2(host["output"], r, c, int(fmt), O.q8k_quantize_row(host_in["h"][:c]))
+    output_ms = (time.perf_counter() - t0) * 1e3
+    best = min(samples) * 1e3
+    return {"cpu_ms_per_layer_chunk": best, "cpu_chunk_positions": positions,
+            "cpu_ms_extrapolated": best * 28 * 2 + output_ms,
+            "cpu_sample": (f"restated reference QuantizeRow + ExecuteQuantizedTiled over {positions} positions "
+                           f"(oracle/satori_oracle_avx2.c) for the 7 projections of one layer, {repeats} runs, "
+                           "1 thread pinned, min reported; cpu_ms_extrapolated = 56 layer-chunks + the output "
+                           "projection of the last position")}
+
+
 def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
     """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample."""
     from oracle import oracle as O
@@ -837,7 +918,13 @@ def other_formats(ctx):
             (BQ.Q4_K, 8960, 1536, True, "q4_k-8960x1536-q8k"),
             (BQ.Q4_K, 1536, 8960, True, "q4_k-1536x8960-q8k"),
             (BQ.Q6_K, 8960, 1536, True, "q6_k-8960x1536-q8k"),
-            (BQ.Q6_K, 1536, 8960, True, "q6_k-1536x8960-q8k")):
+            (BQ.Q6_K, 1536, 8960, True, "q6_k-1536x8960-q8k"),
+            # The K formats' FP32-activation MatVec (IQuantizedMatrix.Execute / ExecuteScalar's DotBlock; CPU:
+            # QuantizedKAvx2Kernel.ExecuteQ4K / ExecuteQ6K).
+            (BQ.Q4_K, 8960, 1536, False, "q4_k-8960x1536-f32"),
+            (BQ.Q4_K, 1536, 8960, False, "q4_k-1536x8960-f32"),
+            (BQ.Q6_K, 8960, 1536, False, "q6_k-8960x1536-f32"),
+            (BQ.Q6_K, 1536, 8960, False, "q6_k-1536x8960-f32")):
         def make(fmt=fmt, r=r, cc=cc, quantized=quantized, label=label):
             data, xf = make_gguf(fmt, r, cc)
             shape = S.QuantizedMatrixShape(r, cc, fmt)
@@ -855,6 +942,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-format-seconds", type=float, default=1.0,
                     help="CPU sample per format (restated reference AVX2 path, one core)")
+    ap.add_argument("--cpu-decode-seconds", type=float, default=4.0,
+                    help="CPU sample of the decode step's 197 projections (restated reference path, one core)")
     ap.add_argument("--warmup-seconds", type=float, default=1.5,
                     help="untimed headline launches before the first timed region (steady-state clocks)")
     ap.add_argument("--quick", action="store_true", help="headline workload only, no other formats")
@@ -992,6 +1081,7 @@ def run(args, ctx, events) -> int:
         if not args.quick:
             progress("decode step (197 projections per token)")
             model = DecodeModel(ctx)
+            model_host, model_shapes = model.host, model.shapes
             decode = decode_step(ctx, events, model, 50, 5)
             progress("whole decode token (operators + projections, position 511)")
             token = decode_token(ctx, events, model, 30, 3)
@@ -1013,6 +1103,11 @@ def run(args, ctx, events) -> int:
         for label, case in cpu_cases.items():
             formats[label].update(cpu_format(*case, args.cpu_format_seconds))
             formats[label]["gpu_over_cpu"] = formats[label]["gbs"] / formats[label]["cpu_gbs"]
+        progress("cpu baseline: decode step and one prefill layer-chunk")
+        decode.update(cpu_decode_step(model_host, model_shapes, decode_inputs(model), args.cpu_decode_seconds))
+        decode["gpu_over_cpu"] = decode["cpu_ms_per_token"] * 1e3 / decode["us_per_token"]
+        pre.update(cpu_prefill_chunk(model_host, model_shapes, prefill_inputs(model, 512), 256, 2))
+        pre["gpu_over_cpu"] = pre["cpu_ms_extrapolated"] / pre["ms"]
     value = headline["gbs"]
     traffic, traffic_source = profiled_traffic("ternary2_4096_b128_grouped.md")
     line = {

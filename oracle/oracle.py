@@ -100,6 +100,7 @@ def _declare(l):
         "or_q8k_quantize_row": (I, [P, I, P, SZ]),
         "or_q_matvec_batch": (I, [P, I, I, I, P, I, P]),
         "or_qk_matvec_quantized_avx2": (None, [P, I, I, I, P, P]),
+        "or_qk_matvec_quantized_tiled_avx2": (None, [P, I, I, I, P, I, P]),
         "or_corpus_random_matrix": (None, [I, I, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -255,6 +256,18 @@ def qk_matvec_quantized_avx2(data, rows: int, columns: int, fmt: int, activation
     if y is None:
         y = np.zeros(rows, dtype=np.float32)
     lib().or_qk_matvec_quantized_avx2(_ptr(d), rows, columns, fmt, _ptr(a), _ptr(y))
+    return y
+
+
+def qk_matvec_quantized_tiled_avx2(data, rows: int, columns: int, fmt: int, activations, positions: int,
+                                   y: np.ndarray | None = None):
+    """ExecuteQuantizedTiled over `positions` (1..256) Q8_K rows at once: output [positions][rows]."""
+    d, a = _u8(data), _u8(activations)
+    if not 1 <= positions <= 256 or a.size != positions * (columns // 256) * 292:
+        raise ValueError("positions must be 1..256 with one Q8_K row each")
+    if y is None:
+        y = np.zeros(positions * rows, dtype=np.float32)
+    lib().or_qk_matvec_quantized_tiled_avx2(_ptr(d), rows, columns, fmt, _ptr(a), positions, _ptr(y))
     return y
 
 

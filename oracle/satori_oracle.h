@@ -79,6 +79,10 @@ int or_q_matvec_batch(const uint8_t* data, int rows, int columns, int format, co
 /* K formats at one position against a Q8_K row, AVX2 integer kernel (the decode hot loop). */
 void or_qk_matvec_quantized_avx2(const uint8_t* weights, int rows, int columns, int format,
                                  const uint8_t* activations, float* y);
+/* ExecuteQuantizedTiled over 1..256 positions: activations [positions][columns / 256 * 292], output
+ * [positions][rows] (QuantizedKAvx2Kernel.cs:47-99). */
+void or_qk_matvec_quantized_tiled_avx2(const uint8_t* weights, int rows, int columns, int format,
+                                       const uint8_t* activations, int positions, float* output);
 
 /* NumericalCorpus.RandomMatrix: xorshift32 seed 1729 corpus (weights then input). */
 /* TransformerOps (src/Satori.Core/TransformerOps.cs): FP64 arithmetic in the reference's order, FP32 out. */

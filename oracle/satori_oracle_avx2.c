@@ -292,3 +292,42 @@ void or_qk_matvec_quantized_avx2(const uint8_t* weights, int rows, int columns, 
         output[row] = accumulator;
     }
 }
+
+/* QuantizedKAvx2Kernel.ExecuteQuantizedTiled over `positions` (1..256) positions and all rows, with the
+ * activations already quantized by Q8KCodec.QuantizeRow, [positions][columns / 256 * 292]
+ * (QuantizedKAvx2Kernel.cs:47-99): per row and block the scales once, then each position's term into that
+ * position's accumulator; output [positions][rows]. */
+void or_qk_matvec_quantized_tiled_avx2(const uint8_t* weights, int rows, int columns, int format,
+                                       const uint8_t* activations, int positions, float* output) {
+    int blocks_per_row = columns / 256;
+    int block_bytes = format == OR_Q4_K ? 144 : 210;
+    int q4 = format == OR_Q4_K;
+    int64_t row_bytes = (int64_t)blocks_per_row * 292;
+    int sub_scales[8], sub_mins[8];
+    float accumulator[256];
+    if (positions < 1 || positions > 256) return;
+    for (int row = 0; row < rows; row++) {
+        for (int p = 0; p < positions; p++) accumulator[p] = 0;
+        const uint8_t* weight_row = weights + (int64_t)row * blocks_per_row * block_bytes;
+        for (int block = 0; block < blocks_per_row; block++) {
+            const uint8_t* bw = weight_row + block * block_bytes;
+            float d, dmin = 0;
+            if (q4) {
+                for (int sub = 0; sub < 8; sub++) or_q4k_get_scale_min(sub, bw + 4, &sub_scales[sub], &sub_mins[sub]);
+                d = or_half_to_float(rd16(bw));
+                dmin = or_half_to_float(rd16(bw + 2));
+            } else {
+                d = or_half_to_float(rd16(bw + 208));
+            }
+            for (int p = 0; p < positions; p++) {
+                const uint8_t* activation = activations + p * row_bytes + (int64_t)block * 292;
+                float activation_scale = rdf32(activation);
+                if (activation_scale == 0) continue;
+                accumulator[p] += q4 ? q4k_dot_quantized_avx2(bw, activation, sub_scales, sub_mins, d * activation_scale,
+                                                              dmin * activation_scale)
+                                     : activation_scale * d * (float)q6k_dot_product_avx2(bw, activation);
+            }
+        }
+        for (int p = 0; p < positions; p++) output[(int64_t)p * rows + row] = accumulator[p];
+    }
+}

@@ -451,6 +451,31 @@ def test_batch_restatements_agree_and_equal_compose_row(fmt):
         assert total.view(np.uint32) == batch[r].view(np.uint32)
 
 
+@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q6_K])
+def test_tiled_restatement_equals_per_position(fmt):
+    # ExecuteQuantizedTiled over several positions (the tiled form the CPU baseline of the prefill times)
+    # gives, position by position, the bits of the one-position restatement and of the scalar ExecuteBatch
+    # (QuantizedMatVec.cs:136-219), including a zero position and positions with zero blocks.
+    g = rng(7 + fmt)
+    rows, columns, positions = 40, 1024, 7
+    w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    import satori_amd as S
+    payload = S.quantize_weights(w, rows, columns, S.BlockQuantization(fmt))
+    x = g.standard_normal((positions, columns)).astype(np.float32)
+    x[2] = 0.0
+    x[4, 256:512] = 0.0
+    x[5] *= np.float32(1e-30)
+    acts = np.concatenate([O.q8k_quantize_row(x[p]) for p in range(positions)])
+    tiled = O.qk_matvec_quantized_tiled_avx2(payload, rows, columns, fmt, acts, positions)
+    batch = O.q_matvec_batch(payload, rows, columns, fmt, x.reshape(-1), positions)
+    assert np.array_equal(tiled.view(np.uint32), batch.view(np.uint32))
+    for p in range(positions):
+        single = O.qk_matvec_quantized_avx2(payload, rows, columns, fmt, O.q8k_quantize_row(x[p]))
+        assert np.array_equal(tiled[p * rows:(p + 1) * rows].view(np.uint32), single.view(np.uint32)), p
+    with pytest.raises(ValueError):
+        O.qk_matvec_quantized_tiled_avx2(payload, rows, columns, fmt, np.zeros(257 * 4 * 292, np.uint8), 257)
+
+
 @pytest.mark.parametrize("fmt,fixture,rows,columns,positions", [
     (O.Q4_K, "q4k-v1.json", 2, 512, 4), (O.Q4_K, "q4k-v1.json", 3, 512, 1), (O.Q6_K, "q6k-v1.json", 2, 256, 8)])
 def test_batch_within_activation_quantization_bound(fmt, fixture, rows, columns, positions):
