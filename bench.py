@@ -368,10 +368,12 @@ def prefill_inputs(model: "DecodeModel", positions: int) -> dict:
 def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_only: bool = False) -> dict:
     """The projection sequence of one decode token (197 projections, batch 1) on the Q8_K integer path, launched
     as the whole token launches them. Projections that share an input form one group (q/k/v, gate/up); the
-    113 groups of a token are captured once as a graph (satori_hip_step) and replayed. Attention, norms and
-    SwiGLU are not part of the path: their outputs are fixed random vectors. q/k/v, o and gate/up quantize
-    their FP32 input inside their launch; down reads the Q8_K bytes its producer (SwiGLU) writes in the whole
-    token, here quantized once before timing. Also timed: the same groups launched eagerly."""
+    113 groups of a token are captured once as a graph (satori_hip_step) and replayed. Attention and the norms
+    are not part of the path: their outputs are fixed random vectors. q/k/v, o and gate/up quantize their FP32
+    input inside their launch; the gate/up launch also writes SwiGLU of its outputs, which down reads and
+    quantizes in its own launch, so every projection's Q8_K input is produced inside the timed step (the
+    reference's ExecuteBatch quantizes each input per call, QuantizedMatVec.cs:144-149). Also timed: the same
+    groups launched eagerly."""
     d, ffn, vocab = model.D, model.FFN, model.VOCAB
     host_in = decode_inputs(model)
     h, attn, h2, act = (model.device(host_in[k]) for k in ("h", "attn", "h2", "act"))
@@ -387,17 +389,19 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
         members += [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
     groups.append(S.HipGroup(ctx, [model.output], [h], [logits], True))
     members.append(("output",))
-    act_q8k = model.device(np.zeros(ffn // 256 * 73, np.float32))  # 292 bytes per Q8_K block
-    S.DeviceOps(ctx).quantize_q8k(act, ffn, 1, act_q8k)
     for grp, names in zip(groups, members):
-        if names == ("down",):
-            grp.set_input_q8k(act_q8k)
+        if names == ("gate", "up"):
+            grp.set_output_swiglu(act)  # SwiGLU of the gate/up outputs, in the same launch; down quantizes it
     # Parity before timing: every launch of the step, one at a time, against the oracle (checker only).
     from oracle import oracle as O
     expected = {}
     for name, (r, c, fmt) in model.shapes.items():
+        if name == "down":
+            continue
         expected[name] = O.qk_matvec_quantized_avx2(model.host[name], r, c, int(fmt),
                                                     O.q8k_quantize_row(host_in[FEEDS[name]]))
+    activated = O.swiglu(expected["gate"], expected["up"])  # down's input: SwiGLU of the gate/up outputs
+    expected["down"] = O.qk_matvec_quantized_avx2(model.host["down"], d, ffn, int(BQ.Q6_K), O.q8k_quantize_row(activated))
     for grp, names in zip(groups, members):
         for name in names:
             ctx.upload(out[name], np.full(model.shapes[name][0], np.nan, np.float32))

@@ -233,6 +233,27 @@ int satori_hip_group_execute_batch(satori_hip_group* group, int positions, void*
 #define SATORI_HIP_INPUT_Q8K 3
 int satori_hip_group_set_input(satori_hip_group* group, int kind, const float* a, const float* b,
                                const float* weights, float epsilon, float* residual_out);
+/* Output transforms: a K-format group with quantized activations of two members with the same row count, a
+ * multiple of 256 (gate, then up), can carry the SwiGlu that follows it inside its own launch:
+ *  SATORI_HIP_OUTPUT_SWIGLU: besides the members' outputs (unchanged, bit for bit), the launch writes
+ *    SwiGlu(gate output, up output) to `activated` (rows floats), exactly what satori_hip_swiglu writes from
+ *    the two outputs; each workgroup computes the same rows of both members. When `q8k` is not NULL the
+ *    launch also writes the Q8KCodec.QuantizeRow bytes of that vector there (rows / 256 * 292 bytes), as
+ *    satori_hip_swiglu_q8k does, for a down group reading them through SATORI_HIP_INPUT_Q8K: the last
+ *    workgroup to finish a run of 256 rows, found by an arrival count in a device buffer the group owns,
+ *    quantizes that run;
+ *  SATORI_HIP_OUTPUT_PLAIN: back to the members' outputs only.
+ * `activated` and `q8k` must not overlap each other, the inputs or the outputs. Combines with any input
+ * transform but SATORI_HIP_INPUT_SWIGLU. One-position launches only (satori_hip_group_execute_batch fails
+ * with SATORI_HIP_E_NOT_SUPPORTED). Not while steps replay the group (SATORI_HIP_E_ARGUMENT) or while
+ * capturing. Launches of one such group must not overlap (two streams at once): with `q8k` the arrival
+ * counts are shared, and overlapping launches leave `activated` and `q8k` undefined for those launches
+ * (later ones are unaffected). No counterpart in the reference, whose DenseForward.Step
+ * (src/Satori.Core/Model/DenseForward.cs:152-158) runs the gate and up projections, then SwiGlu, then the
+ * down projection, which quantizes its input (QuantizedMatVec.ExecuteBatch, QuantizedMatVec.cs:144-149). */
+#define SATORI_HIP_OUTPUT_PLAIN 0
+#define SATORI_HIP_OUTPUT_SWIGLU 1
+int satori_hip_group_set_output(satori_hip_group* group, int kind, float* activated, void* q8k);
 /* Fails with SATORI_HIP_E_ARGUMENT while a step replays the group. A matrix cannot be destroyed while a
  * group launches it (same status). */
 int satori_hip_group_destroy(satori_hip_group* group);

@@ -398,6 +398,18 @@ class HipGroup:
         """The group reads its creation inputs again."""
         _check(_ffi.lib().satori_hip_group_set_input(self._handle, 0, None, None, None, 0.0, None))
 
+    def set_output_swiglu(self, activated: int, q8k: int = 0) -> None:
+        """A two-member group (gate, up; equal row counts, a multiple of 256) also writes SwiGlu(gate, up) to
+        `activated` inside its launch (device pointer), bit-identical to DeviceOps.swiglu over the two outputs;
+        with `q8k`, also that vector's Q8_K bytes, as DeviceOps.swiglu_q8k writes them (a down group reads
+        them through set_input_q8k)."""
+        _check(_ffi.lib().satori_hip_group_set_output(self._handle, 1, ctypes.c_void_p(activated),
+                                                      ctypes.c_void_p(q8k or None)))
+
+    def set_output_plain(self) -> None:
+        """The group writes its members' outputs only."""
+        _check(_ffi.lib().satori_hip_group_set_output(self._handle, 0, None, None))
+
     def dispose(self) -> None:
         _check(_ffi.lib().satori_hip_group_destroy(self._handle))
 

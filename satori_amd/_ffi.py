@@ -40,6 +40,7 @@ SIGNATURES = {
     "satori_hip_group_execute": (I, [P, P]),
     "satori_hip_group_execute_batch": (I, [P, I, P]),
     "satori_hip_group_set_input": (I, [P, I, P, P, P, ctypes.c_float, P]),
+    "satori_hip_group_set_output": (I, [P, I, P, P]),
     "satori_hip_group_destroy": (I, [P]),
     "satori_hip_step_create": (I, [P, P, I, PP]),
     "satori_hip_step_execute": (I, [P, P]),

@@ -157,21 +157,28 @@ struct KintMembers {
     MatDesc m[kKintInlineMembers];
 };
 
-template <int FORMAT, int XF, bool INLINE>
+// PAIRED: a two-member launch (gate, up) whose workgroups own the same s.rows_per_wg rows of both members
+// (2 * rows_per_wg <= 64 row sums, all in the first wave), carrying SwiGlu and its Q8_K bytes on (see
+// OutputSwiGluQ8K).
+template <int FORMAT, int XF, bool INLINE, bool PAIRED>
 __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_members,
                                                               const MatDesc* __restrict__ group, LaunchShape s,
-                                                              InputTransform xf) {
+                                                              InputTransform xf, OutputSwiGluQ8K out) {
+    static_assert(!PAIRED || INLINE, "paired launches pass their two members in the kernel arguments");
     constexpr int G = 4;  // lanes per (row, block) pair
     constexpr int kBlockBytes = FORMAT == kQ4_K ? 144 : 210;
     constexpr int kPairsPerStep = kThreads / G;
     using Raw = typename std::conditional<FORMAT == kQ4_K, Q4KRaw, Q6KRaw>::type;
     // Inline members come from the kernel arguments through the scalar cache; a larger group's descriptor is
     // one global load.
-    const MatDesc m = INLINE ? inline_members.m[blockIdx.y] : group[blockIdx.y];
+    const MatDesc m = INLINE ? inline_members.m[PAIRED ? 0 : blockIdx.y] : group[blockIdx.y];
     const int tile_rows = s.rows_per_wg;
     const int row_begin = blockIdx.x * tile_rows;
     if (row_begin >= m.rows) return;
     const int rows = min(tile_rows, m.rows - row_begin);
+    // Rows of the workgroup's terms: its rows of m, then (paired) the same rows of the second member.
+    const int vrows = PAIRED ? 2 * rows : rows;
+    const int vtile = PAIRED ? 2 * tile_rows : tile_rows;
     const int position = blockIdx.z;
     const int nb = s.blocks;
     // Blocks staged at a time: the whole row when it fits the LDS, else chunks of K blocks walked in block
@@ -190,16 +197,23 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
     // current one is reduced.
     const int lane = threadIdx.x & 63;
     const int c = lane % G;
-    const uint8_t* tile = m.w + static_cast<int64_t>(row_begin) * s.row_bytes;
-    // Pair p of the chunk starting at block b0 with kb blocks: row p / kb of the tile, block b0 + p % kb.
+    const uint8_t* w1 = PAIRED ? inline_members.m[1].w : m.w;  // the second member's payload (paired)
+    // Pair p of the chunk starting at block b0 with kb blocks: row p / kb of the tile (paired: rows past
+    // `rows` are the second member's), block b0 + p % kb.
     auto load_pair = [&](int b0, int kb, int p, Raw& r) {
-        const int row = p / kb, b = b0 + p % kb;
+        int row = p / kb;
+        const int b = b0 + p % kb;
+        const uint8_t* w = m.w;
+        if (PAIRED && row >= rows) {
+            row -= rows;
+            w = w1;
+        }
         if constexpr (FORMAT == kQ4_K) {
-            q4k_load(tile + row * s.row_bytes + b * kBlockBytes, c, r);
+            q4k_load(w + static_cast<int64_t>(row_begin + row) * s.row_bytes + b * kBlockBytes, c, r);
         } else {
             // Q6_K: block b of tile row `row` is block (row_begin + row) * nb + b of the matrix.
-            q6k_load_quarter(m.w, static_cast<int64_t>(m.rows) * nb,
-                             static_cast<int64_t>(row_begin + row) * nb + b, c, r);
+            q6k_load_quarter(w, static_cast<int64_t>(m.rows) * nb, static_cast<int64_t>(row_begin + row) * nb + b,
+                             c, r);
         }
     };
     // This slot's pairs are p0, p0 + kPairsPerStep, ...; kDepth of them are loaded before the activations
@@ -208,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
     constexpr int kDepth = 3;
     const int p0 = threadIdx.x / G;
     int kb = min(K, nb);
-    int mine = p0 < rows * kb ? (rows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
+    int mine = p0 < vrows * kb ? (vrows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
     const float* xrow = m.x + static_cast<int64_t>(position) * s.columns;
     auto quad = [](const float* p, int i) {
         const u32x4 raw = load16_a4(reinterpret_cast<const uint8_t*>(p + i));
@@ -258,17 +272,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
     }
     Raw buf[kDepth];
 #pragma unroll
-    for (int i = 0; i < kDepth; ++i) load_pair(0, kb, min(p0 + i * kPairsPerStep, rows * kb - 1), buf[i]);
+    for (int i = 0; i < kDepth; ++i) load_pair(0, kb, min(p0 + i * kPairsPerStep, vrows * kb - 1), buf[i]);
 
     // Q8_K of the position's activations: one 16-lane row per block, sixteen blocks per pass. With an input
     // transform the activations are computed here from the operator's operands, in the operator's own
     // arithmetic (the RmsNorm sum of squares over the same 256-thread partition and tree, over the whole row).
     double scale = 0.0;
     // Summed RmsNorm input (residual + addend) kept in LDS after the reduction's 256 doubles.
-    float* rstage = reinterpret_cast<float*>(smem + kint_red_offset(K, tile_rows) + 2 * kThreads);
+    float* rstage = reinterpret_cast<float*>(smem + kint_red_offset(K, vtile) + 2 * kThreads);
     const bool rstaged = XF == kInputAddRmsNorm && s.columns <= kNormStageColumns;
     if constexpr (XF == kInputAddRmsNorm) {
-        double* red = reinterpret_cast<double*>(smem + kint_red_offset(K, tile_rows));
+        double* red = reinterpret_cast<double*>(smem + kint_red_offset(K, vtile));
         const bool writer = xf.residual_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
         double part = 0;
         auto term = [&](int i, float a, float b) {
@@ -406,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
             }
         }
         __syncthreads();  // the chunk's terms are in LDS
-        if (threadIdx.x < rows) {
+        if (threadIdx.x < vrows) {
             const float* t = terms + threadIdx.x * kb;
             for (int b = 0; b < kb; ++b) acc = __fadd_rn(acc, t[b]);
         }
@@ -414,12 +428,56 @@ __global__ __launch_bounds__(kThreads) void gemv_kint_kernel(KintMembers inline_
         if (b0 >= nb) break;
         // Next chunk: its first pairs' payload is requested before the LDS is released.
         kb = min(K, nb - b0);
-        mine = p0 < rows * kb ? (rows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
+        mine = p0 < vrows * kb ? (vrows * kb - 1 - p0) / kPairsPerStep + 1 : 0;
 #pragma unroll
-        for (int i = 0; i < kDepth; ++i) load_pair(b0, kb, min(p0 + i * kPairsPerStep, rows * kb - 1), buf[i]);
+        for (int i = 0; i < kDepth; ++i) load_pair(b0, kb, min(p0 + i * kPairsPerStep, vrows * kb - 1), buf[i]);
         __syncthreads();  // every thread is done with this chunk's activations and terms
     }
-    if (threadIdx.x < rows) store_f32(m.y + static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x, acc);
+    if constexpr (!PAIRED) {
+        if (threadIdx.x < rows) store_f32(m.y + static_cast<int64_t>(position) * m.rows + row_begin + threadIdx.x, acc);
+    } else if (threadIdx.x < 64) {
+        // The first wave holds every row sum: lane t < rows the first member's row row_begin + t, lane rows + t
+        // the second member's.
+        const int t = threadIdx.x;
+        if (t < vrows) store_f32((t < rows ? m.y : inline_members.m[1].y) + row_begin + (t < rows ? t : t - rows), acc);
+        const float up = __shfl(acc, (t + rows) & 63, 64);
+        const float activated = swiglu_value(acc, up);
+        if (!out.q8k) {  // SwiGlu only
+            if (t < rows) store_f32(out.activated + row_begin + t, activated);
+            return;
+        }
+        // SwiGlu of the workgroup's rows, stored as agent-scope atomics so the workgroup that quantizes the run
+        // reads them coherently from any XCD, then waited for (every store of this wave acknowledged) before
+        // this workgroup is counted in: a count the quantizer sees implies the values it reads are there.
+        if (t < rows)
+            __hip_atomic_store(out.activated + row_begin + t, activated, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint32_t seen = 0;
+        if (t == 0)
+            seen = __hip_atomic_fetch_add(out.counters + (row_begin >> 8), 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        seen = static_cast<uint32_t>(__shfl(static_cast<int>(seen), 0, 64));
+        const uint32_t arrivals = 256u / static_cast<uint32_t>(tile_rows);  // a power of two
+        if (((seen + 1u) & (arrivals - 1u)) == 0u) {
+            // The last of the run's workgroups: Q8_K of its 256 SwiGlu values (Q8KCodec.QuantizeBlock).
+            const int run = row_begin >> 8;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                v[i] = __hip_atomic_load(out.activated + 256 * run + 4 * t + i, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            const Q8KLane q = q8k_quantize_values(v, t);
+            uint8_t* dst = out.q8k + static_cast<int64_t>(run) * kQ8KBlockBytes;
+            if (q.zero) {
+                uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+                for (int i = t; i < kQ8KBlockBytes / 4; i += 64) d32[i] = 0u;
+            } else {
+                reinterpret_cast<uint32_t*>(dst + 4)[t] = q.packed;
+                if ((t & 3) == 0) reinterpret_cast<int16_t*>(dst + 260)[t >> 2] = static_cast<int16_t>(q.group_sum);
+                if (t == 0) reinterpret_cast<float*>(dst)[0] = q.scale;
+            }
+        }
+    }
 }
 
 }  // namespace
@@ -443,11 +501,14 @@ int kint_max_blocks() {
 
 namespace {
 
-template <int XF>
+template <int XF, bool PAIRED = false>
 hipError_t launch_kint(const MatDesc* members, const MatDesc* device_members, int count, LaunchShape s,
-                       const InputTransform& xf, hipStream_t stream) {
+                       const InputTransform& xf, hipStream_t stream, const OutputSwiGluQ8K& out = {}) {
     if (count <= 0 || s.rows_max <= 0 || s.positions <= 0) return hipSuccess;
     if (count > kKintInlineMembers && !device_members) return hipErrorInvalidValue;
+    if (PAIRED && (count != 2 || s.positions != 1 || s.rows_max % 256 != 0 || members[0].rows != s.rows_max ||
+                   members[1].rows != s.rows_max))
+        return hipErrorInvalidValue;
     // Rows per workgroup: 64, halved (down to 4) while the grid has fewer than 1024 workgroups and either a
     // thread slot would hold more than three (row, block) pairs (the pairs it prefetches before quantizing)
     // or the grid has fewer than 192 workgroups. Measured on the decode step's groups: q/k/v and o take 8-16
@@ -460,10 +521,13 @@ hipError_t launch_kint(const MatDesc* members, const MatDesc* device_members, in
     int tile = kTileRows;
     while (tile > 4 && groups_for(tile) < 1024 && (tile * s.blocks > 192 || groups_for(tile) < 192)) tile /= 2;
     while (tile > 4 && static_cast<int64_t>(tile) * s.row_bytes > 256 * 1024) tile /= 2;
+    // Paired: each workgroup owns `tile` rows of both members, so half the rows of the unpaired tile keep the
+    // work per workgroup and the workgroup count (at most 32 rows, so the 2 * tile row sums fit one wave).
+    if (PAIRED) tile = max(4, min(32, tile / 2));
     s.rows_per_wg = tile;
     // Rows wider than the LDS holds are staged kint_max_blocks() blocks at a time.
     s.chunk_blocks = s.blocks < kint_max_blocks() ? s.blocks : kint_max_blocks();
-    dim3 grid((s.rows_max + tile - 1) / tile, count, s.positions);
+    dim3 grid((s.rows_max + tile - 1) / tile, PAIRED ? 1 : count, s.positions);
     const size_t lds = kint_lds_bytes(s.chunk_blocks, XF == kInputAddRmsNorm ? s.columns : 0);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     KintMembers inline_members{};
@@ -472,14 +536,23 @@ hipError_t launch_kint(const MatDesc* members, const MatDesc* device_members, in
         for (int i = 0; i < count; ++i) inline_members.m[i] = members[i];
     else
         group = device_members;
+    if constexpr (PAIRED) {
+        if (s.format == kQ4_K)
+            gemv_kint_kernel<kQ4_K, XF, true, true><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf, out);
+        else if (s.format == kQ6_K)
+            gemv_kint_kernel<kQ6_K, XF, true, true><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf, out);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     if (s.format == kQ4_K && group)
-        gemv_kint_kernel<kQ4_K, XF, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
+        gemv_kint_kernel<kQ4_K, XF, false, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf, out);
     else if (s.format == kQ4_K)
-        gemv_kint_kernel<kQ4_K, XF, true><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
+        gemv_kint_kernel<kQ4_K, XF, true, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf, out);
     else if (s.format == kQ6_K && group)
-        gemv_kint_kernel<kQ6_K, XF, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
+        gemv_kint_kernel<kQ6_K, XF, false, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf, out);
     else if (s.format == kQ6_K)
-        gemv_kint_kernel<kQ6_K, XF, true><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf);
+        gemv_kint_kernel<kQ6_K, XF, true, false><<<grid, kThreads, lds, stream>>>(inline_members, group, s, xf, out);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -504,6 +577,21 @@ hipError_t launch_gemv_kint_transformed(const MatDesc* members, const MatDesc* d
             if (!xf.b) return hipErrorInvalidValue;
             return launch_kint<kInputSwiGlu>(members, device_members, count, s, xf, stream);
         case kInputQ8K: return launch_kint<kInputQ8K>(members, device_members, count, s, xf, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemv_kint_swiglu(const MatDesc* members, LaunchShape s, const InputTransform& xf,
+                                   const OutputSwiGluQ8K& out, hipStream_t stream) {
+    if (s.positions != 1 || !out.activated || (out.q8k && !out.counters)) return hipErrorInvalidValue;
+    switch (xf.kind) {
+        case kInputPlain: return launch_kint<kInputPlain, true>(members, nullptr, 2, s, xf, stream, out);
+        case kInputAddRmsNorm:
+            if (!xf.a || !xf.w) return hipErrorInvalidValue;
+            return launch_kint<kInputAddRmsNorm, true>(members, nullptr, 2, s, xf, stream, out);
+        case kInputQ8K:
+            if (!xf.a) return hipErrorInvalidValue;
+            return launch_kint<kInputQ8K, true>(members, nullptr, 2, s, xf, stream, out);
         default: return hipErrorInvalidValue;
     }
 }

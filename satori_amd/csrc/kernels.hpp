@@ -168,6 +168,21 @@ struct InputTransform {
 hipError_t launch_gemv_kint_transformed(const MatDesc* members, const MatDesc* device_members, int count,
                                         LaunchShape shape, const InputTransform& input, hipStream_t stream);
 
+// The output of a two-member one-position K launch (members[0] = gate, members[1] = up, equal row counts, a
+// multiple of 256) carried on inside it: each workgroup owns the same rows of both members, writes both
+// members' outputs as the plain launch does, and SwiGlu(gate, up) of its rows to `activated`. With `q8k`, the
+// last workgroup to finish a run of 256 rows also writes that run's Q8_K block (Q8KCodec.QuantizeBlock of the
+// SwiGlu values) there, the down projection's input; `counters` holds one arrival count per 256 rows, zeroed
+// once when the buffer is made: every launch adds exactly its arrivals per run (a power of two), so the count
+// is never reset and wraps harmlessly.
+struct OutputSwiGluQ8K {
+    float* activated;
+    uint8_t* q8k;
+    uint32_t* counters;
+};
+hipError_t launch_gemv_kint_swiglu(const MatDesc* members, LaunchShape shape, const InputTransform& input,
+                                   const OutputSwiGluQ8K& output, hipStream_t stream);
+
 // Integer K-format product (Q4_K or Q6_K) over `positions` positions on the matrix cores: quantizes the FP32
 // activations x ([positions][blocks * 256]) to Q8_K into `workspace` (kmfma_workspace_bytes), then the
 // product; outputs bit-exact with launch_gemv_kint's. Used from kmfma_min_positions() positions on. `w` is

@@ -128,6 +128,8 @@ struct satori_hip_group {
     std::vector<satori::MatDesc> host;         // the same descriptors on the host
     satori::DeviceBuffer batch;                // K groups: packed Q8_K activations of many-position calls
     satori::InputTransform input{};            // K groups: input computed in the launch (kInputPlain: read x)
+    satori::OutputSwiGluQ8K output{};          // gate/up K groups: SwiGlu and its Q8_K bytes carried on (or none)
+    satori::DeviceBuffer counters;             // the arrival counts of `output` (one per 256 rows)
     satori::T2Plan plan{};                     // Ternary2 groups
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
     uint32_t t2_generation = 0;                // the last Ternary2 launch's tag in the scratch's exchange slots
@@ -523,7 +525,9 @@ void host_matvec(satori_hip_matrix* m, const float* input, size_t input_length, 
 void enqueue_group(satori_hip_group* g, hipStream_t st) {
     const LaunchShape l = launch_shape(g->shape, 1, g->rows_max);
     const MatDesc none{};
-    if (g->quantized && g->input.kind != kInputPlain) {
+    if (g->quantized && g->output.activated) {
+        check_hip(launch_gemv_kint_swiglu(g->host.data(), l, g->input, g->output, st), "integer gemv launch");
+    } else if (g->quantized && g->input.kind != kInputPlain) {
         check_hip(launch_gemv_kint_transformed(g->host.data(), g->descriptors, g->count, l, g->input, st),
                   "integer gemv launch");
     } else if (g->quantized) {
@@ -544,6 +548,8 @@ void enqueue_group_batch(satori_hip_group* g, int positions, hipStream_t st) {
     const Shape& s = g->shape;
     if (g->input.kind != kInputPlain)
         fail(SATORI_HIP_E_NOT_SUPPORTED, "An input transform applies to one-position group launches only.");
+    if (g->output.activated)
+        fail(SATORI_HIP_E_NOT_SUPPORTED, "An output transform applies to one-position group launches only.");
     if (positions < kmfma_min_positions()) {
         check_hip(launch_gemv_kint(g->host.data(), g->descriptors, g->count, launch_shape(s, positions, g->rows_max), st),
                   "integer gemv launch");
@@ -1208,6 +1214,8 @@ int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, co
             case SATORI_HIP_INPUT_SWIGLU:
                 require(a, "a");
                 require(b, "b");
+                if (g->output.activated)
+                    fail(SATORI_HIP_E_NOT_SUPPORTED, "The SwiGlu input transform does not combine with the SwiGlu output.");
                 break;
             case SATORI_HIP_INPUT_Q8K:
                 require(a, "a");
@@ -1234,6 +1242,53 @@ int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, co
     });
 }
 
+int satori_hip_group_set_output(satori_hip_group* g, int kind, float* activated, void* q8k) {
+    return guarded([&] {
+        require(g, "group");
+        satori_hip_context* c = g->context;
+        std::lock_guard<std::mutex> guard(c->lock);
+        if (!g->live || !c->live) fail(SATORI_HIP_E_OBJECT_DISPOSED, "Cannot access a disposed object. Object name: 'satori_hip_group'.");
+        require_not_capturing(c);
+        if (g->steps > 0) fail(SATORI_HIP_E_ARGUMENT, "Steps that replay the group must be destroyed first.");
+        if (kind == SATORI_HIP_OUTPUT_PLAIN) {
+            set_device(c);
+            check_hip(hipStreamSynchronize(c->stream), "stream");  // no launch still counts into the buffer
+            g->output = OutputSwiGluQ8K{};
+            g->counters.release();
+            return;
+        }
+        if (kind != SATORI_HIP_OUTPUT_SWIGLU) fail(SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE, "Unknown output transform.");
+        if (!g->quantized)
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "Output transforms apply to K-format groups with quantized activations.");
+        require(activated, "activated");
+        if (g->count != 2 || g->host[0].rows != g->host[1].rows)
+            fail(SATORI_HIP_E_ARGUMENT, "The SwiGlu output needs two members (gate, up) with the same row count.");
+        if (g->input.kind == kInputSwiGlu)
+            fail(SATORI_HIP_E_NOT_SUPPORTED, "The SwiGlu output does not combine with the SwiGlu input transform.");
+        const int rows = g->host[0].rows;
+        if (rows % 256 != 0)
+            fail(SATORI_HIP_E_ARGUMENT, "The SwiGlu output is quantized to Q8_K: the row count must be a multiple of 256.");
+        const size_t act_bytes = static_cast<size_t>(rows) * sizeof(float);
+        const size_t q_bytes = q8k ? static_cast<size_t>(rows / 256) * kQ8KBlockBytes : 0;
+        const size_t in_bytes = static_cast<size_t>(g->shape.columns) * sizeof(float);
+        bool clash = overlaps(activated, act_bytes, q8k, q_bytes);
+        for (const MatDesc& d : g->host)
+            clash = clash || overlaps(activated, act_bytes, d.y, act_bytes) || overlaps(q8k, q_bytes, d.y, act_bytes) ||
+                    overlaps(activated, act_bytes, d.x, in_bytes) || overlaps(q8k, q_bytes, d.x, in_bytes);
+        if (clash) fail(SATORI_HIP_E_ARGUMENT, "activated and q8k must not overlap each other, the inputs or the outputs.");
+        set_device(c);
+        check_hip(hipStreamSynchronize(c->stream), "stream");
+        if (q8k) {
+            g->counters.reserve(static_cast<size_t>(rows / 256) * sizeof(uint32_t));
+            check_hip(hipMemset(g->counters.ptr, 0, g->counters.bytes), "counter clear");
+        } else {
+            g->counters.release();
+        }
+        g->output = OutputSwiGluQ8K{activated, static_cast<uint8_t*>(q8k),
+                                    q8k ? static_cast<uint32_t*>(g->counters.ptr) : nullptr};
+    });
+}
+
 int satori_hip_group_destroy(satori_hip_group* g) {
     return guarded([&] {
         if (!g) return;
@@ -1253,6 +1308,8 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         if (g->scratch) (void)hipFree(g->scratch);
         g->scratch = nullptr;
         g->batch.release();
+        g->counters.release();
+        g->output = OutputSwiGluQ8K{};
         g->live = false;
     });
 }

@@ -15,9 +15,10 @@ alternates between two buffers, since the launch that writes it is also read by 
 attention inputs run inside the split attention, and the add + RmsNorm before the output projection, whose
 launch has 2,374 workgroups, is one single-workgroup launch that also writes the Q8_K bytes the projection
 reads (computed in each of its workgroups it costs more than the launch; for gate/up, with 560 workgroups,
-the fold measured faster). SwiGlu likewise writes the Q8_K bytes of its output for the down projection
-(folded into down, every workgroup would evaluate the FP64 exponentials of the whole 8960-wide vector:
-measured 2.12 ms per token that way). Again bit-identical results.
+the fold measured faster). SwiGlu is carried by the gate/up launch itself (its workgroups own the same rows
+of gate and up), and the down projection quantizes that vector in its own launch (folded into down instead,
+every down workgroup would evaluate the FP64 exponentials of the whole 8960-wide vector: measured 2.12 ms per
+token that way). Again bit-identical results.
 """
 from __future__ import annotations
 
@@ -118,8 +119,9 @@ class DeviceDecoder:
     def _folded_groups(self):
         """Per layer the q/k/v group reading RmsNorm(residual + previous down output) (layer 0: RmsNorm of the
         embedding row) and writing the sum to the second residual buffer, the gate/up group reading
-        RmsNorm(second residual + o output) and writing the sum back, and the down group reading the Q8_K bytes
-        of SwiGlu; then the output group reading the Q8_K bytes of RmsNorm(residual + last down output)."""
+        RmsNorm(second residual + o output), writing the sum back and carrying SwiGlu, and the down group
+        reading that vector; then the output group reading the Q8_K bytes of RmsNorm(residual + last down
+        output)."""
         if self._folded is None:
             c, ctx = self.cfg, self.ctx
             folded = []
@@ -129,8 +131,8 @@ class DeviceDecoder:
                 qkv.set_input_add_rms_norm(read, self.projected if layer else 0, vec["attn_norm"], c.epsilon, written)
                 gateup = HipGroup(ctx, [m["gate"], m["up"]], [self.normed] * 2, [self.gate, self.up], True)
                 gateup.set_input_add_rms_norm(written, self.projected, vec["ffn_norm"], c.epsilon, read)
+                gateup.set_output_swiglu(self.activated)
                 down = HipGroup(ctx, [m["down"]], [self.activated], [self.projected], True)
-                down.set_input_q8k(self.activated_q8k)
                 folded.append({"qkv": qkv, "gateup": gateup, "down": down})
             final = HipGroup(ctx, [self.output], [self.normed], [self.logits], True)
             final.set_input_q8k(self.normed_q8k)
@@ -155,8 +157,7 @@ class DeviceDecoder:
                                      vec.get("v_bias", 0), self.keys[layer], self.values[layer], c.heads, c.kv_heads,
                                      c.head_dim, position, c.rope_base, c.head_dim, self.context_vec, self.rope)
                 g["o"].execute()
-                fg["gateup"].execute()
-                ops.swiglu_q8k(self.gate, self.up, c.ffn, 0, self.activated_q8k)
+                fg["gateup"].execute()  # also SwiGlu
                 fg["down"].execute()
             ops.add_rms_norm_q8k(self.residual, self.projected, self.output_norm, c.epsilon, c.hidden, self.normed,
                                  self.normed_q8k)
@@ -207,9 +208,9 @@ class DeviceDecoder:
         over several workgroups per head and combined by a second kernel, one more launch per layer."""
         split = position is not None and position + 1 > 32
         extra = len(self.layers) if split else 0
-        if folded:  # q/k/v, the decode attention, o, gate/up, SwiGlu to Q8_K, down; add + RmsNorm to Q8_K, output
+        if folded:  # q/k/v, the decode attention, o, gate/up (and SwiGlu), down; add + RmsNorm to Q8_K, output
             attention = decode_attention_launches(position + 1 if position is not None else 1, self.cfg.head_dim)
-            return 1 + (5 + attention) * len(self.layers) + 2
+            return 1 + (4 + attention) * len(self.layers) + 2
         if fused:
             return 2 + 9 * len(self.layers) + 1 + extra
         per_layer = 14 if all("q_bias" in v for v in self.vectors) else 13

@@ -1636,6 +1636,176 @@ def test_q8k_input_from_the_producer_equals_quantizing_in_the_launch(context, fm
             m.dispose()
 
 
+@pytest.mark.parametrize("fmt,rows,columns,transform,with_q8k", [
+    (BQ.Q4_K, 8960, 1536, "add_rms_norm", True),  # the decode step's gate/up (16 rows per workgroup)
+    (BQ.Q4_K, 8960, 1536, "add_rms_norm", False),
+    (BQ.Q4_K, 8960, 1536, "plain", True),
+    (BQ.Q6_K, 1280, 1536, "q8k", True),
+    (BQ.Q6_K, 1280, 1536, "q8k", False),
+    (BQ.Q4_K, 256, 1536, "plain", True),          # one run of 256 rows, 4 rows per workgroup (64 arrivals)
+    (BQ.Q6_K, 512, 29696, "plain", True),         # input staged in chunks of blocks
+])
+def test_gate_up_group_carrying_swiglu(context, fmt, rows, columns, transform, with_q8k):
+    # A gate/up group with the SwiGlu output (satori_hip_group_set_output): the members' outputs equal the
+    # plain group's bit for bit, `activated` is the oracle's SwiGlu of those outputs and (with q8k) `q8k` its
+    # Q8KCodec.QuantizeRow bytes, on repeated launches (the arrival counts carry over) and in a captured step
+    # replayed several times with new inputs between replays. Rows 256..511 of `up` are zero, so that run's
+    # SwiGlu values are all zeros (the all-zero Q8_K block).
+    g = rng(4242 + rows + columns + int(fmt))
+    wg = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    wu = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+    if rows >= 512:
+        wu[256:512] = 0.0
+    mats = [context.create(S.quantize_weights(w, rows, columns, fmt), S.QuantizedMatrixShape(rows, columns, fmt))
+            for w in (wg, wu)]
+    buffers = []
+
+    def dev(arr):
+        p = context.alloc(arr.nbytes)
+        context.upload(p, arr)
+        buffers.append(p)
+        return p
+
+    q8k_bytes = rows // 256 * 292
+    dx = dev(np.zeros(columns, np.float32))
+    da, db, dw = (dev(np.zeros(columns, np.float32)) for _ in range(3))
+    dres = dev(np.zeros(columns, np.float32))
+    dq_in = dev(np.zeros(columns // 256 * 73, np.float32))
+    plain_out = [dev(np.zeros(rows, np.float32)) for _ in range(2)]
+    paired_out = [dev(np.zeros(rows, np.float32)) for _ in range(2)]
+    dact = dev(np.zeros(rows, np.float32))
+    dq = dev(np.zeros(q8k_bytes // 4, np.float32))
+    ops = S.DeviceOps(context)
+    plain = S.HipGroup(context, mats, [dx, dx], plain_out, True)
+    paired = S.HipGroup(context, mats, [dx, dx], paired_out, True)
+    step = None
+    try:
+        if transform == "add_rms_norm":
+            paired.set_input_add_rms_norm(da, db, dw, 1e-6, dres)
+        elif transform == "q8k":
+            paired.set_input_q8k(dq_in)
+        paired.set_output_swiglu(dact, dq if with_q8k else 0)
+
+        def feed(seed):
+            # New operands; x is what the plain group reads (the operator's output for the transforms).
+            h = rng(seed)
+            a, b = h.standard_normal(columns).astype(np.float32), h.standard_normal(columns).astype(np.float32)
+            w = h.uniform(0.5, 1.5, columns).astype(np.float32)
+            for p, v in ((da, a), (db, b), (dw, w)):
+                context.upload(p, v)
+            if transform == "add_rms_norm":
+                dsum = dev(a.copy())
+                ops.add_rms_norm(dsum, db, dw, 1e-6, columns, dx)
+            else:
+                context.upload(dx, a)
+                if transform == "q8k":
+                    context.upload(dq_in, O.q8k_quantize_row(a).view(np.float32))
+            context.upload(dact, np.full(rows, np.nan, np.float32))
+            context.upload(dq, np.full(q8k_bytes // 4, np.nan, np.float32))
+            plain.execute()
+
+        def check(tag):
+            outs = []
+            for k in range(2):
+                want = context.download(np.zeros(rows, np.float32), plain_out[k])
+                got = context.download(np.zeros(rows, np.float32), paired_out[k])
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{tag}: member {k}"
+                outs.append(want)
+            act = O.swiglu(outs[0], outs[1])
+            got_act = context.download(np.zeros(rows, np.float32), dact)
+            assert np.array_equal(got_act.view(np.uint32), act.view(np.uint32)), f"{tag}: SwiGlu"
+            got_q = context.download(np.zeros(q8k_bytes, np.uint8), dq)
+            if not with_q8k:
+                assert np.isnan(got_q.view(np.float32)).all(), f"{tag}: q8k written without being asked for"
+                return
+            assert np.array_equal(got_q, O.q8k_quantize_row(act)), f"{tag}: Q8_K bytes"
+            if rows >= 512:
+                assert not got_q[292:584].any(), f"{tag}: the zero run"
+
+        for seed in (1, 2, 3):  # repeated launches
+            feed(seed)
+            paired.execute()
+            check(f"launch {seed}")
+        step = S.HipStep(context, [paired])
+        for seed in (4, 5, 6):  # graph replays, eager work between them
+            feed(seed)
+            step.execute()
+            check(f"replay {seed}")
+        with pytest.raises(S.NotSupportedException):
+            paired.execute_batch(16)
+    finally:
+        if step is not None:
+            step.dispose()
+        plain.dispose()
+        paired.dispose()
+        for p in buffers:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
+def test_swiglu_output_argument_checks(context):
+    # The SwiGlu output's preconditions: two K members with equal row counts, a multiple of 256, quantized
+    # activations, no overlap, no SwiGlu input transform; SATORI_HIP_OUTPUT_PLAIN restores the plain launch.
+    g = rng(77)
+    columns = 1536
+
+    def mat(rows, fmt=BQ.Q4_K):
+        w = (g.standard_normal((rows, columns)) * 0.02).astype(np.float32)
+        return context.create(S.quantize_weights(w, rows, columns, fmt), S.QuantizedMatrixShape(rows, columns, fmt))
+
+    mats = [mat(512), mat(512), mat(384), mat(300), mat(300)]
+    buffers = []
+
+    def dev(n):
+        p = context.alloc(4 * n)
+        context.upload(p, np.zeros(n, np.float32))
+        buffers.append(p)
+        return p
+
+    dx, dact, dq = dev(columns), dev(512), dev(2 * 73)
+    ys = [dev(512) for _ in range(4)]
+    groups = []
+    try:
+        def group(ms, quantized=True):
+            grp = S.HipGroup(context, ms, [dx] * len(ms), ys[:len(ms)], quantized)
+            groups.append(grp)
+            return grp
+
+        good = group(mats[:2])
+        with pytest.raises(S.ArgumentException):  # three members
+            group(mats[:3]).set_output_swiglu(dact, dq)
+        with pytest.raises(S.ArgumentException):  # different row counts
+            group([mats[0], mats[2]]).set_output_swiglu(dact, dq)
+        with pytest.raises(S.ArgumentException):  # rows not a multiple of 256
+            group(mats[3:5]).set_output_swiglu(dact, dq)
+        with pytest.raises(S.NotSupportedException):  # FP32-activation group
+            group(mats[:2], False).set_output_swiglu(dact, dq)
+        with pytest.raises(S.ArgumentException):  # activated overlaps an output
+            good.set_output_swiglu(ys[0], dq)
+        with pytest.raises(S.ArgumentException):  # q8k overlaps the input
+            good.set_output_swiglu(dact, dx)
+        with pytest.raises(S.ArgumentNullException):
+            good.set_output_swiglu(0, dq)
+        with pytest.raises(S.ArgumentOutOfRangeException):
+            _check_status(S._ffi.lib().satori_hip_group_set_output(good._handle, 7, None, None))
+        good.set_output_swiglu(dact)  # SwiGlu without its Q8_K bytes
+        good.set_output_swiglu(dact, dq)
+        with pytest.raises(S.NotSupportedException):
+            good.set_input_swiglu(dx, dx)
+        good.set_output_plain()
+        good.set_input_swiglu(dx, dx)
+        with pytest.raises(S.NotSupportedException):
+            good.set_output_swiglu(dact, dq)
+    finally:
+        for grp in groups:
+            grp.dispose()
+        for p in buffers:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
 @pytest.mark.parametrize("columns", [1536, 8960, 12288, 16384])
 def test_add_rms_norm_q8k_equals_add_rms_norm_then_quantizer(context, columns):
     # satori_hip_add_rms_norm_q8k: residual, normed and the Q8_K bytes equal satori_hip_add_rms_norm followed
@@ -1797,7 +1967,7 @@ def test_device_decode_token_matches_host_composition(context):
         dec.enqueue(7, 41, folded=True)  # eager work between replays
         folded.execute()
         assert np.array_equal(dec.read_logits().view(np.uint32), eager.view(np.uint32)), ("folded", replay)
-    assert dec.launches_per_token(folded=True, position=position) == 3 + 7 * n_layers  # inputs inside the attention
+    assert dec.launches_per_token(folded=True, position=position) == 3 + 6 * n_layers  # inputs inside the attention
     with pytest.raises(S.ArgumentException):
         dev_layers[0]["q"].dispose()  # held by the decoder's group
     with pytest.raises(S.InvalidOperationException):
