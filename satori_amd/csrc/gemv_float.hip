@@ -42,8 +42,10 @@ struct Q8_0Chunk {
         uint32_t q[8];
         uint32_t scale;  // FP16 bits, converted where the dot uses them (not at the load, which would wait)
     };
+    static constexpr int kSums = 0;
     struct Consts {};
-    __device__ static Consts consts() { return Consts{}; }
+    __device__ static Consts consts(int) { return Consts{}; }
+    __device__ static void sums(const float (&)[kWeights], float (&)[1]) {}
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
     // Regrouped device layout: 32-byte code records, then the FP16 scales. A row's records and scales start
@@ -70,7 +72,7 @@ struct Q8_0Chunk {
 #pragma unroll
         for (int j = 0; j < kWeights; j += 4) xf.quad(32 * chunk + j, x + j);
     }
-    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const float (&)[1], const Consts&) {
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
@@ -103,8 +105,10 @@ struct Q4_0Chunk {
         uint32_t q[4];
         uint32_t scale;  // FP16 bits, converted where the dot uses them (not at the load, which would wait)
     };
+    static constexpr int kSums = 0;
     struct Consts {};
-    __device__ static Consts consts() { return Consts{}; }
+    __device__ static Consts consts(int) { return Consts{}; }
+    __device__ static void sums(const float (&)[kWeights], float (&)[1]) {}
     __device__ static int chunks(const LaunchShape& s) { return s.blocks; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
     // Regrouped device layout: 16-byte code records (bytes XOR 0x88), then the FP16 scales.
@@ -129,7 +133,7 @@ struct Q4_0Chunk {
 #pragma unroll
         for (int j = 0; j < kWeights; j += 4) xf.quad(32 * chunk + j, x + j);
     }
-    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const float (&)[1], const Consts&) {
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -151,7 +155,14 @@ struct Q4_0Chunk {
 // f16 d @0, f16 dmin @2, 6-bit scales/mins @4..15 (Q4KCodec.GetScaleMin, :24-36), nibbles @16.
 // Chunk k of a block (k = 0..7) is qs[16k .. 16k + 16): low nibbles are weights 64g + 16h + i of
 // sub-block 2g, high nibbles weights 64g + 32 + 16h + i of sub-block 2g + 1 (g = k / 2, h = k % 2).
-// The weight d*s*q - dmin*m is one FMA.
+// The chunk's dot is factored per sub-block half: sum (d s q - dmin m) x = (d s) sum q x - (dmin m) sum x,
+// so a weight costs one conversion and one FMA; the two sums of 16 activations (low and high half) are the
+// same for every row and are computed once per workgroup (Sums). The high nibbles are used in place (the
+// bytes 16 q) and the factor 16 is removed with the power-of-two 1/16. A chunk's position k within its
+// block is the same for all of a lane's chunks (k = chunk % 8, and a row's lanes step by a multiple of 8),
+// so the scale and min fields a lane reads are fixed per lane (Consts).
+// Non-finite activations: a product whose decoded weight is nonzero but whose code is 0 comes out NaN here
+// where the reference's w * x gives +-Inf; the GGUF MatVec surface rejects non-finite inputs.
 // ------------------------------------------------------------------------------------------------
 
 struct Q4_KChunk {
@@ -160,13 +171,26 @@ struct Q4_KChunk {
     static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 32;
     static constexpr int kPadShift = 6;
+    static constexpr int kSums = 2;  // sum of the low-nibble half's 16 activations, of the high half's
     struct Regs {
         u32x4 head;
         u32x4 qs;
-        int g;
     };
-    struct Consts {};
-    __device__ static Consts consts() { return Consts{}; }
+    // Bit offsets of the 6-bit scale and min of sub-blocks 2g and 2g + 1 (GetScaleMin): for g < 2 they are
+    // bytes 2g, 2g + 1 of scales[0..3] / scales[4..7]; for g >= 2 their low 4 bits are the nibbles of
+    // scales[8 + 2(g - 2)], [9 + 2(g - 2)] and their high 2 bits the top bits of scales[2(g - 2)], ... .
+    struct Consts {
+        bool high;              // g >= 2: low bits from dword 3
+        uint32_t scale_lo;      // offset of the scale's low 4 bits (in dword 1, or 3 when high)
+        uint32_t min_lo;        // offset of the min's low 4 bits (in dword 2, or 3 when high)
+        uint32_t top;           // offset of the 2 high bits (scale: dword 1, min: dword 2)
+    };
+    __device__ static Consts consts(int chunk) {
+        const int g = (chunk & 7) >> 1;
+        if (g < 2) return Consts{false, 16u * g, 16u * g, 16u * g + 4};
+        const uint32_t o = 16u * (g - 2);
+        return Consts{true, o, o + 4, o + 6};
+    }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks * 8; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
     using Row = const uint8_t*;  // the row's first block
@@ -177,7 +201,6 @@ struct Q4_KChunk {
         const uint8_t* block = w + (chunk >> 3) * 144;
         r.head = load16_a4(block);
         r.qs = load16_a4(block + 16 + 16 * (chunk & 7));
-        r.g = (chunk & 7) >> 1;
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
@@ -188,26 +211,47 @@ struct Q4_KChunk {
             xf.quad(base + 32 + i, x + 16 + i);
         }
     }
-    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
+    // The chunk's activation sums from its loaded activations (pairwise).
+    __device__ static void sums(const float (&x)[kWeights], float (&out)[kSums]) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            float t[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t[i] = x[16 * half + i] + x[16 * half + 8 + i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t[i] += t[i + 4];
+            out[half] = (t[0] + t[2]) + (t[1] + t[3]);
+        }
+    }
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const float (&xs)[kSums],
+                                const Consts& k) {
         const float d = half_bits_to_float(r.head[0] & 0xFFFFu);
         const float dmin = half_bits_to_float(r.head[0] >> 16);
-        int s0, m0, s1, m1;
-        q4k_scale_min(2 * r.g, r.head, s0, m0);
-        q4k_scale_min(2 * r.g + 1, r.head, s1, m1);
-        const float dl = d * static_cast<float>(s0), ml = dmin * static_cast<float>(m0);
-        const float dh = d * static_cast<float>(s1), mh = dmin * static_cast<float>(m1);
-        float acc0 = 0.0f, acc1 = 0.0f;
+        const uint32_t ls = k.high ? r.head[3] : r.head[1], lm = k.high ? r.head[3] : r.head[2];
+        const uint32_t s0 = __builtin_amdgcn_ubfe(ls, k.scale_lo, 4) | (__builtin_amdgcn_ubfe(r.head[1], k.top, 2) << 4);
+        const uint32_t s1 = __builtin_amdgcn_ubfe(ls, k.scale_lo + 8, 4) |
+                            (__builtin_amdgcn_ubfe(r.head[1], k.top + 8, 2) << 4);
+        const uint32_t m0 = __builtin_amdgcn_ubfe(lm, k.min_lo, 4) | (__builtin_amdgcn_ubfe(r.head[2], k.top, 2) << 4);
+        const uint32_t m1 = __builtin_amdgcn_ubfe(lm, k.min_lo + 8, 4) |
+                            (__builtin_amdgcn_ubfe(r.head[2], k.top + 8, 2) << 4);
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const uint32_t lo = r.qs[w] & 0x0F0F0F0Fu;
-            const uint32_t hi = (r.qs[w] >> 4) & 0x0F0F0F0Fu;
+            // Bytes q and bytes 16 q, each converted by one byte-select conversion: the empty asm keeps the
+            // compiler from folding the mask into a bit-field extract per weight (two instructions a weight).
+            uint32_t lo = r.qs[w] & 0x0F0F0F0Fu, hi = r.qs[w] & 0xF0F0F0F0u;
+            asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc0 = __builtin_fmaf(__builtin_fmaf(dl, byte_to_float(lo, i), -ml), x[4 * w + i], acc0);
-                acc1 = __builtin_fmaf(__builtin_fmaf(dh, byte_to_float(hi, i), -mh), x[16 + 4 * w + i], acc1);
+            for (int i = 0; i < 4; i += 2) {
+                a0 = __builtin_fmaf(byte_to_float(lo, i), x[4 * w + i], a0);
+                a1 = __builtin_fmaf(byte_to_float(lo, i + 1), x[4 * w + i + 1], a1);
+                b0 = __builtin_fmaf(byte_to_float(hi, i), x[16 + 4 * w + i], b0);
+                b1 = __builtin_fmaf(byte_to_float(hi, i + 1), x[16 + 4 * w + i + 1], b1);
             }
         }
-        return acc0 + acc1;
+        const float dl = d * static_cast<float>(s0), dh = (d * static_cast<float>(s1)) * 0.0625f;
+        const float ml = dmin * static_cast<float>(m0), mh = dmin * static_cast<float>(m1);
+        return __builtin_fmaf(dl, a0 + a1, __builtin_fmaf(dh, b0 + b1, -__builtin_fmaf(ml, xs[0], mh * xs[1])));
     }
 };
 
@@ -215,8 +259,11 @@ struct Q4_KChunk {
 // Q6_K, FP32 activations (Q6KCodec.DotBlock, src/Satori.Core/Q6KCodec.cs:22-51): 210-byte super-block,
 // ql[128] @0, qh[64] @128, int8 scales[16] @192, f16 d @208, read from the regrouped device layout
 // (Q6KLayout). Chunk = quarter c = 2h + t of a block: l in [16t, 16t + 16) for all four k, i.e. weights
-// 128h + 32k + l with scale 8h + 2k + t. Weight d*sc*(q - 32) is fma(d*sc, q, -32*d*sc), the same single
-// rounding of the same product as the reference's (d*sc)*(q-32) since 32*d*sc is exact.
+// 128h + 32k + l with scale 8h + 2k + t. Weight d * sc * (q - 32): the chunk's dot is sum over k of
+// (d * sc_k / 4) * sum 4 (q - 32) x. Each code byte is assembled as the signed byte 4 (q - 32) (the 6-bit
+// q ^ 32, i.e. q - 32 in 6-bit two's complement, in the byte's top six bits; the flip of q's bit 5 is one XOR
+// on the high-bit dword for all four k), so a weight costs one signed-byte conversion and one FMA, exact
+// products of the reference's integer (q - 32) with x up to the factor 4 removed with the scale.
 // ------------------------------------------------------------------------------------------------
 struct Q6_KChunk {
     static constexpr int kRowUnroll = 1;
@@ -224,9 +271,10 @@ struct Q6_KChunk {
     static constexpr int kMaxWorkgroupPayload = 0;
     static constexpr int kWeights = 64;
     static constexpr int kPadShift = 7;
+    static constexpr int kSums = 0;
     using Regs = Q6KQuarter;
     struct Consts {};
-    __device__ static Consts consts() { return Consts{}; }
+    __device__ static Consts consts(int) { return Consts{}; }
     __device__ static int chunks(const LaunchShape& s) { return s.blocks * 4; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
     struct Row {
@@ -247,39 +295,41 @@ struct Q6_KChunk {
 #pragma unroll
             for (int i = 0; i < 16; i += 4) xf.quad(base + 32 * k + i, x + 16 * k + i);
     }
-    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const Consts&) {
-        float ds[4], bias[4];
-        const float d = q6k_d(r);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int8_t s = static_cast<int8_t>(r.sc >> (8 * k));  // scale 8h + 2k + t
-            ds[k] = d * static_cast<float>(s);
-            bias[k] = -32.0f * ds[k];
-        }
-        float acc0 = 0.0f, acc1 = 0.0f;
+    __device__ static void sums(const float (&)[kWeights], float (&)[1]) {}
+    __device__ static float dot(const Regs& r, const float (&x)[kWeights], const float (&)[1], const Consts&) {
+        float acc[4][2] = {};
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const uint32_t a = r.qla[w], b = r.qlb[w], h = r.qh[w];
+            const uint32_t a = r.qla[w], b = r.qlb[w];
+            const uint32_t h = r.qh[w] ^ 0xAAAAAAAAu;  // bit 1 of each 2-bit field (q's bit 5) flipped
             const uint32_t q[4] = {
-                (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u),
-                (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u),
-                ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u),
-                ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u),
-            };
+                ((a << 2) & 0x3C3C3C3Cu) | ((h << 6) & 0xC0C0C0C0u),
+                ((b << 2) & 0x3C3C3C3Cu) | ((h << 4) & 0xC0C0C0C0u),
+                ((a >> 2) & 0x3C3C3C3Cu) | ((h << 2) & 0xC0C0C0C0u),
+                ((b >> 2) & 0x3C3C3C3Cu) | (h & 0xC0C0C0C0u),
+            };  // bytes 4 (q - 32)
 #pragma unroll
             for (int k = 0; k < 4; ++k)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float weight = __builtin_fmaf(ds[k], byte_to_float(q[k], i), bias[k]);
-                    if (i & 1)
-                        acc1 = __builtin_fmaf(weight, x[16 * k + 4 * w + i], acc1);
-                    else
-                        acc0 = __builtin_fmaf(weight, x[16 * k + 4 * w + i], acc0);
-                }
+                for (int i = 0; i < 4; ++i)
+                    acc[k][i & 1] = __builtin_fmaf(sbyte_to_float(q[k], i), x[16 * k + 4 * w + i], acc[k][i & 1]);
         }
-        return acc0 + acc1;
+        const float d4 = q6k_d(r) * 0.25f;
+        float total = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float s = static_cast<float>(static_cast<int8_t>(r.sc >> (8 * k)));  // scale 8h + 2k + t
+            total = __builtin_fmaf(d4 * s, acc[k][0] + acc[k][1], total);
+        }
+        return total;
     }
 };
+
+// Floats of the staged activation copy (element i at i + 4 * (i >> PAD)), before the per-chunk sums.
+template <class F>
+__host__ __device__ inline int staged_floats(int padded) {
+    return padded + 4 * (padded >> F::kPadShift) + 4;
+}
 
 // Reads of the activations by aligned quads (i % 4 == 0): one 16-byte LDS read of the staged copy (element i
 // at i + 4 * (i >> PAD), so a quad stays contiguous and the quads of neighbouring lanes, 32, 64 or 128
@@ -344,19 +394,50 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
     const int sub = lane / L;
     const int lr = lane % L;
     const int nchunks = F::chunks(s);
-    const typename F::Consts k = F::consts();
+    // Per-lane constants: a lane's chunks all sit at the same position within their block (L is a multiple of
+    // the chunks per block, 8 or 4, or the row has a single pass).
+    const typename F::Consts k = F::consts(lr);
     const int first = row_begin + wave * kRowsPerPass;  // wave-uniform
 
+    // Formats that factor their dot need per-chunk sums of the activations (F::kSums per chunk): with staged
+    // activations and several chunks per lane they are computed once per workgroup into a table after the
+    // staged copy; otherwise from the loaded activations.
+    constexpr int kS = F::kSums > 0 ? F::kSums : 1;
+    constexpr bool kTable = !ONE && XLDS && F::kSums > 0;
+    float* xsum_table = xs + staged_floats<F>(F::padded_columns(s));
+    if constexpr (kTable) {
+        for (int c = threadIdx.x; c < nchunks; c += THREADS) {
+            float t[F::kWeights], o[kS];
+            F::load_x(xf, c, t);
+            F::sums(t, o);
+#pragma unroll
+            for (int j = 0; j < kS; ++j) xsum_table[kS * c + j] = o[j];
+        }
+        __syncthreads();
+    }
     float xr[F::kWeights];
+    float xsv[kS];
+    // The activations of chunk c (and their sums).
+    auto load_chunk = [&](int c) {
+        F::load_x(xf, c, xr);
+        if constexpr (kTable) {
+#pragma unroll
+            for (int j = 0; j < kS; ++j) xsv[j] = xsum_table[kS * c + j];
+        } else if constexpr (F::kSums > 0) {
+            F::sums(xr, xsv);
+        }
+    };
     if constexpr (ONE) {
         // Each lane owns one chunk of every row: its activations stay in registers, and the next
         // iteration's rows are loaded while the current ones are computed.
         const bool active = lr < nchunks;
         if (active) {
-            F::load_x(xf, lr, xr);
+            load_chunk(lr);
         } else {
 #pragma unroll
             for (int j = 0; j < F::kWeights; ++j) xr[j] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kS; ++j) xsv[j] = 0.0f;
         }
         typename F::Regs cur[kRowUnroll], nxt[kRowUnroll];
 #pragma unroll
@@ -373,7 +454,7 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) {
                 const int row = base + u * kStride + sub;
-                const float partial = (active && row < row_end) ? F::dot(cur[u], xr, k) : 0.0f;
+                const float partial = (active && row < row_end) ? F::dot(cur[u], xr, xsv, k) : 0.0f;
                 const float total = group_sum_last<L>(partial);
                 if (lr == L - 1 && row < row_end) store_f32(y + row, total);
             }
@@ -408,12 +489,12 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
                 };
                 auto dot_pair = [&](int cc, const typename F::Regs (&r0)[kRowUnroll],
                                     const typename F::Regs (&r1)[kRowUnroll]) {
-                    F::load_x(xf, cc, xr);
+                    load_chunk(cc);
 #pragma unroll
-                    for (int u = 0; u < kRowUnroll; ++u) acc[u] += F::dot(r0[u], xr, k);
-                    F::load_x(xf, cc + L, xr);
+                    for (int u = 0; u < kRowUnroll; ++u) acc[u] += F::dot(r0[u], xr, xsv, k);
+                    load_chunk(cc + L);
 #pragma unroll
-                    for (int u = 0; u < kRowUnroll; ++u) acc[u] += F::dot(r1[u], xr, k);
+                    for (int u = 0; u < kRowUnroll; ++u) acc[u] += F::dot(r1[u], xr, xsv, k);
                 };
                 // The steady-state loop issues its loads unconditionally, so the compiler's wait before each
                 // step counts exactly the loads issued after that step's own.
@@ -453,22 +534,22 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
                             F::load(rows[u], c + L, rb[u]);
                         }
                     }
-                    F::load_x(xf, c, xr);
+                    load_chunk(c);
 #pragma unroll
                     for (int u = 0; u < kRowUnroll; ++u) {
                         const int row = base + u * kStride + sub;
-                        if (row < row_end) acc[u] += F::dot(ra[u], xr, k);
+                        if (row < row_end) acc[u] += F::dot(ra[u], xr, xsv, k);
                     }
-                    F::load_x(xf, c + L, xr);
+                    load_chunk(c + L);
 #pragma unroll
                     for (int u = 0; u < kRowUnroll; ++u) {
                         const int row = base + u * kStride + sub;
-                        if (row < row_end) acc[u] += F::dot(rb[u], xr, k);
+                        if (row < row_end) acc[u] += F::dot(rb[u], xr, xsv, k);
                     }
                 }
             }
             for (; c < nchunks; c += L) {
-                F::load_x(xf, c, xr);
+                load_chunk(c);
                 typename F::Regs regs[kRowUnroll];
 #pragma unroll
                 for (int u = 0; u < kRowUnroll; ++u) {
@@ -478,7 +559,7 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
 #pragma unroll
                 for (int u = 0; u < kRowUnroll; ++u) {
                     const int row = base + u * kStride + sub;
-                    if (row < row_end) acc[u] += F::dot(regs[u], xr, k);
+                    if (row < row_end) acc[u] += F::dot(regs[u], xr, xsv, k);
                 }
             }
 #pragma unroll
@@ -491,18 +572,18 @@ __global__ __launch_bounds__(THREADS) void gemv_float_kernel(MatDesc one, const 
     }
 }
 
-// LDS budget for the staged activations.
+// LDS budget for the staged activations and their per-chunk sums.
 constexpr int kMaxLdsBytes = 64 * 1024;
 
 template <class F>
-size_t staged_lds_bytes(int padded) {
-    return static_cast<size_t>(padded + 4 * (padded >> F::kPadShift) + 4) * sizeof(float);
+size_t staged_lds_bytes(int padded, int chunks) {
+    return static_cast<size_t>(staged_floats<F>(padded) + chunks * F::kSums) * sizeof(float);
 }
 
 template <class F, int L, bool ONE, int THREADS>
 hipError_t launch_variant(const MatDesc& one, const MatDesc* group, const LaunchShape& s, dim3 grid, int padded,
-                          hipStream_t stream) {
-    const size_t lds = staged_lds_bytes<F>(padded);
+                          int chunks, hipStream_t stream) {
+    const size_t lds = staged_lds_bytes<F>(padded, chunks);
     if (lds <= kMaxLdsBytes)
         gemv_float_kernel<F, L, ONE, true, THREADS><<<grid, THREADS, lds, stream>>>(one, group, s);
     else
@@ -512,10 +593,10 @@ hipError_t launch_variant(const MatDesc& one, const MatDesc* group, const Launch
 
 template <class F, int L>
 hipError_t launch_lanes(const MatDesc& one, const MatDesc* group, const LaunchShape& s, dim3 grid, int padded,
-                        bool one_chunk, bool wide, hipStream_t stream) {
-    if (one_chunk) return launch_variant<F, L, true, kThreads>(one, group, s, grid, padded, stream);
-    if (wide) return launch_variant<F, L, false, kWideThreads>(one, group, s, grid, padded, stream);
-    return launch_variant<F, L, false, kThreads>(one, group, s, grid, padded, stream);
+                        int chunks, bool one_chunk, bool wide, hipStream_t stream) {
+    if (one_chunk) return launch_variant<F, L, true, kThreads>(one, group, s, grid, padded, chunks, stream);
+    if (wide) return launch_variant<F, L, false, kWideThreads>(one, group, s, grid, padded, chunks, stream);
+    return launch_variant<F, L, false, kThreads>(one, group, s, grid, padded, chunks, stream);
 }
 
 template <class F>
@@ -528,8 +609,8 @@ hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, La
     // fewer rows per wave pass mean more rows per workgroup, so a single matrix keeps 64.
     int lanes = 8;
     while (lanes < 64 && lanes < chunks) lanes <<= 1;
-    const bool one_chunk = chunks <= lanes;
-    const size_t lds = staged_lds_bytes<F>(padded);
+    const bool one_chunk = chunks <= lanes && chunks * 8 >= lanes * 7;
+    const size_t lds = staged_lds_bytes<F>(padded, chunks);
     const bool wide = !one_chunk && lds > kWideLdsBytes && lds <= kMaxLdsBytes;
     const int64_t launched = static_cast<int64_t>(count) * s.positions;
     if (!one_chunk) {
@@ -562,10 +643,10 @@ hipError_t launch_format(const MatDesc& one, const MatDesc* group, int count, La
     s.rows_per_wg = rows_per_wg;
     dim3 grid((s.rows_max + rows_per_wg - 1) / rows_per_wg, count, s.positions);
     switch (lanes) {
-        case 8: return launch_lanes<F, 8>(one, group, s, grid, padded, one_chunk, wide, stream);
-        case 16: return launch_lanes<F, 16>(one, group, s, grid, padded, one_chunk, wide, stream);
-        case 32: return launch_lanes<F, 32>(one, group, s, grid, padded, one_chunk, wide, stream);
-        default: return launch_lanes<F, 64>(one, group, s, grid, padded, one_chunk, wide, stream);
+        case 8: return launch_lanes<F, 8>(one, group, s, grid, padded, chunks, one_chunk, wide, stream);
+        case 16: return launch_lanes<F, 16>(one, group, s, grid, padded, chunks, one_chunk, wide, stream);
+        case 32: return launch_lanes<F, 32>(one, group, s, grid, padded, chunks, one_chunk, wide, stream);
+        default: return launch_lanes<F, 64>(one, group, s, grid, padded, chunks, one_chunk, wide, stream);
     }
 }
 
