@@ -153,28 +153,28 @@ struct Q4_0Chunk {
 // ------------------------------------------------------------------------------------------------
 // Q4_K, FP32 activations (Q4KCodec.DotBlock, src/Satori.Core/Q4KCodec.cs:39-65): 144-byte super-block,
 // f16 d @0, f16 dmin @2, 6-bit scales/mins @4..15 (Q4KCodec.GetScaleMin, :24-36), nibbles @16.
-// Chunk k of a block (k = 0..7) is qs[16k .. 16k + 16): low nibbles are weights 64g + 16h + i of
-// sub-block 2g, high nibbles weights 64g + 32 + 16h + i of sub-block 2g + 1 (g = k / 2, h = k % 2).
-// The chunk's dot is factored per sub-block half: sum (d s q - dmin m) x = (d s) sum q x - (dmin m) sum x,
-// so a weight costs one conversion and one FMA; the two sums of 16 activations (low and high half) are the
-// same for every row and are computed once per workgroup (Sums). The high nibbles are used in place (the
-// bytes 16 q) and the factor 16 is removed with the power-of-two 1/16. A chunk's position k within its
-// block is the same for all of a lane's chunks (k = chunk % 8, and a row's lanes step by a multiple of 8),
-// so the scale and min fields a lane reads are fixed per lane (Consts).
+// Chunk g of a block (g = 0..3) is qs[32g .. 32g + 32): the low nibbles are weights 64g + i of sub-block 2g,
+// the high nibbles weights 64g + 32 + i of sub-block 2g + 1, so the chunk's 64 activations are contiguous.
+// The chunk's dot is factored per sub-block: sum (d s q - dmin m) x = (d s) sum q x - (dmin m) sum x, so a
+// weight costs one conversion and one FMA; the two sums of 32 activations are the same for every row and are
+// computed once per workgroup (Sums). The high nibbles are used in place (the bytes 16 q) and the factor 16
+// is removed with the power-of-two 1/16. A chunk's position g within its block is the same for all of a
+// lane's chunks (g = chunk % 4, and a row's lanes step by a multiple of 4), so the scale and min fields a
+// lane reads are fixed per lane (Consts).
 // Non-finite activations: a product whose decoded weight is nonzero but whose code is 0 comes out NaN here
 // where the reference's w * x gives +-Inf; the GGUF MatVec surface rejects non-finite inputs.
 // ------------------------------------------------------------------------------------------------
 
 struct Q4_KChunk {
-    static constexpr int kRowUnroll = 2;
+    static constexpr int kRowUnroll = 1;
     static constexpr bool kPipelineShortLanes = false;
     static constexpr int kMaxWorkgroupPayload = 0;
-    static constexpr int kWeights = 32;
+    static constexpr int kWeights = 64;
     static constexpr int kPadShift = 6;
-    static constexpr int kSums = 2;  // sum of the low-nibble half's 16 activations, of the high half's
+    static constexpr int kSums = 2;  // sum of the low-nibble sub-block's 32 activations, of the high one's
     struct Regs {
         u32x4 head;
-        u32x4 qs;
+        u32x4 qs0, qs1;
     };
     // Bit offsets of the 6-bit scale and min of sub-blocks 2g and 2g + 1 (GetScaleMin): for g < 2 they are
     // bytes 2g, 2g + 1 of scales[0..3] / scales[4..7]; for g >= 2 their low 4 bits are the nibbles of
@@ -186,41 +186,41 @@ struct Q4_KChunk {
         uint32_t top;           // offset of the 2 high bits (scale: dword 1, min: dword 2)
     };
     __device__ static Consts consts(int chunk) {
-        const int g = (chunk & 7) >> 1;
+        const int g = chunk & 3;
         if (g < 2) return Consts{false, 16u * g, 16u * g, 16u * g + 4};
         const uint32_t o = 16u * (g - 2);
         return Consts{true, o, o + 4, o + 6};
     }
-    __device__ static int chunks(const LaunchShape& s) { return s.blocks * 8; }
+    __device__ static int chunks(const LaunchShape& s) { return s.blocks * 4; }
     __device__ static int padded_columns(const LaunchShape& s) { return s.columns; }
     using Row = const uint8_t*;  // the row's first block
     __device__ static Row row_ref(const MatDesc& m, const LaunchShape& s, int row) {
         return m.w + static_cast<int64_t>(row) * s.row_bytes;
     }
     __device__ static void load(Row w, int chunk, Regs& r) {
-        const uint8_t* block = w + (chunk >> 3) * 144;
+        const uint8_t* block = w + (chunk >> 2) * 144;
         r.head = load16_a4(block);
-        r.qs = load16_a4(block + 16 + 16 * (chunk & 7));
+        r.qs0 = load16_a4(block + 16 + 32 * (chunk & 3));
+        r.qs1 = load16_a4(block + 32 + 32 * (chunk & 3));
     }
     template <class XF>
     __device__ static void load_x(XF xf, int chunk, float (&x)[kWeights]) {
-        const int base = (chunk >> 3) * 256 + 64 * ((chunk & 7) >> 1) + 16 * (chunk & 1);
+        const int base = (chunk >> 2) * 256 + 64 * (chunk & 3);
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            xf.quad(base + i, x + i);
-            xf.quad(base + 32 + i, x + 16 + i);
-        }
+        for (int i = 0; i < kWeights; i += 4) xf.quad(base + i, x + i);
     }
     // The chunk's activation sums from its loaded activations (pairwise).
     __device__ static void sums(const float (&x)[kWeights], float (&out)[kSums]) {
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            float t[8];
+            float t[16];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) t[i] = x[16 * half + i] + x[16 * half + 8 + i];
+            for (int i = 0; i < 16; ++i) t[i] = x[32 * half + i] + x[32 * half + 16 + i];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t[i] += t[i + 4];
-            out[half] = (t[0] + t[2]) + (t[1] + t[3]);
+            for (int n = 8; n > 0; n >>= 1)
+#pragma unroll
+                for (int i = 0; i < n; ++i) t[i] += t[i + n];
+            out[half] = t[0];
         }
     }
     __device__ static float dot(const Regs& r, const float (&x)[kWeights], const float (&xs)[kSums],
@@ -236,17 +236,18 @@ struct Q4_KChunk {
                             (__builtin_amdgcn_ubfe(r.head[2], k.top + 8, 2) << 4);
         float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t raw = w < 4 ? r.qs0[w] : r.qs1[w - 4];
             // Bytes q and bytes 16 q, each converted by one byte-select conversion: the empty asm keeps the
             // compiler from folding the mask into a bit-field extract per weight (two instructions a weight).
-            uint32_t lo = r.qs[w] & 0x0F0F0F0Fu, hi = r.qs[w] & 0xF0F0F0F0u;
+            uint32_t lo = raw & 0x0F0F0F0Fu, hi = raw & 0xF0F0F0F0u;
             asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
                 a0 = __builtin_fmaf(byte_to_float(lo, i), x[4 * w + i], a0);
                 a1 = __builtin_fmaf(byte_to_float(lo, i + 1), x[4 * w + i + 1], a1);
-                b0 = __builtin_fmaf(byte_to_float(hi, i), x[16 + 4 * w + i], b0);
-                b1 = __builtin_fmaf(byte_to_float(hi, i + 1), x[16 + 4 * w + i + 1], b1);
+                b0 = __builtin_fmaf(byte_to_float(hi, i), x[32 + 4 * w + i], b0);
+                b1 = __builtin_fmaf(byte_to_float(hi, i + 1), x[32 + 4 * w + i + 1], b1);
             }
         }
         const float dl = d * static_cast<float>(s0), dh = (d * static_cast<float>(s1)) * 0.0625f;
@@ -658,7 +659,7 @@ hipError_t launch_gemv_float(const MatDesc& one, const MatDesc* group, int count
     switch (s.format) {
         case kQ8_0: return launch_format<Q8_0Chunk>(one, group, count, s, s.blocks, s.columns, stream);
         case kQ4_0: return launch_format<Q4_0Chunk>(one, group, count, s, s.blocks, s.columns, stream);
-        case kQ4_K: return launch_format<Q4_KChunk>(one, group, count, s, s.blocks * 8, s.columns, stream);
+        case kQ4_K: return launch_format<Q4_KChunk>(one, group, count, s, s.blocks * 4, s.columns, stream);
         case kQ6_K: return launch_format<Q6_KChunk>(one, group, count, s, s.blocks * 4, s.columns, stream);
         default: return hipErrorInvalidValue;
     }
