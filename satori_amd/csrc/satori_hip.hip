@@ -130,6 +130,7 @@ struct satori_hip_group {
     satori::InputTransform input{};            // K groups: input computed in the launch (kInputPlain: read x)
     satori::OutputSwiGluQ8K output{};          // gate/up K groups: SwiGlu and its Q8_K bytes carried on (or none)
     satori::DeviceBuffer counters;             // the arrival counts of `output` (one per 256 rows)
+    satori::DeviceBuffer shared_q8k;           // large K groups sharing one input: its Q8_K bytes, made per launch
     satori::T2Plan plan{};                     // Ternary2 groups
     void* scratch = nullptr;                   // Ternary2 range scratch (device)
     uint32_t t2_generation = 0;                // the last Ternary2 launch's tag in the scratch's exchange slots
@@ -529,6 +530,16 @@ void enqueue_group(satori_hip_group* g, hipStream_t st) {
         check_hip(launch_gemv_kint_swiglu(g->host.data(), l, g->input, g->output, st), "integer gemv launch");
     } else if (g->quantized && g->input.kind != kInputPlain) {
         check_hip(launch_gemv_kint_transformed(g->host.data(), g->descriptors, g->count, l, g->input, st),
+                  "integer gemv launch");
+    } else if (g->quantized && g->shared_q8k.ptr) {
+        // One input shared by many members: quantized once by a small launch, each workgroup copies its bytes
+        // (the same bytes every workgroup would compute).
+        check_hip(launch_q8k_quantize(g->host[0].x, g->shape.columns, 1, static_cast<uint8_t*>(g->shared_q8k.ptr), st),
+                  "Q8_K quantization launch");
+        InputTransform t{};
+        t.kind = kInputQ8K;
+        t.a = static_cast<const float*>(g->shared_q8k.ptr);
+        check_hip(launch_gemv_kint_transformed(g->host.data(), g->descriptors, g->count, l, t, st),
                   "integer gemv launch");
     } else if (g->quantized) {
         check_hip(launch_gemv_kint(g->host.data(), g->descriptors, g->count, l, st), "integer gemv launch");
@@ -1139,6 +1150,14 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
                 g->scratch = allocate_t2_scratch(g->plan);
             }
             set_device(c);
+            // Groups of more members than a launch passes in its arguments (large launches that stream from HBM)
+            // whose members all read one input of more than 16 blocks quantize it once per launch instead of in
+            // every workgroup (a workgroup quantizes 16 blocks per pass: 1536 x 8960 grouped, Q4_K 5.65 -> 5.83
+            // TB/s, Q6_K 5.82 -> 5.89; for rows of one pass the extra launch cost more, 8960 x 1536 -2%).
+            bool shared_input = true;
+            for (int i = 1; i < count; ++i) shared_input = shared_input && host[i].x == host[0].x;
+            if (g->quantized && count > kKintInlineMembers && shared_input && first.columns / 256 > 16)
+                g->shared_q8k.reserve(static_cast<size_t>(first.columns / 256) * kQ8KBlockBytes);
             check_hip(hipMalloc(reinterpret_cast<void**>(&g->descriptors), sizeof(MatDesc) * count), "hipMalloc");
             check_hip(hipMemcpy(g->descriptors, host.data(), sizeof(MatDesc) * count, hipMemcpyHostToDevice),
                       "descriptor upload");
@@ -1146,6 +1165,7 @@ int satori_hip_group_create(satori_hip_context* c, satori_hip_matrix* const* mat
         } catch (...) {
             if (g->descriptors) (void)hipFree(g->descriptors);
             if (g->scratch) (void)hipFree(g->scratch);
+            g->shared_q8k.release();
             delete g;
             throw;
         }
@@ -1309,6 +1329,7 @@ int satori_hip_group_destroy(satori_hip_group* g) {
         g->scratch = nullptr;
         g->batch.release();
         g->counters.release();
+        g->shared_q8k.release();
         g->output = OutputSwiGluQ8K{};
         g->live = false;
     });

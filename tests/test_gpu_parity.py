@@ -690,6 +690,56 @@ def test_k_group_batch_equals_member_batches(context, fmt, positions):
             m.dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
+@pytest.mark.parametrize("columns,inputs", [(4608, "shared"), (4096, "shared"), (4608, "mixed")])
+def test_large_one_position_k_group(context, fmt, columns, inputs):
+    # One-position K groups of more members than a launch passes in its arguments (the descriptor array):
+    # with one shared input of more than 16 blocks the library quantizes it once per launch and every
+    # workgroup copies the bytes; at 16 blocks, or with several inputs, each workgroup quantizes. Every member
+    # equals the oracle's ExecuteQuantizedTiled composition bit for bit, on repeated launches and replayed
+    # from a captured step with new inputs between the replays.
+    g = rng(515 + columns + int(fmt) + (inputs == "mixed"))
+    row_counts = [300, 1, 64, 129, 256, 33]
+    datas, mats = [], []
+    for r in row_counts:
+        w = (g.standard_normal((r, columns)) * 0.02).astype(np.float32)
+        datas.append(S.quantize_weights(w, r, columns, fmt))
+        mats.append(context.create(datas[-1], S.QuantizedMatrixShape(r, columns, fmt)))
+    which = [0] * 6 if inputs == "shared" else [0, 1, 0, 1, 1, 0]
+    dx = [context.alloc(4 * columns) for _ in range(2)]
+    dy = [context.alloc(4 * r) for r in row_counts]
+    group = S.HipGroup(context, mats, [dx[i] for i in which], dy, True)
+    step = None
+    try:
+        def check(seed, run):
+            x = [rng(seed + i).standard_normal(columns).astype(np.float32) for i in range(2)]
+            x[1][:256] = 0.0  # an all-zero activation block
+            for p, a in zip(dx, x):
+                context.upload(p, a)
+            for p, r in zip(dy, row_counts):
+                context.upload(p, np.full(r, np.nan, np.float32))
+            run()
+            context.synchronize()
+            for i, r in enumerate(row_counts):
+                got = context.download(np.zeros(r, np.float32), dy[i])
+                want = O.qk_matvec_quantized_avx2(datas[i], r, columns, int(fmt), O.q8k_quantize_row(x[which[i]]))
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seed, i, r)
+
+        check(1, group.execute)
+        check(2, group.execute)
+        step = S.HipStep(context, [group])
+        check(3, step.execute)
+        check(4, step.execute)
+    finally:
+        if step is not None:
+            step.dispose()
+        group.dispose()
+        for p in dx + dy:
+            context.free(p)
+        for m in mats:
+            m.dispose()
+
+
 def test_randomized_shapes_sweep(context):
     # A seeded sweep over every MatVec path and random shapes (rows 1-3000, so rows end inside panels and
     # tiles; ragged Ternary2 columns; odd block counts; long and short rows): the FP32 paths within the
