@@ -55,6 +55,11 @@ CALIBRATION_BYTES = 1 << 30
 BQ = S.BlockQuantization
 METRIC = "effective quantized-payload GB/s (% of MI355X HBM peak) per format, 4096² batch 1"
 PUBLISHED_AVX2_T2_4096_B128 = 1.31  # GB/s, Ternary2 AVX2 4096^2 B128, docs/benchmarks/avx2-2026-10-12 run 1
+# The same run's AVX2 figures for the whole size x block grid (docs/benchmarks/avx2-2026-10-12/README.md:5-17,
+# run 1, EffectiveWeightGBPerSecond), GB/s by (size, block).
+PUBLISHED_AVX2_T2 = {(1024, 64): 1.33, (1024, 128): 1.23, (1024, 256): 1.15,
+                     (2048, 64): 1.29, (2048, 128): 1.32, (2048, 256): 1.22,
+                     (4096, 64): 1.37, (4096, 128): 1.31, (4096, 256): 1.22}
 
 
 class HipEvents:
@@ -902,6 +907,35 @@ def host_cpu() -> dict:
     return {"model": model, "logical_cpus": os.cpu_count(), "available": available}
 
 
+def ternary2_sweep(ctx, events, formats: dict) -> dict:
+    """The Ternary2 size x block grid of the reference's own CPU benchmark (1024^2, 2048^2, 4096^2 x B64 / B128 /
+    B256): for the two smaller sizes, a grouped launch over >= 1 GiB of distinct copies (HBM-streaming, every
+    copy's output checked against the oracle first) and the single-matrix launch replayed from a graph; the
+    4096^2 rows repeat the format entries measured above. The CPU column is filled in later."""
+    out = {}
+    for size in (1024, 2048, 4096):
+        for b in (64, 128, 256):
+            label = f"ternary2-{size}-b{b}"
+            if size == 4096:
+                f = formats.get(label)
+                if f is None:
+                    continue
+                out[label] = {k: f[k] for k in ("payload_bytes", "copies", "gbs", "pct_hbm", "single_launch_graph_us",
+                                                "parity_checked") if k in f}
+            else:
+                p, xb = make_ternary2(size, size, b)
+                c = Case(ctx, label, lambda p=p, b=b, size=size: ctx.create_ternary2(size, size, b, p), p.size, size,
+                         size, xb, False)
+                parity = check_case(ctx, c, p, size, size, None, xb, b)
+                m = measure(ctx, events, c, 50, 10)
+                c.close()
+                out[label] = {k: m[k] for k in ("payload_bytes", "copies", "gbs", "pct_hbm", "single_launch_graph_us")}
+                out[label].update(parity)
+            out[label]["published_avx2_gbs"] = PUBLISHED_AVX2_T2[(size, b)]
+            out[label]["vs_published_avx2"] = out[label]["gbs"] / PUBLISHED_AVX2_T2[(size, b)]
+    return out
+
+
 def other_formats(ctx):
     """(label, make) for the Ternary2 block sizes besides 128 and the GGUF formats at their configurations;
     make() returns the grouped Case and the CPU baseline's arguments (payload, rows, columns, format or None
@@ -1070,7 +1104,7 @@ def run(args, ctx, events) -> int:
 
     formats = {"ternary2-4096-b128": headline}
     cpu_cases = {"ternary2-4096-b128": (payload, rows, columns, None, x, block)}
-    decode = pre = token = load = fbatch = None
+    decode = pre = token = load = fbatch = sweep = None
     try:
         if not args.quick:
             for label, make in other_formats(ctx):
@@ -1081,6 +1115,8 @@ def run(args, ctx, events) -> int:
                 formats[label].update(host_call_latency(c))
                 cpu_cases[label] = cpu_case
                 c.close()
+            progress("Ternary2 size x block sweep (1024^2, 2048^2)")
+            sweep = ternary2_sweep(ctx, events, formats)
 
         if not args.quick:
             progress("decode step (197 projections per token)")
@@ -1107,6 +1143,15 @@ def run(args, ctx, events) -> int:
         for label, case in cpu_cases.items():
             formats[label].update(cpu_format(*case, args.cpu_format_seconds))
             formats[label]["gpu_over_cpu"] = formats[label]["gbs"] / formats[label]["cpu_gbs"]
+        progress("cpu baseline: Ternary2 sweep")
+        for label, entry in sweep.items():
+            if label in formats:
+                entry["cpu_gbs"] = formats[label]["cpu_gbs"]
+            else:
+                size, b = int(label.split("-")[1]), int(label.split("-b")[1])
+                p, xb = make_ternary2(size, size, b)
+                entry["cpu_gbs"] = cpu_format(p, size, size, None, xb, b, 0.5)["cpu_gbs"]
+            entry["gpu_over_cpu"] = entry["gbs"] / entry["cpu_gbs"]
         progress("cpu baseline: decode step and one prefill layer-chunk")
         decode.update(cpu_decode_step(model_host, model_shapes, decode_inputs(model), args.cpu_decode_seconds))
         decode["gpu_over_cpu"] = decode["cpu_ms_per_token"] * 1e3 / decode["us_per_token"]
@@ -1159,6 +1204,8 @@ def run(args, ctx, events) -> int:
         "batch_fp32": ({label: {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
                         for label, r in fbatch.items()} if fbatch else None),
         "loading": ({k: round(v, 2) for k, v in load.items()} if load else None),
+        "ternary2_sweep": ({label: {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+                            for label, r in sweep.items()} if sweep else None),
         "formats": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in formats.items()},
     }
