@@ -949,6 +949,17 @@ def other_formats(ctx):
                      columns, xb, False)
             return c, (p, rows, columns, None, xb, b)
         out.append((f"ternary2-4096-b{b}", make))
+
+    # The like-for-like input of the reference's own benchmark: NumericalCorpus.RandomMatrix (xorshift32
+    # weights and x, as the oracle restates it), quantized to B128 (the payload bytes do not depend on values).
+    def make_corpus():
+        from oracle import oracle as O
+        wc, xc = O.corpus_random_matrix(rows, columns)
+        p = S.Ternary2Matrix.quantize(wc, rows, columns, 128).data
+        c = Case(ctx, "ternary2-4096-b128-corpus", lambda: ctx.create_ternary2(rows, columns, 128, p), p.size, rows,
+                 columns, xc, False)
+        return c, (p, rows, columns, None, xc, 128)
+    out.append(("ternary2-4096-b128-corpus", make_corpus))
     for fmt, r, cc, quantized, label in (
             (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
             (BQ.Q4_0, 11008, 4096, False, "q4_0-11008x4096"),
