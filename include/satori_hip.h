@@ -175,7 +175,9 @@ int satori_hip_quantize_q8k(satori_hip_context* context, const float* input, int
  * launch tags its exchanges with its own number, so nothing an overlapping launch leaves behind is added
  * in), except the replays of a captured step or capture that overlapped: those reuse their recorded
  * launch's number, so recreate such a step. For concurrent streams, give each stream its own copy
- * (satori_hip_matrix_clone). The same holds for groups (satori_hip_group_execute). */
+ * (satori_hip_matrix_clone). The same holds for groups (satori_hip_group_execute; a K group of more than four
+ * members that share one input of more than 16 blocks also keeps that input's Q8_K bytes in a workspace of
+ * its own, quantized once per launch). */
 int satori_hip_matvec_device(satori_hip_matrix* matrix, const float* input, float* output, void* stream);
 int satori_hip_matvec_batch_device(satori_hip_matrix* matrix, const float* input, int positions, float* output,
                                    void* stream);
