@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SATORI_HIP_ABI_VERSION 3
+#define SATORI_HIP_ABI_VERSION 4
 
 typedef struct satori_hip_context satori_hip_context;
 typedef struct satori_hip_matrix satori_hip_matrix;

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_entry_point():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in include/satori_hip.h but not exported"
     assert set(names) == set(S._ffi.SIGNATURES), "ctypes binding and header disagree"
-    assert S._ffi.lib().satori_hip_abi_version() == 3
+    assert S._ffi.lib().satori_hip_abi_version() == 4
 
 
 def test_context_without_gfx950_device_is_platform_not_supported():
