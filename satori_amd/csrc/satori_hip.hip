@@ -307,6 +307,19 @@ bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
     return a0 < b0 + b_bytes && b0 < a0 + a_bytes;
 }
 
+// Whether [p, p + bytes) overlaps a buffer that input transform t reads or writes (columns: the group's width).
+bool overlaps_transform(const void* p, size_t bytes, const InputTransform& t, int columns) {
+    const size_t n = static_cast<size_t>(columns) * sizeof(float);
+    switch (t.kind) {
+        case kInputAddRmsNorm:
+            return overlaps(p, bytes, t.a, n) || (t.b && overlaps(p, bytes, t.b, n)) || overlaps(p, bytes, t.w, n) ||
+                   (t.residual_out && overlaps(p, bytes, t.residual_out, n));
+        case kInputSwiGlu: return overlaps(p, bytes, t.a, n) || overlaps(p, bytes, t.b, n);
+        case kInputQ8K: return overlaps(p, bytes, t.a, static_cast<size_t>(columns / 256) * kQ8KBlockBytes);
+        default: return false;
+    }
+}
+
 // One 16-byte code record rotated left by 2 bits as a 128-bit little-endian integer.
 void rotate_record(uint8_t* out, const uint8_t* in) {
     uint32_t w[4], r[4];
@@ -1258,6 +1271,14 @@ int satori_hip_group_set_input(satori_hip_group* g, int kind, const float* a, co
                 if (clash) fail(SATORI_HIP_E_ARGUMENT, "residual_out must not overlap the operands or the outputs.");
             }
         }
+        if (g->output.activated) {  // the SwiGlu output's buffers, written by the launch that reads t's operands
+            const int rows = g->host[0].rows;
+            const size_t act_bytes = static_cast<size_t>(rows) * sizeof(float);
+            const size_t q_bytes = g->output.q8k ? static_cast<size_t>(rows / 256) * kQ8KBlockBytes : 0;
+            if (overlaps_transform(g->output.activated, act_bytes, t, g->shape.columns) ||
+                (q_bytes && overlaps_transform(g->output.q8k, q_bytes, t, g->shape.columns)))
+                fail(SATORI_HIP_E_ARGUMENT, "The input transform's buffers must not overlap activated or q8k.");
+        }
         g->input = t;
     });
 }
@@ -1295,6 +1316,9 @@ int satori_hip_group_set_output(satori_hip_group* g, int kind, float* activated,
         for (const MatDesc& d : g->host)
             clash = clash || overlaps(activated, act_bytes, d.y, act_bytes) || overlaps(q8k, q_bytes, d.y, act_bytes) ||
                     overlaps(activated, act_bytes, d.x, in_bytes) || overlaps(q8k, q_bytes, d.x, in_bytes);
+        // With an input transform the launch reads its operands (and may write residual_out) instead of x.
+        clash = clash || overlaps_transform(activated, act_bytes, g->input, g->shape.columns) ||
+                (q_bytes && overlaps_transform(q8k, q_bytes, g->input, g->shape.columns));
         if (clash) fail(SATORI_HIP_E_ARGUMENT, "activated and q8k must not overlap each other, the inputs or the outputs.");
         set_device(c);
         check_hip(hipStreamSynchronize(c->stream), "stream");

@@ -1847,6 +1847,24 @@ def test_swiglu_output_argument_checks(context):
         good.set_input_swiglu(dx, dx)
         with pytest.raises(S.NotSupportedException):
             good.set_output_swiglu(dact, dq)
+        # An input transform's operands (and residual_out) are the launch's inputs: neither output buffer may
+        # overlap them, whichever of the two calls comes second.
+        good.set_input_plain()
+        dres, dadd, dnw, dres_out = dev(columns), dev(columns), dev(columns), dev(columns)
+        good.set_input_add_rms_norm(dres, dadd, dnw, 1e-6, dres_out)
+        for operand in (dres, dadd, dnw, dres_out):
+            with pytest.raises(S.ArgumentException):
+                good.set_output_swiglu(operand, dq)
+        with pytest.raises(S.ArgumentException):  # q8k over the residual
+            good.set_output_swiglu(dact, dres)
+        good.set_output_swiglu(dact, dq)
+        with pytest.raises(S.ArgumentException):  # the residual over activated
+            good.set_input_add_rms_norm(dact, dadd, dnw, 1e-6)
+        with pytest.raises(S.ArgumentException):  # residual_out over q8k
+            good.set_input_add_rms_norm(dres, dadd, dnw, 1e-6, dq)
+        with pytest.raises(S.ArgumentException):  # producer Q8_K bytes over activated
+            good.set_input_q8k(dact)
+        good.set_input_add_rms_norm(dres, dadd, dnw, 1e-6, dres_out)  # disjoint operands are accepted
     finally:
         for grp in groups:
             grp.dispose()
