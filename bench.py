@@ -968,10 +968,15 @@ def other_formats(ctx):
             (BQ.Q4_K, 1536, 8960, True, "q4_k-1536x8960-q8k"),
             (BQ.Q6_K, 8960, 1536, True, "q6_k-8960x1536-q8k"),
             (BQ.Q6_K, 1536, 8960, True, "q6_k-1536x8960-q8k"),
+            # Q4_K at 4096 x 4096 and at larger FFN shapes (an 8B-class model's gate/up and down).
+            (BQ.Q4_K, 4096, 4096, True, "q4_k-4096x4096-q8k"),
+            (BQ.Q4_K, 14336, 4096, True, "q4_k-14336x4096-q8k"),
+            (BQ.Q4_K, 4096, 14336, True, "q4_k-4096x14336-q8k"),
             # The K formats' FP32-activation MatVec (IQuantizedMatrix.Execute / ExecuteScalar's DotBlock; CPU:
             # QuantizedKAvx2Kernel.ExecuteQ4K / ExecuteQ6K).
             (BQ.Q4_K, 8960, 1536, False, "q4_k-8960x1536-f32"),
             (BQ.Q4_K, 1536, 8960, False, "q4_k-1536x8960-f32"),
+            (BQ.Q4_K, 4096, 4096, False, "q4_k-4096x4096-f32"),
             (BQ.Q6_K, 8960, 1536, False, "q6_k-8960x1536-f32"),
             (BQ.Q6_K, 1536, 8960, False, "q6_k-1536x8960-f32")):
         def make(fmt=fmt, r=r, cc=cc, quantized=quantized, label=label):

@@ -441,7 +441,8 @@ def test_k_real_tensor_blocks(context):
 
 
 @pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
-@pytest.mark.parametrize("rows,columns", [(8960, 1536), (1536, 8960), (1536, 1536), (256, 1536), (17, 512)])
+@pytest.mark.parametrize("rows,columns", [(8960, 1536), (1536, 8960), (1536, 1536), (256, 1536), (17, 512),
+                                          (4096, 4096)])
 def test_k_float_path_matches_scalar_reference(context, fmt, rows, columns):
     g = rng(20261014 + rows * 7 + columns)
     w = (g.standard_normal((rows, columns), dtype=np.float32) * 0.02).astype(np.float32)
@@ -498,7 +499,8 @@ def test_q8k_quantizer_matches_oracle_on_edge_cases(context):
 
 
 @pytest.mark.parametrize("fmt", [BQ.Q4_K, BQ.Q6_K])
-@pytest.mark.parametrize("rows,columns", [(8960, 1536), (1536, 8960), (1536, 1536), (256, 1536), (17, 3584)])
+@pytest.mark.parametrize("rows,columns", [(8960, 1536), (1536, 8960), (1536, 1536), (256, 1536), (17, 3584),
+                                          (4096, 4096), (14336, 4096), (4096, 14336)])
 def test_k_integer_batch_is_bit_exact(context, fmt, rows, columns):
     # Q6KQuantizedProductTests.cs:284-308 and KParityTests.cs:214-244: the projection equals the
     # composition of the public codecs, summed block by block; here the oracle's restatement of
