@@ -960,6 +960,14 @@ def other_formats(ctx):
                  columns, xc, False)
         return c, (p, rows, columns, None, xc, 128)
     out.append(("ternary2-4096-b128-corpus", make_corpus))
+    # Ternary2 beyond 4096 x 4096 (B = 128): FFN shapes of a 7B-class model and an 8192 x 8192 matrix.
+    for r, cc in ((11008, 4096), (4096, 11008), (8192, 8192)):
+        def make_large(r=r, cc=cc):
+            label = f"ternary2-{r}x{cc}-b128"
+            p, xb = make_ternary2(r, cc, 128)
+            c = Case(ctx, label, lambda: ctx.create_ternary2(r, cc, 128, p), p.size, r, cc, xb, False)
+            return c, (p, r, cc, None, xb, 128)
+        out.append((f"ternary2-{r}x{cc}-b128", make_large))
     for fmt, r, cc, quantized, label in (
             (BQ.Q8_0, 4096, 4096, False, "q8_0-4096x4096"),
             (BQ.Q4_0, 11008, 4096, False, "q4_0-11008x4096"),
