@@ -552,9 +552,8 @@ def token_eager(ctx, events, model: DecodeModel, steps: int, warmup: int, positi
 def batch_fp32(ctx, events, steps: int = 20, warmup: int = 3, positions: int = 256) -> dict:
     """ExecuteBatch of the FP32-activation formats (QuantizedMatVec.ExecuteBatchFloat / ExecuteBatchRows) at
     256 positions on the Q8_0 4096 x 4096 and Q4_0 11008 x 4096 / 4096 x 11008 shapes, through the device
-    entry point: the activations are
-    split into exact bf16 parts once per call and the matrix-core product reads each matrix once per
-    32-position tile. Parity first (sampled positions within 1e-5 * sum|w x| of the oracle's scalar
+    entry point: the activations are split into exact bf16 parts once per call and the matrix-core product
+    reads each matrix once per 32-position tile. Parity first (sampled positions within 1e-5 * sum|w x| of the oracle's scalar
     product), then timed. `per_position_gbs` is the payload bytes times positions over the time, the rate a
     per-position MatVec would have to stream at to match."""
     from oracle import oracle as O
