@@ -55,6 +55,8 @@ CALIBRATION_BYTES = 1 << 30
 BQ = S.BlockQuantization
 METRIC = "effective quantized-payload GB/s (% of MI355X HBM peak) per format, 4096² batch 1"
 PUBLISHED_AVX2_T2_4096_B128 = 1.31  # GB/s, Ternary2 AVX2 4096^2 B128, docs/benchmarks/avx2-2026-10-12 run 1
+# The same run's scalar figure for that shape (ExecuteScalarCore): 114.150 ms, 4,718,592 B (run 1).
+PUBLISHED_SCALAR_T2_4096_B128_MS = 114.150
 # The same run's AVX2 figures for the whole size x block grid (docs/benchmarks/avx2-2026-10-12/README.md:5-17,
 # run 1, EffectiveWeightGBPerSecond), GB/s by (size, block).
 PUBLISHED_AVX2_T2 = {(1024, 64): 1.33, (1024, 128): 1.23, (1024, 256): 1.15,
@@ -860,8 +862,9 @@ def cpu_prefill_chunk(host, shapes, host_in, positions: int, repeats: int) -> di
                            "projection of the last position")}
 
 
-def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
-    """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample."""
+def cpu_baseline(payload, rows, columns, block, x, seconds, scalar_seconds: float = 3.0) -> dict:
+    """Restated reference AVX2 Ternary2 kernel (oracle), one host core, warm payload, bounded sample; and the
+    scalar reference beside it (`scalar`)."""
     from oracle import oracle as O
 
     host = host_cpu()  # before pinning: the CPUs available to the process
@@ -876,6 +879,26 @@ def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
         samples.append(time.perf_counter() - t0)
         iterations += 1
     elapsed = time.perf_counter() - start
+    # The scalar reference (Ternary2MatVec.ExecuteScalarCore, restated in oracle/satori_oracle.c: sequential
+    # FP32 adds, no fast-math), a bounded sample on the same pinned core.
+    scalar_samples, s0 = [], time.perf_counter()
+    while time.perf_counter() - s0 < scalar_seconds or len(scalar_samples) < 3:
+        t0 = time.perf_counter()
+        O.t2_matvec_scalar(payload, rows, columns, block, x)
+        scalar_samples.append(time.perf_counter() - t0)
+    scalar_best = min(scalar_samples)
+    scalar = {
+        "gbs": payload.size / scalar_best / 1e9,
+        "ms_min": scalar_best * 1e3,
+        "ms_median": sorted(scalar_samples)[len(scalar_samples) // 2] * 1e3,
+        "runs": len(scalar_samples),
+        "kind": "port",
+        "sample": (f"restated reference scalar Ternary2MatVec.ExecuteScalarCore (oracle/satori_oracle.c) on the "
+                   f"same payload and x, {len(scalar_samples)} MatVecs, 1 thread pinned to core {core}, min reported"),
+        "published_ms": PUBLISHED_SCALAR_T2_4096_B128_MS,
+        "published_gbs": payload.size / (PUBLISHED_SCALAR_T2_4096_B128_MS * 1e-3) / 1e9,
+        "published_reference": "docs/benchmarks/avx2-2026-10-12 run 1, one thread of a Core Ultra 7 155H",
+    }
     return {
         "value": payload.size * iterations / elapsed / 1e9,
         "unit": "GB/s",
@@ -889,6 +912,7 @@ def cpu_baseline(payload, rows, columns, block, x, seconds) -> dict:
                    f"1 thread pinned to core {core}; min {min(samples) * 1e3:.3f} ms, "
                    f"median {sorted(samples)[len(samples) // 2] * 1e3:.3f} ms; host: {host['model']}, "
                    f"{host['logical_cpus']} logical CPUs ({host['available']} available to this process)"),
+        "scalar": scalar,
     }
 
 
