@@ -773,7 +773,8 @@ def pin_one_core():
 def cpu_format(data, rows, columns, fmt, x, quantized, seconds) -> dict:
     """Restated reference AVX2 path of one format (oracle) on one host core, warm payload, bounded sample:
     Ternary2Avx2Kernel for Ternary2, QuantizedAvx2Kernel for Q8_0 / Q4_0, and for the K formats the decode
-    path (Q8KCodec.QuantizeRow of x, then QuantizedKAvx2Kernel.ExecuteQuantizedTiled at one position)."""
+    path (Q8KCodec.QuantizeRow of x, then QuantizedKAvx2Kernel.ExecuteQuantizedTiled at one position); and the
+    scalar reference of the format (`cpu_scalar_*`)."""
     from oracle import oracle as O
 
     y = np.zeros(rows, np.float32)
@@ -790,8 +791,21 @@ def cpu_format(data, rows, columns, fmt, x, quantized, seconds) -> dict:
         run()
         samples.append(time.perf_counter() - t0)
     best = min(samples)
+    # The scalar reference beside it (Ternary2MatVec.ExecuteScalarCore / QuantizedMatVec.ExecuteScalar,
+    # restated in oracle/satori_oracle.c), a short bounded sample: at least three runs, min reported.
+    if fmt is None:
+        scalar_run = lambda: O.t2_matvec_scalar(data, rows, columns, quantized, x)
+    else:
+        scalar_run = lambda: O.q_matvec_scalar(data, rows, columns, int(fmt), x)
+    scalar_samples, s0 = [], time.perf_counter()
+    while time.perf_counter() - s0 < 0.5 or len(scalar_samples) < 3:
+        t0 = time.perf_counter()
+        scalar_run()
+        scalar_samples.append(time.perf_counter() - t0)
     return {"cpu_gbs": data.size / best / 1e9, "cpu_ms_min": best * 1e3,
-            "cpu_ms_median": sorted(samples)[len(samples) // 2] * 1e3, "cpu_runs": len(samples)}
+            "cpu_ms_median": sorted(samples)[len(samples) // 2] * 1e3, "cpu_runs": len(samples),
+            "cpu_scalar_gbs": data.size / min(scalar_samples) / 1e9, "cpu_scalar_ms_min": min(scalar_samples) * 1e3,
+            "cpu_scalar_runs": len(scalar_samples)}
 
 
 def cpu_decode_step(host, shapes, host_in, seconds) -> dict:
