@@ -205,7 +205,7 @@ def fp32_bound(data, rows, columns, fmt, x, block=None) -> np.ndarray:
 def check_case(ctx, case: Case, data, rows, columns, fmt, x, quantized) -> dict:
     """Parity of the launch that is timed, before it is timed (the reference benchmark validates before it
     measures, benchmarks/Satori.Benchmarks/Program.cs:38-61): one grouped launch, then every copy's output
-    against the oracle (checker only): Ternary2, Q8_0 and Q4_0 within 1e-5 * sum|w x| per row of the scalar
+    against the oracle, which only checks: Ternary2, Q8_0 and Q4_0 within 1e-5 * sum|w x| per row of the scalar
     restatement, K formats on the Q8_K path identical to the ExecuteQuantizedTiled composition."""
     from oracle import oracle as O
 
@@ -399,7 +399,7 @@ def decode_step(ctx, events, model: DecodeModel, steps: int, warmup: int, eager_
     for grp, names in zip(groups, members):
         if names == ("gate", "up"):
             grp.set_output_swiglu(act)  # SwiGLU of the gate/up outputs, in the same launch; down quantizes it
-    # Parity before timing: every launch of the step, one at a time, against the oracle (checker only).
+    # Parity before timing: every launch of the step, one at a time, against the oracle (not timed).
     from oracle import oracle as O
     expected = {}
     for name, (r, c, fmt) in model.shapes.items():
@@ -633,7 +633,7 @@ def prefill(ctx, events, model: DecodeModel, steps: int, warmup: int, positions:
     run()
     ctx.synchronize()
     first_ms = (time.perf_counter() - t0) * 1e3
-    # Parity before timing (checker only): the last layer's outputs at sampled positions of both chunks
+    # Parity before timing (the oracle is not timed): the last layer's outputs at sampled positions of both chunks
     # (tile edges 0/31/32, chunk edges 255/256, the last position) and the output projection, bit-exact.
     from oracle import oracle as O
     sampled = [p for p in (0, 1, 31, 32, 100, 255, 256, 257, 300, 400, 511) if p < positions]
