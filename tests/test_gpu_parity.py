@@ -175,6 +175,62 @@ def test_ternary2_grouped_pair_tables(context, block, columns, members):
         m.dispose()
 
 
+# Groups whose ranges cut items into two pieces (the pieces' row sums are added by the fix-up kernel). 64 members
+# of 4096^2 make 16,384 (panel group, tile) units over 1,024 workgroups: every range is exactly half an item, a
+# lone earlier or later piece; 160 members make 40,960 units, 40 a range, so a range holds a whole item and an
+# item's earlier tiles, or a later piece and an earlier piece. Each group runs eagerly twice and replays three
+# times from a captured step, with eager launches between the replays; every launch gives the eager bits, within
+# the reference's bound of the scalar restatement and of the FP64 product.
+@pytest.mark.parametrize("members", [64, 160])
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_ternary2_grouped_cut_items_eager_and_replayed(context, block, members):
+    g = rng(4242 + block + members)
+    rows = columns = 4096
+    payload = _t2_random_payload(g, rows, columns, block)
+    m = context.create_ternary2(rows, columns, block, payload)
+    xs = [g.uniform(-1, 1, columns).astype(np.float32) for _ in range(3)]
+    dxs = [context.alloc(x.nbytes) for x in xs]
+    for p, x in zip(dxs, xs):
+        context.upload(p, x)
+    ys = [context.alloc(4 * rows) for _ in range(members)]
+    group = S.HipGroup(context, [m] * members, [dxs[i % 3] for i in range(members)], ys)
+    step = None
+
+    def run(launch):
+        for p in ys:
+            context.upload(p, np.full(rows, np.nan, np.float32))
+        launch()
+        context.synchronize()
+        return [context.download(np.zeros(rows, np.float32), p).view(np.uint32) for p in ys]
+
+    try:
+        eager = run(group.execute)
+        wq = O.t2_dequantize(payload, rows, columns, block)
+        for j, x in enumerate(xs):
+            bound = relative_bound(wq, x)
+            scalar = O.t2_matvec_scalar(payload, rows, columns, block, x)
+            exact = fp64_matvec(wq, x)
+            for i in range(j, members, 3):
+                assert_within(eager[i].view(np.float32), scalar, bound, f"member {i} B{block} vs scalar")
+                assert_within(eager[i].view(np.float32), exact, bound, f"member {i} B{block} vs FP64")
+        again = run(group.execute)
+        assert all(np.array_equal(a, b) for a, b in zip(again, eager)), "second eager launch differs"
+        step = S.HipStep(context, [group])
+        for replay in range(3):
+            got = run(step.execute)
+            for i, (a, b) in enumerate(zip(got, eager)):
+                assert np.array_equal(a, b), f"replay {replay}: member {i} differs from the eager launch"
+            group.execute()  # eager launch between replays
+            context.synchronize()
+    finally:
+        if step is not None:
+            step.dispose()
+        group.dispose()
+        for p in ys + dxs:
+            context.free(p)
+        m.dispose()
+
+
 # A single matrix at one position takes the sliced plan when the chip holds all of its workgroups at once:
 # eight waves per workgroup when at most eight slices of eight tiles cover a row and the workgroups fit,
 # else sixteen; rows too wide for eight slices of sixteen tiles get sixteen waves taking several tiles each.
