@@ -86,13 +86,17 @@ int satori_hip_context_stream(satori_hip_context* context, void** stream);
 
 /* Ternary2Matrix.FromPacked (src/Satori.Core/Ternary2Matrix.cs:73-81) + ValidatePayload (:83-101),
  * then upload. Also the upload step of MappedTernary2Matrix (src/Satori.Core/MappedTernary2Matrix.cs:9-35):
- * pass the mapped payload window. */
+ * pass the mapped payload window. The payload is copied to the device as is, regrouped and checked there;
+ * a failing payload is named by the reference's rule (first failing block, its scale before its codes) and
+ * fails with its message. */
 int satori_hip_ternary2_create(satori_hip_context* context, int rows, int columns, int block_size,
                                const void* payload, size_t payload_length, satori_hip_matrix** matrix);
 
 /* IQuantizedMatrixFactory.Create (src/Satori.Core/IQuantizedMatrixFactory.cs:6) with the
  * QuantizedMatrixShape checks (src/Satori.Core/QuantizedMatrixShape.cs:5-22) and
- * QuantizedMatVec.ValidatePayload (src/Satori.Core/QuantizedMatVec.cs:28-42), then upload. */
+ * QuantizedMatVec.ValidatePayload (src/Satori.Core/QuantizedMatVec.cs:28-42): the payload is uploaded (Q6_K,
+ * Q8_0 and Q4_0 regrouped on the device) and its block scales checked there; a non-finite scale frees the
+ * copy and fails with the first bad block's offset, as the reference names it. */
 int satori_hip_quantized_create(satori_hip_context* context, int rows, int columns, int format,
                                 const void* payload, size_t payload_length, satori_hip_matrix** matrix);
 
@@ -105,7 +109,8 @@ int satori_hip_ternary2_open(satori_hip_context* context, const char* path, sato
  * and byte length as Ternary2. The device copy is the lossless Ternary2 equivalent, so execution is the
  * Ternary2 MatVec (TernaryBitplaneMatVec.Execute, src/Satori.Core/TernaryBitplaneMatVec.cs:8-12) and the
  * matrix reports format SATORI_HIP_TERNARY2. */
-/* TernaryBitplaneMatrix.FromPacked (TernaryBitplaneMatrix.cs:56-62) + Validate (:64-85), then upload. */
+/* TernaryBitplaneMatrix.FromPacked (TernaryBitplaneMatrix.cs:56-62) + Validate (:64-85), then upload: the
+ * bitplane payload is copied to the device as is, converted, regrouped and checked there. */
 int satori_hip_bitplane_create(satori_hip_context* context, int rows, int columns, int block_size,
                                const void* payload, size_t payload_length, satori_hip_matrix** matrix);
 /* TernaryBitplaneMatrix.Load (TernaryBitplaneMatrix.cs:98-117) of an STB1 file, then upload; every file

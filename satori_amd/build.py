@@ -22,7 +22,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["satori_hip.hip", "gemv_float.hip", "gemv_t2.hip", "gemv_kint.hip", "gemv_kmfma.hip", "gemv_fbatch.hip",
-           "scale_check.hip", "host_copy.hip",
+           "scale_check.hip", "host_copy.hip", "upload.hip",
            "transformer_ops.hip",
            "host_cpu.cpp", "gguf.cpp"]
 

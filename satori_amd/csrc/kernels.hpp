@@ -74,6 +74,29 @@ inline T2Layout t2_layout(int rows, int columns, int block_size) {
     return l;
 }
 
+// Upload-time regrouping on the device (upload.hip), one chunk of whole units at a time, into a destination
+// the caller has zeroed. Ternary2: rows [64 first_panel, 64 first_panel + chunk_rows) of the packed payload
+// (their bytes start at `packed`; Ternary2 or ternary bitplane blocks) into the panel layout; *bad is set to 1
+// when a block breaks the payload rule of Ternary2Matrix.ValidatePayload (for bitplanes, equivalently,
+// TernaryBitplaneMatrix.Validate; the caller names it from the host bytes).
+struct T2Regroup {
+    int first_panel, chunk_rows;      // the chunk: whole panels
+    int columns, block_size, blocks;  // the matrix
+    int block_bytes;
+    int64_t row_bytes;
+    int chunks, slots;                // T2Layout of the matrix
+    int64_t codes_bytes;
+    int bitplanes;                    // nonzero: the source blocks are ternary bitplane blocks
+};
+hipError_t launch_t2_regroup(const uint8_t* packed, const T2Regroup& r, uint8_t* out, uint32_t* bad,
+                             hipStream_t stream);
+// Q6_K: blocks [first, first + count) of a matrix of n blocks, their packed bytes at `packed`.
+hipError_t launch_q6k_regroup(const uint8_t* packed, int64_t first, int64_t count, int64_t n, uint8_t* out,
+                              hipStream_t stream);
+// Q8_0 / Q4_0: likewise.
+hipError_t launch_legacy_regroup(const uint8_t* packed, int64_t first, int64_t count, int64_t n, int format,
+                                 uint8_t* out, hipStream_t stream);
+
 // ---- Q6_K device layout ----
 // The device copy of a Q6_K matrix holds the same bytes regrouped so that every load is aligned: for its
 // n = rows * blocks blocks in row-major order, n records of 192 code bytes (block quarter c = 2h + t at

@@ -33,6 +33,11 @@ namespace {
 // Slack after every payload: the misaligned-block loaders read up to 4 bytes past a block.
 constexpr size_t kPayloadSlack = 256;
 
+// The ABI's format codes are the kernels' own (shapes carry the ABI code into the launches).
+static_assert(SATORI_HIP_Q8_0 == satori::kQ8_0 && SATORI_HIP_Q4_0 == satori::kQ4_0 && SATORI_HIP_Q4_K == satori::kQ4_K &&
+                  SATORI_HIP_Q6_K == satori::kQ6_K && SATORI_HIP_TERNARY2 == satori::kTernary2,
+              "format codes");
+
 void check_hip(hipError_t e, const char* what) {
     if (e != hipSuccess)
         fail(e == hipErrorOutOfMemory ? SATORI_HIP_E_OUT_OF_MEMORY : SATORI_HIP_E_DEVICE,
@@ -86,6 +91,7 @@ struct satori_hip_context {
     bool live = true;
     int matrices = 0;
     satori::DeviceBuffer x, y, q8k;
+    satori::DeviceBuffer upload_stage, upload_flag;  // packed payloads on their way into the device layouts
     // Split-attention partials (grouped attention over long prefixes), one buffer per stream the attention
     // runs on, so attentions on different streams never share one; attentions on one stream run in order.
     std::vector<std::pair<hipStream_t, satori::DeviceBuffer>> attention;
@@ -320,36 +326,6 @@ bool overlaps_transform(const void* p, size_t bytes, const InputTransform& t, in
     }
 }
 
-// One 16-byte code record rotated left by 2 bits as a 128-bit little-endian integer.
-void rotate_record(uint8_t* out, const uint8_t* in) {
-    uint32_t w[4], r[4];
-    std::memcpy(w, in, 16);
-    for (int d = 0; d < 4; ++d) r[d] = (w[d] << 2) | (w[(d + 3) & 3] >> 30);
-    std::memcpy(out, r, 16);
-}
-
-// Regroups a validated packed Ternary2 payload (rows of [f32 scale][B / 4 code bytes] blocks) into the
-// panel layout: row r is lane r % 64 of panel r / 64; its 16-byte code chunks (rotated) and block scales
-// land at the T2Layout positions; padding stays zero.
-std::vector<uint8_t> ternary2_panels(const Shape& s, const uint8_t* packed) {
-    const T2Layout l = t2_layout(s.rows, s.columns, s.block_size);
-    std::vector<uint8_t> out(static_cast<size_t>(l.bytes), 0);
-    const int chunks_per_block = s.block_size / 64;
-    for (int r = 0; r < s.rows; ++r) {
-        const int64_t panel = r / kT2PanelRows, lane = r % kT2PanelRows;
-        const uint8_t* row = packed + static_cast<int64_t>(r) * s.row_bytes;
-        for (int b = 0; b < s.blocks; ++b) {
-            const uint8_t* block = row + static_cast<int64_t>(b) * s.block_bytes;
-            std::memcpy(&out[l.codes_bytes + ((panel * l.slots + b) * 64 + lane) * 4], block, 4);
-            for (int i = 0; i < chunks_per_block; ++i) {
-                const int64_t chunk = static_cast<int64_t>(b) * chunks_per_block + i;
-                rotate_record(&out[((panel * l.chunks + chunk) * 64 + lane) * 16], block + 4 + 16 * i);
-            }
-        }
-    }
-    return out;
-}
-
 // Scratch of a Ternary2 plan, with the plan's tables copied to its start.
 void* allocate_t2_scratch(const T2Plan& plan) {
     if (plan.workgroups < 1)
@@ -364,48 +340,66 @@ void* allocate_t2_scratch(const T2Plan& plan) {
     return p;
 }
 
-// Regroups a validated Q6_K payload into the device layout described with kernels.hpp's Q6_K layout:
-// aligned 48-byte quarter records, then each quarter's four scales, then the FP16 d values.
-std::vector<uint8_t> q6k_regroup(const Shape& s, const uint8_t* packed) {
-    const int64_t n = static_cast<int64_t>(s.rows) * s.blocks;  // blocks are contiguous row after row
-    std::vector<uint8_t> out(static_cast<size_t>(n) * 210);
-    uint8_t* codes = out.data();
-    uint8_t* scales = codes + n * 192;
-    uint8_t* ds = codes + n * 208;
-    for (int64_t i = 0; i < n; ++i) {
-        const uint8_t* block = packed + i * 210;
-        for (int c = 0; c < 4; ++c) {
-            const int h = c >> 1, t = c & 1;
-            uint8_t* record = codes + i * 192 + 48 * c;
-            std::memcpy(record, block + 64 * h + 16 * t, 16);
-            std::memcpy(record + 16, block + 64 * h + 32 + 16 * t, 16);
-            std::memcpy(record + 32, block + 128 + 32 * h + 16 * t, 16);
-            for (int k = 0; k < 4; ++k) scales[i * 16 + 4 * c + k] = block[192 + 8 * h + 2 * k + t];
-        }
-        std::memcpy(ds + i * 2, block + 208, 2);
-    }
-    return out;
+// Packed bytes staged on the device per chunk of the regrouping uploads (a chunk holds at least one unit).
+constexpr int64_t kUploadStageBytes = 64ll << 20;
+
+// Bytes of the device layout of a matrix of shape s.
+int64_t device_layout_bytes(const Shape& s) {
+    if (s.format == SATORI_HIP_TERNARY2) return t2_layout(s.rows, s.columns, s.block_size).bytes;
+    return s.byte_length;
 }
 
-// Regroups a validated Q8_0 / Q4_0 payload into the device layout of kernels.hpp: aligned code records, then
-// the FP16 scales. Q4_0 code bytes are stored XOR 0x88 (each nibble q as q ^ 8, the two's-complement nibble
-// of q - 8).
-std::vector<uint8_t> legacy_regroup(const Shape& s, const uint8_t* packed) {
-    const int64_t n = static_cast<int64_t>(s.rows) * s.blocks;
-    const int record = legacy_record_bytes(s.format);
-    std::vector<uint8_t> out(static_cast<size_t>(n) * s.block_bytes);
-    uint8_t* codes = out.data();
-    uint8_t* scales = codes + n * record;
-    const bool q4 = s.format == SATORI_HIP_Q4_0;
-    for (int64_t i = 0; i < n; ++i) {
-        const uint8_t* block = packed + i * s.block_bytes;
-        std::memcpy(scales + i * 2, block, 2);
-        uint8_t* dst = codes + i * record;
-        std::memcpy(dst, block + 2, static_cast<size_t>(record));
-        if (q4)
-            for (int k = 0; k < record; ++k) dst[k] ^= 0x88;
+// Copies a packed payload into the device layout at `out` (device_layout_bytes of it, zeroed here): formats
+// stored as packed are copied, the others pass through the context's staging buffer in chunks of whole units
+// (Ternary2: 64-row panels; Q6_K, Q8_0, Q4_0: blocks) and are regrouped on the device (upload.hip); with
+// `bitplanes` a Ternary2-shaped payload holds ternary bitplane blocks, converted on the way. Returns false when
+// a Ternary2 block breaks the payload rule (the device check of Ternary2Matrix.ValidatePayload).
+bool upload_layout(satori_hip_context* c, const Shape& s, const uint8_t* payload, uint8_t* out, bool bitplanes) {
+    const int64_t out_bytes = device_layout_bytes(s);
+    const bool t2 = s.format == SATORI_HIP_TERNARY2;
+    if (!t2 && s.format != SATORI_HIP_Q6_K && s.format != SATORI_HIP_Q8_0 && s.format != SATORI_HIP_Q4_0) {
+        check_hip(hipMemcpy(out, payload, static_cast<size_t>(out_bytes), hipMemcpyHostToDevice), "weight upload");
+        return true;
     }
-    return out;
+    hipStream_t st = c->stream;
+    check_hip(hipMemsetAsync(out, 0, static_cast<size_t>(out_bytes), st), "weight upload");
+    const int64_t n = static_cast<int64_t>(s.rows) * s.blocks;
+    const int panels = (s.rows + kT2PanelRows - 1) / kT2PanelRows;
+    const int64_t unit_bytes = t2 ? kT2PanelRows * s.row_bytes : s.block_bytes;
+    const int64_t units = t2 ? panels : n;
+    const int64_t per_chunk = std::max<int64_t>(1, kUploadStageBytes / unit_bytes);
+    c->upload_stage.reserve(static_cast<size_t>(std::min(per_chunk * unit_bytes, s.byte_length)));
+    uint8_t* stage = static_cast<uint8_t*>(c->upload_stage.ptr);
+    uint32_t* flag = nullptr;
+    if (t2) {
+        c->upload_flag.reserve(sizeof(uint32_t));
+        flag = static_cast<uint32_t*>(c->upload_flag.ptr);
+        check_hip(hipMemsetAsync(flag, 0, sizeof(uint32_t), st), "weight upload");
+    }
+    const T2Layout l = t2 ? t2_layout(s.rows, s.columns, s.block_size) : T2Layout{};
+    for (int64_t u0 = 0; u0 < units; u0 += per_chunk) {
+        const int64_t count = std::min(per_chunk, units - u0);
+        const uint8_t* src = payload + u0 * unit_bytes;
+        if (t2) {
+            const int rows = static_cast<int>(std::min<int64_t>(count * kT2PanelRows, s.rows - u0 * kT2PanelRows));
+            check_hip(hipMemcpyAsync(stage, src, static_cast<size_t>(rows * s.row_bytes), hipMemcpyHostToDevice, st),
+                      "weight upload");
+            const T2Regroup r{static_cast<int>(u0), rows, s.columns, s.block_size, s.blocks, s.block_bytes,
+                              s.row_bytes, l.chunks, l.slots, l.codes_bytes, bitplanes ? 1 : 0};
+            check_hip(launch_t2_regroup(stage, r, out, flag, st), "weight regroup");
+        } else {
+            check_hip(hipMemcpyAsync(stage, src, static_cast<size_t>(count * unit_bytes), hipMemcpyHostToDevice, st),
+                      "weight upload");
+            if (s.format == SATORI_HIP_Q6_K)
+                check_hip(launch_q6k_regroup(stage, u0, count, n, out, st), "weight regroup");
+            else
+                check_hip(launch_legacy_regroup(stage, u0, count, n, s.format, out, st), "weight regroup");
+        }
+    }
+    uint32_t bad = 0;
+    if (t2) check_hip(hipMemcpyAsync(&bad, flag, sizeof(bad), hipMemcpyDeviceToHost, st), "weight upload");
+    check_hip(hipStreamSynchronize(st), "weight upload");
+    return bad == 0;
 }
 
 // Device allocations of one matrix: the weights (+ slack) and, for a split Ternary2 plan, its scratch.
@@ -430,35 +424,69 @@ void free_matrix(satori_hip_matrix* m) {
     m->scratch = nullptr;
 }
 
-satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
+// A device matrix holding `payload` (already checked against the shape) in its device layout. A Ternary2 payload
+// (or, with `bitplanes`, a ternary bitplane payload, converted to its Ternary2 equivalent) is checked on the
+// device as it is regrouped; one that breaks the rule is named by the host restatement of
+// Ternary2Matrix.ValidatePayload (TernaryBitplaneMatrix.Validate), which throws the reference's error (the device
+// copy is freed first).
+satori_hip_matrix* upload(satori_hip_context* c, const Shape& s, const uint8_t* payload, bool bitplanes = false) {
     require_not_capturing(c);
     set_device(c);
-    std::vector<uint8_t> regrouped;
-    const uint8_t* source = payload;
-    int64_t bytes = s.byte_length;
-    if (s.format == SATORI_HIP_TERNARY2)
-        regrouped = ternary2_panels(s, payload);
-    else if (s.format == SATORI_HIP_Q6_K)
-        regrouped = q6k_regroup(s, payload);
-    else if (s.format == SATORI_HIP_Q8_0 || s.format == SATORI_HIP_Q4_0)
-        regrouped = legacy_regroup(s, payload);
-    if (!regrouped.empty()) {
-        source = regrouped.data();
-        bytes = static_cast<int64_t>(regrouped.size());
-    }
+    const int64_t bytes = device_layout_bytes(s);
     auto* m = new satori_hip_matrix();
     m->context = c;
     m->shape = s;
+    bool valid = true;
     try {
         allocate_matrix(m, bytes);
-        check_hip(hipMemcpy(m->payload, source, static_cast<size_t>(bytes), hipMemcpyHostToDevice), "weight upload");
+        valid = upload_layout(c, s, payload, m->payload, bitplanes);
         check_hip(hipMemset(m->payload + bytes, 0, kPayloadSlack), "weight upload");
     } catch (...) {
         free_matrix(m);
         delete m;
         throw;
     }
+    if (!valid) {
+        free_matrix(m);
+        delete m;
+        if (bitplanes) {
+            validate_bitplane(s, payload);
+            fail(SATORI_HIP_E_ARGUMENT, "Overlapping bits, invalid padding or noncanonical zero. (Parameter 'data')");
+        }
+        validate_ternary2(s, payload);
+        fail(SATORI_HIP_E_ARGUMENT, "Invalid weight code or padding.");
+    }
     c->matrices++;
+    return m;
+}
+
+// upload() of a GGUF-format payload whose block scales are then checked on the device (QuantizedMatVec's
+// finiteness rule, scale_check.hip). A payload that fails is named by the host restatement of the rule
+// (validate_quantized), which throws the reference's error with the first bad block's offset.
+satori_hip_matrix* upload_checked(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
+    satori_hip_matrix* m = upload(c, s, payload);
+    uint32_t bad = 0;
+    try {
+        c->upload_flag.reserve(sizeof(uint32_t));
+        uint32_t* flag = static_cast<uint32_t*>(c->upload_flag.ptr);
+        check_hip(hipMemsetAsync(flag, 0, sizeof(uint32_t), c->stream), "scale check");
+        check_hip(launch_scale_check(m->payload, static_cast<int64_t>(s.rows) * s.blocks, s.format, flag, c->stream),
+                  "scale check");
+        check_hip(hipMemcpyAsync(&bad, flag, sizeof(bad), hipMemcpyDeviceToHost, c->stream), "scale check");
+        check_hip(hipStreamSynchronize(c->stream), "scale check");
+    } catch (...) {
+        free_matrix(m);
+        delete m;
+        c->matrices--;
+        throw;
+    }
+    if (bad != 0) {
+        free_matrix(m);
+        delete m;
+        c->matrices--;
+        validate_quantized(s, payload);  // names the first bad block
+        fail(SATORI_HIP_E_INVALID_DATA, "Nonfinite block scale.");
+    }
     return m;
 }
 
@@ -649,7 +677,17 @@ struct MappedFile {
 // TernaryBitplaneMatrix.Load (src/Satori.Core/TernaryBitplaneMatrix.cs:98-117) with
 // TernaryBitplaneFileFormat.ReadHeader (src/Satori.Core/TernaryBitplaneFileFormat.cs:13-19): the STQ2 header
 // with magic "STB1"; every failure is InvalidDataException. Returns the shape of a valid file.
-Shape read_bitplane_file(const MappedFile& f) {
+// MappedTernaryBitplaneMatrix: shape and payload failures of a file surface as InvalidDataException.
+[[noreturn]] void bitplane_file_failure(const Failure& e) {
+    if (e.status == SATORI_HIP_E_ARGUMENT || e.status == SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE ||
+        e.status == SATORI_HIP_E_OVERFLOW)
+        fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane file.");
+    throw e;
+}
+
+// Shape of an STB1 file; its payload is validated here only when `validate` (an upload validates it on the
+// device instead, bitplane_file_failure naming its failures as this function does).
+Shape read_bitplane_file(const MappedFile& f, bool validate = true) {
     if (f.length < 32) fail(SATORI_HIP_E_INVALID_DATA, "Truncated bitplane header.");
     const uint8_t* h = f.bytes;
     if (std::memcmp(h, "STB1", 4) != 0) fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane magic.");
@@ -668,21 +706,17 @@ Shape read_bitplane_file(const MappedFile& f) {
         if (declared != s.byte_length) fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane header fields.");
         if (static_cast<int64_t>(f.length) != 32 + s.byte_length)
             fail(SATORI_HIP_E_INVALID_DATA, "Incorrect bitplane file length.");
-        validate_bitplane(s, h + 32);
+        if (validate) validate_bitplane(s, h + 32);
     } catch (const Failure& e) {
-        if (e.status == SATORI_HIP_E_ARGUMENT || e.status == SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE ||
-            e.status == SATORI_HIP_E_OVERFLOW)
-            fail(SATORI_HIP_E_INVALID_DATA, "Invalid bitplane file.");
-        throw;
+        bitplane_file_failure(e);
     }
     return s;
 }
 
-// A bitplane payload executes as its lossless Ternary2 equivalent (same bytes per block, same scales).
+// A bitplane payload executes as its lossless Ternary2 equivalent (same bytes per block, same scales): upload()
+// converts and validates it on the device.
 satori_hip_matrix* upload_bitplane(satori_hip_context* c, const Shape& s, const uint8_t* payload) {
-    std::vector<uint8_t> ternary(static_cast<size_t>(s.byte_length));
-    bitplane_to_ternary2(s, payload, ternary.data());
-    return upload(c, s, ternary.data());
+    return upload(c, s, payload, true);
 }
 
 const satori::GgufFile& live_file(const satori_hip_gguf* f) {
@@ -775,6 +809,8 @@ int satori_hip_context_destroy(satori_hip_context* c) {
         c->x.release();
         c->y.release();
         c->q8k.release();
+        c->upload_stage.release();
+        c->upload_flag.release();
         for (auto& entry : c->attention) entry.second.release();
         c->attention.clear();
         c->host_x.release();
@@ -803,10 +839,9 @@ int satori_hip_ternary2_create(satori_hip_context* c, int rows, int columns, int
         require(payload, "payload");
         if (static_cast<int64_t>(payload_length) != s.byte_length)
             fail(SATORI_HIP_E_ARGUMENT, "Payload length must match matrix dimensions.");
-        validate_ternary2(s, static_cast<const uint8_t*>(payload));
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(c);
-        *matrix = upload(c, s, static_cast<const uint8_t*>(payload));
+        *matrix = upload(c, s, static_cast<const uint8_t*>(payload));  // validates the payload as it regroups it
     });
 }
 
@@ -820,10 +855,9 @@ int satori_hip_quantized_create(satori_hip_context* c, int rows, int columns, in
         require(payload, "payload");
         if (static_cast<int64_t>(payload_length) != s.byte_length)
             fail(SATORI_HIP_E_ARGUMENT, "Incorrect quantized payload length.");
-        validate_quantized(s, static_cast<const uint8_t*>(payload));
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(c);
-        *matrix = upload(c, s, static_cast<const uint8_t*>(payload));
+        *matrix = upload_checked(c, s, static_cast<const uint8_t*>(payload));  // scales checked on the device
     });
 }
 
@@ -870,7 +904,9 @@ int satori_hip_ternary2_open(satori_hip_context* c, const char* path, satori_hip
             if (declared != s.byte_length) fail(SATORI_HIP_E_INVALID_DATA, "Payload length disagrees with matrix shape.");
             if (static_cast<int64_t>(length) != 32 + s.byte_length)
                 fail(SATORI_HIP_E_INVALID_DATA, "Truncated payload or trailing file data.");
-            validate_ternary2(s, h + 32);
+            std::lock_guard<std::mutex> guard(c->lock);
+            require_live(c);
+            *matrix = upload(c, s, h + 32);  // validates the payload as it regroups it
         } catch (const Failure& f) {
             // MappedTernary2Matrix.cs:25-28: shape and payload failures surface as InvalidDataException.
             if (f.status == SATORI_HIP_E_ARGUMENT || f.status == SATORI_HIP_E_ARGUMENT_OUT_OF_RANGE ||
@@ -878,9 +914,6 @@ int satori_hip_ternary2_open(satori_hip_context* c, const char* path, satori_hip
                 fail(SATORI_HIP_E_INVALID_DATA, "Invalid Ternary2 shape or payload.");
             throw;
         }
-        std::lock_guard<std::mutex> guard(c->lock);
-        require_live(c);
-        *matrix = upload(c, s, h + 32);
     });
 }
 
@@ -894,10 +927,9 @@ int satori_hip_bitplane_create(satori_hip_context* c, int rows, int columns, int
         require(payload, "payload");
         if (static_cast<int64_t>(payload_length) != s.byte_length)
             fail(SATORI_HIP_E_ARGUMENT, "Incorrect bitplane payload length. (Parameter 'payload')");
-        validate_bitplane(s, static_cast<const uint8_t*>(payload));
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(c);
-        *matrix = upload_bitplane(c, s, static_cast<const uint8_t*>(payload));
+        *matrix = upload_bitplane(c, s, static_cast<const uint8_t*>(payload));  // validates as it converts
     });
 }
 
@@ -908,10 +940,14 @@ int satori_hip_bitplane_open(satori_hip_context* c, const char* path, satori_hip
         require_live(c);
         require(path, "path");
         MappedFile f(path);
-        const Shape s = read_bitplane_file(f);
+        const Shape s = read_bitplane_file(f, false);
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(c);
-        *matrix = upload_bitplane(c, s, f.bytes + 32);
+        try {
+            *matrix = upload_bitplane(c, s, f.bytes + 32);  // validates the payload as it converts it
+        } catch (const Failure& e) {
+            bitplane_file_failure(e);
+        }
     });
 }
 
@@ -1645,35 +1681,7 @@ int satori_hip_gguf_matrix_create(satori_hip_context* c, const satori_hip_gguf* 
         const uint8_t* bytes = f.bytes() + t.offset;  // the whole payload: ReadTensor(name, 0, ByteLength)
         std::lock_guard<std::mutex> guard(c->lock);
         require_live(c);
-        satori_hip_matrix* m = upload(c, s, bytes);
-        uint32_t bad = 0;
-        DeviceBuffer flag;
-        struct Release {
-            DeviceBuffer& buffer;
-            ~Release() { buffer.release(); }
-        } release_flag{flag};
-        try {
-            flag.reserve(sizeof(uint32_t));
-            check_hip(hipMemsetAsync(flag.ptr, 0, sizeof(uint32_t), c->stream), "scale check");
-            check_hip(launch_scale_check(m->payload, static_cast<int64_t>(s.rows) * s.blocks, format,
-                                         static_cast<uint32_t*>(flag.ptr), c->stream),
-                      "scale check");
-            check_hip(hipMemcpyAsync(&bad, flag.ptr, sizeof(bad), hipMemcpyDeviceToHost, c->stream), "scale check");
-            check_hip(hipStreamSynchronize(c->stream), "scale check");
-        } catch (...) {
-            free_matrix(m);
-            delete m;
-            c->matrices--;
-            throw;
-        }
-        if (bad != 0) {
-            free_matrix(m);
-            delete m;
-            c->matrices--;
-            validate_quantized(s, bytes);  // names the first bad block, as the host check does
-            fail(SATORI_HIP_E_INVALID_DATA, "Nonfinite block scale.");
-        }
-        *matrix = m;
+        *matrix = upload_checked(c, s, bytes);
     });
 }
 

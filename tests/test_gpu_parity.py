@@ -1125,6 +1125,97 @@ def test_create_rejects_invalid_payloads(context):
         context.create_ternary2(1, 1, 64, payload)
 
 
+def _t2_block_offset(columns: int, block: int, row: int, index: int) -> int:
+    blocks = -(-columns // block)
+    return (row * blocks + index) * (4 + block // 4)
+
+
+def test_device_checked_uploads_name_the_first_failure(context):
+    # Ternary2, bitplane and GGUF-format payloads are checked on the device as they are regrouped; a failure is
+    # then named by the host rule: the first failing block in row-major order, its scale checked before its
+    # codes (Ternary2Matrix.cs:83-101, TernaryBitplaneMatrix.cs:64-85, QuantizedMatVec.cs:28-42), with the
+    # reference's message. A failed upload leaves nothing behind: the next valid one succeeds.
+    rows, columns, block = 130, 1000, 128  # ragged last panel and last block
+    good = S.Ternary2Matrix.quantize(rng(5).standard_normal((rows, columns)).astype(np.float32), rows, columns,
+                                     block).data.copy()
+
+    def expect(payload, error, message):
+        with pytest.raises(error) as e:
+            context.create_ternary2(rows, columns, block, payload).dispose()
+        assert message in str(e.value), str(e.value)
+
+    bad = good.copy()
+    bad[_t2_block_offset(columns, block, 70, 3) + 4] |= 3  # code 3 in row 70
+    o = _t2_block_offset(columns, block, 100, 0)
+    bad[o:o + 4] = np.frombuffer(np.float32(np.nan).tobytes(), np.uint8)  # a later bad scale
+    expect(bad, S.ArgumentException, "Invalid weight code or padding.")
+    o = _t2_block_offset(columns, block, 70, 3)
+    bad[o:o + 4] = np.frombuffer(np.uint32(0x80000000).tobytes(), np.uint8)  # -0 scale in the same block
+    expect(bad, S.ArgumentException, "Invalid block scale.")
+    pad = good.copy()
+    pad[_t2_block_offset(columns, block, 129, 7) + 4 + (1000 - 7 * 128) // 4] |= 1  # a code past column 999
+    expect(pad, S.ArgumentException, "Invalid weight code or padding.")
+    zero = good.copy()
+    o = _t2_block_offset(columns, block, 0, 0)
+    zero[o:o + 4] = 0  # scale 0 with nonzero codes
+    expect(zero, S.ArgumentException, "Invalid weight code or padding.")
+    with context.create_ternary2(rows, columns, block, good) as m:
+        y = np.zeros(rows, np.float32)
+        x = rng(6).uniform(-1, 1, columns).astype(np.float32)
+        m.execute(x, y)
+        wq = O.t2_dequantize(good, rows, columns, block)
+        assert_within(y, O.t2_matvec_scalar(good, rows, columns, block, x), relative_bound(wq, x), "after failures")
+
+    tb = O.tb_from_t2(good, rows, columns, block)
+    overlap = tb.copy()
+    o = _t2_block_offset(columns, block, 65, 2)
+    overlap[o + 4] |= 1
+    overlap[o + 4 + block // 8] |= 1  # weight 0 in both planes
+    with pytest.raises(S.ArgumentException) as e:
+        context.create_bitplane(rows, columns, block, overlap).dispose()
+    assert "Overlapping bits, invalid padding or noncanonical zero." in str(e.value)
+    scale = tb.copy()
+    scale[o:o + 4] = np.frombuffer(np.float32(-1).tobytes(), np.uint8)
+    with pytest.raises(S.ArgumentException) as e:
+        context.create_bitplane(rows, columns, block, scale).dispose()
+    assert "Invalid bitplane scale." in str(e.value)
+
+    for fmt, at in ((BQ.Q6_K, 208), (BQ.Q4_K, 2), (BQ.Q8_0, 0), (BQ.Q4_0, 0)):
+        r, c = 40, 512
+        data = S.quantize_weights(rng(7).standard_normal((r, c)).astype(np.float32) * 0.1, r, c, fmt).copy()
+        block_bytes = {BQ.Q6_K: 210, BQ.Q4_K: 144, BQ.Q8_0: 34, BQ.Q4_0: 18}[fmt]
+        for k in (37, 12):  # blocks 37 and 12 get an FP16 infinity; 12 comes first
+            data[k * block_bytes + at:k * block_bytes + at + 2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)
+        with pytest.raises(S.InvalidDataException) as e:
+            context.create(data, S.QuantizedMatrixShape(r, c, fmt)).dispose()
+        assert f"Nonfinite block scale at {12 * block_bytes}." in str(e.value), (fmt, str(e.value))
+
+
+def test_ternary2_upload_in_several_staged_chunks(context):
+    # A payload larger than the 64 MB staging chunk is regrouped panel range by panel range (257 panels of
+    # 16,384 columns at B = 256, 240 panels a chunk); every row of both chunks equals the oracle, and a bad code
+    # in the second chunk is found.
+    rows, columns, block = 257 * 64, 16384, 256
+    g = rng(8080)
+    payload = _t2_random_payload(g, rows, columns, block)
+    assert payload.size > 64 << 20
+    x = g.uniform(-1, 1, columns).astype(np.float32)
+    with context.create_ternary2(rows, columns, block, payload) as m:
+        y = np.zeros(rows, np.float32)
+        m.execute(x, y)
+    want = O.t2_matvec_scalar(payload, rows, columns, block, x)
+    # The bound 1e-5 * sum|w * x| per row, as a MatVec of the payload with every -1 code made +1 over |x| (the
+    # whole dequantized matrix would take a gigabyte).
+    absolute = payload.copy().reshape(-1, 4 + block // 4)
+    absolute[:, 4:] = (absolute[:, 4:] & 0x55) | ((absolute[:, 4:] >> 1) & 0x55)
+    bound = 1e-5 * O.t2_matvec_scalar(absolute.reshape(-1), rows, columns, block, np.abs(x)).astype(np.float64)
+    assert_within(y, want, bound + columns * TINY, "two staged chunks vs scalar")
+    bad = payload.copy()
+    bad[_t2_block_offset(columns, block, rows - 1, 63) + 4] |= 3
+    with pytest.raises(S.ArgumentException):
+        context.create_ternary2(rows, columns, block, bad).dispose()
+
+
 def test_k_batch_rejects_too_many_positions(context):
     data = S.quantize_weights(np.zeros((2, 256), np.float32), 2, 256, BQ.Q4_K)
     m = context.create(data, S.QuantizedMatrixShape(2, 256, BQ.Q4_K))
