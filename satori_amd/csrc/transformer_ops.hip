@@ -386,8 +386,31 @@ constexpr int kStagedQuery = 8192;     // query lanes staged in LDS; wider heads
 constexpr int kCombineChunk = 16;      // splits whose values one combine thread loads at a time
 constexpr int kCombineWeights = 1024;  // split weights the combine kernel holds in LDS at a time
 
+// Workgroup reduction of THREADS doubles (256: block_tree_256; 512: each of the first 64 threads first folds
+// its eight values in thread order, then the same shuffle tree), every thread getting the result.
+template <int THREADS>
 __device__ __forceinline__ double split_reduce(double v, double* red, bool take_max) {
-    return block_tree_256(v, red, take_max);
+    if constexpr (THREADS == 256) {
+        return block_tree_256(v, red, take_max);
+    } else {
+        static_assert(THREADS == 512, "split workgroups of 256 or 512 threads");
+        const int t = threadIdx.x;
+        auto op = [take_max](double a, double b) { return take_max ? fmax(a, b) : a + b; };
+        red[t] = v;
+        __syncthreads();
+        if (t < 64) {
+            double x = red[t];
+#pragma unroll
+            for (int k = 1; k < THREADS / 64; ++k) x = op(x, red[t + 64 * k]);
+#pragma unroll
+            for (int s2 = 32; s2 > 0; s2 >>= 1) x = op(x, __shfl_down(x, s2, 64));
+            if (t == 0) red[0] = x;
+        }
+        __syncthreads();
+        const double r = red[0];
+        __syncthreads();
+        return r;
+    }
 }
 
 // Workgroup reduction of 256 doubles through wave shuffles and four partials in LDS (every thread gets it).
@@ -440,15 +463,15 @@ int split_grid(int query_heads, int kv_heads, int splits) {
     return 8 * ((kv_heads * splits + 7) / 8) * group;
 }
 
-template <bool INPUTS>
-__global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const float* __restrict__ q,
+template <bool INPUTS, int THREADS>
+__global__ __launch_bounds__(THREADS) void attention_split_kernel(const float* __restrict__ q,
                                                                         const float* __restrict__ k,
                                                                         const float* __restrict__ v, int query_heads,
                                                                         int kv_heads, int head_dim, int tokens, int per,
                                                                         int splits, double* __restrict__ partial,
                                                                         DecodeInputs in, float* k_cache, float* v_cache) {
     extern __shared__ double es[];  // this split's exponentials (per), then the staged query lanes
-    __shared__ double red[kSplitThreads];
+    __shared__ double red[THREADS];
     // Workgroup -> (query head, split): the query heads that share a key/value head and a split run on one
     // XCD (workgroup ids are dealt to the 8 XCDs round-robin), so that XCD's L2 fetches their key and value
     // rows once for all of them (split_unit).
@@ -491,13 +514,15 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
         sn = rope[kk];
         cs = rope[pairs + kk];
     }
-    // The first 16 values of this thread's output lane and token half are loaded before anything else, so
-    // they arrive while the scores are computed.
-    const int count = t1 - t0, half = (count + 1) / 2;
+    // The first 16 values of this thread's output lane and token part are loaded before anything else, so
+    // they arrive while the scores are computed. Lane j of the head is summed in THREADS / 128 consecutive
+    // token parts (threads j, j + 128, ...).
+    constexpr int kParts = THREADS / 128;
+    const int count = t1 - t0, half = (count + kParts - 1) / kParts;
     const int vj0 = threadIdx.x & 127, vgroup = threadIdx.x >> 7;
     const int va = t0 + vgroup * half, vb = min(t1, va + half);
-    const bool v_new_here = has_new && vb == t1 && va < vb;  // this token half ends with the new row
-    const int vbc = v_new_here ? vb - 1 : vb;                // the half's rows read from the cache
+    const bool v_new_here = has_new && vb == t1 && va < vb;  // this token part ends with the new row
+    const int vbc = v_new_here ? vb - 1 : vb;                // the part's rows read from the cache
     float vpre[16];
     if (vj0 < head_dim) {
         const float* vj = v + kv_head * head_dim + vj0;
@@ -563,14 +588,14 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
             }
         }
     } else if (staged) {
-        for (int j = threadIdx.x; j < head_dim; j += kSplitThreads) qs[j] = qh[j];
+        for (int j = threadIdx.x; j < head_dim; j += THREADS) qs[j] = qh[j];
     }
     __syncthreads();
     // Scores: eight threads per token, thread p summing lanes [p * piece, (p + 1) * piece) of the key row in
     // order (16-byte loads, all in flight, when the eighths are whole quads), the eight partial sums then
     // added in order.
     double local_max = -INFINITY;
-    for (int base = t0; base < ts; base += kSplitThreads / 8) {
+    for (int base = t0; base < ts; base += THREADS / 8) {
         const int t = base + (threadIdx.x >> 3);
         double dot = 0;
         if (t < ts) {
@@ -630,20 +655,20 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
         }
         __syncthreads();
     }
-    const double m = split_reduce(local_max, red, true);
+    const double m = split_reduce<THREADS>(local_max, red, true);
     double part = 0;
-    for (int t = t0 + threadIdx.x; t < t1; t += kSplitThreads) {
+    for (int t = t0 + threadIdx.x; t < t1; t += THREADS) {
         const double e = exp(es[t - t0] - m);
         es[t - t0] = e;
         part = part + e;
     }
-    const double l = split_reduce(part, red, false);
+    const double l = split_reduce<THREADS>(part, red, false);
     double* out = partial + (static_cast<int64_t>(head) * splits + split) * (2 + head_dim);
     if (threadIdx.x == 0) {
         out[0] = m;
         out[1] = l;
     }
-    // Unnormalised sums: lane j of the head over two token halves (threads j and j + 128), added in order.
+    // Unnormalised sums: lane j of the head over its token parts (threads j, j + 128, ...), added in order.
     for (int j0 = 0; j0 < head_dim; j0 += 128) {
         const int j = j0 + vj0;
         double sum = 0;
@@ -668,7 +693,12 @@ __global__ __launch_bounds__(kSplitThreads) void attention_split_kernel(const fl
         }
         red[threadIdx.x] = sum;
         __syncthreads();
-        if (threadIdx.x < 128 && j < head_dim) out[2 + j] = red[threadIdx.x] + red[threadIdx.x + 128];
+        if (threadIdx.x < 128 && j < head_dim) {
+            double total = red[threadIdx.x] + red[threadIdx.x + 128];
+#pragma unroll
+            for (int k = 2; k < kParts; ++k) total = total + red[threadIdx.x + 128 * k];
+            out[2 + j] = total;
+        }
         __syncthreads();
     }
 }
@@ -919,6 +949,27 @@ size_t attention_scratch_bytes(int query_heads, int head_dim, int tokens) {
 
 namespace {
 
+// Threads of a split workgroup: 512 once a split holds at least kWideSplitTokens tokens (its score passes and
+// value loops, each a dependent round of key / value loads, then half as long: a 128-token split's value parts
+// are its 16 preloaded rows and one round of 16) while the launch's workgroups fit the CUs at two each (16
+// waves: more would run in a second round), else 256. Measured on the whole Qwen-1.5B-shaped token (12 / 2 heads
+// of 128 lanes): 1,420 against 1,460 us at 4,095 tokens (32 splits of 128); 512 threads at 96-token splits
+// (3,072 tokens) measured slower, 1,514 against 1,462 (their 24-row value parts end in 8 rows read one at a
+// time), and at 8,191 tokens (768 workgroups) 1,648 against 1,556.
+constexpr int kWideSplitTokens = 128;
+
+int device_cus() {
+    int device = 0, cus = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+        return 256;
+    return cus;
+}
+
+int split_threads(int per, int workgroups) {
+    return per >= kWideSplitTokens && workgroups <= 2 * device_cus() ? 512 : 256;
+}
+
 size_t split_lds_bytes(int per, int head_dim) {
     return static_cast<size_t>(per) * sizeof(double) +
            (head_dim <= kStagedQuery ? static_cast<size_t>(head_dim) * sizeof(float) : 0);
@@ -930,7 +981,7 @@ bool attention_supported(int tokens, int head_dim) {
     const int splits = attention_splits(tokens);
     if (splits == 1) return true;
     const int per = (tokens + splits - 1) / splits;
-    return split_lds_bytes(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
+    return split_lds_bytes(per, head_dim) + 512 * sizeof(double) <= 64 * 1024;  // either workgroup size
 }
 
 namespace {
@@ -951,7 +1002,7 @@ bool decode_fusable(int tokens, int head_dim) {
     const int splits = attention_splits(tokens);
     if (splits == 1 || head_dim > kSplitThreads || (tokens + splits - 1) / splits > kFusedSplitTokens) return false;
     const int per = (tokens + splits - 1) / splits;
-    return split_lds_bytes_inputs(per, head_dim) + kSplitThreads * sizeof(double) <= 64 * 1024;
+    return split_lds_bytes_inputs(per, head_dim) + 512 * sizeof(double) <= 64 * 1024;  // either workgroup size
 }
 
 }  // namespace
@@ -980,9 +1031,14 @@ hipError_t launch_attention_decode(float* q, const float* q_bias, const float* k
     const int splits = attention_splits(tokens);
     const int per = (tokens + splits - 1) / splits;
     const DecodeInputs in{q_bias, k_new, k_bias, v_new, v_bias, rope, position, rotary, base};
-    attention_split_kernel<true><<<split_grid(query_heads, kv_heads, splits), kSplitThreads,
-                                   split_lds_bytes_inputs(per, head_dim), stream>>>(
-        q, k_cache, v_cache, query_heads, kv_heads, head_dim, tokens, per, splits, partials, in, k_cache, v_cache);
+    const int grid = split_grid(query_heads, kv_heads, splits);
+    const size_t lds = split_lds_bytes_inputs(per, head_dim);
+    if (split_threads(per, grid) == 512)
+        attention_split_kernel<true, 512><<<grid, 512, lds, stream>>>(q, k_cache, v_cache, query_heads, kv_heads, head_dim,
+                                                                    tokens, per, splits, partials, in, k_cache, v_cache);
+    else
+        attention_split_kernel<true, 256><<<grid, 256, lds, stream>>>(q, k_cache, v_cache, query_heads, kv_heads, head_dim,
+                                                                    tokens, per, splits, partials, in, k_cache, v_cache);
     attention_combine_kernel<true><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out, q, in);
     return hipGetLastError();
 }
@@ -998,9 +1054,16 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, int 
     }
     if (!partials) return hipErrorInvalidValue;
     const int per = (tokens + splits - 1) / splits;
-    attention_split_kernel<false><<<split_grid(query_heads, kv_heads, splits), kSplitThreads,
-                                    split_lds_bytes(per, head_dim), stream>>>(
-        q, k, v, query_heads, kv_heads, head_dim, tokens, per, splits, partials, DecodeInputs{}, nullptr, nullptr);
+    const int grid = split_grid(query_heads, kv_heads, splits);
+    const size_t lds = split_lds_bytes(per, head_dim);
+    if (split_threads(per, grid) == 512)
+        attention_split_kernel<false, 512><<<grid, 512, lds, stream>>>(q, k, v, query_heads, kv_heads, head_dim, tokens,
+                                                                     per, splits, partials, DecodeInputs{}, nullptr,
+                                                                     nullptr);
+    else
+        attention_split_kernel<false, 256><<<grid, 256, lds, stream>>>(q, k, v, query_heads, kv_heads, head_dim, tokens,
+                                                                     per, splits, partials, DecodeInputs{}, nullptr,
+                                                                     nullptr);
     attention_combine_kernel<false><<<query_heads, kSplitThreads, 0, stream>>>(partials, splits, head_dim, out,
                                                                               nullptr, DecodeInputs{});
     return hipGetLastError();

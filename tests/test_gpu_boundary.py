@@ -294,10 +294,13 @@ def test_attention_long_prefixes_match_oracle(context, tokens):
 
 @pytest.mark.parametrize("head_dim,tokens,query_heads,kv_heads", [(80, 300, 14, 2), (80, 7000, 4, 1),
                                                                   (24, 100, 3, 3), (1024, 100, 4, 2),
-                                                                  (8320, 40, 2, 1), (130, 33, 6, 3)])
+                                                                  (8320, 40, 2, 1), (130, 33, 6, 3),
+                                                                  (1024, 4096, 2, 1), (200, 4096, 2, 1),
+                                                                  (8320, 4096, 2, 1)])
 def test_attention_odd_head_widths_match_oracle(context, head_dim, tokens, query_heads, kv_heads):
-    # Head widths whose eighths are not whole 16-byte quads (80, 24, 130), wider than one workgroup's lanes
-    # (1024) and wider than the staged query (8,320 lanes: read from global memory).
+    # Head widths whose eighths are not whole 16-byte quads (80, 24, 130, 200), wider than one workgroup's lanes
+    # (1024) and wider than the staged query (8,320 lanes: read from global memory); at 4,096 and 7,000 tokens
+    # the splits hold 128 tokens and run on 512-thread workgroups (four token parts per lane).
     g = rng(head_dim * 7 + tokens)
     q = g.standard_normal(query_heads * head_dim).astype(np.float32)
     keys = (g.standard_normal(tokens * kv_heads * head_dim) * 0.2).astype(np.float32)
