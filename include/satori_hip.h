@@ -76,6 +76,10 @@ int satori_hip_device_count(int* count);
 /* ---- context: stands in for VulkanContext.TryCreate / Dispose
  *      (src/Satori.Backends.Vulkan/VulkanContext.cs:57), the IQuantizedMatrixFactory owner ---- */
 
+/* Besides its stream, a context keeps grow-only device buffers until it is destroyed: the host-call staging
+ * of inputs and outputs, the split-attention partials per stream, and the upload staging of the formats
+ * regrouped on the device (Ternary2, bitplanes, Q6_K, Q8_0, Q4_0: at most 64 MB, or one 64-row Ternary2
+ * panel of a wider matrix). */
 int satori_hip_context_create(int device, satori_hip_context** context);
 /* Idempotent: NULL is accepted. Matrices created on the context must be destroyed first. */
 int satori_hip_context_destroy(satori_hip_context* context);
