@@ -24,6 +24,8 @@
 // chains over the block's K steps and one combination, 128 hi + lo.
 #include <type_traits>
 
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "q8k_device.hpp"
@@ -302,6 +304,9 @@ __device__ __forceinline__ void block_terms(PlaneRegs& r, const uint8_t* next, c
                                             float (&term)[16]) {
     const int h = lane >> 5;
     i32x16 hi = {}, lo = {};
+    // The next block's d is requested before its planes, so the wait for it at the end leaves them in flight.
+    const float d = r.d;
+    const float d_next = load_plane_d(next, lane);
     i32x4 c_next = staged_codes16(sb, 0, lane);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -311,10 +316,9 @@ __device__ __forceinline__ void block_terms(PlaneRegs& r, const uint8_t* next, c
         lo = mfma32(c, r.w[1][j], lo);
         r.w[0][j] = load_plane(next, 0, j, lane);
         r.w[1][j] = load_plane(next, 1, j, lane);
-        __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, a block ahead of its use
+        __builtin_amdgcn_sched_barrier(0);  // the refill is issued here, ahead of its use
     }
-    const float d = r.d;
-    r.d = load_plane_d(next, lane);
+    r.d = d_next;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const f32x4 a4 = staged_scales(sb, q, h);
@@ -373,38 +377,44 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
     // Staging of round k (blocks kS .. kS + S - 1): thread i holds bytes [16i, 16i + 16) and [4096 + 16i, +16)
     // of each block's codes (16-byte slices at a 16-byte stride: the LDS writes of a wave touch every bank once
     // per pass), bytes [4i, 4i + 4) of its group sums and, for i < 8 S, four scales.
+    // With the weight planes (EXACT) every thread issues and stores the same bytes whatever k: blocks past the
+    // last read (and store into their unused slots) the last block's bytes, and threads past the first 8 S
+    // repeat thread i mod 8 S's scales. With no branch around them the compiler counts the loads in flight
+    // exactly, and its waits leave the planes two blocks ahead in flight (below).
+    constexpr bool EXACT = FORMAT == kQ6_K;
     u32x4 sc0[S], sc1[S];
     uint32_t ssum[S];
     u32x4 sscale = {0u, 0u, 0u, 0u};
     auto stage_load = [&](int k) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const int b = k * S + s;
-            if (b < blocks) {
+            const int b = EXACT ? min(k * S + s, blocks - 1) : k * S + s;
+            if (EXACT || b < blocks) {
                 const uint8_t* src = codes + (static_cast<int64_t>(b) * tiles + t) * 8192 + 16 * threadIdx.x;
                 sc0[s] = load16_a4(src);
                 sc1[s] = load16_a4(src + 4096);
                 ssum[s] = load4_a4(sums + (static_cast<int64_t>(b) * tiles + t) * 1024 + 4 * threadIdx.x);
             }
         }
-        if (threadIdx.x < 8 * S) {
-            const int s = threadIdx.x >> 3, b = k * S + s;
-            if (b < blocks)
-                sscale = load16_a4(reinterpret_cast<const uint8_t*>(scales + (static_cast<int64_t>(b) * tiles + t) * 32 +
-                                                                    4 * (threadIdx.x & 7)));
+        const int q = EXACT ? static_cast<int>(threadIdx.x & (8 * S - 1)) : static_cast<int>(threadIdx.x);
+        if (EXACT || q < 8 * S) {
+            const int b = EXACT ? min(k * S + (q >> 3), blocks - 1) : k * S + (q >> 3);
+            if (EXACT || b < blocks)
+                sscale = load16_a4(
+                    reinterpret_cast<const uint8_t*>(scales + (static_cast<int64_t>(b) * tiles + t) * 32 + 4 * (q & 7)));
         }
     };
     auto stage_store = [&](int k) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            if (k * S + s < blocks) {
+            if (EXACT || k * S + s < blocks) {
                 *reinterpret_cast<u32x4*>(stage[s].codes + 16 * threadIdx.x) = sc0[s];
                 *reinterpret_cast<u32x4*>(stage[s].codes + 4096 + 16 * threadIdx.x) = sc1[s];
                 *reinterpret_cast<uint32_t*>(stage[s].sums + 4 * threadIdx.x) = ssum[s];
             }
         }
-        if (threadIdx.x < 8 * S)
-            *reinterpret_cast<u32x4*>(stage[threadIdx.x >> 3].scales + 4 * (threadIdx.x & 7)) = sscale;
+        const int q = EXACT ? static_cast<int>(threadIdx.x & (8 * S - 1)) : static_cast<int>(threadIdx.x);
+        if (EXACT || q < 8 * S) *reinterpret_cast<u32x4*>(stage[q >> 3].scales + 4 * (q & 7)) = sscale;
     };
 
     // This way's accumulators: outputs way * kOwned + o of the lane (all 16 for S = 1), quads
@@ -476,29 +486,43 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
         if (k < rounds) round(k, ra, rb);
     } else {
         // The row tile's plane records (a tile past the last computes on the last one and stores nothing).
-        // Round k: this way's block k S + way; its block terms refill the plane registers with the way's next
-        // block (k + 1) S + way while they run.
+        // With two or more ways (two waves per SIMD, 256 VGPRs) two plane register sets alternate: round k (this
+        // way's block k S + way) reads set k mod 2 and refills it with block (k + 2) S + way while it runs, so
+        // each block's planes are requested two rounds ahead; the next round's codes are requested once the
+        // block's products are done (their registers are then not live beside the accumulators and both plane
+        // sets). One way (three workgroups per CU) keeps one set, refilled a round ahead. Every round computes
+        // its block and stages the next round, past the last ones too (their bytes are the last block's, and
+        // their terms are dropped), so every path issues the same loads.
+        constexpr bool kTwoAhead = S >= 2;
         const int row_tiles = (rows + kTile - 1) / kTile;
         const uint8_t* tile_rec =
             m.w + static_cast<int64_t>(min(group * SP::R + rt, row_tiles - 1)) * blocks * kPlaneRecord;
         auto rec = [&](int b) { return tile_rec + static_cast<int64_t>(min(b, blocks - 1)) * kPlaneRecord; };
-        PlaneRegs r;
-        auto round = [&](int k) {
+        auto round = [&](int k, PlaneRegs& r) {
             __syncthreads();
             stage_store(k);
-            if (k + 1 < rounds) stage_load(k + 1);
+            stage_load(min(k + 1, rounds - 1));
             __syncthreads();
             const int b = k * S + way;
             float term[16];
-            if (b < blocks)
-                block_terms(r, rec(b + S), stage[way], lane, term);
-            else
-                zero(term);
+            block_terms(r, rec(b + (kTwoAhead ? 2 : 1) * S), stage[way], lane, term);
+            if (b >= blocks) zero(term);
             add_round(term);
         };
+        PlaneRegs ra, rb;
         stage_load(0);
-        load_planes(rec(way), lane, r);
-        for (int k = 0; k < rounds; ++k) round(k);
+        load_planes(rec(way), lane, ra);
+        if constexpr (kTwoAhead) {
+            load_planes(rec(way + S), lane, rb);
+            int k = 0;
+            for (; k + 1 < rounds; k += 2) {
+                round(k, ra);
+                round(k + 1, rb);
+            }
+            if (k < rounds) round(k, ra);
+        } else {
+            for (int k = 0; k < rounds; ++k) round(k, ra);
+        }
     }
 
     if (row >= rows) return;
@@ -535,7 +559,9 @@ template <int FORMAT>
 void launch_format(KmfmaArgs& a, hipStream_t stream) {
     long wave_tiles = 0;
     for (int i = 0; i < a.count; ++i) wave_tiles += static_cast<long>((a.m[i].rows + kTile - 1) / kTile) * a.tiles;
-    switch (choose_split(wave_tiles, a.blocks)) {
+    // Weight planes: at most two ways, whose 256-VGPR budget holds two plane sets (four ways would spill).
+    const int split = choose_split(wave_tiles, a.blocks);
+    switch (FORMAT == kQ6_K ? std::min(split, 2) : split) {
         case 1: launch_split<FORMAT, 1>(a, stream); break;
         case 2: launch_split<FORMAT, 2>(a, stream); break;
         default: launch_split<FORMAT, 4>(a, stream); break;
