@@ -486,13 +486,13 @@ __global__ __launch_bounds__(256, S == 1 ? 3 : 2) void kmfma_kernel(KmfmaArgs a)
         if (k < rounds) round(k, ra, rb);
     } else {
         // The row tile's plane records (a tile past the last computes on the last one and stores nothing).
-        // With two or more ways (two waves per SIMD, 256 VGPRs) two plane register sets alternate: round k (this
-        // way's block k S + way) reads set k mod 2 and refills it with block (k + 2) S + way while it runs, so
-        // each block's planes are requested two rounds ahead; the next round's codes are requested once the
-        // block's products are done (their registers are then not live beside the accumulators and both plane
-        // sets). One way (three workgroups per CU) keeps one set, refilled a round ahead. Every round computes
-        // its block and stages the next round, past the last ones too (their bytes are the last block's, and
-        // their terms are dropped), so every path issues the same loads.
+        // With two ways (two waves per SIMD, 256 VGPRs; launch_format caps the planes at two) two plane register
+        // sets alternate: round k (this way's block k S + way) reads set k mod 2 and refills it with block
+        // (k + 2) S + way while it runs, so each block's planes are requested two rounds ahead, after the next
+        // round's codes (a wait for those leaves the planes in flight). One way (three workgroups per CU) keeps
+        // one set, refilled a round ahead. Every round computes its block and stages the next round, past the
+        // last ones too (their bytes are the last block's, and their terms are dropped), so every path issues the
+        // same loads.
         constexpr bool kTwoAhead = S >= 2;
         const int row_tiles = (rows + kTile - 1) / kTile;
         const uint8_t* tile_rec =
