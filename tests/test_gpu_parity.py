@@ -1216,6 +1216,37 @@ def test_ternary2_upload_in_several_staged_chunks(context):
         context.create_ternary2(rows, columns, block, bad).dispose()
 
 
+@pytest.mark.parametrize("fmt", [BQ.Q8_0, BQ.Q4_0])
+def test_legacy_upload_in_several_staged_chunks(context, fmt):
+    # Q8_0 / Q4_0 payloads larger than the 64 MB staging chunk are regrouped block range by block range
+    # (16,384 x 4,096 Q8_0: 71 MB, two chunks; Q4_0 32,768 x 4,096: 75 MB); rows on both sides of every chunk
+    # boundary and the last row equal the oracle's scalar product within the reference's bound.
+    rows = 16384 if fmt == BQ.Q8_0 else 32768
+    columns = 4096
+    block_bytes = 34 if fmt == BQ.Q8_0 else 18
+    g = rng(9393 + int(fmt))
+    w = g.standard_normal((rows, columns), dtype=np.float32) * 0.02
+    data = S.quantize_weights(w, rows, columns, fmt)
+    del w
+    assert data.size > 64 << 20
+    x = g.standard_normal(columns).astype(np.float32)
+    with context.create(data, S.QuantizedMatrixShape(rows, columns, fmt)) as m:
+        y = np.zeros(rows, np.float32)
+        m.execute(x, y)
+    per_chunk = (64 << 20) // block_bytes  # blocks of one staged chunk
+    blocks_per_row = columns // 32
+    edges = {0, rows - 1}
+    for c in range(1, (rows * blocks_per_row + per_chunk - 1) // per_chunk):
+        r = c * per_chunk // blocks_per_row
+        edges.update({max(r - 1, 0), r, min(r + 1, rows - 1)})
+    sample = np.array(sorted(edges))
+    row_bytes = blocks_per_row * block_bytes
+    sub = np.concatenate([data[r * row_bytes:(r + 1) * row_bytes] for r in sample])
+    want = O.q_matvec_scalar(sub, sample.size, columns, int(fmt), x)
+    wq = O.decode_matrix(sub, sample.size, columns, int(fmt))
+    assert_within(y[sample], want, relative_bound(wq, x) + columns * TINY, f"{fmt.name} rows {sample.tolist()}")
+
+
 def test_k_batch_rejects_too_many_positions(context):
     data = S.quantize_weights(np.zeros((2, 256), np.float32), 2, 256, BQ.Q4_K)
     m = context.create(data, S.QuantizedMatrixShape(2, 256, BQ.Q4_K))
