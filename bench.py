@@ -1262,7 +1262,7 @@ def run(args, ctx, events) -> int:
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
-            "kernel": "t2_kernel<128, 8> + t2_fixup_kernel<8> (one grouped launch)",
+            "kernel": "t2_kernel<128, 16> + t2_fixup_kernel<16> (one grouped launch)",
             "launch_us": round(headline["launch_us"], 2),
             "algorithmic_bytes_per_launch": headline["copies"] * int(payload.size),
         },

@@ -129,7 +129,7 @@ struct T2Fixup {
 
 struct T2Plan {
     int rows_max, columns, block_size, count, positions;  // what the plan was made for
-    int waves;                                            // waves per workgroup: 4 or 8 (sliced: 1-16)
+    int waves;                                            // waves per workgroup: 4, 8 or 16 (sliced: 1-16)
     int workgroups;                                       // ranges (one workgroup each)
     int staged_tiles;                                     // longest segment: activation tiles staged in LDS
     int fixups;                                           // items cut between ranges

@@ -176,9 +176,10 @@ def test_ternary2_grouped_pair_tables(context, block, columns, members):
 
 
 # Groups whose ranges cut items into two pieces (the pieces' row sums are added by the fix-up kernel). 64 members
-# of 4096^2 make 16,384 (panel group, tile) units over 1,024 workgroups: every range is exactly half an item, a
-# lone earlier or later piece; 160 members make 40,960 units, 40 a range, so a range holds a whole item and an
-# item's earlier tiles, or a later piece and an earlier piece. Each group runs eagerly twice and replays three
+# of 4096^2 make 16,384 (panel group, tile) units over 1,024 workgroups of eight waves (B = 64, 256): every range
+# is exactly half an item, a lone earlier or later piece; 160 members make 40,960 units, 40 a range, so a range
+# holds a whole item and an item's earlier tiles, or a later piece and an earlier piece. B = 128 takes
+# sixteen-wave workgroups here: items of 16 panels, half the units over half the workgroups, the same cuts. Each group runs eagerly twice and replays three
 # times from a captured step, with eager launches between the replays; every launch gives the eager bits, within
 # the reference's bound of the scalar restatement and of the FP64 product.
 @pytest.mark.parametrize("members", [64, 160])
