@@ -113,7 +113,7 @@ def _t2_random_payload(g, rows: int, columns: int, block: int) -> np.ndarray:
 
 
 # Ternary2 launches split the columns over workgroups (a second kernel adds the splits) unless the rows
-# alone give about 1024 workgroups of 4 or 8 panels of 64 rows. Small shapes above cover the split plans;
+# alone give about 1024 workgroups of 4, 8 or 16 panels of 64 rows. Small shapes above cover the split plans;
 # the tests below cover the unsplit ones (one and two panels per wave) through very tall matrices and
 # grouped launches, with ragged columns, an odd block count for B = 64, members whose rows end inside a
 # panel, the widest slice one workgroup stages (14,336 columns) and a grouped launch split for width.
